@@ -1,0 +1,300 @@
+// attention.hip -- GQA single-token decode attention over the f32 KV cache.
+//
+// Semantics (crates/atlas-model/src/lib.rs:689-721; GPU contract
+// crates/atlas-tensor/src/lib.rs:743-770): for query head h with KV head
+// kvh = h / (n_heads / n_kv), s_t = (q_h . k_t) * scale for t in [t_lo, pos]
+// where t_lo = pos - window + 1 when window > 0 (positions with
+// pos - t >= window are masked out), p = softmax(s), o_h = sum_t p_t v_t.
+// Cache layout [max_seq][n_kv][head_dim] f32 (lib.rs:557-596).
+//
+// Design (split-K flash decode, HBM-bound):
+//  * grid (n_kv, n_splits); a 256-thread block owns one KV head and one
+//    contiguous slice of positions, and serves all G = n_heads / n_kv query
+//    heads of that group from a single read of each K/V row (the reference
+//    kernel re-reads K/V once per query head);
+//  * 16 lanes per position (head_dim / 16 dims each, 128-bit loads), so a
+//    wave covers 4 positions per row step and P of them per iteration; each
+//    lane keeps an online-softmax state (max, sum, partial output) per head;
+//  * scores use exp2 with log2(e) folded into the scale; the SWA start index
+//    is computed, not masked;
+//  * per block, the 16 (wave, row) states merge through LDS into one partial
+//    (m, l, o) per head and split; attn_combine merges the splits.
+//  * the split count is fixed at launch and `pos` may come from device
+//    memory, so the same launch can be captured once and replayed per token.
+#include "common.hpp"
+#include "attention.hpp"
+
+namespace atlas {
+
+__device__ __forceinline__ int load_pos(const int* pos_dev, int pos) {
+    return pos_dev ? *pos_dev : pos;
+}
+
+template <int HD, int G, int P>
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+    constexpr int DPL = HD / 16;              // dims per lane
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int kvh = blockIdx.x, split = blockIdx.y, n_splits = gridDim.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = lane >> 4, dl = lane & 15;     // position row, dim group
+    const int pos = load_pos(a.pos_dev, a.pos);
+    const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
+    const int ctx = pos - t_lo + 1;
+    const int chunk = (ctx + n_splits - 1) / n_splits;
+    const int b0 = t_lo + split * chunk;
+    const int b1 = min(pos + 1, b0 + chunk);
+    const long kv_stride = (long)a.n_kv * HD;
+    const float sc = a.scale * LOG2E;
+
+    // q for the G heads of this group, this lane's dims
+    float q[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float* qh = a.q + (long)(kvh * G + h) * HD + dl * DPL;
+#pragma unroll
+        for (int d = 0; d < DPL; d += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(qh + d);
+            q[h][d] = v.x * sc; q[h][d + 1] = v.y * sc; q[h][d + 2] = v.z * sc; q[h][d + 3] = v.w * sc;
+        }
+    }
+    float m[G], l[G], o[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        m[h] = -INFINITY; l[h] = 0.f;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
+    }
+
+    const float* kbase = a.k_cache + (long)kvh * HD + dl * DPL;
+    const float* vbase = a.v_cache + (long)kvh * HD + dl * DPL;
+    // positions handled by (wave, row): t = b0 + 16*P*it + (wave*4 + row)*P + i
+    for (int t0 = b0 + (wave * 4 + row) * P; t0 < b1; t0 += 16 * P) {
+        float kf[P][DPL], vf[P][DPL];
+        bool valid[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int t = t0 + i;
+            valid[i] = t < b1;
+            const long off = (long)(valid[i] ? t : t0) * kv_stride;
+#pragma unroll
+            for (int d = 0; d < DPL; d += 4) {
+                const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off + d);
+                const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off + d);
+                kf[i][d] = kv.x; kf[i][d + 1] = kv.y; kf[i][d + 2] = kv.z; kf[i][d + 3] = kv.w;
+                vf[i][d] = vv.x; vf[i][d + 1] = vv.y; vf[i][d + 2] = vv.z; vf[i][d + 3] = vv.w;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float s[P];
+            float smax = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                float acc = 0.f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) acc += q[h][d] * kf[i][d];
+                acc = row16_sum(acc);
+                s[i] = valid[i] ? acc : -INFINITY;
+                smax = fmaxf(smax, s[i]);
+            }
+            const float mn = fmaxf(m[h], smax);
+            // mn is finite: position t0 is always valid
+            const float corr = exp2f(m[h] - mn);
+            float psum = 0.f;
+            float p[P];
+#pragma unroll
+            for (int i = 0; i < P; ++i) { p[i] = exp2f(s[i] - mn); psum += p[i]; }
+            l[h] = l[h] * corr + psum;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                float acc = o[h][d] * corr;
+#pragma unroll
+                for (int i = 0; i < P; ++i) acc += p[i] * vf[i][d];
+                o[h][d] = acc;
+            }
+            m[h] = mn;
+        }
+    }
+
+    // ---- merge the 16 (wave,row) states of this block through LDS ---------
+    __shared__ float s_m[16][G], s_l[16][G];
+    __shared__ float s_o[16][G][HD];
+    const int st = wave * 4 + row;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        if (dl == 0) { s_m[st][h] = m[h]; s_l[st][h] = l[h]; }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) s_o[st][h][dl * DPL + d] = o[h][d];
+    }
+    __syncthreads();
+    // thread -> (head, dim) pairs
+    for (int e = threadIdx.x; e < G * HD; e += 256) {
+        const int h = e / HD, d = e % HD;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) mx = fmaxf(mx, s_m[s2][h]);
+        float lsum = 0.f, osum = 0.f;
+        if (mx != -INFINITY) {
+#pragma unroll
+            for (int s2 = 0; s2 < 16; ++s2) {
+                const float w = exp2f(s_m[s2][h] - mx);   // 0 for empty states
+                lsum += s_l[s2][h] * w;
+                osum += s_o[s2][h][d] * w;
+            }
+        }
+        const int qh = kvh * G + h;
+        if (n_splits == 1) {
+            a.out[(long)qh * HD + d] = osum / lsum;
+        } else {
+            const long pi = (long)qh * n_splits + split;
+            a.part_o[pi * HD + d] = osum;
+            if (d == 0) { a.part_m[pi] = mx; a.part_l[pi] = lsum; }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int n_splits, int hd) {
+    const int qh = blockIdx.x;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float mx = -INFINITY;
+        for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, a.part_m[(long)qh * n_splits + s]);
+        float lsum = 0.f, osum = 0.f;
+        for (int s = 0; s < n_splits; ++s) {
+            const long pi = (long)qh * n_splits + s;
+            const float mm = a.part_m[pi];
+            if (mm == -INFINITY) continue;
+            const float w = exp2f(mm - mx);
+            lsum += a.part_l[pi] * w;
+            osum += a.part_o[pi * hd + d] * w;
+        }
+        a.out[(long)qh * hd + d] = osum / lsum;
+    }
+}
+
+// Any head_dim / group size: one block per query head, online softmax over
+// all positions with a wave per position slice (used for small test shapes).
+__global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
+    const int h = blockIdx.x;
+    const int group = a.n_heads / a.n_kv;
+    const int kvh = h / group;
+    const int pos = load_pos(a.pos_dev, a.pos);
+    const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float* qh = a.q + (long)h * hd;
+    const long kv_stride = (long)a.n_kv * hd;
+    __shared__ float s_m[4], s_l[4];
+    __shared__ float s_o[4][256];
+    // each wave handles positions t = t_lo + wave, +4, ...; lanes split dims
+    float m = -INFINITY, l = 0.f;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};   // dims lane + 64*j (hd <= 256)
+    for (int t = t_lo + wave; t <= pos; t += 4) {
+        const float* kt = a.k_cache + (long)t * kv_stride + (long)kvh * hd;
+        const float* vt = a.v_cache + (long)t * kv_stride + (long)kvh * hd;
+        float part = 0.f;
+        for (int d = lane; d < hd; d += 64) part += qh[d] * kt[d];
+        const float s = wave_sum(part) * a.scale;
+        const float mn = fmaxf(m, s);
+        const float corr = expf(m - mn), p = expf(s - mn);
+        l = l * corr + p;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            o[j] = o[j] * corr + (d < hd ? p * vt[d] : 0.f);
+        }
+        m = mn;
+    }
+    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < hd) s_o[wave][lane + 64 * j] = o[j];
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += 256) {
+        float mx = -INFINITY;
+        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w]);
+        float ls = 0.f, os = 0.f;
+        for (int w = 0; w < 4; ++w) {
+            if (s_m[w] == -INFINITY) continue;
+            const float wt = expf(s_m[w] - mx);
+            ls += s_l[w] * wt;
+            os += s_o[w][d] * wt;
+        }
+        a.out[(long)h * hd + d] = os / ls;
+    }
+}
+
+// ---------------------------------------------------------------------------
+
+static float* g_part = nullptr;
+static size_t g_part_bytes = 0;
+
+int attn_reserve(int n_heads, int head_dim, int n_splits) {
+    const size_t need = (size_t)n_heads * n_splits * (head_dim + 2) * sizeof(float);
+    if (need <= g_part_bytes) return ATLAS_OK;
+    if (g_part) {
+        ATLAS_HIP(hipDeviceSynchronize());
+        ATLAS_HIP(hipFree(g_part));
+        g_part = nullptr;
+        g_part_bytes = 0;
+    }
+    ATLAS_HIP(hipMalloc((void**)&g_part, need));
+    g_part_bytes = need;
+    return ATLAS_OK;
+}
+
+int attn_pick_splits(int n_kv, int max_ctx) {
+    // ~2 blocks per CU, each with at least 64 positions
+    int want = (2 * device_cu_count() + n_kv - 1) / n_kv;
+    int cap = (max_ctx + 63) / 64;
+    int s = want < cap ? want : cap;
+    if (s > 128) s = 128;
+    return s < 1 ? 1 : s;
+}
+
+template <int HD, int G>
+static int launch_split(AttnArgs a, int n_splits, hipStream_t st) {
+    hipLaunchKernelGGL((attn_split_kernel<HD, G, 4>), dim3(a.n_kv, n_splits), dim3(256), 0, st, a);
+    ATLAS_LAUNCH_CHECK("attn_split");
+    if (n_splits > 1) {
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_heads), dim3(HD < 256 ? HD : 256), 0, st,
+                           a, n_splits, HD);
+        ATLAS_LAUNCH_CHECK("attn_combine");
+    }
+    return ATLAS_OK;
+}
+
+int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
+    ATLAS_REQUIRE(a.n_heads > 0 && a.n_kv > 0 && a.n_heads % a.n_kv == 0,
+                  "attention: n_heads %d not a multiple of n_kv %d", a.n_heads, a.n_kv);
+    ATLAS_REQUIRE(a.head_dim > 0 && a.head_dim <= 256, "attention: head_dim %d", a.head_dim);
+    ATLAS_REQUIRE(a.pos_dev || a.pos >= 0, "attention: pos < 0");
+    ATLAS_REQUIRE(a.q && a.k_cache && a.v_cache && a.out, "attention: null pointer");
+    const int G = a.n_heads / a.n_kv;
+    const bool aligned =
+        (((uintptr_t)a.q | (uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 15) == 0;
+    const bool fast = aligned && (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) &&
+                      (G == 1 || G == 2 || G == 4 || G == 8);
+    if (!fast) {
+        hipLaunchKernelGGL(attn_generic_kernel, dim3(a.n_heads), dim3(256), 0, st, a, a.head_dim);
+        ATLAS_LAUNCH_CHECK("attn_generic");
+        return ATLAS_OK;
+    }
+    if (n_splits < 1) n_splits = 1;
+    if (n_splits > 1) {
+        int rc = attn_reserve(a.n_heads, a.head_dim, n_splits);
+        if (rc) return rc;
+        a.part_m = g_part;
+        a.part_l = g_part + (size_t)a.n_heads * n_splits;
+        a.part_o = g_part + (size_t)2 * a.n_heads * n_splits;
+    }
+#define ATLAS_ATTN_CASE(HDV, GV) \
+    if (a.head_dim == HDV && G == GV) return launch_split<HDV, GV>(a, n_splits, st);
+    ATLAS_ATTN_CASE(128, 1) ATLAS_ATTN_CASE(128, 2) ATLAS_ATTN_CASE(128, 4) ATLAS_ATTN_CASE(128, 8)
+    ATLAS_ATTN_CASE(64, 1)  ATLAS_ATTN_CASE(64, 2)  ATLAS_ATTN_CASE(64, 4)  ATLAS_ATTN_CASE(64, 8)
+    ATLAS_ATTN_CASE(256, 1) ATLAS_ATTN_CASE(256, 2) ATLAS_ATTN_CASE(256, 4)
+#undef ATLAS_ATTN_CASE
+    hipLaunchKernelGGL(attn_generic_kernel, dim3(a.n_heads), dim3(256), 0, st, a, a.head_dim);
+    ATLAS_LAUNCH_CHECK("attn_generic");
+    return ATLAS_OK;
+}
+
+}  // namespace atlas

@@ -1,0 +1,117 @@
+// common.hpp -- shared helpers for the gfx950 decode kernels.
+//
+// Error model: every C-ABI entry point returns 0 on success or a negative
+// ATLAS_E* code and records a message retrievable with atlas_last_error()
+// (thread-local).  Entry points that keep the reference's `void` signature
+// record the error the same way.  Launches go to the library's current
+// stream (atlas_set_stream; default: the null stream, as the reference uses).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/atlas_kernels.h"   // ATLAS_OK / ATLAS_E* codes
+
+#define ATLAS_API extern "C" __attribute__((visibility("default")))
+
+namespace atlas {
+
+void set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+hipStream_t stream();          // current launch stream
+int device_cu_count();         // CUs of the current device (cached)
+
+// Check a HIP call; on failure record the error and return ATLAS_EHIP.
+#define ATLAS_HIP(call)                                                        \
+    do {                                                                       \
+        hipError_t e_ = (call);                                                \
+        if (e_ != hipSuccess) {                                                \
+            ::atlas::set_error(ATLAS_EHIP, "%s: %s (%s:%d)", #call,            \
+                               hipGetErrorString(e_), __FILE__, __LINE__);     \
+            return ATLAS_EHIP;                                                 \
+        }                                                                      \
+    } while (0)
+
+// Check a kernel launch.
+#define ATLAS_LAUNCH_CHECK(name)                                               \
+    do {                                                                       \
+        hipError_t e_ = hipGetLastError();                                     \
+        if (e_ != hipSuccess) {                                                \
+            ::atlas::set_error(ATLAS_EHIP, "launch %s: %s", name,              \
+                               hipGetErrorString(e_));                         \
+            return ATLAS_EHIP;                                                 \
+        }                                                                      \
+    } while (0)
+
+#define ATLAS_REQUIRE(cond, ...)                                               \
+    do {                                                                       \
+        if (!(cond)) {                                                         \
+            ::atlas::set_error(ATLAS_EINVAL, __VA_ARGS__);                     \
+            return ATLAS_EINVAL;                                               \
+        }                                                                      \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+// bf16 bits -> f32 is a 16-bit left shift (kernels/matmul.cu:321-323).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Sign-extended byte i of w as f32 (one v_cvt_f32_i32 with SDWA byte select).
+__device__ __forceinline__ float s8_at(uint32_t w, int i) {
+    return (float)(int8_t)(w >> (8 * i));
+}
+
+// Wave64 all-lanes sum through DPP: quad swaps, half-row and row mirrors,
+// then row broadcasts 15 and 31 fold the four rows into lane 63, which is
+// read back into every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+    int x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false)); // row_half_mirror
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false)); // row_mirror
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false)); // row_bcast15
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false)); // row_bcast31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum over the 16 lanes of each DPP row; every lane of the row gets it.
+__device__ __forceinline__ float row16_sum(float v) {
+    int x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false));
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false));
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Nontemporal 128-bit load: weights are streamed once per token, so keep
+// them from displacing the activations and KV tiles that are re-read.
+__device__ __forceinline__ u32x4 ldg_stream(const u32x4* p) {
+    return __builtin_nontemporal_load(p);
+}
+
+}  // namespace atlas

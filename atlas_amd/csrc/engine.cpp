@@ -1,0 +1,1249 @@
+// engine.cpp -- MI355X decode engine behind include/atlas_engine.h.
+//
+// Host-side mirror of the reference's decode orchestration
+// (crates/atlas-model/src/lib.rs: OlmoModel 1298-2009, TransformerBlock
+// 982-1091, Attention 598-870, FeedForward 882-924; crates/atlas-infer:
+// InferEngine::generate and StigmergicHook), re-laid out for one MI355X:
+//
+//  * weights live in HBM in the stored format (bf16 / int8 / int4), with
+//    wq|wk|wv concatenated into one [d + 2*kv_dim, d] matrix and gate/up rows
+//    interleaved (gate_i, up_i) so one GEMV launch yields silu(gate)*up;
+//  * one decode step = embed gather, per layer {QKV GEMV, QK-norm+RoPE+KV
+//    write, split-K attention, W_o GEMV, residual RMSNorm, SwiGLU GEMV,
+//    W_down GEMV, residual RMSNorm}, final RMSNorm, lm_head GEMV and (greedy)
+//    device argmax -- no per-op allocation (the reference allocates a fresh
+//    buffer per op, crates/atlas-tensor/src/lib.rs:196-206);
+//  * the step reads its token and position from device memory, so it is
+//    captured once in a HIP graph and replayed per token; greedy decode needs
+//    no host round trip per token (the reference downloads 401 KB of logits
+//    per token, lib.rs:1504);
+//  * sampling with temperature runs the reference's host pipeline on the
+//    downloaded logits (lib.rs:1652-1711).
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/atlas_engine.h"
+#include "attention.hpp"
+#include "common.hpp"
+#include "fused.hpp"
+#include "gemv.hpp"
+
+using namespace atlas;
+
+namespace {
+
+struct DevMat {
+    int fmt = WF_BF16;
+    void* w = nullptr;
+    float* scales = nullptr;
+    int rows = 0, cols = 0, block = 0;
+    size_t row_bytes() const {
+        switch (fmt) {
+        case WF_F32: return (size_t)cols * 4;
+        case WF_BF16: return (size_t)cols * 2;
+        case WF_I8: return (size_t)cols;
+        default: return (size_t)cols / 2;
+        }
+    }
+    size_t scales_per_row() const {
+        if (fmt == WF_I8) return 1;
+        if (fmt == WF_I4) return (size_t)cols / block;
+        return 0;
+    }
+    size_t data_bytes() const { return row_bytes() * rows; }
+    size_t scale_count() const { return scales_per_row() * rows; }
+};
+
+struct LayerW {
+    DevMat qkv, wo, gu, down;
+    float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    float *kc = nullptr, *vc = nullptr;
+    int window = 0;
+};
+
+// XorShift64 of the reference's sampling Rng (lib.rs:1190-1220)
+struct Rng {
+    uint64_t s;
+    float next_f32() {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        return (float)(s >> 33) / (float)(1ULL << 31);
+    }
+};
+
+}  // namespace
+
+struct atlas_model {
+    atlas_model_config cfg{};
+    std::vector<uint8_t> sliding;
+    int hd = 0, kvd = 0, qkv_rows = 0, B = 1;
+    float scale = 1.f;
+    std::vector<LayerW> L;
+    uint16_t* embed = nullptr;
+    DevMat lm_head;
+    float* final_norm = nullptr;
+    float *cos_tab = nullptr, *sin_tab = nullptr;
+    float *x = nullptr, *xn = nullptr, *y = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr,
+          *logits = nullptr;
+    int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
+    uint32_t *tok_dev = nullptr, *hist = nullptr, *suppress_dev = nullptr, *choice_dev = nullptr;
+    int suppress_cap = 0;
+    unsigned long long* argpart = nullptr;
+    long slot_stride = 0;
+    int attn_splits = 1;
+    int pos = 0;
+    hipStream_t st = nullptr;
+    bool use_graph = true;
+    hipGraphExec_t gexec[2] = {nullptr, nullptr};
+    // greedy choice settings baked into the captured graph
+    float g_theta = 1.f;
+    int g_window = 0, g_nsup = 0;
+    std::vector<void*> allocs;
+    Rng rng{0x517cc1b727220a95ULL};
+};
+
+namespace {
+
+int dalloc(atlas_model* m, void** p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) return ATLAS_OK;
+    if (hipMalloc(p, bytes) != hipSuccess || !*p) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        set_error(ATLAS_ENOMEM, "engine: device allocation of %zu bytes failed", bytes);
+        return ATLAS_ENOMEM;
+    }
+    m->allocs.push_back(*p);
+    return ATLAS_OK;
+}
+
+#define TRY(expr)                 \
+    do {                          \
+        int rc_ = (expr);         \
+        if (rc_) return rc_;      \
+    } while (0)
+
+int alloc_mat(atlas_model* m, DevMat& d, int fmt, int rows, int cols, int block) {
+    d.fmt = fmt;
+    d.rows = rows;
+    d.cols = cols;
+    d.block = block;
+    TRY(dalloc(m, &d.w, d.data_bytes()));
+    if (d.scale_count()) TRY(dalloc(m, (void**)&d.scales, d.scale_count() * 4));
+    return ATLAS_OK;
+}
+
+GemvArgs gemv_args(const DevMat& w, const float* x, float* y, int epi) {
+    GemvArgs a{};
+    a.fmt = w.fmt;
+    a.w = w.w;
+    a.scales = w.scales;
+    a.block = w.block;
+    a.x = x;
+    a.y = y;
+    a.M = w.rows;
+    a.K = w.cols;
+    a.epi = epi;
+    a.N = 1;
+    return a;
+}
+
+int gemv(atlas_model* m, const DevMat& w, const float* x, float* y, int epi) {
+    return gemv_launch(gemv_args(w, x, y, epi), m->st);
+}
+
+int skinny(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int epi) {
+    GemvArgs a = gemv_args(w, x, y, epi);
+    a.N = n;
+    a.x_stride_n = w.cols;
+    a.x_stride_k = 1;
+    a.y_stride_n = epi == EPI_SILU_MUL ? w.rows / 2 : w.rows;
+    a.y_stride_m = 1;
+    return skinny_launch(a, m->st);
+}
+
+// ---- RoPE tables: RopeCache::new (crates/atlas-model/src/lib.rs:380-423) on
+// the host with the same f32 libm calls, then uploaded (GpuRopeTables).
+void rope_tables(const atlas_model_config& c, int hd, std::vector<float>& cs,
+                 std::vector<float>& sn) {
+    const int half = hd / 2;
+    const float two_pi = 2.0f * 3.14159265358979323846f;
+    std::vector<float> f(half);
+    for (int i = 0; i < half; ++i) {
+        const float base = 1.0f / powf(c.rope_theta, 2.0f * (float)i / (float)hd);
+        float v = base;
+        if (c.yarn) {
+            const float wl = two_pi / base;
+            const float low = (float)c.yarn_orig_max_pos / (two_pi * c.yarn_beta_slow);
+            const float high = (float)c.yarn_orig_max_pos / (two_pi * c.yarn_beta_fast);
+            if (wl < high) v = base;
+            else if (wl > low) v = base / c.yarn_factor;
+            else {
+                const float alpha = (wl - high) / (low - high);
+                v = base / (alpha * c.yarn_factor + (1.0f - alpha));
+            }
+        }
+        f[i] = v;
+    }
+    cs.resize((size_t)c.max_seq * half);
+    sn.resize((size_t)c.max_seq * half);
+    for (int p = 0; p < c.max_seq; ++p)
+        for (int i = 0; i < half; ++i) {
+            cs[(size_t)p * half + i] = cosf((float)p * f[i]);
+            sn[(size_t)p * half + i] = sinf((float)p * f[i]);
+        }
+}
+
+// ---- one transformer layer, batch 1 -------------------------------------
+int layer_step(atlas_model* m, int li) {
+    const atlas_model_config& c = m->cfg;
+    LayerW& L = m->L[li];
+    const int d = c.d_model;
+    const float* xin = m->x;
+    if (!c.post_norm) {
+        TRY(rmsnorm_launch(m->x, L.attn_norm, m->xn, d, 1, d, c.rms_eps, m->st));
+        xin = m->xn;
+    }
+    TRY(gemv(m, L.qkv, xin, m->qkv, EPI_STORE));
+    QkvPostArgs q{};
+    q.qkv = m->qkv; q.qkv_stride = m->qkv_rows;
+    q.q_norm = L.q_norm; q.k_norm = L.k_norm; q.qk_eps = 1e-6f;
+    q.cos_tab = m->cos_tab; q.sin_tab = m->sin_tab;
+    q.k_cache = L.kc; q.v_cache = L.vc; q.slot_stride = m->slot_stride;
+    q.slot_dev = nullptr; q.pos_dev = m->pos_dev; q.pos = 0;
+    q.n_heads = c.n_heads; q.n_kv = c.n_kv_heads; q.head_dim = m->hd;
+    TRY(qkv_post_launch(q, 1, m->st));
+    AttnArgs a{};
+    a.q = m->qkv; a.k_cache = L.kc; a.v_cache = L.vc; a.out = m->att;
+    a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
+    a.pos = 0; a.pos_dev = m->pos_dev; a.scale = m->scale; a.window = L.window;
+    TRY(attn_launch(a, m->attn_splits, m->st));
+    TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
+    if (c.post_norm) {
+        TRY(residual_rmsnorm_launch(m->x, m->y, L.attn_norm, d, 1, d, c.rms_eps, m->st));
+        TRY(gemv(m, L.gu, m->x, m->h, EPI_SILU_MUL));
+        TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
+        TRY(residual_rmsnorm_launch(m->x, m->y, L.ffn_norm, d, 1, d, c.rms_eps, m->st));
+    } else {
+        TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, d, m->st));
+        TRY(rmsnorm_launch(m->x, L.ffn_norm, m->xn, d, 1, d, c.rms_eps, m->st));
+        TRY(gemv(m, L.gu, m->xn, m->h, EPI_SILU_MUL));
+        TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
+        TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, d, m->st));
+    }
+    return ATLAS_OK;
+}
+
+int head_step(atlas_model* m) {
+    const atlas_model_config& c = m->cfg;
+    TRY(rmsnorm_launch(m->x, m->final_norm, m->xn, c.d_model, 1, c.d_model, c.rms_eps, m->st));
+    TRY(gemv(m, m->lm_head, m->xn, m->logits, EPI_STORE));
+    return ATLAS_OK;
+}
+
+int choose_step(atlas_model* m) {
+    ArgmaxArgs g{};
+    g.x = m->logits; g.n = m->cfg.vocab; g.part = m->argpart;
+    g.out_u32 = m->tok_dev;
+    g.suppress = m->g_nsup ? m->suppress_dev : nullptr; g.n_suppress = m->g_nsup;
+    g.hist = m->hist; g.hist_len = m->hist_len; g.window = m->g_window; g.theta = m->g_theta;
+    g.step = m->step_dev; g.record = 1;
+    return argmax_launch(g, m->st);
+}
+
+// mode 0: forward only; mode 1: forward + greedy choice into tok_dev/hist
+int enqueue_step(atlas_model* m, int mode) {
+    const atlas_model_config& c = m->cfg;
+    TRY(embed_launch(m->embed, c.vocab, c.d_model, m->tok_dev, 0, m->x, c.d_model, 1, m->st));
+    for (int li = 0; li < c.n_layers; ++li) TRY(layer_step(m, li));
+    TRY(head_step(m));
+    if (mode == 1) TRY(choose_step(m));
+    TRY(add_int_launch(m->pos_dev, 1, 1, m->st));
+    return ATLAS_OK;
+}
+
+void drop_graphs(atlas_model* m) {
+    for (auto& g : m->gexec)
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
+}
+
+int run_step(atlas_model* m, int mode) {
+    ATLAS_REQUIRE(m->pos < m->cfg.max_seq, "position %d reaches max_seq %d", m->pos,
+                  m->cfg.max_seq);
+    if (!m->use_graph) {
+        TRY(enqueue_step(m, mode));
+    } else {
+        if (!m->gexec[mode]) {
+            hipGraph_t g = nullptr;
+            ATLAS_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
+            int rc = enqueue_step(m, mode);
+            hipError_t e = hipStreamEndCapture(m->st, &g);
+            if (rc) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            if (e != hipSuccess) {
+                set_error(ATLAS_EHIP, "graph capture: %s", hipGetErrorString(e));
+                return ATLAS_EHIP;
+            }
+            e = hipGraphInstantiate(&m->gexec[mode], g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) {
+                m->gexec[mode] = nullptr;
+                set_error(ATLAS_EHIP, "graph instantiate: %s", hipGetErrorString(e));
+                return ATLAS_EHIP;
+            }
+        }
+        ATLAS_HIP(hipGraphLaunch(m->gexec[mode], m->st));
+    }
+    m->pos += 1;
+    return ATLAS_OK;
+}
+
+int set_token(atlas_model* m, uint32_t tok) {
+    ATLAS_HIP(hipMemcpyAsync(m->tok_dev, &tok, 4, hipMemcpyHostToDevice, m->st));
+    return ATLAS_OK;
+}
+
+int sync_pos(atlas_model* m) {
+    int p = m->pos;
+    ATLAS_HIP(hipMemcpyAsync(m->pos_dev, &p, 4, hipMemcpyHostToDevice, m->st));
+    return ATLAS_OK;
+}
+
+int download_logits(atlas_model* m, float* host) {
+    ATLAS_HIP(hipMemcpyAsync(host, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost,
+                             m->st));
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+// ---- greedy settings baked into the graph --------------------------------
+int set_greedy_cfg(atlas_model* m, const atlas_sampling* s) {
+    float theta = 1.f;
+    int window = 0, nsup = 0;
+    if (s) {
+        theta = s->repetition_penalty;
+        window = s->repetition_window;
+        nsup = s->n_suppress > 0 && s->suppress_initial_tokens ? s->n_suppress : 0;
+    }
+    if (nsup > m->suppress_cap) {
+        void* p = nullptr;
+        TRY(dalloc(m, &p, (size_t)nsup * 4));
+        m->suppress_dev = (uint32_t*)p;
+        m->suppress_cap = nsup;
+        drop_graphs(m);
+    }
+    if (nsup)
+        ATLAS_HIP(hipMemcpyAsync(m->suppress_dev, s->suppress_initial_tokens, (size_t)nsup * 4,
+                                 hipMemcpyHostToDevice, m->st));
+    if (theta != m->g_theta || window != m->g_window || nsup != m->g_nsup) {
+        m->g_theta = theta;
+        m->g_window = window;
+        m->g_nsup = nsup;
+        if (m->gexec[1]) {
+            (void)hipGraphExecDestroy(m->gexec[1]);
+            m->gexec[1] = nullptr;
+        }
+    }
+    return ATLAS_OK;
+}
+
+int reset_state(atlas_model* m) {
+    m->pos = 0;
+    int zeros[3] = {0, 0, 0};
+    TRY(sync_pos(m));
+    ATLAS_HIP(hipMemcpyAsync(m->step_dev, zeros, 4, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipMemcpyAsync(m->hist_len, zeros, 4, hipMemcpyHostToDevice, m->st));
+    return ATLAS_OK;
+}
+
+bool is_stop(const atlas_sampling* s, uint32_t tok) {
+    if (!s) return false;
+    if (s->eos_token_id >= 0 && (int64_t)tok == s->eos_token_id) return true;
+    for (int i = 0; i < s->n_extra_stop; ++i)
+        if (s->extra_stop_tokens[i] == tok) return true;
+    return false;
+}
+
+bool is_greedy(const atlas_sampling* s) {
+    return !s || s->temperature <= 0.0f || s->temperature < 1e-6f;
+}
+
+// ---- host sampling pipeline (lib.rs:1624-1711, 2581-2722) ---------------------
+int host_argmax(const float* x, int n) {
+    int best = 0;
+    for (int i = 1; i < n; ++i) {
+        const float a = x[best], b = x[i];
+        const bool greater = !std::isnan(a) && !std::isnan(b) && a > b;
+        if (!greater) best = i;
+    }
+    return n > 0 ? best : 0;
+}
+
+void rep_penalty(std::vector<float>& lg, const std::vector<uint32_t>& hist, int window,
+                 float theta) {
+    const size_t start = hist.size() > (size_t)window ? hist.size() - window : 0;
+    for (size_t i = start; i < hist.size(); ++i) {
+        const uint32_t t = hist[i];
+        if (t < lg.size()) {
+            if (lg[t] > 0.0f) lg[t] /= theta;
+            else lg[t] *= theta;
+        }
+    }
+}
+
+void top_k(std::vector<float>& lg, size_t k) {
+    if (k == 0 || k >= lg.size()) return;
+    std::vector<float> sorted(lg);
+    std::sort(sorted.begin(), sorted.end(), [](float a, float b) { return a > b; });
+    const float th = sorted[k - 1];
+    size_t at_or_above = 0, above = 0;
+    for (float v : lg) {
+        if (v >= th) ++at_or_above;
+        if (v > th) ++above;
+    }
+    if (at_or_above <= k) {
+        for (float& v : lg)
+            if (v < th) v = -INFINITY;
+    } else {
+        size_t need = k - above, kept = 0;
+        for (float& v : lg) {
+            if (v > th) continue;
+            if (v == th && kept < need) { ++kept; continue; }
+            v = -INFINITY;
+        }
+    }
+}
+
+void top_p(std::vector<float>& lg, float p) {
+    const size_t n = lg.size();
+    if (n == 0) return;
+    float mx = -INFINITY;
+    for (float v : lg) mx = std::isnan(v) ? mx : std::max(mx, v);
+    std::vector<std::pair<size_t, float>> pr(n);
+    float sum = 0.f;
+    for (size_t i = 0; i < n; ++i) pr[i] = {i, expf(lg[i] - mx)};
+    for (auto& e : pr) sum += e.second;
+    if (sum <= 0.f) return;
+    for (auto& e : pr) e.second /= sum;
+    std::stable_sort(pr.begin(), pr.end(),
+                     [](const auto& a, const auto& b) { return a.second > b.second; });
+    float cum = 0.f;
+    size_t cut = n;
+    for (size_t i = 0; i < n; ++i) {
+        cum += pr[i].second;
+        if (cum >= p) { cut = i + 1; break; }
+    }
+    for (size_t i = cut; i < n; ++i) lg[pr[i].first] = -INFINITY;
+}
+
+void min_p(std::vector<float>& lg, float mp) {
+    if (mp <= 0.f) return;
+    float mx = -INFINITY;
+    for (float v : lg) mx = std::isnan(v) ? mx : std::max(mx, v);
+    const float th = mx + logf(mp);
+    for (float& v : lg)
+        if (v < th) v = -INFINITY;
+}
+
+void softmax_host(std::vector<float>& x) {
+    float mx = -INFINITY;
+    for (float v : x) mx = std::isnan(v) ? mx : std::max(mx, v);
+    float sum = 0.f;
+    for (float& v : x) { v = expf(v - mx); sum += v; }
+    const float inv = 1.0f / sum;
+    for (float& v : x) v *= inv;
+}
+
+uint32_t host_choose(atlas_model* m, const float* logits, int step,
+                     const std::vector<uint32_t>& hist, const atlas_sampling* s) {
+    const int V = m->cfg.vocab;
+    std::vector<float> lg(logits, logits + V);
+    if (s && step == 0)
+        for (int i = 0; i < s->n_suppress; ++i)
+            if (s->suppress_initial_tokens[i] < (uint32_t)V) lg[s->suppress_initial_tokens[i]] = -INFINITY;
+    if (s && s->repetition_penalty != 1.0f && !hist.empty())
+        rep_penalty(lg, hist, s->repetition_window, s->repetition_penalty);
+    if (is_greedy(s)) return (uint32_t)host_argmax(lg.data(), V);
+    if (s->frequency_penalty != 0.0f && !hist.empty()) {
+        std::vector<std::pair<uint32_t, size_t>> counts;
+        for (uint32_t t : hist) {
+            auto it = std::find_if(counts.begin(), counts.end(),
+                                   [t](const auto& e) { return e.first == t; });
+            if (it != counts.end()) ++it->second;
+            else counts.push_back({t, 1});
+        }
+        for (auto& e : counts)
+            if (e.first < (uint32_t)V) lg[e.first] -= s->frequency_penalty * (float)e.second;
+    }
+    if (s->presence_penalty != 0.0f && !hist.empty()) {
+        std::vector<uint32_t> seen(hist);
+        std::sort(seen.begin(), seen.end());
+        seen.erase(std::unique(seen.begin(), seen.end()), seen.end());
+        for (uint32_t t : seen)
+            if (t < (uint32_t)V) lg[t] -= s->presence_penalty;
+    }
+    for (float& v : lg) v /= s->temperature;
+    if (s->top_k > 0) top_k(lg, (size_t)s->top_k);
+    if (s->top_p < 1.0f) top_p(lg, s->top_p);
+    if (s->min_p > 0.0f) min_p(lg, s->min_p);
+    softmax_host(lg);
+    const float r = m->rng.next_f32();
+    float cum = 0.f;
+    for (int i = 0; i < V; ++i) {
+        cum += lg[i];
+        if (r < cum) return (uint32_t)i;
+    }
+    return (uint32_t)(V - 1);
+}
+
+void seed_rng(atlas_model* m, const atlas_sampling* s) {
+    if (s && s->rng_seed) {
+        m->rng.s = s->rng_seed | 1ULL;
+    } else {
+        const uint64_t t = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                               std::chrono::system_clock::now().time_since_epoch())
+                               .count();
+        m->rng.s = t ^ 0x517cc1b727220a95ULL;
+    }
+}
+
+// ---- tensor placement ---------------------------------------------------------
+// dst row r of the fused matrix <- src row r of the single matrix; the fused
+// row index is base + r * stride (stride 2 interleaves gate/up).
+int place_rows(atlas_model* m, DevMat& dst, int base, int stride, int rows, const void* data,
+               const float* scales, bool upload) {
+    const size_t rb = dst.row_bytes();
+    const size_t spr = dst.scales_per_row();
+    const hipMemcpyKind kind = upload ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+    char* dptr = (char*)dst.w + (size_t)base * rb;
+    if (upload)
+        ATLAS_HIP(hipMemcpy2DAsync(dptr, rb * stride, data, rb, rb, rows, kind, m->st));
+    else
+        ATLAS_HIP(hipMemcpy2DAsync((void*)data, rb, dptr, rb * stride, rb, rows, kind, m->st));
+    if (spr) {
+        ATLAS_REQUIRE(scales, "tensor needs scales for format %d", dst.fmt);
+        float* sptr = dst.scales + (size_t)base * spr;
+        if (upload)
+            ATLAS_HIP(hipMemcpy2DAsync(sptr, spr * 4 * stride, scales, spr * 4, spr * 4, rows, kind,
+                                       m->st));
+        else
+            ATLAS_HIP(hipMemcpy2DAsync((void*)scales, spr * 4, sptr, spr * 4 * stride, spr * 4, rows,
+                                       kind, m->st));
+    }
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+int tensor_io(atlas_model* m, int kind, int layer, void* data, float* scales, bool upload) {
+    const atlas_model_config& c = m->cfg;
+    const int d = c.d_model;
+    auto vec_io = [&](float* dev, size_t n) -> int {
+        ATLAS_REQUIRE(dev, "tensor kind %d is not present in this model", kind);
+        if (upload) ATLAS_HIP(hipMemcpyAsync(dev, data, n * 4, hipMemcpyHostToDevice, m->st));
+        else ATLAS_HIP(hipMemcpyAsync(data, dev, n * 4, hipMemcpyDeviceToHost, m->st));
+        ATLAS_HIP(hipStreamSynchronize(m->st));
+        return ATLAS_OK;
+    };
+    if (kind == ATLAS_T_EMBED) {
+        const size_t bytes = (size_t)c.vocab * d * 2;
+        if (upload) ATLAS_HIP(hipMemcpyAsync(m->embed, data, bytes, hipMemcpyHostToDevice, m->st));
+        else ATLAS_HIP(hipMemcpyAsync(data, m->embed, bytes, hipMemcpyDeviceToHost, m->st));
+        ATLAS_HIP(hipStreamSynchronize(m->st));
+        return ATLAS_OK;
+    }
+    if (kind == ATLAS_T_LM_HEAD)
+        return place_rows(m, m->lm_head, 0, 1, c.vocab, data, scales, upload);
+    if (kind == ATLAS_T_FINAL_NORM) return vec_io(m->final_norm, d);
+    ATLAS_REQUIRE(layer >= 0 && layer < c.n_layers, "layer %d out of range", layer);
+    LayerW& L = m->L[layer];
+    switch (kind) {
+    case ATLAS_T_WQ: return place_rows(m, L.qkv, 0, 1, d, data, scales, upload);
+    case ATLAS_T_WK: return place_rows(m, L.qkv, d, 1, m->kvd, data, scales, upload);
+    case ATLAS_T_WV: return place_rows(m, L.qkv, d + m->kvd, 1, m->kvd, data, scales, upload);
+    case ATLAS_T_WO: return place_rows(m, L.wo, 0, 1, d, data, scales, upload);
+    case ATLAS_T_W_GATE: return place_rows(m, L.gu, 0, 2, c.ffn_hidden, data, scales, upload);
+    case ATLAS_T_W_UP: return place_rows(m, L.gu, 1, 2, c.ffn_hidden, data, scales, upload);
+    case ATLAS_T_W_DOWN: return place_rows(m, L.down, 0, 1, d, data, scales, upload);
+    case ATLAS_T_ATTN_NORM: return vec_io(L.attn_norm, d);
+    case ATLAS_T_FFN_NORM: return vec_io(L.ffn_norm, d);
+    case ATLAS_T_Q_NORM: return vec_io(L.q_norm, (size_t)c.n_heads * m->hd);
+    case ATLAS_T_K_NORM: return vec_io(L.k_norm, (size_t)m->kvd);
+    }
+    set_error(ATLAS_EINVAL, "unknown tensor kind %d", kind);
+    return ATLAS_EINVAL;
+}
+
+// ---- the ragged batch step ----------------------------------------------------
+int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
+    const atlas_model_config& c = m->cfg;
+    const int d = c.d_model;
+    TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, n, m->st));
+    for (int li = 0; li < c.n_layers; ++li) {
+        LayerW& L = m->L[li];
+        const float* xin = m->x;
+        if (!c.post_norm) {
+            TRY(rmsnorm_launch(m->x, L.attn_norm, m->xn, d, n, d, c.rms_eps, m->st));
+            xin = m->xn;
+        }
+        TRY(skinny(m, L.qkv, xin, m->qkv, n, EPI_STORE));
+        QkvPostArgs q{};
+        q.qkv = m->qkv; q.qkv_stride = m->qkv_rows;
+        q.q_norm = L.q_norm; q.k_norm = L.k_norm; q.qk_eps = 1e-6f;
+        q.cos_tab = m->cos_tab; q.sin_tab = m->sin_tab;
+        q.k_cache = L.kc; q.v_cache = L.vc; q.slot_stride = m->slot_stride;
+        q.slot_dev = m->slot_dev; q.pos_dev = m->pos_dev;
+        q.n_heads = c.n_heads; q.n_kv = c.n_kv_heads; q.head_dim = m->hd;
+        TRY(qkv_post_launch(q, n, m->st));
+        for (int i = 0; i < n; ++i) {
+            AttnArgs a{};
+            a.q = m->qkv + (size_t)i * m->qkv_rows;
+            a.k_cache = L.kc + (size_t)slots[i] * m->slot_stride;
+            a.v_cache = L.vc + (size_t)slots[i] * m->slot_stride;
+            a.out = m->att + (size_t)i * d;
+            a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
+            a.pos_dev = m->pos_dev + i; a.scale = m->scale; a.window = L.window;
+            TRY(attn_launch(a, m->attn_splits, m->st));
+        }
+        TRY(skinny(m, L.wo, m->att, m->y, n, EPI_STORE));
+        if (c.post_norm) {
+            TRY(residual_rmsnorm_launch(m->x, m->y, L.attn_norm, d, n, d, c.rms_eps, m->st));
+            TRY(skinny(m, L.gu, m->x, m->h, n, EPI_SILU_MUL));
+            TRY(skinny(m, L.down, m->h, m->y, n, EPI_STORE));
+            TRY(residual_rmsnorm_launch(m->x, m->y, L.ffn_norm, d, n, d, c.rms_eps, m->st));
+        } else {
+            TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, (long)n * d, m->st));
+            TRY(rmsnorm_launch(m->x, L.ffn_norm, m->xn, d, n, d, c.rms_eps, m->st));
+            TRY(skinny(m, L.gu, m->xn, m->h, n, EPI_SILU_MUL));
+            TRY(skinny(m, L.down, m->h, m->y, n, EPI_STORE));
+            TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, (long)n * d, m->st));
+        }
+    }
+    TRY(rmsnorm_launch(m->x, m->final_norm, m->xn, d, n, d, c.rms_eps, m->st));
+    TRY(skinny(m, m->lm_head, m->xn, m->logits, n, EPI_STORE));
+    return ATLAS_OK;
+}
+
+}  // namespace
+
+// =============================================================================
+// C ABI
+// =============================================================================
+
+ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
+    if (!cfg) {
+        set_error(ATLAS_EINVAL, "atlas_model_create: null config");
+        return nullptr;
+    }
+    const atlas_model_config& c = *cfg;
+    if (c.vocab <= 0 || c.d_model <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
+        c.ffn_hidden <= 0 || c.max_seq <= 0 || c.d_model % c.n_heads || c.n_heads % c.n_kv_heads) {
+        set_error(ATLAS_EINVAL, "atlas_model_create: inconsistent shape");
+        return nullptr;
+    }
+    const int fmt = c.weight_format;
+    if (fmt != WF_BF16 && fmt != WF_I8 && fmt != WF_I4) {
+        set_error(ATLAS_EINVAL, "atlas_model_create: weight_format %d", fmt);
+        return nullptr;
+    }
+    const int hd = c.d_model / c.n_heads;
+    if (hd % 2 || hd > 256) {
+        set_error(ATLAS_EINVAL, "atlas_model_create: head_dim %d", hd);
+        return nullptr;
+    }
+    if (fmt == WF_I4 && (c.int4_block <= 0 || c.int4_block % 32 || c.d_model % c.int4_block ||
+                         c.ffn_hidden % c.int4_block)) {
+        set_error(ATLAS_EINVAL, "atlas_model_create: int4 block %d must be a multiple of 32 "
+                  "dividing d_model and ffn_hidden", c.int4_block);
+        return nullptr;
+    }
+    atlas_model* m = new atlas_model();
+    m->cfg = c;
+    m->sliding.assign(c.n_layers, 0);
+    if (c.layer_sliding) std::memcpy(m->sliding.data(), c.layer_sliding, c.n_layers);
+    m->cfg.layer_sliding = m->sliding.data();
+    m->hd = hd;
+    m->kvd = c.n_kv_heads * hd;
+    m->qkv_rows = c.d_model + 2 * m->kvd;
+    m->B = c.max_batch < 1 ? 1 : c.max_batch;
+    // scale = attn_factor / sqrt(head_dim) (lib.rs:632, 1331-1335)
+    m->scale = 1.0f / sqrtf((float)hd);
+    const float af = c.yarn ? c.yarn_attn_factor : 1.0f;
+    if (fabsf(af - 1.0f) > 1e-6f) m->scale *= af;
+
+    auto fail = [&](atlas_model* mm) -> atlas_model* {
+        atlas_model_destroy(mm);
+        return nullptr;
+    };
+    if (hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking) != hipSuccess) {
+        set_error(ATLAS_EHIP, "atlas_model_create: stream creation failed");
+        m->st = nullptr;
+        return fail(m);
+    }
+    const int d = c.d_model, B = m->B, blk = c.int4_block;
+    m->slot_stride = (long)c.max_seq * m->kvd;
+    m->L.resize(c.n_layers);
+    for (int li = 0; li < c.n_layers; ++li) {
+        LayerW& L = m->L[li];
+        if (alloc_mat(m, L.qkv, fmt, m->qkv_rows, d, blk) || alloc_mat(m, L.wo, fmt, d, d, blk) ||
+            alloc_mat(m, L.gu, fmt, 2 * c.ffn_hidden, d, blk) ||
+            alloc_mat(m, L.down, fmt, d, c.ffn_hidden, blk) ||
+            dalloc(m, (void**)&L.attn_norm, (size_t)d * 4) ||
+            dalloc(m, (void**)&L.ffn_norm, (size_t)d * 4) ||
+            dalloc(m, (void**)&L.kc, (size_t)B * m->slot_stride * 4) ||
+            dalloc(m, (void**)&L.vc, (size_t)B * m->slot_stride * 4))
+            return fail(m);
+        if (c.qk_norm && (dalloc(m, (void**)&L.q_norm, (size_t)c.n_heads * hd * 4) ||
+                          dalloc(m, (void**)&L.k_norm, (size_t)m->kvd * 4)))
+            return fail(m);
+        L.window = (m->sliding[li] && c.sliding_window > 0) ? c.sliding_window : 0;
+    }
+    if (dalloc(m, (void**)&m->embed, (size_t)c.vocab * d * 2) ||
+        alloc_mat(m, m->lm_head, fmt, c.vocab, d, blk) ||
+        dalloc(m, (void**)&m->final_norm, (size_t)d * 4))
+        return fail(m);
+    // scratch
+    const int big = std::max(c.ffn_hidden, d);
+    if (dalloc(m, (void**)&m->x, (size_t)B * d * 4) || dalloc(m, (void**)&m->xn, (size_t)B * d * 4) ||
+        dalloc(m, (void**)&m->y, (size_t)B * d * 4) ||
+        dalloc(m, (void**)&m->qkv, (size_t)B * m->qkv_rows * 4) ||
+        dalloc(m, (void**)&m->att, (size_t)B * d * 4) ||
+        dalloc(m, (void**)&m->h, (size_t)B * big * 4) ||
+        dalloc(m, (void**)&m->logits, (size_t)B * c.vocab * 4) ||
+        dalloc(m, (void**)&m->pos_dev, (size_t)B * 4) || dalloc(m, (void**)&m->slot_dev, (size_t)B * 4) ||
+        dalloc(m, (void**)&m->tok_dev, (size_t)B * 4) || dalloc(m, (void**)&m->step_dev, 4) ||
+        dalloc(m, (void**)&m->hist_len, 4) ||
+        dalloc(m, (void**)&m->hist, (size_t)(c.max_seq + 2) * 4) ||
+        dalloc(m, (void**)&m->choice_dev, (size_t)B * 4) ||
+        dalloc(m, (void**)&m->argpart, (size_t)ARGMAX_MAX_PARTS * 8))
+        return fail(m);
+    // RoPE tables
+    {
+        std::vector<float> cs, sn;
+        rope_tables(c, hd, cs, sn);
+        if (dalloc(m, (void**)&m->cos_tab, cs.size() * 4) ||
+            dalloc(m, (void**)&m->sin_tab, sn.size() * 4))
+            return fail(m);
+        if (hipMemcpy(m->cos_tab, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(m->sin_tab, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            set_error(ATLAS_EHIP, "rope table upload failed");
+            return fail(m);
+        }
+    }
+    m->attn_splits = attn_pick_splits(c.n_kv_heads, c.max_seq);
+    if (attn_reserve(c.n_heads, hd, m->attn_splits)) return fail(m);
+    if (reset_state(m) || hipStreamSynchronize(m->st) != hipSuccess) return fail(m);
+    return m;
+}
+
+ATLAS_API void atlas_model_destroy(atlas_model* m) {
+    if (!m) return;
+    if (m->st) (void)hipStreamSynchronize(m->st);
+    drop_graphs(m);
+    for (void* p : m->allocs) (void)hipFree(p);
+    if (m->st) (void)hipStreamDestroy(m->st);
+    delete m;
+}
+
+ATLAS_API int atlas_model_set_tensor(atlas_model* m, int kind, int layer, const void* data,
+                                     const float* scales) {
+    ATLAS_REQUIRE(m && data, "set_tensor: null argument");
+    return tensor_io(m, kind, layer, const_cast<void*>(data), const_cast<float*>(scales), true);
+}
+
+ATLAS_API int atlas_model_get_tensor(atlas_model* m, int kind, int layer, void* data,
+                                     float* scales) {
+    ATLAS_REQUIRE(m && data, "get_tensor: null argument");
+    return tensor_io(m, kind, layer, data, scales, false);
+}
+
+ATLAS_API int atlas_model_init_random(atlas_model* m, uint64_t seed) {
+    ATLAS_REQUIRE(m, "init_random: null model");
+    const atlas_model_config& c = m->cfg;
+    const int d = c.d_model;
+    auto sub = [&](int kind, int layer) {
+        uint64_t z = seed + 0x9E3779B97F4A7C15ULL * (uint64_t)(kind * 4096 + layer + 1);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        return z ^ (z >> 31);
+    };
+    // temporaries sized for the largest matrix
+    const size_t max_el = std::max((size_t)c.vocab * d, (size_t)c.ffn_hidden * d);
+    float* tmp = nullptr;
+    void* qd = nullptr;
+    float* qs = nullptr;
+    ATLAS_HIP(hipMalloc((void**)&tmp, max_el * 4));
+    int rc = ATLAS_OK;
+    const int fmt = c.weight_format;
+    if (fmt != WF_BF16) {
+        if (hipMalloc(&qd, max_el) != hipSuccess || hipMalloc((void**)&qs, max_el / 8 * 4 + 64) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(tmp);
+            if (qd) (void)hipFree(qd);
+            set_error(ATLAS_ENOMEM, "init_random: temporaries");
+            return ATLAS_ENOMEM;
+        }
+    }
+    // matrix: generate into tmp (bf16 bits or f32), convert, place
+    auto mat = [&](DevMat& dst, int base, int stride, int rows, int kind, int layer) -> int {
+        const long n = (long)rows * dst.cols;
+        if (fmt == WF_BF16) {
+            TRY(init_launch(INIT_NORMAL_BF16, tmp, n, sub(kind, layer), 0.f, 0.02f, m->st));
+            const size_t rb = dst.row_bytes();
+            ATLAS_HIP(hipMemcpy2DAsync((char*)dst.w + (size_t)base * rb, rb * stride, tmp, rb, rb, rows,
+                                       hipMemcpyDeviceToDevice, m->st));
+        } else {
+            TRY(init_launch(INIT_NORMAL_F32, tmp, n, sub(kind, layer), 0.f, 0.02f, m->st));
+            if (fmt == WF_I8) TRY(quant_i8_launch(tmp, 0, rows, dst.cols, (int8_t*)qd, qs, m->st));
+            else TRY(quant_i4_launch(tmp, 0, n, dst.block, (uint8_t*)qd, qs, m->st));
+            const size_t rb = dst.row_bytes(), spr = dst.scales_per_row();
+            ATLAS_HIP(hipMemcpy2DAsync((char*)dst.w + (size_t)base * rb, rb * stride, qd, rb, rb, rows,
+                                       hipMemcpyDeviceToDevice, m->st));
+            ATLAS_HIP(hipMemcpy2DAsync(dst.scales + (size_t)base * spr, spr * 4 * stride, qs, spr * 4,
+                                       spr * 4, rows, hipMemcpyDeviceToDevice, m->st));
+        }
+        ATLAS_HIP(hipStreamSynchronize(m->st));
+        return ATLAS_OK;
+    };
+    auto vec = [&](float* dst, long n, int kind, int layer) -> int {
+        if (!dst) return ATLAS_OK;
+        return init_launch(INIT_UNIFORM_F32, dst, n, sub(kind, layer), 0.5f, 1.5f, m->st);
+    };
+    for (int li = 0; li < c.n_layers && !rc; ++li) {
+        LayerW& L = m->L[li];
+        rc = mat(L.qkv, 0, 1, d, ATLAS_T_WQ, li);
+        if (!rc) rc = mat(L.qkv, d, 1, m->kvd, ATLAS_T_WK, li);
+        if (!rc) rc = mat(L.qkv, d + m->kvd, 1, m->kvd, ATLAS_T_WV, li);
+        if (!rc) rc = mat(L.wo, 0, 1, d, ATLAS_T_WO, li);
+        if (!rc) rc = mat(L.gu, 0, 2, c.ffn_hidden, ATLAS_T_W_GATE, li);
+        if (!rc) rc = mat(L.gu, 1, 2, c.ffn_hidden, ATLAS_T_W_UP, li);
+        if (!rc) rc = mat(L.down, 0, 1, d, ATLAS_T_W_DOWN, li);
+        if (!rc) rc = vec(L.attn_norm, d, ATLAS_T_ATTN_NORM, li);
+        if (!rc) rc = vec(L.ffn_norm, d, ATLAS_T_FFN_NORM, li);
+        if (!rc) rc = vec(L.q_norm, (long)c.n_heads * m->hd, ATLAS_T_Q_NORM, li);
+        if (!rc) rc = vec(L.k_norm, m->kvd, ATLAS_T_K_NORM, li);
+    }
+    if (!rc) rc = init_launch(INIT_NORMAL_BF16, m->embed, (long)c.vocab * d, sub(ATLAS_T_EMBED, 0), 0.f,
+                              0.02f, m->st);
+    if (!rc) rc = mat(m->lm_head, 0, 1, c.vocab, ATLAS_T_LM_HEAD, 0);
+    if (!rc) rc = vec(m->final_norm, d, ATLAS_T_FINAL_NORM, 0);
+    if (!rc && hipStreamSynchronize(m->st) != hipSuccess) {
+        set_error(ATLAS_EHIP, "init_random: sync failed");
+        rc = ATLAS_EHIP;
+    }
+    (void)hipFree(tmp);
+    if (qd) (void)hipFree(qd);
+    if (qs) (void)hipFree(qs);
+    return rc;
+}
+
+ATLAS_API int atlas_model_reset(atlas_model* m) {
+    ATLAS_REQUIRE(m, "reset: null model");
+    TRY(reset_state(m));
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_pos(const atlas_model* m) { return m ? m->pos : -1; }
+ATLAS_API float atlas_model_attn_scale(const atlas_model* m) { return m ? m->scale : 0.f; }
+ATLAS_API void* atlas_model_stream(atlas_model* m) { return m ? (void*)m->st : nullptr; }
+ATLAS_API const float* atlas_model_logits_dev(atlas_model* m) { return m ? m->logits : nullptr; }
+
+ATLAS_API int atlas_model_use_graph(atlas_model* m, int enable) {
+    ATLAS_REQUIRE(m, "use_graph: null model");
+    m->use_graph = enable != 0;
+    if (!m->use_graph) drop_graphs(m);
+    return ATLAS_OK;
+}
+
+ATLAS_API int64_t atlas_model_weight_bytes(const atlas_model* m) {
+    if (!m) return 0;
+    int64_t b = 0;
+    for (const auto& L : m->L)
+        for (const DevMat* w : {&L.qkv, &L.wo, &L.gu, &L.down})
+            b += (int64_t)w->data_bytes() + (int64_t)w->scale_count() * 4;
+    b += (int64_t)m->lm_head.data_bytes() + (int64_t)m->lm_head.scale_count() * 4;
+    return b;
+}
+
+ATLAS_API int atlas_model_forward_one(atlas_model* m, uint32_t token, float* logits) {
+    ATLAS_REQUIRE(m, "forward_one: null model");
+    TRY(sync_pos(m));
+    TRY(set_token(m, token));
+    TRY(run_step(m, 0));
+    if (logits) TRY(download_logits(m, logits));
+    else ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits,
+                                             float* hidden, atlas_hook_fn hook, void* user) {
+    ATLAS_REQUIRE(m, "forward_one_hooked: null model");
+    const atlas_model_config& c = m->cfg;
+    ATLAS_REQUIRE(m->pos < c.max_seq, "position %d reaches max_seq %d", m->pos, c.max_seq);
+    TRY(sync_pos(m));
+    TRY(set_token(m, token));
+    TRY(embed_launch(m->embed, c.vocab, c.d_model, m->tok_dev, 0, m->x, c.d_model, 1, m->st));
+    std::vector<float> hbuf(hidden ? 0 : (size_t)c.d_model);
+    for (int li = 0; li < c.n_layers; ++li) {
+        TRY(layer_step(m, li));
+        float* dst = hidden ? hidden + (size_t)li * c.d_model : hbuf.data();
+        if (hidden || hook) {
+            ATLAS_HIP(hipMemcpyAsync(dst, m->x, (size_t)c.d_model * 4, hipMemcpyDeviceToHost, m->st));
+            ATLAS_HIP(hipStreamSynchronize(m->st));
+            if (hook) {
+                float delta = 0.f;
+                (void)hook(user, li, dst, c.d_model, &delta);
+            }
+        }
+    }
+    TRY(head_step(m));
+    TRY(add_int_launch(m->pos_dev, 1, 1, m->st));
+    m->pos += 1;
+    if (logits) TRY(download_logits(m, logits));
+    else ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+namespace {
+
+// Shared driver of generate / generate_streaming (lib.rs:1599-1732, 1853-1955).
+int generate_impl(atlas_model* m, const uint32_t* prompt, int n_prompt, int max_new,
+                  const atlas_sampling* s, uint32_t* out, int* n_out, atlas_token_fn on_token,
+                  void* user) {
+    ATLAS_REQUIRE(m && n_out && (out || on_token), "generate: null argument");
+    ATLAS_REQUIRE(n_prompt >= 0 && max_new >= 0 && (n_prompt == 0 || prompt), "generate: bad prompt");
+    *n_out = 0;
+    const int V = m->cfg.vocab;
+    TRY(reset_state(m));
+    seed_rng(m, s);
+    ATLAS_REQUIRE(n_prompt + max_new <= m->cfg.max_seq,
+                  "generate: prompt %d + max_new %d exceeds max_seq %d", n_prompt, max_new,
+                  m->cfg.max_seq);
+    std::vector<uint32_t> gen;
+    std::vector<float> logits((size_t)V, 0.0f);
+    const bool greedy = is_greedy(s);
+    const bool device_choice = greedy && !on_token;
+    if (device_choice) TRY(set_greedy_cfg(m, s));
+
+    // prompt: forward all but the last token without choosing
+    for (int i = 0; i + 1 < n_prompt; ++i) {
+        TRY(set_token(m, prompt[i]));
+        TRY(run_step(m, 0));
+    }
+    if (max_new == 0) {
+        if (n_prompt > 0) {
+            TRY(set_token(m, prompt[n_prompt - 1]));
+            TRY(run_step(m, 0));
+        }
+        ATLAS_HIP(hipStreamSynchronize(m->st));
+        return ATLAS_OK;
+    }
+
+    if (device_choice && n_prompt > 0) {
+        // greedy on the device: each replay forwards the last choice and
+        // chooses the next; check for stop tokens every `chunk` replays.
+        TRY(set_token(m, prompt[n_prompt - 1]));
+        TRY(run_step(m, 1));                        // chooses t_1
+        int issued = 1;                              // tokens chosen so far
+        int forwarded = 0;                           // generated tokens forwarded
+        std::vector<uint32_t> h;
+        const int chunk = 16;
+        while (true) {
+            h.resize(issued);
+            ATLAS_HIP(hipMemcpyAsync(h.data(), m->hist, (size_t)issued * 4, hipMemcpyDeviceToHost,
+                                     m->st));
+            ATLAS_HIP(hipStreamSynchronize(m->st));
+            // the output is t_1..t_k: k = max_new, or t_{k+1} is a stop token
+            gen.clear();
+            bool determined = false;
+            for (int j = 0; j < issued; ++j) {
+                if ((int)gen.size() >= max_new || is_stop(s, h[j])) {
+                    determined = true;
+                    break;
+                }
+                gen.push_back(h[j]);
+            }
+            if ((int)gen.size() >= max_new) determined = true;
+            const int k = (int)gen.size();
+            if (determined && forwarded >= k) break;
+            // each replay forwards the latest choice and chooses the next; the
+            // forward of t_k is the reference's final forward (lib.rs:1725-1729)
+            const int want = determined ? k - forwarded : std::min(chunk, max_new - forwarded);
+            for (int r = 0; r < want; ++r) TRY(run_step(m, 1));
+            issued += want;
+            forwarded += want;
+        }
+        // the reference forwarded exactly n_prompt + |gen| tokens; anything
+        // beyond (a chunk that ran past a stop token) is never read again
+        m->pos = n_prompt + (int)gen.size();
+        TRY(sync_pos(m));
+        for (size_t i = 0; i < gen.size(); ++i) out[i] = gen[i];
+        *n_out = (int)gen.size();
+        ATLAS_HIP(hipStreamSynchronize(m->st));
+        return ATLAS_OK;
+    }
+
+    // host choice (sampling, streaming, or an empty prompt)
+    if (n_prompt > 0) {
+        TRY(set_token(m, prompt[n_prompt - 1]));
+        TRY(run_step(m, 0));
+        TRY(download_logits(m, logits.data()));
+    }
+    for (int step = 0; step < max_new; ++step) {
+        const uint32_t tok = host_choose(m, logits.data(), step, gen, s);
+        if (is_stop(s, tok)) break;
+        gen.push_back(tok);
+        if (out) out[gen.size() - 1] = tok;
+        if (on_token && !on_token(user, tok)) break;
+        TRY(set_token(m, tok));
+        TRY(run_step(m, 0));
+        TRY(download_logits(m, logits.data()));
+    }
+    *n_out = (int)gen.size();
+    return ATLAS_OK;
+}
+
+}  // namespace
+
+ATLAS_API int atlas_model_generate(atlas_model* m, const uint32_t* prompt, int n_prompt,
+                                   int max_new, const atlas_sampling* s, uint32_t* out,
+                                   int* n_out) {
+    return generate_impl(m, prompt, n_prompt, max_new, s, out, n_out, nullptr, nullptr);
+}
+
+ATLAS_API int atlas_model_generate_streaming(atlas_model* m, const uint32_t* prompt, int n_prompt,
+                                             int max_new, const atlas_sampling* s,
+                                             atlas_token_fn on_token, void* user, int* n_out) {
+    ATLAS_REQUIRE(on_token, "generate_streaming: null callback");
+    std::vector<uint32_t> out((size_t)std::max(max_new, 1));
+    return generate_impl(m, prompt, n_prompt, max_new, s, out.data(), n_out, on_token, user);
+}
+
+namespace {
+struct HookAcc {
+    atlas_hook_fn fn;
+    void* user;
+    float acc;
+    uint32_t fired;
+};
+int acc_hook(void* u, int li, const float* hidden, int d, float* delta) {
+    HookAcc* h = (HookAcc*)u;
+    float dl = 0.f;
+    if (h->fn(h->user, li, hidden, d, &dl)) {
+        h->acc += dl > 0.f ? dl : 0.f;      // max(delta, 0): lib.rs:1839
+        h->fired += 1;
+    }
+    *delta = dl;
+    return 0;
+}
+}  // namespace
+
+ATLAS_API int atlas_model_generate_hooked(atlas_model* m, const uint32_t* prompt, int n_prompt,
+                                          int max_new, const atlas_sampling* s, atlas_hook_fn hook,
+                                          void* user, uint32_t* out, float* total_delta,
+                                          uint32_t* layers_fired, int* n_out) {
+    ATLAS_REQUIRE(m && hook && out && n_out, "generate_hooked: null argument");
+    ATLAS_REQUIRE(n_prompt >= 0 && max_new >= 0 && (n_prompt == 0 || prompt), "generate_hooked: bad prompt");
+    *n_out = 0;
+    const int V = m->cfg.vocab;
+    TRY(reset_state(m));
+    seed_rng(m, s);
+    ATLAS_REQUIRE(n_prompt + max_new <= m->cfg.max_seq, "generate_hooked: exceeds max_seq");
+    std::vector<float> logits((size_t)V, 0.0f);
+    HookAcc acc{hook, user, 0.f, 0};
+    // prefill: hook runs, deposits discarded (lib.rs:1763-1770)
+    for (int i = 0; i < n_prompt; ++i)
+        TRY(atlas_model_forward_one_hooked(m, prompt[i], logits.data(), nullptr, acc_hook, &acc));
+    std::vector<uint32_t> gen;
+    for (int step = 0; step < max_new; ++step) {
+        const uint32_t tok = host_choose(m, logits.data(), step, gen, s);
+        if (is_stop(s, tok)) break;
+        gen.push_back(tok);
+        out[gen.size() - 1] = tok;
+        acc.acc = 0.f;
+        acc.fired = 0;
+        TRY(atlas_model_forward_one_hooked(m, tok, logits.data(), nullptr, acc_hook, &acc));
+        if (total_delta) total_delta[gen.size() - 1] = acc.acc;
+        if (layers_fired) layers_fired[gen.size() - 1] = acc.fired;
+    }
+    *n_out = (int)gen.size();
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, int n_steps,
+                                        uint32_t* tokens) {
+    ATLAS_REQUIRE(m && n_steps >= 0, "decode_greedy: bad arguments");
+    ATLAS_REQUIRE(m->pos + n_steps <= m->cfg.max_seq, "decode_greedy: exceeds max_seq");
+    TRY(set_greedy_cfg(m, nullptr));
+    int zero = 0;
+    ATLAS_HIP(hipMemcpyAsync(m->hist_len, &zero, 4, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipMemcpyAsync(m->step_dev, &zero, 4, hipMemcpyHostToDevice, m->st));
+    TRY(sync_pos(m));
+    TRY(set_token(m, first_token));
+    for (int i = 0; i < n_steps; ++i) TRY(run_step(m, 1));
+    if (tokens && n_steps > 0)
+        ATLAS_HIP(hipMemcpyAsync(tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost, m->st));
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, float* ms, int* launches,
+                                     int64_t* bytes) {
+    ATLAS_REQUIRE(m && iters > 0 && ms && launches && bytes, "bench_gemv: bad arguments");
+    const atlas_model_config& c = m->cfg;
+    auto mat_bytes = [](const DevMat& w, bool swiglu) {
+        const int64_t out = swiglu ? w.rows / 2 : w.rows;
+        return (int64_t)w.data_bytes() + (int64_t)w.scale_count() * 4 + (int64_t)w.cols * 4 + out * 4;
+    };
+    int64_t b = 0;
+    int n = 0;
+    for (const auto& L : m->L) {
+        b += mat_bytes(L.qkv, false) + mat_bytes(L.wo, false) + mat_bytes(L.gu, true) +
+             mat_bytes(L.down, false);
+        n += 4;
+    }
+    b += mat_bytes(m->lm_head, false);
+    n += 1;
+    hipEvent_t e0, e1;
+    ATLAS_HIP(hipEventCreate(&e0));
+    ATLAS_HIP(hipEventCreate(&e1));
+    ATLAS_HIP(hipEventRecord(e0, m->st));
+    for (int it = 0; it < iters; ++it) {
+        for (auto& L : m->L) {
+            TRY(gemv(m, L.qkv, m->x, m->qkv, EPI_STORE));
+            TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
+            TRY(gemv(m, L.gu, m->x, m->h, EPI_SILU_MUL));
+            TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
+        }
+        TRY(gemv(m, m->lm_head, m->xn, m->logits, EPI_STORE));
+    }
+    ATLAS_HIP(hipEventRecord(e1, m->st));
+    ATLAS_HIP(hipEventSynchronize(e1));
+    float t = 0.f;
+    ATLAS_HIP(hipEventElapsedTime(&t, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *ms = t;
+    *launches = n * iters;
+    *bytes = b;
+    (void)c;
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts,
+                                         const int* prompt_lens, int n_seqs, int max_new,
+                                         const atlas_sampling* s, uint32_t* out, int* n_out) {
+    ATLAS_REQUIRE(m && prompt_lens && out && n_out, "generate_batch: null argument");
+    ATLAS_REQUIRE(n_seqs >= 1 && n_seqs <= m->B && n_seqs <= 8,
+                  "generate_batch: n_seqs %d outside 1..min(max_batch %d, 8)", n_seqs, m->B);
+    ATLAS_REQUIRE(max_new >= 0, "generate_batch: max_new < 0");
+    const int V = m->cfg.vocab;
+    std::vector<size_t> off(n_seqs + 1, 0);
+    for (int i = 0; i < n_seqs; ++i) {
+        ATLAS_REQUIRE(prompt_lens[i] >= 0, "generate_batch: negative prompt length");
+        ATLAS_REQUIRE(prompt_lens[i] + max_new <= m->cfg.max_seq,
+                      "generate_batch: sequence %d exceeds max_seq", i);
+        off[i + 1] = off[i] + prompt_lens[i];
+    }
+    ATLAS_REQUIRE(off[n_seqs] == 0 || prompts, "generate_batch: null prompts");
+    std::vector<int> cursor(n_seqs, 0), pos(n_seqs, 0);
+    std::vector<std::vector<uint32_t>> gen(n_seqs);
+    std::vector<bool> done(n_seqs, false);
+    std::vector<uint32_t> pending(n_seqs, 0);   // token to feed next
+    std::vector<bool> has_pending(n_seqs, false);
+    std::vector<float> zero_logits((size_t)V, 0.f);
+    const bool host_path = !is_greedy(s) || (s && (s->n_suppress > 0 || s->repetition_penalty != 1.0f));
+    seed_rng(m, s);
+    for (int i = 0; i < n_seqs; ++i) {
+        n_out[i] = 0;
+        if (max_new == 0) { done[i] = true; continue; }
+        if (prompt_lens[i] == 0) {
+            // choose from all-zero logits, as the reference does with an empty prompt
+            const uint32_t t = host_choose(m, zero_logits.data(), 0, gen[i], s);
+            if (is_stop(s, t)) { done[i] = true; continue; }
+            gen[i].push_back(t);
+            pending[i] = t;
+            has_pending[i] = true;
+            if ((int)gen[i].size() >= max_new) done[i] = true;
+        }
+    }
+    std::vector<uint32_t> toks(n_seqs), choice(n_seqs);
+    std::vector<int> slots(n_seqs), poss(n_seqs), idx(n_seqs);
+    std::vector<float> lg;
+    while (true) {
+        int n = 0;
+        for (int i = 0; i < n_seqs; ++i) {
+            if (done[i]) continue;
+            uint32_t t;
+            if (cursor[i] < prompt_lens[i]) t = prompts[off[i] + cursor[i]];
+            else if (has_pending[i]) t = pending[i];
+            else continue;
+            toks[n] = t;
+            slots[n] = i;
+            poss[n] = pos[i];
+            idx[n] = i;
+            ++n;
+        }
+        if (n == 0) break;
+        ATLAS_HIP(hipMemcpyAsync(m->tok_dev, toks.data(), (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+        ATLAS_HIP(hipMemcpyAsync(m->pos_dev, poss.data(), (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+        ATLAS_HIP(hipMemcpyAsync(m->slot_dev, slots.data(), (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+        std::vector<int> sl(slots.begin(), slots.begin() + n);
+        TRY(batch_step(m, n, sl));
+        if (!host_path) {
+            for (int j = 0; j < n; ++j) {
+                ArgmaxArgs g{};
+                g.x = m->logits + (size_t)j * V; g.n = V; g.part = m->argpart + 0;
+                g.out_u32 = m->choice_dev + j; g.theta = 1.0f;
+                TRY(argmax_launch(g, m->st));
+            }
+            ATLAS_HIP(hipMemcpyAsync(choice.data(), m->choice_dev, (size_t)n * 4, hipMemcpyDeviceToHost,
+                                     m->st));
+            ATLAS_HIP(hipStreamSynchronize(m->st));
+        } else {
+            lg.resize((size_t)n * V);
+            ATLAS_HIP(hipMemcpyAsync(lg.data(), m->logits, (size_t)n * V * 4, hipMemcpyDeviceToHost,
+                                     m->st));
+            ATLAS_HIP(hipStreamSynchronize(m->st));
+        }
+        for (int j = 0; j < n; ++j) {
+            const int i = idx[j];
+            pos[i] += 1;
+            bool choose;
+            if (cursor[i] < prompt_lens[i]) {
+                cursor[i] += 1;
+                choose = cursor[i] == prompt_lens[i];
+            } else {
+                choose = true;
+            }
+            if (!choose) continue;
+            if ((int)gen[i].size() >= max_new) { done[i] = true; continue; }
+            const uint32_t t = host_path
+                ? host_choose(m, lg.data() + (size_t)j * V, (int)gen[i].size(), gen[i], s)
+                : choice[j];
+            if (is_stop(s, t)) { done[i] = true; continue; }
+            gen[i].push_back(t);
+            pending[i] = t;
+            has_pending[i] = true;
+            // the final forward of the last token changes no output: skip it
+            if ((int)gen[i].size() >= max_new) done[i] = true;
+        }
+    }
+    for (int i = 0; i < n_seqs; ++i) {
+        n_out[i] = (int)gen[i].size();
+        for (size_t k = 0; k < gen[i].size(); ++k) out[(size_t)i * max_new + k] = gen[i][k];
+    }
+    m->pos = 0;
+    TRY(sync_pos(m));
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}

@@ -1,0 +1,577 @@
+// fused.hip -- the small per-token kernels of the decode step.
+//
+//  * residual_rmsnorm: x += rmsnorm(y) * w   (post-norm block,
+//    crates/atlas-model/src/lib.rs:983-993) -- one launch instead of the
+//    reference's rmsnorm + vec_add pair (kernels/matmul.cu:241-283, 91-94);
+//  * rmsnorm: out = x * (1/sqrt(mean(x^2)+eps)) * w  (lib.rs:335-342);
+//  * qkv_post: per-head QK-norm (eps 1e-6, lib.rs:660-672) + rotate-half RoPE
+//    from the precomputed tables (lib.rs:428-437) + K/V cache write at pos
+//    (lib.rs:577-585) in one launch, for a batch of sequences;
+//  * argmax with the reference's tie rule (last maximal index,
+//    lib.rs:2701-2706), optionally after step-0 suppression and the
+//    repetition penalty (lib.rs:1629-1646, 2581-2592);
+//  * embedding gather with the token id clamp (lib.rs:539-542);
+//  * seeded initialisers and device-side atlas-quant quantisers.
+// Position and token ids may be read from device memory so that one
+// captured decode step can be replayed for every token.
+#include "common.hpp"
+#include "fused.hpp"
+
+namespace atlas {
+
+// block-wide sum for blockDim.x <= 1024 (all threads must call)
+__device__ float block_sum(float v) {
+    __shared__ float red[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+// ---- rmsnorm / residual ----------------------------------------------------
+
+// out = rmsnorm(x) * w ; row b of a batch at x + b*ld, out + b*ld
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w,
+                                                       float* __restrict__ out, int n, long ld,
+                                                       float eps) {
+    const float* xb = x + blockIdx.x * ld;
+    float* ob = out + blockIdx.x * ld;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += xb[i] * xb[i];
+    ss = block_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ob[i] = xb[i] * inv * w[i];
+}
+
+// x += (y * inv) * w with inv = 1/sqrt(mean(y^2)+eps); batch row b at +b*ld
+__global__ __launch_bounds__(1024) void residual_rmsnorm_kernel(float* __restrict__ x,
+                                                                const float* __restrict__ y,
+                                                                const float* __restrict__ w, int n,
+                                                                long ld, float eps) {
+    float* xb = x + blockIdx.x * ld;
+    const float* yb = y + blockIdx.x * ld;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += yb[i] * yb[i];
+    ss = block_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) xb[i] += yb[i] * inv * w[i];
+}
+
+int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, long ld, float eps,
+                   hipStream_t st) {
+    ATLAS_REQUIRE(x && w && out && n > 0 && rows > 0, "rmsnorm: bad arguments");
+    const int threads = n >= 1024 ? 1024 : ((n + 63) / 64) * 64;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(threads), 0, st, x, w, out, n, ld, eps);
+    ATLAS_LAUNCH_CHECK("rmsnorm");
+    return ATLAS_OK;
+}
+
+int residual_rmsnorm_launch(float* x, const float* y, const float* w, int n, int rows, long ld,
+                            float eps, hipStream_t st) {
+    ATLAS_REQUIRE(x && y && w && n > 0 && rows > 0, "residual_rmsnorm: bad arguments");
+    const int threads = n >= 1024 ? 1024 : ((n + 63) / 64) * 64;
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(threads), 0, st, x, y, w, n, ld,
+                       eps);
+    ATLAS_LAUNCH_CHECK("residual_rmsnorm");
+    return ATLAS_OK;
+}
+
+// ---- QK-norm + RoPE + KV write ---------------------------------------------
+// grid (n_heads + n_kv [+ n_kv for V], n_seq), block = 64 (one wave per head).
+// Head vector element e = lane + 64*j lives in registers and in LDS for the
+// rotate-half partner e +- half.
+__global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
+    __shared__ float hv[256];
+    const int s = blockIdx.y;
+    const int hidx = blockIdx.x;
+    const int HD = a.head_dim, half = HD / 2, lane = threadIdx.x;
+    const int pos = a.pos_dev ? a.pos_dev[s] : a.pos;
+    float* qkv = a.qkv + (long)s * a.qkv_stride;
+    const int nq = a.n_heads, nkv = a.n_kv;
+    const int slot = a.slot_dev ? a.slot_dev[s] : 0;
+    const long cache_off = (long)slot * a.slot_stride + ((long)pos * nkv) * HD;
+
+    if (hidx >= nq + nkv) {
+        // V head: copy into the cache
+        const int vh = hidx - nq - nkv;
+        const float* src = qkv + (long)(nq + nkv + vh) * HD;
+        float* dst = a.v_cache + cache_off + (long)vh * HD;
+        for (int e = lane; e < HD; e += 64) dst[e] = src[e];
+        return;
+    }
+    const bool is_q = hidx < nq;
+    float* xh = qkv + (long)hidx * HD;
+    const float* nw = is_q ? (a.q_norm ? a.q_norm + (long)hidx * HD : nullptr)
+                           : (a.k_norm ? a.k_norm + (long)(hidx - nq) * HD : nullptr);
+    float v[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < HD ? xh[e] : 0.f;
+        ss += v[j] * v[j];
+    }
+    if (nw) {
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + a.qk_eps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            if (e < HD) v[j] = v[j] * inv * nw[e];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        if (e < HD) hv[e] = v[j];
+    }
+    __syncthreads();
+    const float* c = a.cos_tab + (long)pos * half;
+    const float* sn = a.sin_tab + (long)pos * half;
+    float* dst = is_q ? xh : a.k_cache + cache_off + (long)(hidx - nq) * HD;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        if (e < HD) {
+            float r;
+            if (e < half) r = hv[e] * c[e] - hv[e + half] * sn[e];
+            else r = hv[e - half] * sn[e - half] + hv[e] * c[e - half];
+            dst[e] = r;
+        }
+    }
+}
+
+int qkv_post_launch(const QkvPostArgs& a, int n_seq, hipStream_t st) {
+    ATLAS_REQUIRE(a.head_dim > 0 && a.head_dim <= 256 && a.head_dim % 2 == 0,
+                  "qkv_post: head_dim %d", a.head_dim);
+    ATLAS_REQUIRE(a.qkv && a.k_cache && a.v_cache && a.cos_tab && a.sin_tab, "qkv_post: null");
+    ATLAS_REQUIRE(n_seq >= 1, "qkv_post: n_seq");
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(a.n_heads + 2 * a.n_kv, n_seq), dim3(64), 0, st, a);
+    ATLAS_LAUNCH_CHECK("qkv_post");
+    return ATLAS_OK;
+}
+
+// ---- reference-compatible single ops --------------------------------------
+
+// qk_norm_inplace (kernels/matmul.cu:662-710 contract): grid n_heads
+__global__ __launch_bounds__(64) void qk_norm_kernel(float* x, const float* w, int hd, float eps) {
+    float* xh = x + (long)blockIdx.x * hd;
+    const float* wh = w + (long)blockIdx.x * hd;
+    float ss = 0.f;
+    for (int e = threadIdx.x; e < hd; e += 64) ss += xh[e] * xh[e];
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    for (int e = threadIdx.x; e < hd; e += 64) xh[e] = xh[e] * inv * wh[e];
+}
+
+int qk_norm_launch(float* x, const float* w, int n_heads, int hd, float eps, hipStream_t st) {
+    ATLAS_REQUIRE(x && w && n_heads > 0 && hd > 0, "qk_norm: bad arguments");
+    hipLaunchKernelGGL(qk_norm_kernel, dim3(n_heads), dim3(64), 0, st, x, w, hd, eps);
+    ATLAS_LAUNCH_CHECK("qk_norm");
+    return ATLAS_OK;
+}
+
+// rope_precomputed (kernels/matmul.cu:723-743 contract): grid n_heads
+__global__ __launch_bounds__(64) void rope_tab_kernel(float* x, const float* c, const float* s,
+                                                      int hd, int pos) {
+    float* xh = x + (long)blockIdx.x * hd;
+    const int half = hd / 2;
+    const float* cr = c + (long)pos * half;
+    const float* sr = s + (long)pos * half;
+    for (int i = threadIdx.x; i < half; i += 64) {
+        const float x0 = xh[i], x1 = xh[i + half];
+        xh[i] = x0 * cr[i] - x1 * sr[i];
+        xh[i + half] = x0 * sr[i] + x1 * cr[i];
+    }
+}
+
+int rope_tab_launch(float* x, const float* c, const float* s, int n_heads, int hd, int pos,
+                    int max_seq, hipStream_t st) {
+    ATLAS_REQUIRE(x && c && s && n_heads > 0 && hd > 0 && hd % 2 == 0, "rope: bad arguments");
+    ATLAS_REQUIRE(pos >= 0 && pos < max_seq, "rope: pos %d outside [0, %d)", pos, max_seq);
+    hipLaunchKernelGGL(rope_tab_kernel, dim3(n_heads), dim3(64), 0, st, x, c, s, hd, pos);
+    ATLAS_LAUNCH_CHECK("rope");
+    return ATLAS_OK;
+}
+
+// rope_apply (kernels/matmul.cu:285-300 contract; lib.rs:570-587 CPU form)
+__global__ void rope_apply_kernel(float* x, int pos, int hd, float theta) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int half = hd / 2;
+    if (i >= half) return;
+    const float freq = 1.0f / powf(theta, (float)(2 * i) / (float)hd);
+    const float ang = (float)pos * freq;
+    const float c = cosf(ang), s = sinf(ang);
+    const float x0 = x[i], x1 = x[i + half];
+    x[i] = x0 * c - x1 * s;
+    x[i + half] = x0 * s + x1 * c;
+}
+
+int rope_apply_launch(float* x, int pos, int hd, float theta, hipStream_t st) {
+    ATLAS_REQUIRE(x && hd > 0, "rope_apply: bad arguments");
+    const int half = hd / 2;
+    if (half == 0) return ATLAS_OK;
+    hipLaunchKernelGGL(rope_apply_kernel, dim3((half + 63) / 64), dim3(64), 0, st, x, pos, hd, theta);
+    ATLAS_LAUNCH_CHECK("rope_apply");
+    return ATLAS_OK;
+}
+
+__global__ void kv_write_kernel(float* kc, float* vc, const float* nk, const float* nv, long off,
+                                int total) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < total) { kc[off + i] = nk[i]; vc[off + i] = nv[i]; }
+}
+
+int kv_write_launch(float* kc, float* vc, const float* nk, const float* nv, int pos, int n_kv,
+                    int hd, hipStream_t st) {
+    ATLAS_REQUIRE(kc && vc && nk && nv && pos >= 0 && n_kv > 0 && hd > 0, "kv_write: bad arguments");
+    const int total = n_kv * hd;
+    hipLaunchKernelGGL(kv_write_kernel, dim3((total + 255) / 256), dim3(256), 0, st, kc, vc, nk, nv,
+                       (long)pos * total, total);
+    ATLAS_LAUNCH_CHECK("kv_write");
+    return ATLAS_OK;
+}
+
+// ---- elementwise -------------------------------------------------------------
+__global__ void ew_kernel(int op, const float* a, const float* b, float* out, float s, long n) {
+    for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        switch (op) {
+        case EW_ADD: out[i] = a[i] + b[i]; break;
+        case EW_SCALE: out[i] = a[i] * s; break;
+        case EW_RELU: out[i] = a[i] > 0.f ? a[i] : 0.f; break;
+        case EW_SILU_MUL: { const float g = a[i]; out[i] = g / (1.0f + expf(-g)) * b[i]; } break;
+        case EW_COPY: out[i] = a[i]; break;
+        case EW_FILL: out[i] = s; break;
+        }
+    }
+}
+
+int ew_launch(int op, const float* a, const float* b, float* out, float s, long n, hipStream_t st) {
+    ATLAS_REQUIRE(n >= 0 && out, "elementwise: bad arguments");
+    if (n == 0) return ATLAS_OK;
+    long blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(ew_kernel, dim3((unsigned)blocks), dim3(256), 0, st, op, a, b, out, s, n);
+    ATLAS_LAUNCH_CHECK("elementwise");
+    return ATLAS_OK;
+}
+
+// row softmax (kernels/matmul.cu:96-134 contract): one block per row
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* x, float* out, int cols) {
+    const float* xr = x + (long)blockIdx.x * cols;
+    float* orow = out + (long)blockIdx.x * cols;
+    __shared__ float red[4];
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < cols; i += 256) mx = fmaxf(mx, xr[i]);
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.f;
+    for (int i = threadIdx.x; i < cols; i += 256) sum += expf(xr[i] - mx);
+    sum = block_sum(sum);
+    const float inv = 1.0f / sum;
+    for (int i = threadIdx.x; i < cols; i += 256) orow[i] = expf(xr[i] - mx) * inv;
+}
+
+int softmax_rows_launch(const float* x, float* out, int rows, int cols, hipStream_t st) {
+    ATLAS_REQUIRE(x && out && rows >= 0 && cols > 0, "softmax: bad arguments");
+    if (rows == 0) return ATLAS_OK;
+    hipLaunchKernelGGL(softmax_rows_kernel, dim3(rows), dim3(256), 0, st, x, out, cols);
+    ATLAS_LAUNCH_CHECK("softmax");
+    return ATLAS_OK;
+}
+
+// AdamW (kernels/matmul.cu:138-161 contract; training, kept for ABI parity)
+__global__ void adamw_kernel(float* p, float* m, float* v, const float* g, float lr, float b1,
+                             float b2, float eps, float wd, float bc1, float bc2, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gi = g[i];
+    m[i] = b1 * m[i] + (1.f - b1) * gi;
+    v[i] = b2 * v[i] + (1.f - b2) * gi * gi;
+    const float mh = m[i] / bc1, vh = v[i] / bc2;
+    p[i] -= lr * (mh / (sqrtf(vh) + eps) + wd * p[i]);
+}
+
+int adamw_launch(float* p, float* m, float* v, const float* g, float lr, float b1, float b2,
+                 float eps, float wd, float bc1, float bc2, int n, hipStream_t st) {
+    ATLAS_REQUIRE(p && m && v && g && n >= 0, "adamw: bad arguments");
+    if (n == 0) return ATLAS_OK;
+    hipLaunchKernelGGL(adamw_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, m, v, g, lr, b1, b2,
+                       eps, wd, bc1, bc2, n);
+    ATLAS_LAUNCH_CHECK("adamw");
+    return ATLAS_OK;
+}
+
+// ---- token choice --------------------------------------------------------------
+// ordered key: larger float -> larger key; ties keep the larger index (last max)
+__device__ __forceinline__ unsigned long long argkey(float v, int i) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)i;
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+// Penalties are applied in place to the logits (the caller's buffer is a
+// scratch copy, as the reference clones its logits before choosing).
+__global__ __launch_bounds__(256) void penalize_kernel(float* logits, int n, const int* step_dev,
+                                                       const uint32_t* suppress, int n_suppress,
+                                                       const uint32_t* hist, const int* hist_len_dev,
+                                                       int window, float theta) {
+    if (blockIdx.x != 0) return;
+    const int step = step_dev ? *step_dev : 0;
+    if (step == 0)
+        for (int i = threadIdx.x; i < n_suppress; i += 256)
+            if (suppress[i] < (uint32_t)n) logits[suppress[i]] = -INFINITY;
+    __syncthreads();
+    if (theta != 1.0f && hist && hist_len_dev) {
+        const int len = *hist_len_dev;
+        const int start = len > window ? len - window : 0;
+        // sequential in history order: a token seen twice is penalised twice
+        if (threadIdx.x == 0)
+            for (int i = start; i < len; ++i) {
+                const uint32_t t = hist[i];
+                if (t < (uint32_t)n) {
+                    if (logits[t] > 0.f) logits[t] /= theta;
+                    else logits[t] *= theta;
+                }
+            }
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ x, int n,
+                                                             unsigned long long* __restrict__ part) {
+    __shared__ unsigned long long red[4];
+    unsigned long long best = 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        const unsigned long long k = argkey(x[i], i);
+        best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+        for (int w = 1; w < 4; ++w) b = red[w] > b ? red[w] : b;
+        part[blockIdx.x] = b;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long long* __restrict__ part,
+                                                           int nparts, float* out_f32,
+                                                           uint32_t* out_u32, uint32_t* hist,
+                                                           int* hist_len, int* step) {
+    __shared__ unsigned long long red[4];
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < nparts; i += 256) best = part[i] > best ? part[i] : best;
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+        for (int w = 1; w < 4; ++w) b = red[w] > b ? red[w] : b;
+        const uint32_t idx = (uint32_t)(b & 0xFFFFFFFFu);
+        if (out_f32) *out_f32 = (float)idx;
+        if (out_u32) *out_u32 = idx;
+        if (hist && hist_len) { hist[*hist_len] = idx; *hist_len += 1; }
+        if (step) *step += 1;
+    }
+}
+
+int argmax_launch(const ArgmaxArgs& a, hipStream_t st) {
+    ATLAS_REQUIRE(a.x && a.n > 0 && a.part, "argmax: bad arguments");
+    if (a.suppress || (a.theta != 1.0f && a.hist)) {
+        hipLaunchKernelGGL(penalize_kernel, dim3(1), dim3(256), 0, st, (float*)a.x, a.n, a.step,
+                           a.suppress, a.n_suppress, a.hist, a.hist_len, a.window, a.theta);
+        ATLAS_LAUNCH_CHECK("penalize");
+    }
+    int blocks = (a.n + 255) / 256;
+    if (blocks > ARGMAX_MAX_PARTS) blocks = ARGMAX_MAX_PARTS;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(256), 0, st, a.x, a.n, a.part);
+    ATLAS_LAUNCH_CHECK("argmax_partial");
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, a.part, blocks, a.out_f32,
+                       a.out_u32, a.record ? a.hist : nullptr, a.record ? a.hist_len : nullptr,
+                       a.step);
+    ATLAS_LAUNCH_CHECK("argmax_final");
+    return ATLAS_OK;
+}
+
+// ---- embedding gather -----------------------------------------------------------
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__ table, int vocab,
+                                                    int d, const uint32_t* tok_dev, uint32_t tok,
+                                                    float* __restrict__ out, long ld) {
+    const int s = blockIdx.y;
+    uint32_t t = tok_dev ? tok_dev[s] : tok;
+    if (t >= (uint32_t)vocab) t = (uint32_t)vocab - 1;
+    const uint16_t* row = table + (long)t * d;
+    float* o = out + (long)s * ld;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < d; i += gridDim.x * 256)
+        o[i] = __uint_as_float((uint32_t)row[i] << 16);
+}
+
+int embed_launch(const uint16_t* table, int vocab, int d, const uint32_t* tok_dev, uint32_t tok,
+                 float* out, long ld, int n_seq, hipStream_t st) {
+    ATLAS_REQUIRE(table && out && vocab > 0 && d > 0 && n_seq > 0, "embed: bad arguments");
+    const int bx = (d + 255) / 256 < 16 ? (d + 255) / 256 : 16;
+    hipLaunchKernelGGL(embed_kernel, dim3(bx, n_seq), dim3(256), 0, st, table, vocab, d, tok_dev, tok,
+                       out, ld);
+    ATLAS_LAUNCH_CHECK("embed");
+    return ATLAS_OK;
+}
+
+// ---- device counters ---------------------------------------------------------
+__global__ void add_int_kernel(int* p, int n, int v) {
+    const int i = threadIdx.x;
+    if (i < n) p[i] += v;
+}
+
+int add_int_launch(int* p, int n, int v, hipStream_t st) {
+    ATLAS_REQUIRE(p && n > 0 && n <= 1024, "add_int: bad arguments");
+    hipLaunchKernelGGL(add_int_kernel, dim3(1), dim3(n <= 64 ? 64 : 1024), 0, st, p, n, v);
+    ATLAS_LAUNCH_CHECK("add_int");
+    return ATLAS_OK;
+}
+
+// ---- seeded initialisers (SplitMix64 counter + Box-Muller) ---------------------
+__device__ __forceinline__ unsigned long long splitmix_at(unsigned long long seed,
+                                                          unsigned long long n) {
+    unsigned long long z = seed + (n + 1) * 0x9E3779B97F4A7C15ULL;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+__global__ void init_kernel(int kind, void* out, long n, unsigned long long seed, float a, float b) {
+    for (long i = (blockIdx.x * 256L + threadIdx.x) * 2; i < n; i += (long)gridDim.x * 512) {
+        float v0, v1;
+        if (kind == INIT_UNIFORM_F32) {
+            const double u0 = (double)(splitmix_at(seed, i) >> 11) * (1.0 / 9007199254740992.0);
+            const double u1 = (double)(splitmix_at(seed, i + 1) >> 11) * (1.0 / 9007199254740992.0);
+            v0 = (float)(a + (b - a) * u0);
+            v1 = (float)(a + (b - a) * u1);
+        } else {
+            const double u1 = ((double)(splitmix_at(seed, i) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+            const double u2 = ((double)(splitmix_at(seed, i + 1) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+            const double r = sqrt(-2.0 * log(u1));
+            const double t = 6.283185307179586476925286766559 * u2;
+            v0 = (float)(a + b * r * cos(t));
+            v1 = (float)(a + b * r * sin(t));
+        }
+        if (kind == INIT_NORMAL_BF16) {
+            uint16_t* o = reinterpret_cast<uint16_t*>(out);
+            o[i] = (uint16_t)(__float_as_uint(v0) >> 16);
+            if (i + 1 < n) o[i + 1] = (uint16_t)(__float_as_uint(v1) >> 16);
+        } else {
+            float* o = reinterpret_cast<float*>(out);
+            o[i] = v0;
+            if (i + 1 < n) o[i + 1] = v1;
+        }
+    }
+}
+
+int init_launch(int kind, void* out, long n, unsigned long long seed, float a, float b,
+                hipStream_t st) {
+    ATLAS_REQUIRE(out && n >= 0, "init: bad arguments");
+    if (n == 0) return ATLAS_OK;
+    long blocks = (n / 2 + 255) / 256 + 1;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(init_kernel, dim3((unsigned)blocks), dim3(256), 0, st, kind, out, n, seed, a, b);
+    ATLAS_LAUNCH_CHECK("init");
+    return ATLAS_OK;
+}
+
+// ---- device quantisers, bit-exact to crates/atlas-quant/src/lib.rs:43-145 -------
+// Rust `(v * inv).clamp(lo, hi).round() as i8`: clamp, round half away from zero.
+__device__ __forceinline__ int clamp_round(float v, float lo, float hi) {
+    if (v != v) return 0;
+    const float c = v < lo ? lo : (v > hi ? hi : v);
+    return (int)roundf(c);
+}
+
+// source: f32 (src_bf16 == 0) or bf16 bits (src_bf16 == 1); one block per row
+__global__ __launch_bounds__(256) void quant_i8_kernel(const void* src, int src_bf16, int cols,
+                                                       int8_t* data, float* scales) {
+    const long r = blockIdx.x;
+    auto at = [&](long j) -> float {
+        const long e = r * cols + j;
+        return src_bf16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(src)[e] << 16)
+                        : reinterpret_cast<const float*>(src)[e];
+    };
+    float mx = 0.f;
+    for (int j = threadIdx.x; j < cols; j += 256) mx = fmaxf(mx, fabsf(at(j)));
+    __shared__ float red[4];
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = mx > 0.f ? mx / 127.0f : 1.0f;
+    const float inv = 1.0f / s;
+    if (threadIdx.x == 0) scales[r] = s;
+    for (int j = threadIdx.x; j < cols; j += 256)
+        data[r * cols + j] = (int8_t)clamp_round(at(j) * inv, -127.f, 127.f);
+}
+
+// one wave per block of `block` elements of the flattened tensor
+__global__ __launch_bounds__(256) void quant_i4_kernel(const void* src, int src_bf16, long n,
+                                                       int block, uint8_t* data, float* scales,
+                                                       long n_blocks) {
+    const long b = blockIdx.x * 4L + (threadIdx.x >> 6);
+    if (b >= n_blocks) return;
+    const int lane = threadIdx.x & 63;
+    const long start = b * block;
+    const long end = start + block < n ? start + block : n;
+    auto at = [&](long e) -> float {
+        return src_bf16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(src)[e] << 16)
+                        : reinterpret_cast<const float*>(src)[e];
+    };
+    float mx = 0.f;
+    for (long e = start + lane; e < end; e += 64) mx = fmaxf(mx, fabsf(at(e)));
+    mx = wave_max(mx);
+    const float s = mx > 0.f ? mx / 7.0f : 1.0f;
+    const float inv = 1.0f / s;
+    if (lane == 0) scales[b] = s;
+    // each lane packs whole bytes (element pairs); block starts are even when
+    // block is even, so a byte never straddles two blocks
+    for (long e = start + 2 * lane; e < end; e += 128) {
+        const int q0 = clamp_round(at(e) * inv, -7.f, 7.f);
+        const int q1 = e + 1 < end ? clamp_round(at(e + 1) * inv, -7.f, 7.f) : 0;
+        data[e >> 1] = (uint8_t)(((q0 & 0x0F) << 4) | (q1 & 0x0F));
+    }
+}
+
+int quant_i8_launch(const void* src, int src_bf16, int rows, int cols, int8_t* data, float* scales,
+                    hipStream_t st) {
+    ATLAS_REQUIRE(src && data && scales && rows >= 0 && cols > 0, "quant_i8: bad arguments");
+    if (rows == 0) return ATLAS_OK;
+    hipLaunchKernelGGL(quant_i8_kernel, dim3(rows), dim3(256), 0, st, src, src_bf16, cols, data, scales);
+    ATLAS_LAUNCH_CHECK("quant_i8");
+    return ATLAS_OK;
+}
+
+int quant_i4_launch(const void* src, int src_bf16, long n, int block, uint8_t* data, float* scales,
+                    hipStream_t st) {
+    ATLAS_REQUIRE(src && data && scales && n >= 0 && block > 0, "quant_i4: bad arguments");
+    ATLAS_REQUIRE(block % 2 == 0, "quant_i4: device quantiser needs an even block size");
+    if (n == 0) return ATLAS_OK;
+    const long nb = (n + block - 1) / block;
+    hipLaunchKernelGGL(quant_i4_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, src, src_bf16,
+                       n, block, data, scales, nb);
+    ATLAS_LAUNCH_CHECK("quant_i4");
+    return ATLAS_OK;
+}
+
+}  // namespace atlas

@@ -1,0 +1,70 @@
+// fused.hpp -- launch interface of the small decode-step kernels (internal).
+#pragma once
+#include "common.hpp"
+
+namespace atlas {
+
+enum { EW_ADD = 0, EW_SCALE = 1, EW_RELU = 2, EW_SILU_MUL = 3, EW_COPY = 4, EW_FILL = 5 };
+enum { INIT_NORMAL_F32 = 0, INIT_NORMAL_BF16 = 1, INIT_UNIFORM_F32 = 2 };
+enum { ARGMAX_MAX_PARTS = 1024 };
+
+struct QkvPostArgs {
+    float* qkv;              // per sequence: [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)]
+    long qkv_stride;         // elements between sequences
+    const float* q_norm;     // [n_heads*hd] or null (no QK-norm)
+    const float* k_norm;     // [n_kv*hd] or null
+    float qk_eps;
+    const float* cos_tab;    // [max_seq x hd/2]
+    const float* sin_tab;
+    float* k_cache;          // [slots][max_seq][n_kv][hd]
+    float* v_cache;
+    long slot_stride;        // elements per slot
+    const int* slot_dev;     // [n_seq] slot per sequence, or null (slot 0)
+    const int* pos_dev;      // [n_seq] position per sequence, or null (use pos)
+    int pos;
+    int n_heads, n_kv, head_dim;
+};
+
+struct ArgmaxArgs {
+    float* x;                      // logits (modified in place by penalties)
+    int n;
+    unsigned long long* part;      // scratch [ARGMAX_MAX_PARTS]
+    float* out_f32;                // index as float (reference atlas_gpu_argmax)
+    uint32_t* out_u32;             // index as u32
+    const uint32_t* suppress;      // step-0 suppression list (device) or null
+    int n_suppress;
+    uint32_t* hist;                // generated-token history (device) or null
+    int* hist_len;                 // its length (device)
+    int window;                    // repetition window
+    float theta;                   // repetition penalty (1 = off)
+    int* step;                     // device step counter (step 0 = first token), or null
+    int record;                    // append the choice to hist and bump hist_len
+};
+
+int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, long ld, float eps,
+                   hipStream_t st);
+int residual_rmsnorm_launch(float* x, const float* y, const float* w, int n, int rows, long ld,
+                            float eps, hipStream_t st);
+int qkv_post_launch(const QkvPostArgs& a, int n_seq, hipStream_t st);
+int qk_norm_launch(float* x, const float* w, int n_heads, int hd, float eps, hipStream_t st);
+int rope_tab_launch(float* x, const float* c, const float* s, int n_heads, int hd, int pos,
+                    int max_seq, hipStream_t st);
+int rope_apply_launch(float* x, int pos, int hd, float theta, hipStream_t st);
+int kv_write_launch(float* kc, float* vc, const float* nk, const float* nv, int pos, int n_kv,
+                    int hd, hipStream_t st);
+int ew_launch(int op, const float* a, const float* b, float* out, float s, long n, hipStream_t st);
+int softmax_rows_launch(const float* x, float* out, int rows, int cols, hipStream_t st);
+int adamw_launch(float* p, float* m, float* v, const float* g, float lr, float b1, float b2,
+                 float eps, float wd, float bc1, float bc2, int n, hipStream_t st);
+int argmax_launch(const ArgmaxArgs& a, hipStream_t st);
+int embed_launch(const uint16_t* table, int vocab, int d, const uint32_t* tok_dev, uint32_t tok,
+                 float* out, long ld, int n_seq, hipStream_t st);
+int add_int_launch(int* p, int n, int v, hipStream_t st);
+int init_launch(int kind, void* out, long n, unsigned long long seed, float a, float b,
+                hipStream_t st);
+int quant_i8_launch(const void* src, int src_bf16, int rows, int cols, int8_t* data, float* scales,
+                    hipStream_t st);
+int quant_i4_launch(const void* src, int src_bf16, long n, int block, uint8_t* data, float* scales,
+                    hipStream_t st);
+
+}  // namespace atlas

@@ -1,0 +1,306 @@
+// gemv.hip -- batch-1 decode GEMV y = W x for bf16 / int8 / int4 / f32 weights.
+//
+// Semantics: y[m] = sum_k dequant(W)[m,k] * x[k] with f32 accumulation, the
+// reference's Linear::forward (crates/atlas-model/src/lib.rs:487-499) over
+// weights stored as in crates/atlas-tensor/src/lib.rs:242-292 (bf16 bits) and
+// crates/atlas-quant/src/lib.rs:32-168 (int8 per-row scale, int4 per-block
+// scale over the flattened index, even element in the high nibble).
+//
+// Design (gfx950, HBM-bound, no MFMA):
+//  * a 256-thread block = 4 wave64s; each wave owns ROWS consecutive rows and
+//    walks the whole K with 128-bit nontemporal loads (lane i reads the i-th
+//    16-byte chunk of every row, so one instruction reads 1 KiB contiguous
+//    per row);
+//  * x is staged once per block in LDS as f32 with an XOR swizzle on 16-byte
+//    pieces (piece p lives at p ^ ((p >> 3) & 7)), which makes the per-lane
+//    ds_read_b128 of consecutive chunks bank-conflict free;
+//  * one x read feeds ROWS rows, so LDS traffic stays below HBM traffic even
+//    for int4 (32 f32 of x per 16 bytes of weights);
+//  * int8/int4 dequantise with one SDWA sign-extending convert per value;
+//    int4 uses the byte trick (byte & 0xF0) == 16*q_even and
+//    ((byte << 4) & 0xF0) == 16*q_odd, with 1/16 folded into the block scale;
+//  * wave reduction with DPP (row swaps, mirrors, row broadcasts).
+#include "common.hpp"
+#include "gemv.hpp"
+
+namespace atlas {
+
+__device__ __forceinline__ int swz(int p) { return p ^ ((p >> 3) & 7); }
+
+template <int FMT> struct WT;
+template <> struct WT<WF_F32>  { static constexpr int EPC = 4;  };   // elems per 16 B
+template <> struct WT<WF_BF16> { static constexpr int EPC = 8;  };
+template <> struct WT<WF_I8>   { static constexpr int EPC = 16; };
+template <> struct WT<WF_I4>   { static constexpr int EPC = 32; };
+
+// dot of one 16-byte weight chunk with its EPC x values (from swizzled LDS).
+template <int FMT>
+__device__ __forceinline__ float chunk_dot(const u32x4 w, const f32x4* __restrict__ xs,
+                                           int p0, float acc) {
+    if constexpr (FMT == WF_F32) {
+        f32x4 x = xs[swz(p0)];
+        acc += __uint_as_float(w.x) * x.x;
+        acc += __uint_as_float(w.y) * x.y;
+        acc += __uint_as_float(w.z) * x.z;
+        acc += __uint_as_float(w.w) * x.w;
+    } else if constexpr (FMT == WF_BF16) {
+        f32x4 x0 = xs[swz(p0)], x1 = xs[swz(p0 + 1)];
+        acc += bf16_lo(w.x) * x0.x;  acc += bf16_hi(w.x) * x0.y;
+        acc += bf16_lo(w.y) * x0.z;  acc += bf16_hi(w.y) * x0.w;
+        acc += bf16_lo(w.z) * x1.x;  acc += bf16_hi(w.z) * x1.y;
+        acc += bf16_lo(w.w) * x1.z;  acc += bf16_hi(w.w) * x1.w;
+    } else if constexpr (FMT == WF_I8) {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x4 x = xs[swz(p0 + j)];
+            acc += s8_at(ww[j], 0) * x.x;
+            acc += s8_at(ww[j], 1) * x.y;
+            acc += s8_at(ww[j], 2) * x.z;
+            acc += s8_at(ww[j], 3) * x.w;
+        }
+    } else {  // WF_I4: returns sum of (16*q) * x over the 32 elements
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t hi = ww[j] & 0xF0F0F0F0u;          // even elements * 16
+            const uint32_t lo = (ww[j] << 4) & 0xF0F0F0F0u;   // odd elements * 16
+            f32x4 xa = xs[swz(p0 + 2 * j)], xb = xs[swz(p0 + 2 * j + 1)];
+            acc += s8_at(hi, 0) * xa.x;
+            acc += s8_at(lo, 0) * xa.y;
+            acc += s8_at(hi, 1) * xa.z;
+            acc += s8_at(lo, 1) * xa.w;
+            acc += s8_at(hi, 2) * xb.x;
+            acc += s8_at(lo, 2) * xb.y;
+            acc += s8_at(hi, 3) * xb.z;
+            acc += s8_at(lo, 3) * xb.w;
+        }
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+template <int FMT, int ROWS, int UNROLL>
+__global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
+    extern __shared__ f32x4 xs[];
+    constexpr int EPC = WT<FMT>::EPC;
+    constexpr int PPC = EPC / 4;                  // 16-byte x pieces per chunk
+    const int K = a.K, M = a.M;
+    const int npieces = K >> 2;
+    const f32x4* xg = reinterpret_cast<const f32x4*>(a.x);
+    for (int p = threadIdx.x; p < npieces; p += 256) xs[swz(p)] = xg[p];
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int chunks = K / EPC;
+    // bytes per row / 16
+    const long row_chunks = chunks;
+    const u32x4* W = reinterpret_cast<const u32x4*>(a.w);
+    const int n_groups = (M + ROWS - 1) / ROWS;
+
+    for (int g = blockIdx.x * 4 + wave; g < n_groups; g += gridDim.x * 4) {
+        const int r0 = g * ROWS;
+        float acc[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+
+        for (int c0 = lane; c0 < chunks; c0 += 64 * UNROLL) {
+            u32x4 wv[UNROLL][ROWS];
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                const int c = c0 + 64 * u;
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    const int row = r0 + r < M ? r0 + r : M - 1;
+                    wv[u][r] = c < chunks ? ldg_stream(W + (long)row * row_chunks + c)
+                                          : u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                const int c = c0 + 64 * u;
+                if (c < chunks) {
+                    if constexpr (FMT == WF_I4) {
+                        // one 32-element chunk == one quantisation block (block % 32 == 0)
+#pragma unroll
+                        for (int r = 0; r < ROWS; ++r) {
+                            const int row = r0 + r < M ? r0 + r : M - 1;
+                            long bi;
+                            if (a.bpr > 0) bi = (long)row * a.bpr + (a.cpb == 1 ? c : c / a.cpb);
+                            else bi = ((long)row * K + (long)c * EPC) / a.block;
+                            const float s = a.scales[bi] * 0.0625f;
+                            acc[r] += s * chunk_dot<FMT>(wv[u][r], xs, c * PPC, 0.0f);
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < ROWS; ++r)
+                            acc[r] = chunk_dot<FMT>(wv[u][r], xs, c * PPC, acc[r]);
+                    }
+                }
+            }
+        }
+
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
+        if constexpr (FMT == WF_I8) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+                acc[r] *= a.scales[r0 + r < M ? r0 + r : M - 1];
+        }
+        if (a.epi == EPI_SILU_MUL) {
+            // rows (2i, 2i+1) = (gate_i, up_i): y[i] = silu(gate) * up
+            if constexpr (ROWS % 2 == 0) {
+#pragma unroll
+                for (int r = 0; r < ROWS; r += 2)
+                    if (lane == r && r0 + r + 1 < M)
+                        a.y[(r0 + r) >> 1] = silu_f(acc[r]) * acc[r + 1];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+                if (lane == r && r0 + r < M) a.y[r0 + r] = acc[r];
+        }
+    }
+}
+
+// Any-shape fallback (K not a multiple of the chunk width, tiny matrices):
+// one wave per row, scalar loads.  Used for reference-API compatibility.
+template <int FMT>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(GemvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.M) return;
+    float acc = 0.0f;
+    for (int k = lane; k < a.K; k += 64) {
+        const long e = (long)row * a.K + k;
+        float w;
+        if constexpr (FMT == WF_F32) w = reinterpret_cast<const float*>(a.w)[e];
+        else if constexpr (FMT == WF_BF16)
+            w = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.w)[e] << 16);
+        else if constexpr (FMT == WF_I8)
+            w = (float)reinterpret_cast<const int8_t*>(a.w)[e] * a.scales[row];
+        else {
+            const uint8_t b = reinterpret_cast<const uint8_t*>(a.w)[e >> 1];
+            const int nib = (e & 1) ? (b & 0x0F) : (b >> 4);
+            w = (float)(nib >= 8 ? nib - 16 : nib) * a.scales[e / a.block];
+        }
+        acc += w * a.x[k];
+    }
+    // every lane of the wave reaches this point (row is wave-uniform)
+    acc = wave_sum(acc);
+    if (lane == 0) a.y[row] = acc;
+}
+
+// Generic C[m x n] = A[m x k] B[k x n] (A f32 or bf16 bits, B/C f32
+// row-major), 16x16 output tiles through LDS.  Reference-API compatibility
+// for n > 8 (kernels/matmul.cu:51-87, 384-420 contracts).
+template <int FMT>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(const void* __restrict__ A,
+                                                           const float* __restrict__ B,
+                                                           float* __restrict__ C, int m, int n,
+                                                           int k) {
+    __shared__ float As[16][17], Bs[16][17];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int row = blockIdx.y * 16 + ty, col = blockIdx.x * 16 + tx;
+    float acc = 0.f;
+    for (int k0 = 0; k0 < k; k0 += 16) {
+        const int ka = k0 + tx, kb = k0 + ty;
+        float av = 0.f;
+        if (row < m && ka < k) {
+            const long e = (long)row * k + ka;
+            if constexpr (FMT == WF_F32) av = reinterpret_cast<const float*>(A)[e];
+            else av = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(A)[e] << 16);
+        }
+        As[ty][tx] = av;
+        Bs[ty][tx] = (kb < k && col < n) ? B[(long)kb * n + col] : 0.f;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc += As[ty][j] * Bs[j][tx];
+        __syncthreads();
+    }
+    if (row < m && col < n) C[(long)row * n + col] = acc;
+}
+
+int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,
+                        hipStream_t st) {
+    ATLAS_REQUIRE(A && B && C && m >= 0 && n >= 0 && k >= 0, "gemm: bad arguments");
+    ATLAS_REQUIRE(fmt == WF_F32 || fmt == WF_BF16, "gemm: format %d", fmt);
+    if (m == 0 || n == 0) return ATLAS_OK;
+    dim3 grid((n + 15) / 16, (m + 15) / 16);
+    if (fmt == WF_F32) hipLaunchKernelGGL(gemm_generic_kernel<WF_F32>, grid, dim3(256), 0, st, A, B, C, m, n, k);
+    else hipLaunchKernelGGL(gemm_generic_kernel<WF_BF16>, grid, dim3(256), 0, st, A, B, C, m, n, k);
+    ATLAS_LAUNCH_CHECK("gemm_generic");
+    return ATLAS_OK;
+}
+
+// ---------------------------------------------------------------------------
+
+template <int FMT, int ROWS, int UNROLL>
+static int launch_n1(const GemvArgs& a, hipStream_t st) {
+    const size_t lds = (size_t)a.K * 4;
+    auto kern = gemv_n1_kernel<FMT, ROWS, UNROLL>;
+    if (lds > 64 * 1024) {
+        ATLAS_REQUIRE(lds <= 160 * 1024, "gemv: K=%d exceeds the LDS-staged limit 40960", a.K);
+        static bool raised = false;
+        if (!raised) {
+            ATLAS_HIP(hipFuncSetAttribute((const void*)kern,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          160 * 1024));
+            raised = true;
+        }
+    }
+    const int n_groups = (a.M + ROWS - 1) / ROWS;
+    const int blocks = (n_groups + 3) / 4;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a);
+    ATLAS_LAUNCH_CHECK("gemv_n1");
+    return ATLAS_OK;
+}
+
+int gemv_fast_ok(int fmt, int K, int block) {
+    switch (fmt) {
+    case WF_F32:  return K % 4 == 0;
+    case WF_BF16: return K % 8 == 0;
+    case WF_I8:   return K % 16 == 0;
+    case WF_I4:   return K % 32 == 0 && block > 0 && block % 32 == 0;
+    }
+    return 0;
+}
+
+int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
+    GemvArgs a = a_in;
+    gemv_fill_int4_index(a);
+    ATLAS_REQUIRE(a.M >= 0 && a.K >= 0, "gemv: negative shape");
+    if (a.M == 0) return ATLAS_OK;
+    ATLAS_REQUIRE(a.w && a.x && a.y, "gemv: null pointer");
+    ATLAS_REQUIRE(a.fmt == WF_F32 || a.fmt == WF_BF16 || a.scales, "gemv: null scales");
+    ATLAS_REQUIRE(a.fmt != WF_I4 || a.block > 0, "gemv: int4 block must be > 0");
+    if (a.epi == EPI_SILU_MUL) ATLAS_REQUIRE(a.M % 2 == 0, "gemv: silu-mul needs even rows");
+    if (a.K == 0) {
+        set_error(ATLAS_EUNSUPPORTED, "gemv: K == 0");
+        return ATLAS_EUNSUPPORTED;
+    }
+    const bool aligned = (((uintptr_t)a.w | (uintptr_t)a.x) & 15) == 0;
+    if (aligned && gemv_fast_ok(a.fmt, a.K, a.block) && (size_t)a.K * 4 <= 160 * 1024) {
+        switch (a.fmt) {
+        case WF_F32:  return launch_n1<WF_F32, 4, 2>(a, st);
+        case WF_BF16: return launch_n1<WF_BF16, 4, 2>(a, st);
+        case WF_I8:   return launch_n1<WF_I8, 4, 2>(a, st);
+        case WF_I4:   return launch_n1<WF_I4, 4, 1>(a, st);
+        }
+    }
+    ATLAS_REQUIRE(a.epi == EPI_STORE, "gemv: fused epilogue needs the fast path shape");
+    const int blocks = (a.M + 3) / 4;
+    switch (a.fmt) {
+    case WF_F32:  hipLaunchKernelGGL(gemv_generic_kernel<WF_F32>, dim3(blocks), dim3(256), 0, st, a); break;
+    case WF_BF16: hipLaunchKernelGGL(gemv_generic_kernel<WF_BF16>, dim3(blocks), dim3(256), 0, st, a); break;
+    case WF_I8:   hipLaunchKernelGGL(gemv_generic_kernel<WF_I8>, dim3(blocks), dim3(256), 0, st, a); break;
+    case WF_I4:   hipLaunchKernelGGL(gemv_generic_kernel<WF_I4>, dim3(blocks), dim3(256), 0, st, a); break;
+    default: set_error(ATLAS_EINVAL, "gemv: unknown weight format %d", a.fmt); return ATLAS_EINVAL;
+    }
+    ATLAS_LAUNCH_CHECK("gemv_generic");
+    return ATLAS_OK;
+}
+
+}  // namespace atlas

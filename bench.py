@@ -1,0 +1,370 @@
+"""Benchmark of the decode hot path on one MI355X.
+
+Headline (BASELINE.json metric "decode GEMV HBM GB/s (% of peak) + tok/s,
+7B OLMo-shape bf16/int8/int4"): greedy batch-1 decode of a random-init
+OLMo-3-7B-shaped model (32 layers, d 4096, 32/32 heads of 128, SwiGLU 11008,
+vocab 100278, post-norm, QK-norm, YaRN, 24 sliding-window layers) with bf16
+weights, after a 128-token random prompt.  One step = one decoded token
+(every weight GEMV, attention over the KV cache, lm_head, device argmax).
+`value` = tok/s of the K timed steps (weights resident in HBM).
+
+Also reported: the int8 model's tok/s, the GEMV/attention microbenchmarks of
+BASELINE.json configs 1-4 (GB/s against the 8 TB/s HBM peak, each timed over
+>= 1 GiB of rotating buffers so the 256 MB Infinity Cache cannot serve them),
+the roofline of the dominant kernel (the bf16 decode GEMV) and the CPU
+baseline: the oracle's restatement of the reference CPU path on one host
+core, timed on one 7B decode step of the same weights.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class DevBufs:
+    """`count` rotating device copies of one host array (via the C ABI)."""
+
+    def __init__(self, lib, host: np.ndarray, count: int):
+        self.lib, self.ptrs, self.nbytes = lib, [], host.nbytes
+        for _ in range(count):
+            p = C.c_void_p()
+            assert lib.atlas_dev_malloc_sync(C.byref(p), max(host.nbytes, 4)) == 0
+            assert lib.atlas_memcpy_h2d(p.value, _p(host), host.nbytes) == 0
+            self.ptrs.append(p.value)
+
+    def free(self):
+        for p in self.ptrs:
+            self.lib.atlas_dev_free_sync(p)
+        self.ptrs = []
+
+
+def time_launches(torch, fn, n_iter: int, warm: int = 3) -> float:
+    """Average ms per call of fn(i), HIP events on the library's stream."""
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n_iter):
+        fn(i)
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / n_iter
+
+
+def gemv_bench(torch, lib, orc_free_rng, quick: bool) -> dict:
+    """Configs 1-3: batch-1 GEMVs and the int4 skinny GEMM, GB/s."""
+    out = {}
+    rng = orc_free_rng
+    cases = [("bf16_4096x4096", 1, 4096, 4096, 0), ("int8_11008x4096", 2, 11008, 4096, 0),
+             ("int8_4096x11008", 2, 4096, 11008, 0), ("int4_4096x4096_bs32", 3, 4096, 4096, 32),
+             ("int4_11008x4096_bs32", 3, 11008, 4096, 32)]
+    for name, fmt, M, K, bs in cases:
+        if fmt == 1:
+            data = rng.integers(0, 65535, (M, K), dtype=np.uint16)
+            data = (data & 0x807F) | 0x3C00            # finite bf16 of modest size
+            scales = None
+            wbytes = M * K * 2
+        elif fmt == 2:
+            data = rng.integers(-127, 128, (M, K), dtype=np.int8)
+            scales = rng.uniform(1e-4, 2e-4, M).astype(np.float32)
+            wbytes = M * K + 4 * M
+        else:
+            data = rng.integers(0, 256, M * K // 2, dtype=np.uint8)
+            scales = rng.uniform(1e-3, 2e-3, M * K // bs).astype(np.float32)
+            wbytes = M * K // 2 + 4 * (M * K // bs)
+        alg = wbytes + 4 * K + 4 * M
+        copies = max(2, int(np.ceil(1.1e9 / wbytes)))
+        if quick:
+            copies = max(2, copies // 4)
+        W = DevBufs(lib, data, copies)
+        S = DevBufs(lib, scales, copies) if scales is not None else None
+        X = DevBufs(lib, rng.standard_normal(K).astype(np.float32), 1)
+        Y = DevBufs(lib, np.zeros(M, np.float32), 1)
+
+        def run(i, W=W, S=S, X=X, Y=Y, fmt=fmt, M=M, K=K, bs=bs, copies=copies):
+            j = i % copies
+            rc = lib.atlas_gemv_f32(fmt, W.ptrs[j], S.ptrs[j] if S else None, bs, X.ptrs[0],
+                                    Y.ptrs[0], M, K)
+            assert rc == 0
+
+        ms = time_launches(torch, run, copies * (3 if quick else 10))
+        gbs = alg / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 3), "bytes": alg, "rotating_copies": copies}
+        log(f"gemv {name}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+        W.free()
+        if S:
+            S.free()
+        X.free()
+        Y.free()
+    # int4 skinny (ragged micro-batch) at 11008x4096
+    M, K, bs = 11008, 4096, 32
+    data = rng.integers(0, 256, M * K // 2, dtype=np.uint8)
+    scales = rng.uniform(1e-3, 2e-3, M * K // bs).astype(np.float32)
+    wbytes = M * K // 2 + 4 * (M * K // bs)
+    copies = max(2, int(np.ceil(1.1e9 / wbytes)) // (4 if quick else 1))
+    W, S = DevBufs(lib, data, copies), DevBufs(lib, scales, copies)
+    for n in (1, 3, 5, 8):
+        X = DevBufs(lib, rng.standard_normal((n, K)).astype(np.float32), 1)
+        Y = DevBufs(lib, np.zeros((n, M), np.float32), 1)
+
+        def run(i, X=X, Y=Y, n=n):
+            j = i % copies
+            assert lib.atlas_gemm_skinny_f32(3, W.ptrs[j], S.ptrs[j], bs, X.ptrs[0], Y.ptrs[0],
+                                             M, n, K) == 0
+
+        ms = time_launches(torch, run, copies * (2 if quick else 6))
+        alg = wbytes + n * (4 * K + 4 * M)
+        gbs = alg / (ms * 1e-3) / 1e9
+        out[f"int4_skinny_n{n}_11008x4096_bs32"] = {
+            "us": round(ms * 1e3, 2), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3),
+            "bytes": alg}
+        log(f"skinny int4 n={n}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+        X.free()
+        Y.free()
+    W.free()
+    S.free()
+    return out
+
+
+def attention_bench(torch, lib, rng, quick: bool) -> dict:
+    """Config 4: GQA 32 q / 8 kv heads of 128, f32 cache, one query token."""
+    H, KVH, hd = 32, 8, 128
+    out = {}
+    for ctx, window in ((512, 0), (4096, 0), (16384, 0), (16384, 4096)):
+        eff = min(ctx, window) if window else ctx
+        alg = 2 * eff * KVH * hd * 4 + 2 * H * hd * 4
+        cache_bytes = ctx * KVH * hd * 4
+        copies = max(2, int(np.ceil(1.1e9 / (2 * cache_bytes))) // (4 if quick else 1))
+        kv = rng.standard_normal((ctx, KVH, hd)).astype(np.float32)
+        Kc, Vc = DevBufs(lib, kv, copies), DevBufs(lib, kv, copies)
+        Q = DevBufs(lib, rng.standard_normal(H * hd).astype(np.float32), 1)
+        O = DevBufs(lib, np.zeros(H * hd, np.float32), 1)
+
+        def run(i):
+            j = i % copies
+            lib.atlas_decode_attention(Q.ptrs[0], Kc.ptrs[j], Vc.ptrs[j], O.ptrs[0], H, KVH, hd,
+                                       ctx - 1, 0.1067, window)
+
+        ms = time_launches(torch, run, copies * (3 if quick else 10))
+        assert lib.atlas_last_error_code() == 0, lib.atlas_last_error()
+        gbs = alg / (ms * 1e-3) / 1e9
+        key = f"ctx{ctx}" + (f"_w{window}" if window else "")
+        out[key] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 3), "bytes": alg}
+        log(f"attention {key}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+        Kc.free(); Vc.free(); Q.free(); O.free()
+    return out
+
+
+def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int):
+    import dataclasses
+    cfg = dataclasses.replace(model_mod.ModelConfig.olmo3_actual_7b(),
+                              max_seq_len=len(prompt) + warmup + steps + 8)
+    m = model_mod.OlmoModel(cfg, weight_format=fmt, int4_block=32)
+    t0 = time.perf_counter()
+    m.init_random(seed)
+    log(f"fmt {fmt}: random init {time.perf_counter() - t0:.1f}s, "
+        f"{m.weight_bytes() / 1e9:.2f} GB of weights in HBM")
+    m.reset()
+    t0 = time.perf_counter()
+    for t in prompt[:-1]:
+        m.forward_one(int(t))
+    log(f"fmt {fmt}: prompt of {len(prompt)} fed in {time.perf_counter() - t0:.2f}s")
+    toks = m.decode_greedy(int(prompt[-1]), warmup)
+    t0 = time.perf_counter()
+    toks2 = m.decode_greedy(int(toks[-1]) if warmup else int(prompt[-1]), steps)
+    dt = time.perf_counter() - t0
+    assert len(toks2) == steps
+    return m, dt
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--quick", action="store_true", help="fewer microbenchmark iterations")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-micro", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the decode path runs on a single MI355X and multi-GPU sharding is design-only",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    import atlas_amd
+    from atlas_amd import model as am
+
+    lib = atlas_amd.load()
+    if not lib.atlas_cuda_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        return 1
+    torch.cuda.init()
+    lib.atlas_set_stream(C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    rng = np.random.default_rng(2026)
+    prompt = rng.integers(0, 100278, 128)
+
+    micro = {}
+    attn = {}
+    if not args.no_micro:
+        micro = gemv_bench(torch, lib, rng, args.quick)
+        attn = attention_bench(torch, lib, rng, args.quick)
+
+    # ---- headline: bf16 7B decode -------------------------------------------
+    m, dt = decode_bench(am, am.W_BF16, prompt, args.steps, args.warmup, seed=7)
+    ms_step = dt * 1e3 / args.steps
+    tok_s = args.steps / dt
+    wbytes = m.weight_bytes()
+    log(f"bf16 decode: {ms_step:.3f} ms/token, {tok_s:.1f} tok/s, "
+        f"weights {wbytes / 1e9:.2f} GB -> {wbytes / (ms_step * 1e-3) / 1e9:.0f} GB/s")
+
+    # dominant kernel: the bf16 decode GEMV, all launches of one step
+    ms = C.c_float()
+    launches = C.c_int()
+    gbytes = C.c_int64()
+    assert lib.atlas_model_bench_gemv(m._h, 1, C.byref(ms), C.byref(launches), C.byref(gbytes)) == 0
+    iters = 8
+    assert lib.atlas_model_bench_gemv(m._h, iters, C.byref(ms), C.byref(launches),
+                                      C.byref(gbytes)) == 0
+    per_launch_ms = ms.value / launches.value
+    per_launch_bytes = gbytes.value / (launches.value / iters)
+    gemv_gbs = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
+    step_gemv_ms = ms.value / iters
+    log(f"decode GEMVs: {launches.value // iters} launches/step, {step_gemv_ms:.3f} ms/step, "
+        f"{gemv_gbs:.0f} GB/s ({gemv_gbs / HBM_PEAK_GBS:.1%} of peak)")
+
+    # roofline share of the whole step: weights + KV at 8 TB/s vs measured
+    ctx_mid = len(prompt) + args.warmup + args.steps // 2
+    kv_bytes = 0
+    for li in range(32):
+        eff = ctx_mid if li % 4 == 3 else min(ctx_mid, 4096)
+        kv_bytes += 2 * eff * 32 * 128 * 4
+    step_bytes = wbytes + kv_bytes + 100278 * 4
+    step_floor_ms = step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
+
+    # bench the GPU CPU-baseline inputs before freeing the model
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(m, am, prompt)
+    m.close()
+    del m
+
+    # ---- int8 model ------------------------------------------------------------
+    m8, dt8 = decode_bench(am, am.W_INT8, prompt, args.steps, args.warmup, seed=7)
+    tok_s8 = args.steps / dt8
+    log(f"int8 decode: {dt8 * 1e3 / args.steps:.3f} ms/token, {tok_s8:.1f} tok/s")
+    m8.close()
+    del m8
+
+    res = {
+        "metric": "decode GEMV HBM GB/s (% of peak) + tok/s, 7B OLMo-shape bf16/int8/int4",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 weights, f32 activations/accumulation",
+        "data": "synthetic: random-init weights N(0,0.02) (bf16 by truncation), norms U(0.5,1.5), "
+                "128 random prompt ids",
+        "config": {"workload": "OLMo-3-7B-shaped greedy decode, batch 1, bf16 weights "
+                               "(BASELINE.json configs[4])",
+                   "global_batch": 1, "seq_len": len(prompt) + args.warmup + args.steps,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_n1_kernel<bf16> (all weight GEMVs of one decode step)",
+                     "bytes_per_launch": int(per_launch_bytes),
+                     "us_per_launch": round(per_launch_ms * 1e3, 3)},
+        "step_roofline": {"bytes_per_step": int(step_bytes),
+                          "floor_ms": round(step_floor_ms, 4),
+                          "frac_of_step_at_roofline": round(step_floor_ms / ms_step, 4),
+                          "gemv_ms_per_step": round(step_gemv_ms, 4)},
+        "int8": {"tok_s": round(tok_s8, 2), "ms_per_step": round(dt8 * 1e3 / args.steps, 4)},
+        "gemv_microbench": micro,
+        "attention_microbench": attn,
+        "reference_published": {"olmo3_7b_bf16_tok_s": 61.7, "hardware": "A100-SXM4-40GB"},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def cpu_baseline(m, am, prompt) -> dict:
+    """The oracle (restatement of the reference CPU path, one core) on one
+    7B decode step of the same bf16 weights, downloaded from the GPU."""
+    sys.path.insert(0, ROOT)
+    import oracle as orc
+    cfg = am.ModelConfig.olmo3_actual_7b()
+    d, V, L, f = 4096, 100278, 32, 11008
+    t0 = time.perf_counter()
+    shapes = {am.T_WQ: (d, d), am.T_WK: (d, d), am.T_WV: (d, d), am.T_WO: (d, d),
+              am.T_W_GATE: (f, d), am.T_W_UP: (f, d), am.T_W_DOWN: (d, f)}
+    names = {am.T_WQ: "wq", am.T_WK: "wk", am.T_WV: "wv", am.T_WO: "wo", am.T_W_GATE: "w_gate",
+             am.T_W_UP: "w_up", am.T_W_DOWN: "w_down"}
+    layers = []
+    for li in range(L):
+        ld = {}
+        for k, shp in shapes.items():
+            ld[names[k]] = orc.MatView.bf16(m.get_tensor(k, li, shp, np.uint16), *shp)
+        ld["attn_norm"] = m.get_tensor(am.T_ATTN_NORM, li, (d,), np.float32)
+        ld["ffn_norm"] = m.get_tensor(am.T_FFN_NORM, li, (d,), np.float32)
+        ld["q_norm"] = m.get_tensor(am.T_Q_NORM, li, (d,), np.float32)
+        ld["k_norm"] = m.get_tensor(am.T_K_NORM, li, (d,), np.float32)
+        layers.append(ld)
+    emb = orc.MatView.bf16(m.get_tensor(am.T_EMBED, 0, (V, d), np.uint16), V, d)
+    lm = orc.MatView.bf16(m.get_tensor(am.T_LM_HEAD, 0, (V, d), np.uint16), V, d)
+    fn = m.get_tensor(am.T_FINAL_NORM, 0, (d,), np.float32)
+    log(f"cpu baseline: weights downloaded in {time.perf_counter() - t0:.1f}s")
+    ocfg = dict(vocab=V, d_model=d, n_layers=L, n_heads=32, n_kv_heads=32, ffn_hidden=f,
+                max_seq=8, rope_theta=500000.0, rms_eps=1e-6,
+                yarn=dict(factor=8.0, orig_max_pos=8192, attn_factor=1.2079441541679836,
+                          beta_fast=32.0, beta_slow=1.0),
+                sliding_window=4096, layer_sliding=[0 if i % 4 == 3 else 1 for i in range(L)],
+                post_norm=True)
+    om = orc.Model(ocfg, dict(embed=emb, lm_head=lm, final_norm=fn, layers=layers), threads=1)
+    t0 = time.perf_counter()
+    logits = om.forward_one(int(prompt[0]))
+    dt = time.perf_counter() - t0
+    # the same token through the GPU engine at pos 0 (sanity: top-1 agrees)
+    m.reset()
+    glog = m.forward_one(int(prompt[0]))
+    agree = int(np.argmax(glog[::-1])) == int(np.argmax(logits[::-1]))
+    rel = float(np.max(np.abs(glog - logits)) / np.max(np.abs(logits)))
+    log(f"cpu baseline: one 7B decode step on 1 core in {dt:.1f}s; GPU/CPU logits rel err "
+        f"{rel:.2e}, top-1 {'agrees' if agree else 'DIFFERS'}")
+    return {"value": round(1.0 / dt, 5), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": "one OLMo-3-7B-shaped bf16 decode step (pos 0, all 32 layers + lm_head) "
+                      "of the same weights, oracle/oracle.c single-threaded",
+            "seconds": round(dt, 2), "gpu_vs_cpu_logit_rel_err": rel, "top1_agrees": agree}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,193 @@
+/*
+ * atlas_kernels.h -- C ABI of the MI355X (gfx950) decode kernels.
+ *
+ * Drop-in boundary for the reference's `atlas-tensor` FFI.  Part 1 keeps the
+ * exact names and signatures that crates/atlas-tensor/src/lib.rs:17-92
+ * declares in its `extern "C"` block (int dims, raw device pointers, void
+ * return), implemented in HIP for gfx950, so that block links unchanged.
+ * Part 2 replaces the CUDA runtime calls that crates/atlas-tensor/src/lib.rs:
+ * 151-161 makes directly (cudaMalloc / cudaFree / cudaMemcpy /
+ * cudaMallocAsync / cudaFreeAsync).  Part 3 adds the entry points the
+ * decode hot path needs beyond the reference (int8/int4 dequant-fused GEMV,
+ * skinny ragged-batch GEMM, fused norm/RoPE/KV kernels, quantisers).
+ *
+ * Error behaviour: the reference's launches are unchecked and its Rust
+ * wrappers fall back to the CPU when an allocation fails
+ * (crates/atlas-tensor/src/lib.rs:193-207, 371-400).  Here every `int`
+ * entry point returns 0 or a negative ATLAS_E* code, and the `void` ones of
+ * Part 1 record failures the same way: atlas_last_error_code() /
+ * atlas_last_error() report the most recent failure on the calling thread
+ * (cleared by atlas_clear_error()).
+ *
+ * Streams: every launch goes to the library's current stream
+ * (atlas_set_stream; default = the null stream, as in the reference,
+ * kernels/matmul.cu:17-23).  Launches are asynchronous.
+ */
+#ifndef ATLAS_KERNELS_H
+#define ATLAS_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===== Part 1: reference FFI (crates/atlas-tensor/src/lib.rs:17-92) ======= */
+
+/* lib.rs:21-24 -> kernels/matmul.cu:461-513.  C[m x n] = A[m x k] B[k x n],
+ * all f32 row-major.  n == 1 runs the batch-1 GEMV kernel.                  */
+void atlas_matmul_f32(const float* a, const float* b, float* c, int m, int n, int k);
+/* lib.rs:25 -> matmul.cu:522-526 */
+void atlas_vec_add_f32(const float* a, const float* b, float* out, int n);
+/* lib.rs:26 -> matmul.cu:528-531 */
+void atlas_scale_f32(const float* x, float s, float* out, int n);
+/* lib.rs:27 -> matmul.cu:533-536 */
+void atlas_relu_f32(const float* x, float* out, int n);
+/* lib.rs:28 -> matmul.cu:538-542 (row softmax) */
+void atlas_softmax_f32(const float* x, float* out, int rows, int cols);
+/* lib.rs:29-30 -> matmul.cu:580-595.  Names keep the reference's spelling;
+ * they report HIP devices.                                                  */
+int atlas_cuda_available(void);
+int atlas_cuda_device_count(void);
+/* lib.rs:31-33 -> matmul.cu:597-605 */
+void atlas_rmsnorm_f32(const float* x, const float* w, float* out, int n, float eps);
+/* lib.rs:34 -> matmul.cu:607-612 */
+void atlas_rope_apply_f32(float* x, int pos, int head_dim, float theta_base);
+/* lib.rs:35 -> matmul.cu:614-618 */
+void atlas_silu_mul_f32(const float* gate, const float* up, float* out, int n);
+/* lib.rs:36 -> matmul.cu:620-626 */
+void atlas_vram_copy_f32(const float* src, float* dst, int n);
+/* lib.rs:37-41 -> matmul.cu:546-557 (training; kept for ABI completeness) */
+void atlas_adamw_step(float* param, float* m, float* v, const float* grad, float lr,
+                      float beta1, float beta2, float eps, float wd, float bc1, float bc2,
+                      int n);
+/* lib.rs:44-47 -> matmul.cu:636-651.  A_bf16[m x k] (bf16 bits), B[k x n]
+ * f32 row-major (column j = activation j), C[m x n].  n == 1: batch-1 GEMV;
+ * 2 <= n <= 8: skinny MFMA GEMM; larger n: generic kernel.                  */
+void atlas_sgemm_bf16_f32(const uint16_t* a_bf16, const float* b, float* c, int m, int n,
+                          int k);
+/* lib.rs:51 -> matmul.cu:450-459: drains the current device */
+void atlas_sync(void);
+/* lib.rs:56-59 -> matmul.cu:662-710 */
+void atlas_qk_norm_inplace(float* x, const float* w, int n_heads, int head_dim, float eps);
+/* lib.rs:64-68 -> matmul.cu:723-743, 898-907 */
+void atlas_rope_precomputed(float* x, const float* cos_tab, const float* sin_tab, int n_heads,
+                            int head_dim, int pos, int max_seq);
+/* lib.rs:70-74 -> matmul.cu:752-766, 909-919 */
+void atlas_kv_cache_write(float* k_cache, float* v_cache, const float* new_k,
+                          const float* new_v, int pos, int n_kv_heads, int head_dim);
+/* lib.rs:80-86 -> matmul.cu:786-933.  Split-K flash decode here; any
+ * context length (no dynamic-LDS limit).                                    */
+void atlas_decode_attention(const float* q, const float* k_cache, const float* v_cache,
+                            float* out, int n_heads, int n_kv_heads, int head_dim, int pos,
+                            float scale, int window_size);
+/* lib.rs:90 -> matmul.cu:997-1007.  Index written as f32.  Ties return the
+ * LAST maximal index, the rule of the CPU path this feeds
+ * (crates/atlas-model/src/lib.rs:2701-2706).                                */
+void atlas_gpu_argmax(const float* x, float* out_f32, int n);
+
+/* ===== Part 2: device memory (replaces crates/atlas-tensor/src/lib.rs:151-161) */
+
+enum {
+    ATLAS_OK = 0,
+    ATLAS_EINVAL = -1,
+    ATLAS_EHIP = -2,
+    ATLAS_ENOMEM = -3,
+    ATLAS_EUNSUPPORTED = -4
+};
+
+int atlas_last_error_code(void);
+const char* atlas_last_error(void);
+void atlas_clear_error(void);
+
+/* Stream-ordered allocation on the current stream (cudaMallocAsync,
+ * lib.rs:196-206), falling back to a synchronous allocation.               */
+int atlas_dev_malloc(void** ptr, size_t bytes);
+int atlas_dev_free(void* ptr);
+/* Synchronous allocation for long-lived weights (cudaMalloc, lib.rs:254-258). */
+int atlas_dev_malloc_sync(void** ptr, size_t bytes);
+int atlas_dev_free_sync(void* ptr);
+/* Copies; the d2h copy waits for the current stream (lib.rs:217-224).        */
+int atlas_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int atlas_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int atlas_memcpy_d2d(void* dst, const void* src, size_t bytes);
+int atlas_memset_zero(void* dst, size_t bytes);     /* fill kernel, graph-safe */
+
+int atlas_set_device(int device);
+int atlas_set_stream(void* hip_stream);               /* NULL = null stream */
+void* atlas_get_stream(void);
+int atlas_stream_sync(void);
+int atlas_device_cu_count(void);
+
+/* ===== Part 3: decode hot-path extensions (no reference counterpart) ===== */
+
+/* Weight storage formats of the GEMV family. */
+enum {
+    ATLAS_W_F32 = 0,     /* f32 row-major                                     */
+    ATLAS_W_BF16 = 1,    /* bf16 bits row-major (GpuBufKind::BF16)            */
+    ATLAS_W_INT8 = 2,    /* Int8Tensor: i8 row-major + f32 scale per row      */
+    ATLAS_W_INT4 = 3     /* Int4Tensor: nibbles over the flattened index, even
+                            element in the high nibble, f32 scale per block   */
+};
+
+/* y[m] = sum_k dequant(W)[m,k] x[k] (f32 accumulation).  Batch-1 decode GEMV
+ * semantics of Linear::forward (crates/atlas-model/src/lib.rs:487-499) with
+ * W stored per crates/atlas-quant/src/lib.rs:32-168.  scales: NULL for
+ * f32/bf16; int8 [m]; int4 [ceil(m*k/block)].                               */
+int atlas_gemv_f32(int fmt, const void* w, const float* scales, int block, const float* x,
+                   float* y, int m, int k);
+int atlas_gemv_bf16_f32(const uint16_t* w, const float* x, float* y, int m, int k);
+int atlas_gemv_i8_f32(const int8_t* w, const float* scales, const float* x, float* y, int m,
+                      int k);
+int atlas_gemv_i4_f32(const uint8_t* w, const float* scales, int block, const float* x,
+                      float* y, int m, int k);
+/* Fused SwiGLU GEMV: W has 2*h rows interleaved (gate_0, up_0, gate_1, ...);
+ * h_out[i] = silu(gate_i . x) * (up_i . x)  (FeedForward::forward,
+ * crates/atlas-model/src/lib.rs:911-924).                                   */
+int atlas_gemv_swiglu_f32(int fmt, const void* w, const float* scales, int block,
+                          const float* x, float* h_out, int h, int k);
+
+/* Ragged micro-batch: Y[n, m] = sum_k dequant(W)[m,k] X[n,k] for 1 <= n <= 8
+ * activation rows (X [n x k] row-major, Y [n x m] row-major).  MFMA bf16 with
+ * hi/lo split activations.  fmt: BF16, INT8, INT4.                          */
+int atlas_gemm_skinny_f32(int fmt, const void* w, const float* scales, int block,
+                          const float* x, float* y, int m, int n, int k);
+
+/* out = rmsnorm(x) * w row-wise over `rows` rows of length n (ld = n).      */
+int atlas_rmsnorm_rows_f32(const float* x, const float* w, float* out, int n, int rows,
+                           float eps);
+/* Post-norm residual: x += rmsnorm(y) * w  (crates/atlas-model/src/lib.rs:
+ * 983-993), row-wise over `rows` rows.                                       */
+int atlas_residual_rmsnorm_f32(float* x, const float* y, const float* w, int n, int rows,
+                               float eps);
+/* Fused per-head QK-norm (q_norm/k_norm may be NULL) + RoPE from the tables +
+ * K/V cache write at pos.  qkv = [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)];
+ * q is rotated in place; K, V land in the caches [max_seq][n_kv][hd].        */
+int atlas_qkv_post_f32(float* qkv, const float* q_norm, const float* k_norm, float qk_eps,
+                       const float* cos_tab, const float* sin_tab, float* k_cache,
+                       float* v_cache, int n_heads, int n_kv, int head_dim, int pos);
+/* Greedy choice: index of the last maximum of x[0..n) as u32 (device).      */
+int atlas_argmax_u32(const float* x, int n, uint32_t* out_idx);
+
+/* Device-side quantisers, bit-exact to Int8Tensor::quantize /
+ * Int4Tensor::quantize (crates/atlas-quant/src/lib.rs:43-63, 113-145).
+ * src_is_bf16 selects bf16-bits or f32 input.  int4 needs an even block.     */
+int atlas_quantize_int8_dev(const void* src, int src_is_bf16, int rows, int cols,
+                            int8_t* data, float* scales);
+int atlas_quantize_int4_dev(const void* src, int src_is_bf16, int64_t n, int block,
+                            uint8_t* data, float* scales);
+/* Host-side quantisers (same rules; for callers holding host weights).      */
+int atlas_quantize_int8_host(const float* w, int64_t rows, int64_t cols, int8_t* data,
+                             float* scales);
+int atlas_quantize_int4_host(const float* w, int64_t rows, int64_t cols, int64_t block,
+                             uint8_t* data, float* scales);
+
+/* Seeded synthetic fills on the device: SplitMix64 counter + Box-Muller.
+ * kind 0: N(a, b) f32; 1: N(a, b) bf16 by truncation; 2: U(a, b) f32.        */
+int atlas_fill_random(int kind, void* out, int64_t n, uint64_t seed, float a, float b);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

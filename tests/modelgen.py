@@ -214,3 +214,44 @@ class Ref64:
                 x = x + ffn(self._rms(x, fn, c["rms_eps"]))
         x = self._rms(x, W["final_norm"].astype(np.float64), c["rms_eps"])
         return W["lm_head"].astype(np.float64) @ x
+
+
+# ---------------------------------------------------------------------------
+# the same weights uploaded into the HIP engine
+# ---------------------------------------------------------------------------
+
+def engine_model(W: dict, max_batch: int = 1, use_graph: bool = True):
+    from atlas_amd import model as am
+    c = W["cfg"]
+    y = c.get("yarn")
+    sl = c.get("layer_sliding") or [0] * c["n_layers"]
+    cfg = am.ModelConfig(vocab_size=c["vocab"], d_model=c["d_model"], n_layers=c["n_layers"],
+                         n_heads=c["n_heads"], n_kv_heads=c["n_kv_heads"],
+                         ffn_hidden=c["ffn_hidden"], max_seq_len=c["max_seq"],
+                         rope_theta=c["rope_theta"], rms_norm_eps=c["rms_eps"],
+                         layer_types=["sliding" if s else "full" for s in sl],
+                         sliding_window=c.get("sliding_window") or None,
+                         rope_scaling=am.RopeYarn(**y) if y else None,
+                         post_norm=c.get("post_norm", True), qk_norm=c.get("qk_norm", True))
+    fmt = {"bf16": am.W_BF16, "int8": am.W_INT8, "int4": am.W_INT4}[W["fmt"]]
+    m = am.OlmoModel(cfg, weight_format=fmt, int4_block=W["block"], max_batch=max_batch)
+    m.use_graph(use_graph)
+    kinds = dict(wq=am.T_WQ, wk=am.T_WK, wv=am.T_WV, wo=am.T_WO, w_gate=am.T_W_GATE,
+                 w_up=am.T_W_UP, w_down=am.T_W_DOWN)
+
+    def put(kind, layer, stored):
+        k, arrs = stored
+        m.set_tensor(kind, layer, arrs[0], arrs[1] if len(arrs) > 1 else None)
+
+    for li, lw in enumerate(W["layers"]):
+        for n, kd in kinds.items():
+            put(kd, li, lw[n + "_stored"])
+        m.set_tensor(am.T_ATTN_NORM, li, lw["attn_norm"])
+        m.set_tensor(am.T_FFN_NORM, li, lw["ffn_norm"])
+        if lw["q_norm"] is not None:
+            m.set_tensor(am.T_Q_NORM, li, lw["q_norm"])
+            m.set_tensor(am.T_K_NORM, li, lw["k_norm"])
+    m.set_tensor(am.T_EMBED, 0, W["embed_bits"])
+    put(am.T_LM_HEAD, 0, W["lm_head_stored"])
+    m.set_tensor(am.T_FINAL_NORM, 0, W["final_norm"])
+    return m

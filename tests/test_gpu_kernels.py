@@ -1,0 +1,344 @@
+"""Kernel parity on the MI355X: every HIP entry point against the oracle.
+
+Tolerances: GEMV outputs max-abs <= 1e-3 * max|y_ref|;
+attention outputs <= 2e-3 * max|o_ref|; quantisation and indexing bit-exact.
+Inputs are seeded N(0, 0.02) weights and N(0, 1) activations, as the configs ask.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+from tests.gpu_util import Dev, lib, rel_err, sync
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3
+ATTN_TOL = 2e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    import atlas_amd
+    atlas_amd.load()
+    if not lib().atlas_cuda_available():
+        pytest.fail("no HIP device visible: GPU tests need an MI355X")
+
+
+def _w(shape, seed):
+    return (np.random.default_rng(seed).standard_normal(shape) * 0.02).astype(np.float32)
+
+
+def _x(n, seed):
+    return np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# batch-1 GEMV: bf16 / int8 / int4 / f32
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,K", [(4096, 4096), (11008, 4096), (4096, 11008), (100, 64),
+                                 (37, 200), (4, 3)])
+def test_gemv_bf16(orc, M, K):
+    print(f"gemv_bf16 M={M} K={K}", flush=True)
+    bits = orc.bf16_from_f32(_w((M, K), M + K))
+    x = _x(K, 1)
+    y_ref = orc.linear(orc.MatView.bf16(bits, M, K), x, threads=8)
+    dw, dx, dy = Dev(bits), Dev(x), Dev.empty(M)
+    assert lib().atlas_gemv_bf16_f32(dw.ptr, dx.ptr, dy.ptr, M, K) == 0
+    assert rel_err(dy.get(), y_ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("M,K", [(11008, 4096), (4096, 11008), (64, 48), (5, 7)])
+def test_gemv_int8(orc, M, K):
+    print(f"gemv_int8 M={M} K={K}", flush=True)
+    q, s = orc.int8_quantize(_w((M, K), 3 * M + K))
+    x = _x(K, 2)
+    y_ref = orc.linear(orc.MatView.int8(q, s), x, threads=8)
+    dw, ds, dx, dy = Dev(q), Dev(s), Dev(x), Dev.empty(M)
+    assert lib().atlas_gemv_i8_f32(dw.ptr, ds.ptr, dx.ptr, dy.ptr, M, K) == 0
+    assert rel_err(dy.get(), y_ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("M,K,bs", [(4096, 4096, 32), (11008, 4096, 32), (4096, 11008, 32),
+                                    (256, 4096, 64), (3, 96, 64), (7, 50, 32)])
+def test_gemv_int4(orc, M, K, bs):
+    print(f"gemv_int4 M={M} K={K} bs={bs}", flush=True)
+    q, s = orc.int4_quantize(_w((M, K), 5 * M + K), bs)
+    x = _x(K, 3)
+    y_ref = orc.linear(orc.MatView.int4(q, s, M, K, bs), x, threads=8)
+    dw, ds, dx, dy = Dev(q), Dev(s), Dev(x), Dev.empty(M)
+    assert lib().atlas_gemv_i4_f32(dw.ptr, ds.ptr, bs, dx.ptr, dy.ptr, M, K) == 0
+    assert rel_err(dy.get(), y_ref) <= GEMV_TOL
+
+
+def test_gemv_f32_matmul_n1(orc):
+    w = _w((300, 512), 9)
+    x = _x(512, 4)
+    y_ref = orc.linear(orc.MatView.f32(w), x)
+    dw, dx, dy = Dev(w), Dev(x), Dev.empty(300)
+    lib().atlas_matmul_f32(dw.ptr, dx.ptr, dy.ptr, 300, 1, 512)
+    sync()
+    assert rel_err(dy.get(), y_ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
+def test_gemv_swiglu(orc, fmt):
+    h, K = 512, 256
+    g, u = _w((h, K), 11), _w((h, K), 12)
+    x = _x(K, 5)
+    inter = np.empty((2 * h, K), np.float32)
+    inter[0::2], inter[1::2] = g, u
+    if fmt == "bf16":
+        stored = orc.bf16_from_f32(inter)
+        gv, uv = orc.MatView.bf16(stored[0::2].copy(), h, K), orc.MatView.bf16(stored[1::2].copy(), h, K)
+        args = (1, Dev(stored), None, 0)
+    elif fmt == "int8":
+        q, s = orc.int8_quantize(inter)
+        gv, uv = orc.MatView.int8(q[0::2].copy(), s[0::2].copy()), orc.MatView.int8(q[1::2].copy(), s[1::2].copy())
+        args = (2, Dev(q), Dev(s), 0)
+    else:
+        q, s = orc.int4_quantize(inter, 32)
+        qg, qu = q.reshape(2 * h, K // 2)[0::2].copy(), q.reshape(2 * h, K // 2)[1::2].copy()
+        sg, su = s.reshape(2 * h, K // 32)[0::2].copy(), s.reshape(2 * h, K // 32)[1::2].copy()
+        gv, uv = orc.MatView.int4(qg, sg, h, K, 32), orc.MatView.int4(qu, su, h, K, 32)
+        args = (3, Dev(q), Dev(s), 32)
+    gr, ur = orc.linear(gv, x), orc.linear(uv, x)
+    ref = np.array([orc.silu(float(a)) for a in gr], np.float32) * ur
+    dx, dh = Dev(x), Dev.empty(h)
+    fmt_id, dw, ds, bs = args
+    assert lib().atlas_gemv_swiglu_f32(fmt_id, dw.ptr, ds.ptr if ds else None, bs, dx.ptr, dh.ptr,
+                                       h, K) == 0
+    assert rel_err(dh.get(), ref) <= GEMV_TOL
+
+
+# ---------------------------------------------------------------------------
+# skinny ragged batch (MFMA)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 3, 5, 8])
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
+def test_skinny(orc, fmt, n):
+    M, K = (4096, 4096) if n in (1, 8) else (1000, 512)
+    print(f"skinny {fmt} n={n} M={M} K={K}", flush=True)
+    w = _w((M, K), 21 + n)
+    x = np.random.default_rng(n).standard_normal((n, K)).astype(np.float32)
+    if fmt == "bf16":
+        b = orc.bf16_from_f32(w)
+        view, dw, ds, fid, bs = orc.MatView.bf16(b, M, K), Dev(b), None, 1, 0
+    elif fmt == "int8":
+        q, s = orc.int8_quantize(w)
+        view, dw, ds, fid, bs = orc.MatView.int8(q, s), Dev(q), Dev(s), 2, 0
+    else:
+        q, s = orc.int4_quantize(w, 32)
+        view, dw, ds, fid, bs = orc.MatView.int4(q, s, M, K, 32), Dev(q), Dev(s), 3, 32
+    ref = orc.linear_batch(view, x)
+    dx, dy = Dev(x), Dev.empty((n, M))
+    assert lib().atlas_gemm_skinny_f32(fid, dw.ptr, ds.ptr if ds else None, bs, dx.ptr, dy.ptr,
+                                       M, n, K) == 0
+    y = dy.get()
+    for i in range(n):
+        assert rel_err(y[i], ref[i]) <= GEMV_TOL, i
+
+
+def test_sgemm_bf16_reference_layout(orc):
+    # crates/atlas-tensor/src/lib.rs:44-47: B is [k x n] row-major, C [m x n]
+    M, K = 256, 512
+    b = orc.bf16_from_f32(_w((M, K), 31))
+    view = orc.MatView.bf16(b, M, K)
+    for n in (2, 5, 8, 12):
+        X = np.random.default_rng(n).standard_normal((K, n)).astype(np.float32)
+        ref = np.stack([orc.linear(view, X[:, j].copy()) for j in range(n)], axis=1)
+        dw, dx, dc = Dev(b), Dev(X), Dev.empty((M, n))
+        lib().atlas_sgemm_bf16_f32(dw.ptr, dx.ptr, dc.ptr, M, n, K)
+        sync()
+        assert rel_err(dc.get(), ref) <= GEMV_TOL, n
+
+
+def test_sgemm_vec_ones_literal():
+    # crates/atlas-tensor/src/lib.rs:1207-1220
+    from atlas_amd.tensor import GpuMatrix, GpuVec
+    gm = GpuMatrix.upload(np.ones(12, np.float32), 4, 3)
+    out = gm.sgemm_vec(GpuVec.from_slice([1.0, 1.0, 1.0]), 1)
+    assert out.len == 4
+    assert np.allclose(out.download(), 3.0)
+
+
+# ---------------------------------------------------------------------------
+# attention (config 4: 32 q heads, 8 kv heads, hd 128)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ctx,window", [(512, 0), (4096, 0), (16384, 0), (16384, 4096),
+                                        (4096, 4096), (1, 0), (300, 64)])
+def test_decode_attention_gqa(orc, ctx, window):
+    H, KVH, hd = 32, 8, 128
+    print(f"attention ctx={ctx} window={window}", flush=True)
+    rng = np.random.default_rng(ctx + window)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    K = rng.standard_normal((ctx, KVH, hd)).astype(np.float32)
+    V = rng.standard_normal((ctx, KVH, hd)).astype(np.float32)
+    scale = 1.2079441541679836 / math.sqrt(hd)
+    pos = ctx - 1
+    ref = orc.attention(q, K, V, H, KVH, hd, pos, scale, window)
+    dq, dk, dv, do = Dev(q), Dev(K), Dev(V), Dev.empty(H * hd)
+    lib().atlas_decode_attention(dq.ptr, dk.ptr, dv.ptr, do.ptr, H, KVH, hd, pos, scale, window)
+    sync()
+    assert rel_err(do.get(), ref) <= ATTN_TOL
+
+
+@pytest.mark.parametrize("H,KVH,hd", [(4, 2, 16), (8, 8, 64), (4, 1, 64), (32, 32, 128),
+                                      (6, 3, 32), (8, 2, 256)])
+def test_decode_attention_shapes(orc, H, KVH, hd):
+    rng = np.random.default_rng(H * hd)
+    ctx = 77
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    K = rng.standard_normal((ctx, KVH, hd)).astype(np.float32)
+    V = rng.standard_normal((ctx, KVH, hd)).astype(np.float32)
+    for pos, window in ((ctx - 1, 0), (40, 7), (0, 0)):
+        ref = orc.attention(q, K, V, H, KVH, hd, pos, 0.1, window)
+        dq, dk, dv, do = Dev(q), Dev(K), Dev(V), Dev.empty(H * hd)
+        lib().atlas_decode_attention(dq.ptr, dk.ptr, dv.ptr, do.ptr, H, KVH, hd, pos, 0.1, window)
+        sync()
+        assert rel_err(do.get(), ref) <= ATTN_TOL, (pos, window)
+
+
+# ---------------------------------------------------------------------------
+# fused norm / RoPE / KV write
+# ---------------------------------------------------------------------------
+
+def test_qkv_post_matches_oracle(orc):
+    H, KVH, hd, max_seq, pos = 32, 8, 128, 64, 37
+    yarn = dict(factor=8.0, orig_max_pos=8192, attn_factor=1.2079441541679836,
+                beta_fast=32.0, beta_slow=1.0)
+    cos, sin, _ = orc.rope_tables(hd, max_seq, 500000.0, yarn)
+    rng = np.random.default_rng(8)
+    qkv = rng.standard_normal((H + 2 * KVH) * hd).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, H * hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, KVH * hd).astype(np.float32)
+    q_ref = orc.qk_norm(qkv[:H * hd], qn, H, hd, 1e-6)
+    k_ref = orc.qk_norm(qkv[H * hd:(H + KVH) * hd], kn, KVH, hd, 1e-6)
+    q_ref = np.concatenate([orc.rope_apply(q_ref[h * hd:(h + 1) * hd], cos[pos], sin[pos]) for h in range(H)])
+    k_ref = np.concatenate([orc.rope_apply(k_ref[h * hd:(h + 1) * hd], cos[pos], sin[pos]) for h in range(KVH)])
+    d_qkv, dqn, dkn = Dev(qkv), Dev(qn), Dev(kn)
+    dcos, dsin = Dev(cos), Dev(sin)
+    kc, vc = Dev.empty((max_seq, KVH, hd)), Dev.empty((max_seq, KVH, hd))
+    assert lib().atlas_qkv_post_f32(d_qkv.ptr, dqn.ptr, dkn.ptr, 1e-6, dcos.ptr, dsin.ptr, kc.ptr,
+                                    vc.ptr, H, KVH, hd, pos) == 0
+    out = d_qkv.get()
+    assert np.max(np.abs(out[:H * hd] - q_ref)) <= 1e-5 * np.max(np.abs(q_ref))
+    assert np.max(np.abs(kc.get()[pos].reshape(-1) - k_ref)) <= 1e-5 * np.max(np.abs(k_ref))
+    assert np.array_equal(vc.get()[pos].reshape(-1), qkv[(H + KVH) * hd:])
+    assert np.all(kc.get()[pos + 1:] == 0) and np.all(kc.get()[:pos] == 0)
+
+
+def test_reference_qk_norm_rope_kv_ops(orc):
+    H, hd, max_seq, pos = 4, 64, 16, 5
+    cos, sin, _ = orc.rope_tables(hd, max_seq, 10000.0)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(H * hd).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, H * hd).astype(np.float32)
+    ref = orc.qk_norm(x, w, H, hd, 1e-6)
+    ref = np.concatenate([orc.rope_apply(ref[h * hd:(h + 1) * hd], cos[pos], sin[pos]) for h in range(H)])
+    dx, dw, dc, ds = Dev(x), Dev(w), Dev(cos), Dev(sin)
+    lib().atlas_qk_norm_inplace(dx.ptr, dw.ptr, H, hd, 1e-6)
+    lib().atlas_rope_precomputed(dx.ptr, dc.ptr, ds.ptr, H, hd, pos, max_seq)
+    sync()
+    assert np.max(np.abs(dx.get() - ref)) <= 1e-5 * np.max(np.abs(ref))
+    kc, vc = Dev.empty((max_seq, H * hd)), Dev.empty((max_seq, H * hd))
+    nk, nv = Dev(x), Dev(w)
+    lib().atlas_kv_cache_write(kc.ptr, vc.ptr, nk.ptr, nv.ptr, pos, H, hd)
+    sync()
+    assert np.array_equal(kc.get()[pos], x) and np.array_equal(vc.get()[pos], w)
+
+
+def test_rmsnorm_and_residual(orc):
+    # crates/atlas-tensor/src/lib.rs:1171-1181 literal
+    from atlas_amd.tensor import GpuVec
+    x = GpuVec.from_slice([1.0, 2.0, 3.0, 4.0])
+    x.rmsnorm_inplace(GpuVec.from_slice([1.0] * 4), 1e-5)
+    out = x.download()
+    r = math.sqrt(7.5)
+    assert abs(out[0] - 1 / r) < 1e-6 and abs(out[3] - 4 / r) < 1e-6
+    rng = np.random.default_rng(4)
+    for n in (4096, 11008, 77):
+        xs, ys = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        ref = xs + orc.rmsnorm(ys, w, 1e-6)
+        dx, dy, dw = Dev(xs), Dev(ys), Dev(w)
+        assert lib().atlas_residual_rmsnorm_f32(dx.ptr, dy.ptr, dw.ptr, n, 1, 1e-6) == 0
+        assert np.max(np.abs(dx.get() - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+def test_reference_tensor_ops():
+    # crates/atlas-tensor/src/lib.rs:1144-1205 (GpuVec tests)
+    from atlas_amd import tensor as t
+    assert t.cuda_available() and t.cuda_device_count() >= 1
+    z = t.GpuVec.zeros(64)
+    assert z.len == 64 and np.all(z.download() == 0)
+    v = t.GpuVec.from_slice(np.arange(16, dtype=np.float32))
+    assert np.array_equal(v.download(), np.arange(16, dtype=np.float32))
+    a = t.GpuVec.from_slice([1.0, 2.0, 3.0, 4.0])
+    a.add_inplace(t.GpuVec.from_slice([0.5] * 4))
+    assert np.allclose(a.download(), [1.5, 2.5, 3.5, 4.5])
+    s = t.silu_mul_gpu(t.GpuVec.from_slice([0.0, 1.0, -1.0, 2.0]), t.GpuVec.from_slice([1.0] * 4))
+    assert abs(s.download()[0]) < 1e-6 and abs(s.download()[1] - 0.7310586) < 1e-6
+    r = t.GpuVec.from_slice([1.0, 2.0, 3.0, 4.0])
+    t.rope_apply_gpu(r, 0, 4, 10000.0)
+    assert np.allclose(r.download(), [1.0, 2.0, 3.0, 4.0])
+
+
+# ---------------------------------------------------------------------------
+# argmax, quantisers, initialisers
+# ---------------------------------------------------------------------------
+
+def test_argmax_tie_rule_and_values(orc):
+    from atlas_amd.tensor import GpuVec, gpu_argmax
+    assert gpu_argmax(GpuVec.from_slice([1.0, 3.0, 3.0, 2.0])) == 2
+    rng = np.random.default_rng(0)
+    for n in (100278, 1, 257, 300000):
+        x = rng.standard_normal(n).astype(np.float32)
+        if n > 10:
+            x[n // 3] = x[n - 5] = x.max() + 1.0      # tie: the later index wins
+        dx, do = Dev(x), Dev.empty(1, np.uint32)
+        assert lib().atlas_argmax_u32(dx.ptr, n, do.ptr) == 0
+        assert int(do.get()[0]) == orc.argmax(x)
+
+
+def test_device_quantisers_bit_exact(orc):
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((257, 192)) * 0.02).astype(np.float32)
+    w[3] = 0.0                                      # all-zero row -> scale 1
+    w[5, :10] = [127 * 0.01, 2.5 * 0.01, -2.5 * 0.01, 0, 0, 0, 0, 0, 0, 0]
+    q_ref, s_ref = orc.int8_quantize(w)
+    dq, ds = Dev.empty(w.shape, np.int8), Dev.empty(257)
+    assert lib().atlas_quantize_int8_dev(Dev(w).ptr, 0, 257, 192, dq.ptr, ds.ptr) == 0
+    assert np.array_equal(dq.get(), q_ref) and np.array_equal(ds.get(), s_ref)
+    for bs in (32, 64, 50):
+        q4, s4 = orc.int4_quantize(w, bs)
+        d4, d4s = Dev.empty(q4.shape, np.uint8), Dev.empty(s4.shape)
+        assert lib().atlas_quantize_int4_dev(Dev(w).ptr, 0, w.size, bs, d4.ptr, d4s.ptr) == 0
+        assert np.array_equal(d4.get(), q4) and np.array_equal(d4s.get(), s4), bs
+    # bf16-bits input quantises the widened values
+    bits = orc.bf16_from_f32(w)
+    q_ref, s_ref = orc.int8_quantize(orc.bf16_to_f32(bits))
+    assert lib().atlas_quantize_int8_dev(Dev(bits).ptr, 1, 257, 192, dq.ptr, ds.ptr) == 0
+    assert np.array_equal(dq.get(), q_ref) and np.array_equal(ds.get(), s_ref)
+
+
+def test_fill_random_distribution():
+    n = 1 << 20
+    d = Dev.empty(n)
+    assert lib().atlas_fill_random(0, d.ptr, n, 7, 0.0, 0.02) == 0
+    v = d.get().astype(np.float64)
+    assert abs(v.mean()) < 1e-4 and abs(v.std() - 0.02) < 1e-4
+    assert lib().atlas_fill_random(2, d.ptr, n, 7, 0.5, 1.5) == 0
+    u = d.get()
+    assert u.min() >= 0.5 and u.max() < 1.5 and abs(u.mean() - 1.0) < 2e-3
+
+
+def test_errors_are_reported():
+    from atlas_amd._lib import AtlasError, check
+    with pytest.raises(AtlasError):
+        check(lib().atlas_gemv_i4_f32(None, None, 32, None, None, 4, 32))
+    assert lib().atlas_gemv_f32(7, None, None, 0, None, None, 0, 0) == 0   # empty is a no-op
