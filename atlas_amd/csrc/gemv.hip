@@ -86,81 +86,107 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
     extern __shared__ f32x4 xs[];
     constexpr int EPC = WT<FMT>::EPC;
     constexpr int PPC = EPC / 4;                  // 16-byte x pieces per chunk
+    constexpr int STEP = 64 * UNROLL;             // chunks per wave iteration
     const int K = a.K, M = a.M;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int chunks = K / EPC;                   // 16-byte chunks per row
+    const u32x4* W = reinterpret_cast<const u32x4*>(a.w);
+    const int n_groups = (M + ROWS - 1) / ROWS;
+    // persistent waves: wave w of the grid takes row groups w, w + S, ...
+    const int S = gridDim.x * 4;
+    const int g0 = blockIdx.x * 4 + wave;
+    const int iters = (chunks + STEP - 1) / STEP;
+    const int my_groups = g0 < n_groups ? (n_groups - 1 - g0) / S + 1 : 0;
+    const int total = my_groups * iters;          // (group, k-slice) steps of this wave
+
+    // weights (and int4 block scales) of step `it` into registers
+    auto load = [&](int it, u32x4 (&wb)[UNROLL][ROWS], float (&sb)[UNROLL][ROWS]) {
+        const int g = g0 + (it / iters) * S;
+        const int c0 = lane + (it % iters) * STEP;
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int c = c0 + 64 * u;
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const int row = g * ROWS + r < M ? g * ROWS + r : M - 1;
+                wb[u][r] = c < chunks ? ldg_stream(W + (long)row * chunks + c)
+                                      : u32x4{0u, 0u, 0u, 0u};
+                if constexpr (FMT == WF_I4) {
+                    long bi;
+                    if (a.bpr > 0) bi = (long)row * a.bpr + (a.cpb == 1 ? c : c / a.cpb);
+                    else bi = ((long)row * K + (long)c * EPC) / a.block;
+                    sb[u][r] = c < chunks ? a.scales[bi] * 0.0625f : 0.0f;
+                }
+            }
+        }
+    };
+
+    u32x4 cur[UNROLL][ROWS];
+    float scur[UNROLL][ROWS];
+    // the first weight loads go out before x is staged, hiding the staging
+    if (total > 0) load(0, cur, scur);
     const int npieces = K >> 2;
     const f32x4* xg = reinterpret_cast<const f32x4*>(a.x);
     for (int p = threadIdx.x; p < npieces; p += 256) xs[swz(p)] = xg[p];
     __syncthreads();
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int chunks = K / EPC;
-    // bytes per row / 16
-    const long row_chunks = chunks;
-    const u32x4* W = reinterpret_cast<const u32x4*>(a.w);
-    const int n_groups = (M + ROWS - 1) / ROWS;
-
-    for (int g = blockIdx.x * 4 + wave; g < n_groups; g += gridDim.x * 4) {
-        const int r0 = g * ROWS;
-        float acc[ROWS];
+    float acc[ROWS];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
 
-        for (int c0 = lane; c0 < chunks; c0 += 64 * UNROLL) {
-            u32x4 wv[UNROLL][ROWS];
+    for (int it = 0; it < total; ++it) {
+        u32x4 nxt[UNROLL][ROWS];
+        float snx[UNROLL][ROWS];
+        if (it + 1 < total) load(it + 1, nxt, snx);     // one step of prefetch
+        const int ks = it % iters;
+        const int c0 = lane + ks * STEP;
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                const int c = c0 + 64 * u;
+        for (int u = 0; u < UNROLL; ++u) {
+            const int c = c0 + 64 * u;
+            if (c < chunks) {
 #pragma unroll
                 for (int r = 0; r < ROWS; ++r) {
-                    const int row = r0 + r < M ? r0 + r : M - 1;
-                    wv[u][r] = c < chunks ? ldg_stream(W + (long)row * row_chunks + c)
-                                          : u32x4{0u, 0u, 0u, 0u};
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                const int c = c0 + 64 * u;
-                if (c < chunks) {
-                    if constexpr (FMT == WF_I4) {
-                        // one 32-element chunk == one quantisation block (block % 32 == 0)
-#pragma unroll
-                        for (int r = 0; r < ROWS; ++r) {
-                            const int row = r0 + r < M ? r0 + r : M - 1;
-                            long bi;
-                            if (a.bpr > 0) bi = (long)row * a.bpr + (a.cpb == 1 ? c : c / a.cpb);
-                            else bi = ((long)row * K + (long)c * EPC) / a.block;
-                            const float s = a.scales[bi] * 0.0625f;
-                            acc[r] += s * chunk_dot<FMT>(wv[u][r], xs, c * PPC, 0.0f);
-                        }
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < ROWS; ++r)
-                            acc[r] = chunk_dot<FMT>(wv[u][r], xs, c * PPC, acc[r]);
-                    }
+                    if constexpr (FMT == WF_I4)
+                        acc[r] += scur[u][r] * chunk_dot<FMT>(cur[u][r], xs, c * PPC, 0.0f);
+                    else
+                        acc[r] = chunk_dot<FMT>(cur[u][r], xs, c * PPC, acc[r]);
                 }
             }
         }
-
+        if (ks == iters - 1) {
+            // end of this row group: reduce across the wave and store
+            const int r0 = (g0 + (it / iters) * S) * ROWS;
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
-        if constexpr (FMT == WF_I8) {
+            for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
+            if constexpr (FMT == WF_I8) {
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-                acc[r] *= a.scales[r0 + r < M ? r0 + r : M - 1];
-        }
-        if (a.epi == EPI_SILU_MUL) {
-            // rows (2i, 2i+1) = (gate_i, up_i): y[i] = silu(gate) * up
-            if constexpr (ROWS % 2 == 0) {
-#pragma unroll
-                for (int r = 0; r < ROWS; r += 2)
-                    if (lane == r && r0 + r + 1 < M)
-                        a.y[(r0 + r) >> 1] = silu_f(acc[r]) * acc[r + 1];
+                for (int r = 0; r < ROWS; ++r) acc[r] *= a.scales[r0 + r < M ? r0 + r : M - 1];
             }
-        } else {
+            if (a.epi == EPI_SILU_MUL) {
+                // rows (2i, 2i+1) = (gate_i, up_i): y[i] = silu(gate) * up
+                if constexpr (ROWS % 2 == 0) {
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-                if (lane == r && r0 + r < M) a.y[r0 + r] = acc[r];
+                    for (int r = 0; r < ROWS; r += 2)
+                        if (lane == r && r0 + r + 1 < M)
+                            a.y[(r0 + r) >> 1] = silu_f(acc[r]) * acc[r + 1];
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r)
+                    if (lane == r && r0 + r < M) a.y[r0 + r] = acc[r];
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+        }
+        if (it + 1 < total) {
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    cur[u][r] = nxt[u][r];
+                    scur[u][r] = snx[u][r];
+                }
         }
     }
 }
@@ -238,7 +264,7 @@ int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m,
 // ---------------------------------------------------------------------------
 
 template <int FMT, int ROWS, int UNROLL>
-static int launch_n1(const GemvArgs& a, hipStream_t st) {
+int launch_n1(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
     const size_t lds = (size_t)a.K * 4;
     auto kern = gemv_n1_kernel<FMT, ROWS, UNROLL>;
     if (lds > 64 * 1024) {
@@ -252,7 +278,13 @@ static int launch_n1(const GemvArgs& a, hipStream_t st) {
         }
     }
     const int n_groups = (a.M + ROWS - 1) / ROWS;
-    const int blocks = (n_groups + 3) / 4;
+    int blocks = (n_groups + 3) / 4;
+    // LDS bounds the resident blocks per CU; never ask for more than fit
+    int fit = (int)((160 * 1024) / (lds ? lds : 1));
+    if (fit < 1) fit = 1;
+    int bpc = blocks_per_cu < fit ? blocks_per_cu : fit;
+    const int cap = bpc * device_cu_count();
+    if (blocks > cap) blocks = cap;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a);
     ATLAS_LAUNCH_CHECK("gemv_n1");
     return ATLAS_OK;
@@ -284,10 +316,10 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     const bool aligned = (((uintptr_t)a.w | (uintptr_t)a.x) & 15) == 0;
     if (aligned && gemv_fast_ok(a.fmt, a.K, a.block) && (size_t)a.K * 4 <= 160 * 1024) {
         switch (a.fmt) {
-        case WF_F32:  return launch_n1<WF_F32, 4, 2>(a, st);
-        case WF_BF16: return launch_n1<WF_BF16, 4, 2>(a, st);
-        case WF_I8:   return launch_n1<WF_I8, 4, 2>(a, st);
-        case WF_I4:   return launch_n1<WF_I4, 4, 1>(a, st);
+        case WF_F32:  return launch_n1<WF_F32, 2, 4>(a, st, 8);
+        case WF_BF16: return launch_n1<WF_BF16, 2, 4>(a, st, 8);
+        case WF_I8:   return launch_n1<WF_I8, 2, 2>(a, st, 8);
+        case WF_I4:   return launch_n1<WF_I4, 4, 1>(a, st, 8);
         }
     }
     ATLAS_REQUIRE(a.epi == EPI_STORE, "gemv: fused epilogue needs the fast path shape");
