@@ -95,10 +95,12 @@ SIGNATURES = {
     "atlas_gemv_i8_f32": (I, [P, P, P, P, I, I]),
     "atlas_gemv_i4_f32": (I, [P, P, I, P, P, I, I]),
     "atlas_gemv_swiglu_f32": (I, [I, P, P, I, P, P, I, I]),
+    "atlas_gemv_fused_f32": (I, [I, P, P, I, P, P, I, I, I, P, P, F, P]),
     "atlas_gemm_skinny_f32": (I, [I, P, P, I, P, P, I, I, I]),
     "atlas_rmsnorm_rows_f32": (I, [P, P, P, I, I, F]),
     "atlas_residual_rmsnorm_f32": (I, [P, P, P, I, I, F]),
     "atlas_qkv_post_f32": (I, [P, P, P, F, P, P, P, P, I, I, I, I]),
+    "atlas_attention_fused_f32": (I, [P, P, P, F, P, P, P, P, P, I, I, I, I, F, I, I]),
     "atlas_argmax_u32": (I, [P, I, P]),
     "atlas_quantize_int8_dev": (I, [P, I, I, I, P, P]),
     "atlas_quantize_int4_dev": (I, [P, I, I64, I, P, P]),
@@ -123,7 +125,7 @@ SIGNATURES = {
                                            C.POINTER(C.c_int)]),
     "atlas_model_generate_batch": (I, [P, P, P, I, I, C.POINTER(SamplingC), P, P]),
     "atlas_model_decode_greedy": (I, [P, U32, I, P]),
-    "atlas_model_bench_gemv": (I, [P, I, P, P, P]),
+    "atlas_model_bench_gemv": (I, [P, I, I, P, P, P]),
     "atlas_model_use_graph": (I, [P, I]),
     "atlas_model_stream": (P, [P]),
     "atlas_model_logits_dev": (P, [P]),

@@ -223,6 +223,280 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
 }
 
 // ---------------------------------------------------------------------------
+// Fused decode attention for one layer: per-head QK-norm (eps 1e-6,
+// crates/atlas-model/src/lib.rs:660-672) and rotate-half RoPE from the tables
+// (lib.rs:428-437) of the raw q|k|v GEMV output, K/V cache write at pos
+// (lib.rs:577-585), split-K attention (lib.rs:689-721) and the split merge,
+// in one launch.  grid (n_kv, n_splits, n_seq).
+//  * every block recomputes the normalised+rotated q of its G heads and k
+//    (a few hundred flops) into LDS;
+//  * the block whose slice contains pos writes k/v into the cache and scores
+//    position pos from LDS, so no block reads a cache row written in this
+//    launch;
+//  * the splits of a (sequence, kv head) merge in the block that finishes
+//    last: each block publishes its partial, fences, and bumps a counter; the
+//    block that sees n_splits - 1 merges and resets the counter to 0 (no
+//    waiting anywhere, and the counters are clean for the next launch).
+// ---------------------------------------------------------------------------
+template <int HD, int G, int P>
+__global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
+    constexpr int DPL = HD / 16;
+    constexpr int EPL = HD / 64;              // head elements per lane in the prep
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int kvh = blockIdx.x, split = blockIdx.y, n_splits = gridDim.y, seq = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = lane >> 4, dl = lane & 15;
+    const int pos = a.pos_dev[seq];
+    const int slot = a.slot_dev ? a.slot_dev[seq] : 0;
+    const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
+    const int ctx = pos - t_lo + 1;
+    const int chunk = (ctx + n_splits - 1) / n_splits;
+    const int b0 = t_lo + split * chunk;
+    const int b1 = min(pos + 1, b0 + chunk);
+    const bool owner = b0 <= pos && pos < b0 + chunk;
+    const int e1 = min(b1, pos);              // cache rows [b0, e1) are read here
+    const long kv_stride = (long)a.n_kv * HD;
+    const float* qkv = a.qkv + (long)seq * a.qkv_stride;
+    float* kc = a.k_cache + (long)slot * a.slot_stride;
+    float* vc = a.v_cache + (long)slot * a.slot_stride;
+
+    __shared__ float sq[G][HD], sk[HD], sv[HD];
+    // ---- prep: QK-norm + RoPE of the G q heads and k, wave per vector -----
+    const float* cr = a.cos_tab + (long)pos * (HD / 2);
+    const float* sr = a.sin_tab + (long)pos * (HD / 2);
+    for (int vi = wave; vi < G + 1; vi += 4) {
+        const bool isq = vi < G;
+        const int head = isq ? kvh * G + vi : kvh;
+        const float* src = qkv + (isq ? (long)head * HD : (long)(a.n_heads + kvh) * HD);
+        const float* nw = isq ? (a.q_norm ? a.q_norm + (long)head * HD : nullptr)
+                              : (a.k_norm ? a.k_norm + (long)kvh * HD : nullptr);
+        float v[EPL];
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            v[j] = src[lane + 64 * j];
+            ss += v[j] * v[j];
+        }
+        if (nw) {
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + a.qk_eps);
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) v[j] = v[j] * inv * nw[lane + 64 * j];
+        }
+        float r[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            if constexpr (HD == 64) {
+                const float other = __shfl_xor(v[j], 32, 64);   // partner e +- 32
+                r[j] = e < 32 ? v[j] * cr[e] - other * sr[e] : other * sr[e - 32] + v[j] * cr[e - 32];
+            } else {
+                constexpr int HJ = EPL / 2;                     // partner is j +- HJ
+                r[j] = j < HJ ? v[j] * cr[e] - v[j + HJ] * sr[e]
+                              : v[j - HJ] * sr[e - HD / 2] + v[j] * cr[e - HD / 2];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            if (isq) sq[vi][e] = r[j] * (a.scale * LOG2E);
+            else sk[e] = r[j];
+        }
+    }
+    for (int e = threadIdx.x; e < HD; e += 256) sv[e] = qkv[(long)(a.n_heads + a.n_kv + kvh) * HD + e];
+    __syncthreads();
+    if (owner) {
+        for (int e = threadIdx.x; e < HD; e += 256) {
+            kc[(long)pos * kv_stride + (long)kvh * HD + e] = sk[e];
+            vc[(long)pos * kv_stride + (long)kvh * HD + e] = sv[e];
+        }
+    }
+
+    float q[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) q[h][d] = sq[h][dl * DPL + d];
+    float m[G], l[G], o[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        m[h] = -INFINITY; l[h] = 0.f;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
+    }
+
+    auto update = [&](const float (&kf)[P][DPL], const float (&vf)[P][DPL], const bool (&valid)[P]) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float s[P];
+            float smax = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                float acc = 0.f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) acc += q[h][d] * kf[i][d];
+                acc = row16_sum(acc);
+                s[i] = valid[i] ? acc : -INFINITY;
+                smax = fmaxf(smax, s[i]);
+            }
+            const float mn = fmaxf(m[h], smax);
+            const float corr = exp2f(m[h] - mn);
+            float psum = 0.f, p[P];
+#pragma unroll
+            for (int i = 0; i < P; ++i) { p[i] = exp2f(s[i] - mn); psum += p[i]; }
+            l[h] = l[h] * corr + psum;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                float acc = o[h][d] * corr;
+#pragma unroll
+                for (int i = 0; i < P; ++i) acc += p[i] * vf[i][d];
+                o[h][d] = acc;
+            }
+            m[h] = mn;
+        }
+    };
+
+    const float* kbase = kc + (long)kvh * HD + dl * DPL;
+    const float* vbase = vc + (long)kvh * HD + dl * DPL;
+    for (int t0 = b0 + (wave * 4 + row) * P; t0 < e1; t0 += 16 * P) {
+        float kf[P][DPL], vf[P][DPL];
+        bool valid[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int t = t0 + i;
+            valid[i] = t < e1;
+            const long off = (long)(valid[i] ? t : t0) * kv_stride;
+#pragma unroll
+            for (int d = 0; d < DPL; d += 4) {
+                const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off + d);
+                const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off + d);
+                kf[i][d] = kv.x; kf[i][d + 1] = kv.y; kf[i][d + 2] = kv.z; kf[i][d + 3] = kv.w;
+                vf[i][d] = vv.x; vf[i][d + 1] = vv.y; vf[i][d + 2] = vv.z; vf[i][d + 3] = vv.w;
+            }
+        }
+        update(kf, vf, valid);
+    }
+    if (owner && wave == 0 && row == 0) {
+        // position pos from LDS (the 16 lanes of row 0 of wave 0)
+        float kf[P][DPL], vf[P][DPL];
+        bool valid[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            valid[i] = i == 0;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                kf[i][d] = sk[dl * DPL + d];
+                vf[i][d] = sv[dl * DPL + d];
+            }
+        }
+        update(kf, vf, valid);
+    }
+
+    // ---- merge the 16 (wave,row) states of this block ------------------------
+    __shared__ float s_m[16][G], s_l[16][G];
+    __shared__ float s_o[16][G][HD];
+    __shared__ int s_last;
+    const int st = wave * 4 + row;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        if (dl == 0) { s_m[st][h] = m[h]; s_l[st][h] = l[h]; }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) s_o[st][h][dl * DPL + d] = o[h][d];
+    }
+    __syncthreads();
+    const long pbase = (long)seq * a.n_heads * n_splits;
+    for (int e = threadIdx.x; e < G * HD; e += 256) {
+        const int h = e / HD, d = e % HD;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) mx = fmaxf(mx, s_m[s2][h]);
+        float lsum = 0.f, osum = 0.f;
+        if (mx != -INFINITY) {
+#pragma unroll
+            for (int s2 = 0; s2 < 16; ++s2) {
+                const float w = exp2f(s_m[s2][h] - mx);
+                lsum += s_l[s2][h] * w;
+                osum += s_o[s2][h][d] * w;
+            }
+        }
+        const int qh = kvh * G + h;
+        if (n_splits == 1) {
+            a.out[(long)seq * a.out_stride + (long)qh * HD + d] = osum / lsum;
+        } else {
+            const long pi = pbase + (long)qh * n_splits + split;
+            a.part_o[pi * HD + d] = osum;
+            if (d == 0) { a.part_m[pi] = mx; a.part_l[pi] = lsum; }
+        }
+    }
+    if (n_splits == 1) return;
+    // ---- the last block of this (seq, kv head) merges the splits -------------
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = atomicAdd(&a.counters[seq * a.n_kv + kvh], 1);
+        s_last = prev == n_splits - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int e = threadIdx.x; e < G * HD; e += 256) {
+        const int h = e / HD, d = e % HD;
+        const int qh = kvh * G + h;
+        const long p0 = pbase + (long)qh * n_splits;
+        float mx = -INFINITY;
+        for (int s2 = 0; s2 < n_splits; ++s2)
+            mx = fmaxf(mx, __hip_atomic_load(&a.part_m[p0 + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        float lsum = 0.f, osum = 0.f;
+        for (int s2 = 0; s2 < n_splits; ++s2) {
+            const float mm = __hip_atomic_load(&a.part_m[p0 + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (mm == -INFINITY) continue;
+            const float w = exp2f(mm - mx);
+            lsum += __hip_atomic_load(&a.part_l[p0 + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * w;
+            osum += __hip_atomic_load(&a.part_o[(p0 + s2) * HD + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * w;
+        }
+        a.out[(long)seq * a.out_stride + (long)qh * HD + d] = osum / lsum;
+    }
+    if (threadIdx.x == 0) atomicExch(&a.counters[seq * a.n_kv + kvh], 0);
+}
+
+template <int HD, int G>
+static int launch_fused(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st) {
+    hipLaunchKernelGGL((attn_fused_kernel<HD, G, 4>), dim3(a.n_kv, n_splits, n_seq), dim3(256), 0,
+                       st, a);
+    ATLAS_LAUNCH_CHECK("attn_fused");
+    return ATLAS_OK;
+}
+
+bool attn_fused_supported(int n_heads, int n_kv, int head_dim) {
+    if (n_kv <= 0 || n_heads % n_kv) return false;
+    const int G = n_heads / n_kv;
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+           (G == 1 || G == 2 || G == 4 || G == 8) && !(head_dim == 256 && G == 8);
+}
+
+int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st) {
+    ATLAS_REQUIRE(attn_fused_supported(a.n_heads, a.n_kv, a.head_dim),
+                  "attention: fused path needs head_dim 64/128/256 and group 1/2/4/8");
+    ATLAS_REQUIRE(a.qkv && a.k_cache && a.v_cache && a.out && a.pos_dev && a.cos_tab && a.sin_tab,
+                  "attention: null pointer");
+    ATLAS_REQUIRE(n_splits == 1 || (a.part_m && a.part_l && a.part_o && a.counters),
+                  "attention: split partials missing");
+    ATLAS_REQUIRE(n_seq >= 1 && n_splits >= 1, "attention: empty grid");
+    const uintptr_t al = (uintptr_t)a.qkv | (uintptr_t)a.k_cache | (uintptr_t)a.v_cache;
+    ATLAS_REQUIRE((al & 15) == 0 && a.qkv_stride % 4 == 0 && a.slot_stride % 4 == 0,
+                  "attention: 16-byte alignment");
+    const int G = a.n_heads / a.n_kv;
+#define ATLAS_FUSED_CASE(HDV, GV) \
+    if (a.head_dim == HDV && G == GV) return launch_fused<HDV, GV>(a, n_splits, n_seq, st);
+    ATLAS_FUSED_CASE(128, 1) ATLAS_FUSED_CASE(128, 2) ATLAS_FUSED_CASE(128, 4) ATLAS_FUSED_CASE(128, 8)
+    ATLAS_FUSED_CASE(64, 1)  ATLAS_FUSED_CASE(64, 2)  ATLAS_FUSED_CASE(64, 4)  ATLAS_FUSED_CASE(64, 8)
+    ATLAS_FUSED_CASE(256, 1) ATLAS_FUSED_CASE(256, 2) ATLAS_FUSED_CASE(256, 4)
+#undef ATLAS_FUSED_CASE
+    set_error(ATLAS_EUNSUPPORTED, "attention: fused shape");
+    return ATLAS_EUNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
 
 static float* g_part = nullptr;
 static size_t g_part_bytes = 0;

@@ -19,6 +19,33 @@ struct AttnArgs {
     float* part_o;
 };
 
+// Fused QK-norm + RoPE + KV write + split-K attention + split merge.
+struct AttnFusedArgs {
+    const float* qkv;        // per sequence [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)]
+    long qkv_stride;         // elements between sequences
+    const float* q_norm;     // [n_heads*hd] or null
+    const float* k_norm;     // [n_kv*hd] or null
+    float qk_eps;
+    const float* cos_tab;    // [max_seq x hd/2]
+    const float* sin_tab;
+    float* k_cache;          // [slots][max_seq][n_kv][hd]
+    float* v_cache;
+    long slot_stride;
+    const int* slot_dev;     // [n_seq] or null (slot 0)
+    const int* pos_dev;      // [n_seq]
+    float* out;              // per sequence [n_heads*hd]
+    long out_stride;
+    int n_heads, n_kv, head_dim;
+    float scale;
+    int window;
+    float* part_m;           // [n_seq][n_heads][n_splits]
+    float* part_l;
+    float* part_o;           // [n_seq][n_heads][n_splits][hd]
+    int* counters;           // [n_seq][n_kv], zero before the first launch
+};
+
+bool attn_fused_supported(int n_heads, int n_kv, int head_dim);
+int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st);
 int attn_pick_splits(int n_kv, int max_ctx);
 int attn_reserve(int n_heads, int head_dim, int n_splits);
 int attn_launch(AttnArgs a, int n_splits, hipStream_t st);

@@ -146,6 +146,18 @@ ATLAS_API int atlas_gemv_i4_f32(const uint8_t* w, const float* scales, int block
     return atlas_gemv_f32(ATLAS_W_INT4, w, scales, block, x, y, m, k);
 }
 
+ATLAS_API int atlas_gemv_fused_f32(int fmt, const void* w, const float* scales, int block,
+                                   const float* x, float* yout, int m, int k, int pro,
+                                   const float* y, const float* norm_w, float eps, float* x_out) {
+    ATLAS_REQUIRE(pro >= PRO_X && pro <= PRO_SILU, "gemv_fused: prologue %d", pro);
+    ATLAS_REQUIRE(pro != PRO_RESNORM || x_out, "gemv_fused: residual prologue needs x_out");
+    GemvArgs a{};
+    a.fmt = fmt; a.w = w; a.scales = scales; a.block = block; a.x = x; a.y = yout;
+    a.M = m; a.K = k; a.epi = EPI_STORE; a.N = 1;
+    a.pro = pro; a.pro_y = y; a.pro_w = norm_w; a.pro_eps = eps; a.pro_out = x_out;
+    return gemv_launch(a, stream());
+}
+
 ATLAS_API int atlas_gemv_swiglu_f32(int fmt, const void* w, const float* scales, int block,
                                     const float* x, float* h_out, int h, int k) {
     GemvArgs a{};
@@ -184,6 +196,51 @@ ATLAS_API int atlas_qkv_post_f32(float* qkv, const float* q_norm, const float* k
     a.slot_stride = 0; a.slot_dev = nullptr; a.pos_dev = nullptr; a.pos = pos;
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = head_dim;
     return qkv_post_launch(a, 1, stream());
+}
+
+ATLAS_API int atlas_attention_fused_f32(const float* qkv, const float* q_norm,
+                                        const float* k_norm, float qk_eps, const float* cos_tab,
+                                        const float* sin_tab, float* k_cache, float* v_cache,
+                                        float* out, int n_heads, int n_kv, int head_dim, int pos,
+                                        float scale, int window, int n_splits) {
+    ATLAS_REQUIRE(pos >= 0, "attention_fused: pos < 0");
+    ATLAS_REQUIRE(attn_fused_supported(n_heads, n_kv, head_dim), "attention_fused: shape");
+    const int ctx = (window > 0 && pos + 1 > window) ? window : pos + 1;
+    if (n_splits <= 0) n_splits = attn_pick_splits(n_kv, ctx);
+    ATLAS_REQUIRE(n_splits <= 1024, "attention_fused: n_splits %d", n_splits);
+    // scratch: position, merge counters (zeroed once; the kernel leaves them
+    // at zero), split partials
+    static int* d_pos = nullptr;
+    static int* d_cnt = nullptr;
+    static int cnt_cap = 0;
+    static float* d_part = nullptr;
+    static size_t part_cap = 0;
+    if (!d_pos) ATLAS_HIP(hipMalloc((void**)&d_pos, sizeof(int)));
+    if (n_kv > cnt_cap) {
+        ATLAS_HIP(hipDeviceSynchronize());
+        if (d_cnt) ATLAS_HIP(hipFree(d_cnt));
+        ATLAS_HIP(hipMalloc((void**)&d_cnt, (size_t)n_kv * sizeof(int)));
+        ATLAS_HIP(hipMemset(d_cnt, 0, (size_t)n_kv * sizeof(int)));
+        cnt_cap = n_kv;
+    }
+    const size_t need = (size_t)n_heads * n_splits * (head_dim + 2);
+    if (need > part_cap) {
+        ATLAS_HIP(hipDeviceSynchronize());
+        if (d_part) ATLAS_HIP(hipFree(d_part));
+        ATLAS_HIP(hipMalloc((void**)&d_part, need * sizeof(float)));
+        part_cap = need;
+    }
+    ATLAS_HIP(hipMemcpyAsync(d_pos, &pos, sizeof(int), hipMemcpyHostToDevice, stream()));
+    AttnFusedArgs a{};
+    a.qkv = qkv; a.qkv_stride = 0; a.q_norm = q_norm; a.k_norm = k_norm; a.qk_eps = qk_eps;
+    a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.k_cache = k_cache; a.v_cache = v_cache;
+    a.slot_stride = 0; a.slot_dev = nullptr; a.pos_dev = d_pos; a.out = out; a.out_stride = 0;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.scale = scale; a.window = window;
+    a.part_m = d_part;
+    a.part_l = d_part + (size_t)n_heads * n_splits;
+    a.part_o = d_part + (size_t)2 * n_heads * n_splits;
+    a.counters = d_cnt;
+    return attn_fused_launch(a, n_splits, 1, stream());
 }
 
 ATLAS_API int atlas_argmax_u32(const float* x, int n, uint32_t* out_idx) {

@@ -89,6 +89,12 @@ struct atlas_model {
     float *cos_tab = nullptr, *sin_tab = nullptr;
     float *x = nullptr, *xn = nullptr, *y = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr,
           *logits = nullptr;
+    // fused step: residual ping-pong partner of x, the W_down output, split
+    // partials and merge counters of the fused attention
+    float *xb = nullptr, *y2 = nullptr;
+    float* attn_part = nullptr;
+    int* attn_counters = nullptr;
+    bool fused = false;
     int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
     uint32_t *tok_dev = nullptr, *hist = nullptr, *suppress_dev = nullptr, *choice_dev = nullptr;
     int suppress_cap = 0;
@@ -255,8 +261,87 @@ int choose_step(atlas_model* m) {
     return argmax_launch(g, m->st);
 }
 
+GemvArgs pro_args(const DevMat& w, const float* x, float* y, int pro, const float* py,
+                  const float* pw, float eps, float* pout) {
+    GemvArgs a = gemv_args(w, x, y, EPI_STORE);
+    a.pro = pro;
+    a.pro_y = py;
+    a.pro_w = pw;
+    a.pro_eps = eps;
+    a.pro_out = pout;
+    return a;
+}
+
+// The post-norm decode step with the norms folded into the GEMV prologues
+// and one attention launch per layer (5 launches per layer):
+//   QKV    x_l = x'_{l-1} + rmsnorm(y2) * ffn_norm_{l-1}   (layer 0: embedding)
+//   ATTN   QK-norm + RoPE + KV write + split-K attention + merge
+//   WO     y1 = W_o att
+//   GU     x'_l = x_l + rmsnorm(y1) * attn_norm_l;  h = [gate | up](x'_l)
+//   DOWN   y2 = W_down (silu(gate) * up)
+// x_l lives in m->x, x'_l in m->xb.
+int enqueue_step_fused(atlas_model* m, int mode) {
+    const atlas_model_config& c = m->cfg;
+    const int d = c.d_model;
+    const float eps = c.rms_eps;
+    TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, 1, m->st));
+    for (int li = 0; li < c.n_layers; ++li) {
+        LayerW& L = m->L[li];
+        if (li == 0)
+            TRY(gemv_launch(pro_args(L.qkv, m->x, m->qkv, PRO_X, nullptr, nullptr, 0.f, nullptr), m->st));
+        else
+            TRY(gemv_launch(pro_args(L.qkv, m->xb, m->qkv, PRO_RESNORM, m->y2, m->L[li - 1].ffn_norm,
+                                     eps, m->x), m->st));
+        AttnFusedArgs a{};
+        a.qkv = m->qkv; a.qkv_stride = m->qkv_rows;
+        a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.qk_eps = 1e-6f;
+        a.cos_tab = m->cos_tab; a.sin_tab = m->sin_tab;
+        a.k_cache = L.kc; a.v_cache = L.vc; a.slot_stride = m->slot_stride;
+        a.slot_dev = nullptr; a.pos_dev = m->pos_dev;
+        a.out = m->att; a.out_stride = d;
+        a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
+        a.scale = m->scale; a.window = L.window;
+        a.part_m = m->attn_part;
+        a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
+        a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
+        a.counters = m->attn_counters;
+        TRY(attn_fused_launch(a, m->attn_splits, 1, m->st));
+        TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
+        TRY(gemv_launch(pro_args(L.gu, m->x, m->h, PRO_RESNORM, m->y, L.attn_norm, eps, m->xb),
+                        m->st));
+        TRY(gemv_launch(pro_args(L.down, nullptr, m->y2, PRO_SILU, m->h, nullptr, 0.f, nullptr),
+                        m->st));
+    }
+    // x_L = x'_{L-1} + rmsnorm(y2) * ffn_norm_{L-1}, in place in xb
+    TRY(residual_rmsnorm_launch(m->xb, m->y2, m->L[c.n_layers - 1].ffn_norm, d, 1, d, eps, m->st));
+    const bool penalties = m->g_nsup > 0 || m->g_theta != 1.0f;
+    GemvArgs h = pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm, eps,
+                          m->xn);
+    const bool fused_choice = mode == 1 && !penalties;
+    if (fused_choice) {
+        h.epi = EPI_ARGMAX;
+        h.arg_part = m->argpart;
+    }
+    TRY(gemv_launch(h, m->st));
+    if (mode == 1) {
+        ArgmaxArgs g{};
+        g.x = m->logits; g.n = c.vocab; g.part = m->argpart;
+        g.out_u32 = m->tok_dev;
+        g.suppress = m->g_nsup ? m->suppress_dev : nullptr; g.n_suppress = m->g_nsup;
+        g.hist = m->hist; g.hist_len = m->hist_len; g.window = m->g_window; g.theta = m->g_theta;
+        g.step = m->step_dev; g.record = 1;
+        g.n_parts = fused_choice ? gemv_waves(h) : 0;
+        g.pos_inc = m->pos_dev;
+        TRY(argmax_launch(g, m->st));
+    } else {
+        TRY(add_int_launch(m->pos_dev, 1, 1, m->st));
+    }
+    return ATLAS_OK;
+}
+
 // mode 0: forward only; mode 1: forward + greedy choice into tok_dev/hist
 int enqueue_step(atlas_model* m, int mode) {
+    if (m->fused) return enqueue_step_fused(m, mode);
     const atlas_model_config& c = m->cfg;
     TRY(embed_launch(m->embed, c.vocab, c.d_model, m->tok_dev, 0, m->x, c.d_model, 1, m->st));
     for (int li = 0; li < c.n_layers; ++li) TRY(layer_step(m, li));
@@ -595,6 +680,23 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             xin = m->xn;
         }
         TRY(skinny(m, L.qkv, xin, m->qkv, n, EPI_STORE));
+        if (m->fused) {
+            // one launch: every sequence's QK-norm/RoPE/KV write and attention
+            AttnFusedArgs a{};
+            a.qkv = m->qkv; a.qkv_stride = m->qkv_rows;
+            a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.qk_eps = 1e-6f;
+            a.cos_tab = m->cos_tab; a.sin_tab = m->sin_tab;
+            a.k_cache = L.kc; a.v_cache = L.vc; a.slot_stride = m->slot_stride;
+            a.slot_dev = m->slot_dev; a.pos_dev = m->pos_dev;
+            a.out = m->att; a.out_stride = d;
+            a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
+            a.scale = m->scale; a.window = L.window;
+            a.part_m = m->attn_part;
+            a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
+            a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
+            a.counters = m->attn_counters;
+            TRY(attn_fused_launch(a, m->attn_splits, n, m->st));
+        }
         QkvPostArgs q{};
         q.qkv = m->qkv; q.qkv_stride = m->qkv_rows;
         q.q_norm = L.q_norm; q.k_norm = L.k_norm; q.qk_eps = 1e-6f;
@@ -602,8 +704,8 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
         q.k_cache = L.kc; q.v_cache = L.vc; q.slot_stride = m->slot_stride;
         q.slot_dev = m->slot_dev; q.pos_dev = m->pos_dev;
         q.n_heads = c.n_heads; q.n_kv = c.n_kv_heads; q.head_dim = m->hd;
-        TRY(qkv_post_launch(q, n, m->st));
-        for (int i = 0; i < n; ++i) {
+        if (!m->fused) TRY(qkv_post_launch(q, n, m->st));
+        for (int i = 0; i < n && !m->fused; ++i) {
             AttnArgs a{};
             a.q = m->qkv + (size_t)i * m->qkv_rows;
             a.k_cache = L.kc + (size_t)slots[i] * m->slot_stride;
@@ -716,7 +818,8 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         dalloc(m, (void**)&m->y, (size_t)B * d * 4) ||
         dalloc(m, (void**)&m->qkv, (size_t)B * m->qkv_rows * 4) ||
         dalloc(m, (void**)&m->att, (size_t)B * d * 4) ||
-        dalloc(m, (void**)&m->h, (size_t)B * big * 4) ||
+        dalloc(m, (void**)&m->h, (size_t)B * 2 * big * 4) ||
+        dalloc(m, (void**)&m->xb, (size_t)B * d * 4) || dalloc(m, (void**)&m->y2, (size_t)B * d * 4) ||
         dalloc(m, (void**)&m->logits, (size_t)B * c.vocab * 4) ||
         dalloc(m, (void**)&m->pos_dev, (size_t)B * 4) || dalloc(m, (void**)&m->slot_dev, (size_t)B * 4) ||
         dalloc(m, (void**)&m->tok_dev, (size_t)B * 4) || dalloc(m, (void**)&m->step_dev, 4) ||
@@ -740,6 +843,18 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     }
     m->attn_splits = attn_pick_splits(c.n_kv_heads, c.max_seq);
     if (attn_reserve(c.n_heads, hd, m->attn_splits)) return fail(m);
+    // fused step: post-norm model whose attention shape the fused kernel
+    // covers and whose GEMVs take the aligned fast path (d % 32 == 0)
+    m->fused = c.post_norm && attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
+               d % 32 == 0 && c.ffn_hidden % 32 == 0;
+    if (dalloc(m, (void**)&m->attn_part,
+               (size_t)B * c.n_heads * m->attn_splits * (hd + 2) * 4) ||
+        dalloc(m, (void**)&m->attn_counters, (size_t)B * c.n_kv_heads * 4))
+        return fail(m);
+    if (hipMemset(m->attn_counters, 0, (size_t)B * c.n_kv_heads * 4) != hipSuccess) {
+        set_error(ATLAS_EHIP, "counter init failed");
+        return fail(m);
+    }
     if (reset_state(m) || hipStreamSynchronize(m->st) != hipSuccess) return fail(m);
     return m;
 }
@@ -1096,35 +1211,62 @@ ATLAS_API int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, in
     return ATLAS_OK;
 }
 
-ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, float* ms, int* launches,
-                                     int64_t* bytes) {
-    ATLAS_REQUIRE(m && iters > 0 && ms && launches && bytes, "bench_gemv: bad arguments");
-    const atlas_model_config& c = m->cfg;
-    auto mat_bytes = [](const DevMat& w, bool swiglu) {
-        const int64_t out = swiglu ? w.rows / 2 : w.rows;
+ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float* ms,
+                                     int* launches, int64_t* bytes) {
+    ATLAS_REQUIRE(m && iters > 0 && ms && launches && bytes && which >= 0 && which <= 2,
+                  "bench_gemv: bad arguments");
+    const float eps = m->cfg.rms_eps;
+    auto mat_bytes = [](const DevMat& w, int64_t out) {
         return (int64_t)w.data_bytes() + (int64_t)w.scale_count() * 4 + (int64_t)w.cols * 4 + out * 4;
     };
+    const bool k_set = which == 0 || which == 1, down_set = which == 0 || which == 2;
     int64_t b = 0;
     int n = 0;
     for (const auto& L : m->L) {
-        b += mat_bytes(L.qkv, false) + mat_bytes(L.wo, false) + mat_bytes(L.gu, true) +
-             mat_bytes(L.down, false);
-        n += 4;
+        if (k_set) {
+            b += mat_bytes(L.qkv, L.qkv.rows) + mat_bytes(L.wo, L.wo.rows) + mat_bytes(L.gu, L.gu.rows);
+            n += 3;
+        }
+        if (down_set) {
+            b += mat_bytes(L.down, L.down.rows) + (int64_t)L.down.cols * 4;   // pairs read twice as wide
+            n += 1;
+        }
     }
-    b += mat_bytes(m->lm_head, false);
-    n += 1;
+    if (k_set) {
+        b += mat_bytes(m->lm_head, m->lm_head.rows);
+        n += 1;
+    }
     hipEvent_t e0, e1;
     ATLAS_HIP(hipEventCreate(&e0));
     ATLAS_HIP(hipEventCreate(&e1));
     ATLAS_HIP(hipEventRecord(e0, m->st));
     for (int it = 0; it < iters; ++it) {
-        for (auto& L : m->L) {
-            TRY(gemv(m, L.qkv, m->x, m->qkv, EPI_STORE));
-            TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
-            TRY(gemv(m, L.gu, m->x, m->h, EPI_SILU_MUL));
-            TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
+        for (size_t li = 0; li < m->L.size(); ++li) {
+            LayerW& L = m->L[li];
+            if (k_set) {
+                if (m->fused) {
+                    TRY(gemv_launch(pro_args(L.qkv, m->xb, m->qkv, PRO_RESNORM, m->y2, L.ffn_norm, eps, m->x), m->st));
+                    TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
+                    TRY(gemv_launch(pro_args(L.gu, m->x, m->h, PRO_RESNORM, m->y, L.attn_norm, eps, m->xb), m->st));
+                } else {
+                    TRY(gemv(m, L.qkv, m->x, m->qkv, EPI_STORE));
+                    TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
+                    TRY(gemv(m, L.gu, m->x, m->h, EPI_SILU_MUL));
+                }
+            }
+            if (down_set) {
+                if (m->fused)
+                    TRY(gemv_launch(pro_args(L.down, nullptr, m->y2, PRO_SILU, m->h, nullptr, 0.f, nullptr), m->st));
+                else
+                    TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
+            }
         }
-        TRY(gemv(m, m->lm_head, m->xn, m->logits, EPI_STORE));
+        if (k_set) {
+            if (m->fused)
+                TRY(gemv_launch(pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm, eps, m->xn), m->st));
+            else
+                TRY(gemv(m, m->lm_head, m->xn, m->logits, EPI_STORE));
+        }
     }
     ATLAS_HIP(hipEventRecord(e1, m->st));
     ATLAS_HIP(hipEventSynchronize(e1));
@@ -1135,7 +1277,6 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, float* ms, int* 
     *ms = t;
     *launches = n * iters;
     *bytes = b;
-    (void)c;
     return ATLAS_OK;
 }
 

@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
 __global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long long* __restrict__ part,
                                                            int nparts, float* out_f32,
                                                            uint32_t* out_u32, uint32_t* hist,
-                                                           int* hist_len, int* step) {
+                                                           int* hist_len, int* step, int* pos_inc) {
     __shared__ unsigned long long red[4];
     unsigned long long best = 0;
     for (int i = threadIdx.x; i < nparts; i += 256) best = part[i] > best ? part[i] : best;
@@ -389,23 +389,28 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long l
         if (out_u32) *out_u32 = idx;
         if (hist && hist_len) { hist[*hist_len] = idx; *hist_len += 1; }
         if (step) *step += 1;
+        if (pos_inc) *pos_inc += 1;
     }
 }
 
 int argmax_launch(const ArgmaxArgs& a, hipStream_t st) {
     ATLAS_REQUIRE(a.x && a.n > 0 && a.part, "argmax: bad arguments");
-    if (a.suppress || (a.theta != 1.0f && a.hist)) {
+    if (a.n_parts <= 0 && (a.suppress || (a.theta != 1.0f && a.hist))) {
         hipLaunchKernelGGL(penalize_kernel, dim3(1), dim3(256), 0, st, (float*)a.x, a.n, a.step,
                            a.suppress, a.n_suppress, a.hist, a.hist_len, a.window, a.theta);
         ATLAS_LAUNCH_CHECK("penalize");
     }
-    int blocks = (a.n + 255) / 256;
-    if (blocks > ARGMAX_MAX_PARTS) blocks = ARGMAX_MAX_PARTS;
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(256), 0, st, a.x, a.n, a.part);
-    ATLAS_LAUNCH_CHECK("argmax_partial");
+    int blocks = a.n_parts;
+    if (blocks <= 0) {
+        // partials not precomputed (by a GEMV epilogue): reduce the logits here
+        blocks = (a.n + 255) / 256;
+        if (blocks > ARGMAX_MAX_PARTS) blocks = ARGMAX_MAX_PARTS;
+        hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(256), 0, st, a.x, a.n, a.part);
+        ATLAS_LAUNCH_CHECK("argmax_partial");
+    }
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, a.part, blocks, a.out_f32,
                        a.out_u32, a.record ? a.hist : nullptr, a.record ? a.hist_len : nullptr,
-                       a.step);
+                       a.step, a.pos_inc);
     ATLAS_LAUNCH_CHECK("argmax_final");
     return ATLAS_OK;
 }

@@ -6,7 +6,7 @@ namespace atlas {
 
 enum { EW_ADD = 0, EW_SCALE = 1, EW_RELU = 2, EW_SILU_MUL = 3, EW_COPY = 4, EW_FILL = 5 };
 enum { INIT_NORMAL_F32 = 0, INIT_NORMAL_BF16 = 1, INIT_UNIFORM_F32 = 2 };
-enum { ARGMAX_MAX_PARTS = 1024 };
+enum { ARGMAX_MAX_PARTS = 16384 };
 
 struct QkvPostArgs {
     float* qkv;              // per sequence: [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)]
@@ -39,6 +39,8 @@ struct ArgmaxArgs {
     float theta;                   // repetition penalty (1 = off)
     int* step;                     // device step counter (step 0 = first token), or null
     int record;                    // append the choice to hist and bump hist_len
+    int n_parts;                   // > 0: part[] already holds this many partial keys
+    int* pos_inc;                  // device position bumped after the choice, or null
 };
 
 int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, long ld, float eps,

@@ -79,7 +79,196 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const f32x4* __restric
     return acc;
 }
 
+
+// ---------------------------------------------------------------------------
+// x staging with the fused prologues (all 256 threads of the block call it).
+// PRO_RESNORM / PRO_RMSNORM follow rmsnorm_inplace (crates/atlas-model/src/
+// lib.rs:335-342): inv = 1/sqrt(sum(v^2)/n + eps), v*inv*w, and the post-norm
+// residual x + normed (lib.rs:985-993); PRO_SILU is FeedForward's
+// silu(gate) * up (lib.rs:918-921) over interleaved (gate, up) pairs.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_sum256(float v, float* red4) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red4[0] + red4[1] + red4[2] + red4[3];
+}
+
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+template <bool SWZ>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, f32x4* xs, int K) {
+    __shared__ float red4[4];
+    const int np = K >> 2;
+    const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
+    float inv = 1.0f;
+    if (a.pro == PRO_RESNORM || a.pro == PRO_RMSNORM) {
+        const f32x4* v = reinterpret_cast<const f32x4*>(a.pro == PRO_RESNORM ? a.pro_y : a.x);
+        float ss = 0.f;
+        for (int p = threadIdx.x; p < np; p += 256) {
+            const f32x4 t = v[p];
+            ss += t.x * t.x;
+            ss += t.y * t.y;
+            ss += t.z * t.z;
+            ss += t.w * t.w;
+        }
+        ss = block_sum256(ss, red4);
+        inv = 1.0f / sqrtf(ss / (float)K + a.pro_eps);
+    }
+    const bool write_out = a.pro_out && blockIdx.x == 0 &&
+                           (a.pro == PRO_RESNORM || a.pro == PRO_RMSNORM);
+    for (int p = threadIdx.x; p < np; p += 256) {
+        f32x4 r;
+        if (a.pro == PRO_X) {
+            r = xin[p];
+        } else if (a.pro == PRO_RESNORM) {
+            const f32x4 yi = reinterpret_cast<const f32x4*>(a.pro_y)[p];
+            const f32x4 wi = reinterpret_cast<const f32x4*>(a.pro_w)[p];
+            r = xin[p] + (yi * inv) * wi;
+        } else if (a.pro == PRO_RMSNORM) {
+            const f32x4 wi = reinterpret_cast<const f32x4*>(a.pro_w)[p];
+            r = (xin[p] * inv) * wi;
+        } else {   // PRO_SILU
+            const f32x4* pr = reinterpret_cast<const f32x4*>(a.pro_y);
+            const f32x4 g0 = pr[2 * p], g1 = pr[2 * p + 1];
+            r = f32x4{silu_f(g0.x) * g0.y, silu_f(g0.z) * g0.w, silu_f(g1.x) * g1.y,
+                      silu_f(g1.z) * g1.w};
+        }
+        xs[SWZ ? swz(p) : p] = r;
+        if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = r;
+    }
+}
+
+// dot of one 16-byte weight chunk with its EPC x values held in registers
+template <int FMT>
+__device__ __forceinline__ float chunk_dot_r(const u32x4 w, const float* x, float acc) {
+    if constexpr (FMT == WF_F32) {
+        acc += __uint_as_float(w.x) * x[0];
+        acc += __uint_as_float(w.y) * x[1];
+        acc += __uint_as_float(w.z) * x[2];
+        acc += __uint_as_float(w.w) * x[3];
+    } else if constexpr (FMT == WF_BF16) {
+        acc += bf16_lo(w.x) * x[0];  acc += bf16_hi(w.x) * x[1];
+        acc += bf16_lo(w.y) * x[2];  acc += bf16_hi(w.y) * x[3];
+        acc += bf16_lo(w.z) * x[4];  acc += bf16_hi(w.z) * x[5];
+        acc += bf16_lo(w.w) * x[6];  acc += bf16_hi(w.w) * x[7];
+    } else if constexpr (FMT == WF_I8) {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc += s8_at(ww[j], b) * x[4 * j + b];
+    } else {   // int4: sum of (16*q) * x
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t hi = ww[j] & 0xF0F0F0F0u;
+            const uint32_t lo = (ww[j] << 4) & 0xF0F0F0F0u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                acc += s8_at(hi, b) * x[8 * j + 2 * b];
+                acc += s8_at(lo, b) * x[8 * j + 2 * b + 1];
+            }
+        }
+    }
+    return acc;
+}
+
+// ordered (value, index) key: larger value wins, ties keep the larger index
+__device__ __forceinline__ unsigned long long argkey_f(float v, int i) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)i;
+}
+
+// ---------------------------------------------------------------------------
+// K <= 64*CPL*EPC: x lives in registers (each lane keeps the x values of its
+// CPL chunks for the whole kernel), weights stream through raw buffer loads
+// (32-bit offsets; offsets past the matrix return 0, which also serves the
+// per-row tail), one full row per wave with the next row prefetched.  No LDS
+// traffic in the loop and no barriers after the prologue.
+// ---------------------------------------------------------------------------
+#define ATLAS_BUF_DWORD3 0x00020000
+#define ATLAS_OOB 0x80000000u
+
+template <int FMT, int CPL>
+__global__ __launch_bounds__(256) void gemv_xreg_kernel(GemvArgs a) {
+    extern __shared__ f32x4 xs[];
+    constexpr int EPC = WT<FMT>::EPC;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = a.K, M = a.M;
+    const int chunks = K / EPC;
+    const uint32_t row_bytes = (uint32_t)chunks * 16u;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(a.w), (short)0, (int)((uint64_t)M * row_bytes), ATLAS_BUF_DWORD3);
+    const int n_scales = FMT == WF_I4 ? M * a.bpr : M;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.scales), (short)0, (FMT == WF_I4 || FMT == WF_I8) ? n_scales * 4 : 0,
+        ATLAS_BUF_DWORD3);
+    int lcpb = 0;
+    while ((1 << lcpb) < a.cpb) ++lcpb;
+
+    auto load_row = [&](int r, u32x4 (&w)[CPL], float (&sc)[CPL]) {
+        const uint32_t base = (uint32_t)r * row_bytes;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = lane + 64 * j;
+            const uint32_t off = c < chunks ? base + (uint32_t)c * 16u : ATLAS_OOB;
+            w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 2));
+            if constexpr (FMT == WF_I4) {
+                const uint32_t bi = (uint32_t)r * (uint32_t)a.bpr + ((uint32_t)c >> lcpb);
+                const uint32_t so = c < chunks ? bi * 4u : ATLAS_OOB;
+                sc[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0)) *
+                        0.0625f;
+            }
+        }
+    };
+
+    const int S = gridDim.x * 4;
+    int row = blockIdx.x * 4 + wave;
+    u32x4 wa[CPL], wb[CPL];
+    float sa[CPL], sb[CPL];
+    if (row < M) load_row(row, wa, sa);      // first row in flight during the prologue
+    stage_x<false>(a, xs, K);
+    __syncthreads();
+    float xr[CPL][EPC];
+    const float* xf = reinterpret_cast<const float*>(xs);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) xr[j][e] = c < chunks ? xf[c * EPC + e] : 0.0f;
+    }
+
+    unsigned long long best = 0;
+    auto finish = [&](int r, const u32x4 (&w)[CPL], const float (&sc)[CPL]) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if constexpr (FMT == WF_I4) acc += sc[j] * chunk_dot_r<FMT>(w[j], xr[j], 0.0f);
+            else acc = chunk_dot_r<FMT>(w[j], xr[j], acc);
+        }
+        acc = wave_sum(acc);
+        if constexpr (FMT == WF_I8) acc *= a.scales[r];
+        if (lane == 0) a.y[r] = acc;
+        if (a.epi == EPI_ARGMAX) {
+            const unsigned long long k = argkey_f(acc, r);
+            best = k > best ? k : best;
+        }
+    };
+
+    while (row < M) {
+        const int r1 = row + S;
+        if (r1 < M) load_row(r1, wb, sb);
+        finish(row, wa, sa);
+        if (r1 >= M) break;
+        const int r2 = r1 + S;
+        if (r2 < M) load_row(r2, wa, sa);
+        finish(r1, wb, sb);
+        row = r2;
+    }
+    if (a.epi == EPI_ARGMAX && lane == 0) a.arg_part[blockIdx.x * 4 + wave] = best;
+}
 
 template <int FMT, int ROWS, int UNROLL>
 __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
@@ -126,9 +315,7 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
     float scur[UNROLL][ROWS];
     // the first weight loads go out before x is staged, hiding the staging
     if (total > 0) load(0, cur, scur);
-    const int npieces = K >> 2;
-    const f32x4* xg = reinterpret_cast<const f32x4*>(a.x);
-    for (int p = threadIdx.x; p < npieces; p += 256) xs[swz(p)] = xg[p];
+    stage_x<true>(a, xs, K);
     __syncthreads();
 
     float acc[ROWS];
@@ -300,29 +487,103 @@ int gemv_fast_ok(int fmt, int K, int block) {
     return 0;
 }
 
+// resident blocks per CU of the register-x kernel (also fixes the number of
+// argmax partials it writes: 4 per block)
+constexpr int XREG_BPC = 2;
+
+template <int FMT, int CPL>
+static int launch_xreg(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
+    int blocks = (a.M + 3) / 4;
+    const int cap = blocks_per_cu * device_cu_count();
+    if (blocks > cap) blocks = cap;
+    if (a.epi == EPI_ARGMAX)
+        ATLAS_REQUIRE(blocks * 4 <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
+    hipLaunchKernelGGL((gemv_xreg_kernel<FMT, CPL>), dim3(blocks), dim3(256), (size_t)a.K * 4, st, a);
+    ATLAS_LAUNCH_CHECK("gemv_xreg");
+    return ATLAS_OK;
+}
+
+// CPL is bounded so that a lane keeps at most 64 x values in registers
+template <int FMT>
+static int dispatch_xreg(const GemvArgs& a, hipStream_t st, int cpl, int bpc) {
+    constexpr int MAXC = 64 / WT<FMT>::EPC < 8 ? 64 / WT<FMT>::EPC : 8;
+    if (cpl <= 1) return launch_xreg<FMT, 1>(a, st, bpc);
+    if (cpl <= 2 || MAXC == 2) return launch_xreg<FMT, (MAXC < 2 ? MAXC : 2)>(a, st, bpc);
+    if (cpl <= 4 || MAXC == 4) return launch_xreg<FMT, (MAXC < 4 ? MAXC : 4)>(a, st, bpc);
+    return launch_xreg<FMT, MAXC>(a, st, bpc);
+}
+
+static int elem_per_chunk(int fmt) {
+    return fmt == WF_F32 ? 4 : fmt == WF_BF16 ? 8 : fmt == WF_I8 ? 16 : 32;
+}
+
+// number of persistent waves the batch-1 kernel launches (argmax partial count)
+int gemv_waves(const GemvArgs& a) {
+    const int blocks = (a.M + 3) / 4;
+    const int cap = XREG_BPC * device_cu_count();
+    return 4 * (blocks < cap ? blocks : cap);
+}
+
 int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     GemvArgs a = a_in;
     gemv_fill_int4_index(a);
     ATLAS_REQUIRE(a.M >= 0 && a.K >= 0, "gemv: negative shape");
     if (a.M == 0) return ATLAS_OK;
-    ATLAS_REQUIRE(a.w && a.x && a.y, "gemv: null pointer");
+    ATLAS_REQUIRE(a.w && a.y, "gemv: null pointer");
+    ATLAS_REQUIRE(a.pro == PRO_SILU || a.x, "gemv: null x");
+    ATLAS_REQUIRE(a.pro != PRO_RESNORM || (a.pro_y && a.pro_w), "gemv: residual norm needs y and w");
+    ATLAS_REQUIRE(a.pro != PRO_RMSNORM || a.pro_w, "gemv: rmsnorm prologue needs w");
+    ATLAS_REQUIRE(a.pro != PRO_SILU || a.pro_y, "gemv: silu prologue needs the gate/up pairs");
+    ATLAS_REQUIRE(a.pro_out == nullptr || (a.pro_out != a.x && a.pro_out != a.pro_y),
+                  "gemv: the materialised x must not alias the prologue inputs");
     ATLAS_REQUIRE(a.fmt == WF_F32 || a.fmt == WF_BF16 || a.scales, "gemv: null scales");
     ATLAS_REQUIRE(a.fmt != WF_I4 || a.block > 0, "gemv: int4 block must be > 0");
     if (a.epi == EPI_SILU_MUL) ATLAS_REQUIRE(a.M % 2 == 0, "gemv: silu-mul needs even rows");
+    if (a.epi == EPI_ARGMAX) ATLAS_REQUIRE(a.arg_part, "gemv: argmax epilogue needs partials");
     if (a.K == 0) {
         set_error(ATLAS_EUNSUPPORTED, "gemv: K == 0");
         return ATLAS_EUNSUPPORTED;
     }
-    const bool aligned = (((uintptr_t)a.w | (uintptr_t)a.x) & 15) == 0;
-    if (aligned && gemv_fast_ok(a.fmt, a.K, a.block) && (size_t)a.K * 4 <= 160 * 1024) {
+    const uintptr_t align = (uintptr_t)a.w | (uintptr_t)a.x | (uintptr_t)a.pro_y |
+                            (uintptr_t)a.pro_w | (uintptr_t)a.pro_out;
+    const bool fast = (align & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
+                      (size_t)a.K * 4 <= 160 * 1024;
+    if (fast) {
+        const int chunks = a.K / elem_per_chunk(a.fmt);
+        const uint64_t wbytes = (uint64_t)a.M * chunks * 16;
+        const bool pow2_cpb = (a.cpb & (a.cpb - 1)) == 0;
+        const bool xreg_ok = chunks <= 64 * (64 / elem_per_chunk(a.fmt) < 8 ? 64 / elem_per_chunk(a.fmt) : 8) &&
+                             wbytes < (1ull << 31) && a.epi != EPI_SILU_MUL &&
+                             (a.fmt != WF_I4 || (a.bpr > 0 && pow2_cpb &&
+                                                 (uint64_t)a.M * a.bpr * 4 < (1ull << 31)));
+        if (xreg_ok) {
+            const int need = (chunks + 63) / 64;
+            const int cpl = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+            switch (a.fmt) {
+            case WF_F32:  return dispatch_xreg<WF_F32>(a, st, cpl, XREG_BPC);
+            case WF_BF16: return dispatch_xreg<WF_BF16>(a, st, cpl, XREG_BPC);
+            case WF_I8:   return dispatch_xreg<WF_I8>(a, st, cpl, 2);
+            case WF_I4:   return dispatch_xreg<WF_I4>(a, st, cpl, 2);
+            }
+        }
+        ATLAS_REQUIRE(a.epi != EPI_ARGMAX, "gemv: argmax epilogue needs K <= 4096 shapes");
+        if (a.epi == EPI_SILU_MUL) {
+            switch (a.fmt) {
+            case WF_F32:  return launch_n1<WF_F32, 2, 4>(a, st, 8);
+            case WF_BF16: return launch_n1<WF_BF16, 2, 4>(a, st, 8);
+            case WF_I8:   return launch_n1<WF_I8, 2, 4>(a, st, 8);
+            case WF_I4:   return launch_n1<WF_I4, 2, 2>(a, st, 8);
+            }
+        }
         switch (a.fmt) {
-        case WF_F32:  return launch_n1<WF_F32, 2, 4>(a, st, 8);
-        case WF_BF16: return launch_n1<WF_BF16, 2, 4>(a, st, 8);
-        case WF_I8:   return launch_n1<WF_I8, 2, 2>(a, st, 8);
-        case WF_I4:   return launch_n1<WF_I4, 4, 1>(a, st, 8);
+        case WF_F32:  return launch_n1<WF_F32, 1, 4>(a, st, 8);
+        case WF_BF16: return launch_n1<WF_BF16, 1, 8>(a, st, 2);
+        case WF_I8:   return launch_n1<WF_I8, 1, 8>(a, st, 16);
+        case WF_I4:   return launch_n1<WF_I4, 2, 2>(a, st, 8);
         }
     }
-    ATLAS_REQUIRE(a.epi == EPI_STORE, "gemv: fused epilogue needs the fast path shape");
+    ATLAS_REQUIRE(a.epi == EPI_STORE && a.pro == PRO_X,
+                  "gemv: fused prologue/epilogue needs an aligned fast-path shape");
     const int blocks = (a.M + 3) / 4;
     switch (a.fmt) {
     case WF_F32:  hipLaunchKernelGGL(gemv_generic_kernel<WF_F32>, dim3(blocks), dim3(256), 0, st, a); break;

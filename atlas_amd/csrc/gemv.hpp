@@ -5,7 +5,14 @@
 namespace atlas {
 
 enum { WF_F32 = 0, WF_BF16 = 1, WF_I8 = 2, WF_I4 = 3 };   // weight formats
-enum { EPI_STORE = 0, EPI_SILU_MUL = 1 };                 // epilogues
+enum { EPI_STORE = 0, EPI_SILU_MUL = 1, EPI_ARGMAX = 2 };  // epilogues
+// prologues: how the GEMV input x is formed while it is loaded
+enum {
+    PRO_X = 0,        // x as given
+    PRO_RESNORM = 1,  // x = x_in + (y * inv(y)) * w   (post-norm residual; materialised)
+    PRO_RMSNORM = 2,  // x = (x_in * inv(x_in)) * w
+    PRO_SILU = 3      // x[k] = silu(y[2k]) * y[2k+1]   (SwiGLU of interleaved gate/up)
+};
 
 struct GemvArgs {
     int fmt;                 // WF_*
@@ -22,10 +29,19 @@ struct GemvArgs {
     long x_stride_n, x_stride_k;   // skinny: x element (n, k) at n*sn + k*sk
     long y_stride_n, y_stride_m;   // skinny: y element (n, m) at n*sn + m*sm
     int x_vec;               // skinny: x rows 16-byte aligned with x_stride_k == 1
+    int pro;                 // PRO_*
+    const float* pro_y;      // RESNORM: normalised addend [K]; SILU: pairs [2K]
+    const float* pro_w;      // RESNORM / RMSNORM: norm weight [K]
+    float pro_eps;
+    float* pro_out;          // RESNORM / RMSNORM: x written out by block 0 (nullable)
+    unsigned long long* arg_part;   // EPI_ARGMAX: per-wave (value, index) keys
 };
+
+enum { GEMV_MAX_WAVES = 16384 };    // bound on persistent waves (argmax partials)
 
 int gemv_fast_ok(int fmt, int K, int block);
 int gemv_launch(const GemvArgs& a, hipStream_t st);     // N == 1
+int gemv_waves(const GemvArgs& a);                       // persistent waves of gemv_launch
 int skinny_launch(const GemvArgs& a, hipStream_t st);   // 1 <= N <= 8
 int skinny_reserve(int M, int N, int K);
 int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,

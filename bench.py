@@ -241,20 +241,28 @@ def main() -> int:
     log(f"bf16 decode: {ms_step:.3f} ms/token, {tok_s:.1f} tok/s, "
         f"weights {wbytes / 1e9:.2f} GB -> {wbytes / (ms_step * 1e-3) / 1e9:.0f} GB/s")
 
-    # dominant kernel: the bf16 decode GEMV, all launches of one step
-    ms = C.c_float()
-    launches = C.c_int()
-    gbytes = C.c_int64()
-    assert lib.atlas_model_bench_gemv(m._h, 1, C.byref(ms), C.byref(launches), C.byref(gbytes)) == 0
-    iters = 8
-    assert lib.atlas_model_bench_gemv(m._h, iters, C.byref(ms), C.byref(launches),
-                                      C.byref(gbytes)) == 0
-    per_launch_ms = ms.value / launches.value
-    per_launch_bytes = gbytes.value / (launches.value / iters)
-    gemv_gbs = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
-    step_gemv_ms = ms.value / iters
-    log(f"decode GEMVs: {launches.value // iters} launches/step, {step_gemv_ms:.3f} ms/step, "
-        f"{gemv_gbs:.0f} GB/s ({gemv_gbs / HBM_PEAK_GBS:.1%} of peak)")
+    # dominant kernel: the register-x bf16 GEMV (QKV, W_o, gate/up, lm_head:
+    # 79% of the step's weight bytes); W_down runs the LDS-staged kernel
+    def gemv_set(which, iters=8):
+        ms, launches, nbytes = C.c_float(), C.c_int(), C.c_int64()
+        assert lib.atlas_model_bench_gemv(m._h, 1, which, C.byref(ms), C.byref(launches),
+                                          C.byref(nbytes)) == 0
+        assert lib.atlas_model_bench_gemv(m._h, iters, which, C.byref(ms), C.byref(launches),
+                                          C.byref(nbytes)) == 0
+        per_launch_ms = ms.value / launches.value
+        per_launch_bytes = nbytes.value / (launches.value / iters)
+        return (per_launch_ms, per_launch_bytes, ms.value / iters, launches.value // iters)
+
+    k_ms, k_bytes, k_step_ms, k_n = gemv_set(1)
+    d_ms, d_bytes, d_step_ms, d_n = gemv_set(2)
+    gemv_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    down_gbs = d_bytes / (d_ms * 1e-3) / 1e9
+    step_gemv_ms = k_step_ms + d_step_ms
+    per_launch_ms, per_launch_bytes = k_ms, k_bytes
+    all_gbs = (k_bytes * k_n + d_bytes * d_n) / (step_gemv_ms * 1e-3) / 1e9
+    log(f"decode GEMVs (K=4096 kernel): {k_n} launches/step, {k_step_ms:.3f} ms, "
+        f"{gemv_gbs:.0f} GB/s ({gemv_gbs / HBM_PEAK_GBS:.1%}); W_down: {d_n} launches, "
+        f"{d_step_ms:.3f} ms, {down_gbs:.0f} GB/s; all GEMVs {all_gbs:.0f} GB/s")
 
     # roofline share of the whole step: weights + KV at 8 TB/s vs measured
     ctx_mid = len(prompt) + args.warmup + args.steps // 2
@@ -299,13 +307,16 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_n1_kernel<bf16> (all weight GEMVs of one decode step)",
+                     "kernel": "gemv_xreg_kernel<bf16,8>: QKV, W_o, gate/up, lm_head GEMVs "
+                               "of one decode step (fused-prologue launches)",
                      "bytes_per_launch": int(per_launch_bytes),
                      "us_per_launch": round(per_launch_ms * 1e3, 3)},
         "step_roofline": {"bytes_per_step": int(step_bytes),
                           "floor_ms": round(step_floor_ms, 4),
                           "frac_of_step_at_roofline": round(step_floor_ms / ms_step, 4),
-                          "gemv_ms_per_step": round(step_gemv_ms, 4)},
+                          "gemv_ms_per_step": round(step_gemv_ms, 4),
+                          "gemv_all_GB_s": round(all_gbs, 1),
+                          "w_down_GB_s": round(down_gbs, 1)},
         "int8": {"tok_s": round(tok_s8, 2), "ms_per_step": round(dt8 * 1e3 / args.steps, 4)},
         "gemv_microbench": micro,
         "attention_microbench": attn,

@@ -136,12 +136,15 @@ int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts, const in
  * in between.  tokens (host, may be NULL) receives the chosen ids.          */
 int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, int n_steps,
                               uint32_t* tokens);
-/* Benchmark helper: enqueue `iters` copies of exactly the weight GEMV
- * launches of one decode step (same kernels, shapes and weights; activations
- * from the engine's scratch) and time them with HIP events on the engine
- * stream.  *ms = elapsed milliseconds, *launches = GEMV launches issued,
- * *bytes = algorithmic bytes of one copy (weights + scales + x + y).         */
-int atlas_model_bench_gemv(atlas_model* m, int iters, float* ms, int* launches, int64_t* bytes);
+/* Benchmark helper: enqueue `iters` copies of the weight GEMV launches of one
+ * decode step (same kernels, shapes, prologues and weights; activations from
+ * the engine's scratch) and time them with HIP events on the engine stream.
+ * which: 0 = all of them, 1 = the K = d_model GEMVs (QKV, W_o, gate/up,
+ * lm_head: one kernel), 2 = the W_down GEMVs.  *ms = elapsed milliseconds,
+ * *launches = GEMV launches issued, *bytes = algorithmic bytes of one copy
+ * (weights + scales + x + y).                                                */
+int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float* ms, int* launches,
+                           int64_t* bytes);
 /* 1 = capture the decode step in a HIP graph (default), 0 = plain launches */
 int atlas_model_use_graph(atlas_model* m, int enable);
 /* The engine's stream (for timing with events on the same stream). */

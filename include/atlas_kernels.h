@@ -148,6 +148,20 @@ int atlas_gemv_i4_f32(const uint8_t* w, const float* scales, int block, const fl
 int atlas_gemv_swiglu_f32(int fmt, const void* w, const float* scales, int block,
                           const float* x, float* h_out, int h, int k);
 
+/* Batch-1 GEMV whose input is formed while it is loaded (one launch instead
+ * of a norm kernel plus a GEMV):
+ *   pro 0: x as given;
+ *   pro 1: x' = x + rmsnorm(y) * w  (post-norm residual, crates/atlas-model/
+ *          src/lib.rs:983-993); x' is also written to x_out (non-NULL,
+ *          distinct from x and y);
+ *   pro 2: x' = rmsnorm(x) * w  (x_out may be NULL);
+ *   pro 3: x'[j] = silu(y[2j]) * y[2j+1]  (SwiGLU over interleaved gate/up
+ *          outputs, lib.rs:918-921); x unused.
+ * eps is the RMSNorm epsilon.  yout[m] = dequant(W) x'.                       */
+int atlas_gemv_fused_f32(int fmt, const void* w, const float* scales, int block,
+                         const float* x, float* yout, int m, int k, int pro, const float* y,
+                         const float* norm_w, float eps, float* x_out);
+
 /* Ragged micro-batch: Y[n, m] = sum_k dequant(W)[m,k] X[n,k] for 1 <= n <= 8
  * activation rows (X [n x k] row-major, Y [n x m] row-major).  MFMA bf16 with
  * hi/lo split activations.  fmt: BF16, INT8, INT4.                          */
@@ -167,6 +181,17 @@ int atlas_residual_rmsnorm_f32(float* x, const float* y, const float* w, int n, 
 int atlas_qkv_post_f32(float* qkv, const float* q_norm, const float* k_norm, float qk_eps,
                        const float* cos_tab, const float* sin_tab, float* k_cache,
                        float* v_cache, int n_heads, int n_kv, int head_dim, int pos);
+/* Fused decode attention for one token: per-head QK-norm (norm weights may be
+ * NULL) + RoPE of the raw qkv = [q | k | v] projections, K/V cache write at
+ * pos, split-K GQA attention over [max(0, pos - window + 1), pos] and the
+ * split merge, in one launch (atlas_qkv_post_f32 + atlas_decode_attention
+ * semantics).  head_dim 64/128/256, n_heads / n_kv in {1, 2, 4, 8}.
+ * n_splits <= 0 picks a split count for the context.                        */
+int atlas_attention_fused_f32(const float* qkv, const float* q_norm, const float* k_norm,
+                              float qk_eps, const float* cos_tab, const float* sin_tab,
+                              float* k_cache, float* v_cache, float* out, int n_heads, int n_kv,
+                              int head_dim, int pos, float scale, int window, int n_splits);
+
 /* Greedy choice: index of the last maximum of x[0..n) as u32 (device).      */
 int atlas_argmax_u32(const float* x, int n, uint32_t* out_idx);
 

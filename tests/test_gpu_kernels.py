@@ -342,3 +342,93 @@ def test_errors_are_reported():
     with pytest.raises(AtlasError):
         check(lib().atlas_gemv_i4_f32(None, None, 32, None, None, 4, 32))
     assert lib().atlas_gemv_f32(7, None, None, 0, None, None, 0, 0) == 0   # empty is a no-op
+
+
+# ---------------------------------------------------------------------------
+# fused-prologue GEMVs (residual RMSNorm, RMSNorm, SwiGLU folded into x)
+# ---------------------------------------------------------------------------
+
+def _stored(orc, fmt, w, bs=32):
+    M, K = w.shape
+    if fmt == "bf16":
+        b = orc.bf16_from_f32(w)
+        return orc.MatView.bf16(b, M, K), Dev(b), None, 1, 0
+    if fmt == "int8":
+        q, s = orc.int8_quantize(w)
+        return orc.MatView.int8(q, s), Dev(q), Dev(s), 2, 0
+    q, s = orc.int4_quantize(w, bs)
+    return orc.MatView.int4(q, s, M, K, bs), Dev(q), Dev(s), 3, bs
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
+@pytest.mark.parametrize("M,K", [(12288, 4096), (100278, 4096), (333, 1024), (4096, 11008)])
+def test_gemv_fused_prologues(orc, fmt, M, K):
+    print(f"gemv_fused {fmt} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(M + K)
+    view, dw, ds, fid, bs = _stored(orc, fmt, _w((M, K), M * 7 + K))
+    x = rng.standard_normal(K).astype(np.float32)
+    y = rng.standard_normal(K).astype(np.float32) * 3.0
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    dx, dyv, dnw = Dev(x), Dev(y), Dev(nw)
+    out, xo = Dev.empty(M), Dev.empty(K)
+    L = lib()
+    # residual norm: x' = x + rmsnorm(y) * w
+    xr = x + orc.rmsnorm(y, nw, 1e-6)
+    assert L.atlas_gemv_fused_f32(fid, dw.ptr, ds.ptr if ds else None, bs, dx.ptr, out.ptr, M, K,
+                                  1, dyv.ptr, dnw.ptr, 1e-6, xo.ptr) == 0
+    assert np.max(np.abs(xo.get() - xr)) <= 1e-5 * np.max(np.abs(xr))
+    assert rel_err(out.get(), orc.linear(view, xr, threads=8)) <= GEMV_TOL
+    # rmsnorm prologue
+    xn = orc.rmsnorm(x, nw, 1e-5)
+    assert L.atlas_gemv_fused_f32(fid, dw.ptr, ds.ptr if ds else None, bs, dx.ptr, out.ptr, M, K,
+                                  2, None, dnw.ptr, 1e-5, xo.ptr) == 0
+    assert np.max(np.abs(xo.get() - xn)) <= 1e-5 * np.max(np.abs(xn))
+    assert rel_err(out.get(), orc.linear(view, xn, threads=8)) <= GEMV_TOL
+    # silu prologue over interleaved pairs
+    pairs = rng.standard_normal(2 * K).astype(np.float32) * 2.0
+    xs = np.array([orc.silu(float(g)) for g in pairs[0::2]], np.float32) * pairs[1::2]
+    dp = Dev(pairs)
+    assert L.atlas_gemv_fused_f32(fid, dw.ptr, ds.ptr if ds else None, bs, None, out.ptr, M, K,
+                                  3, dp.ptr, None, 0.0, None) == 0
+    assert rel_err(out.get(), orc.linear(view, xs, threads=8)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("H,KVH,hd,ctx,window,splits", [
+    (32, 8, 128, 512, 0, 0), (32, 8, 128, 4096, 0, 0), (32, 8, 128, 16384, 0, 0),
+    (32, 8, 128, 16384, 4096, 0), (32, 8, 128, 1, 0, 0), (32, 8, 128, 300, 64, 7),
+    (32, 32, 128, 200, 0, 4), (8, 8, 64, 77, 0, 3), (4, 1, 64, 50, 16, 1), (8, 2, 256, 90, 0, 5),
+    (16, 2, 128, 1000, 0, 64)])
+def test_attention_fused(orc, H, KVH, hd, ctx, window, splits):
+    print(f"attention_fused H={H} KVH={KVH} hd={hd} ctx={ctx} w={window} s={splits}", flush=True)
+    rng = np.random.default_rng(ctx * 7 + hd)
+    max_seq = ctx + 2
+    yarn = dict(factor=8.0, orig_max_pos=8192, attn_factor=1.2079441541679836,
+                beta_fast=32.0, beta_slow=1.0)
+    cos, sin, _ = orc.rope_tables(hd, max_seq, 500000.0, yarn)
+    pos = ctx - 1
+    K = np.zeros((max_seq, KVH, hd), np.float32)
+    V = np.zeros((max_seq, KVH, hd), np.float32)
+    K[:pos] = rng.standard_normal((pos, KVH, hd))
+    V[:pos] = rng.standard_normal((pos, KVH, hd))
+    qkv = rng.standard_normal((H + 2 * KVH) * hd).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, H * hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, KVH * hd).astype(np.float32)
+    # oracle: QK-norm, RoPE, cache write at pos, attention
+    q = orc.qk_norm(qkv[:H * hd], qn, H, hd, 1e-6)
+    k = orc.qk_norm(qkv[H * hd:(H + KVH) * hd], kn, KVH, hd, 1e-6)
+    q = np.concatenate([orc.rope_apply(q[h * hd:(h + 1) * hd], cos[pos], sin[pos]) for h in range(H)])
+    k = np.concatenate([orc.rope_apply(k[h * hd:(h + 1) * hd], cos[pos], sin[pos]) for h in range(KVH)])
+    Kr, Vr = K.copy(), V.copy()
+    Kr[pos] = k.reshape(KVH, hd)
+    Vr[pos] = qkv[(H + KVH) * hd:].reshape(KVH, hd)
+    scale = 1.2079441541679836 / math.sqrt(hd)
+    ref = orc.attention(q, Kr, Vr, H, KVH, hd, pos, scale, window)
+    d_qkv, dqn, dkn, dc, ds = Dev(qkv), Dev(qn), Dev(kn), Dev(cos), Dev(sin)
+    dk, dv, do = Dev(K), Dev(V), Dev.empty(H * hd)
+    for rep in range(2):          # a second launch reuses the merge counters
+        assert lib().atlas_attention_fused_f32(d_qkv.ptr, dqn.ptr, dkn.ptr, 1e-6, dc.ptr, ds.ptr,
+                                               dk.ptr, dv.ptr, do.ptr, H, KVH, hd, pos, scale,
+                                               window, splits) == 0
+        assert rel_err(do.get(), ref) <= ATTN_TOL, rep
+    assert np.max(np.abs(dk.get()[pos] - Kr[pos])) <= 1e-5 * np.max(np.abs(k))
+    assert np.array_equal(dv.get()[pos], Vr[pos])
