@@ -12,9 +12,10 @@
 //    contiguous slice of positions, and serves all G = n_heads / n_kv query
 //    heads of that group from a single read of each K/V row (the reference
 //    kernel re-reads K/V once per query head);
-//  * 16 lanes per position (head_dim / 16 dims each, 128-bit loads), so a
-//    wave covers 4 positions per row step and P of them per iteration; each
-//    lane keeps an online-softmax state (max, sum, partial output) per head;
+//  * 16 lanes per position (head_dim / 16 dims each, 128-bit loads); each of
+//    the block's 16 lane groups keeps an online-softmax state (max, sum,
+//    partial output) per head and scans its positions with the next step's
+//    K/V rows already in flight (attn_scan);
 //  * scores use exp2 with log2(e) folded into the scale; the SWA start index
 //    is computed, not masked;
 //  * per block, the 16 (wave, row) states merge through LDS into one partial
@@ -30,7 +31,152 @@ __device__ __forceinline__ int load_pos(const int* pos_dev, int pos) {
     return pos_dev ? *pos_dev : pos;
 }
 
-template <int HD, int G, int P>
+// ---- the K/V scan shared by the split and fused kernels --------------------
+// A block has 16 (wave, row) groups of 16 lanes; a group owns one position at
+// a time, each lane DPL = HD/16 dims of it.  Group w handles the P
+// consecutive positions b0 + 16*P*s + w*P + i of step s, so one step issues
+// 2*P*DPL/4 = 16 128-bit loads per lane (P = 8, 4, 2 for HD 64, 128, 256).
+//
+// Decode attention is latency-bound per block: a CU sees ~1 us of HBM latency
+// and streams at most (bytes in flight) / latency.  The scan therefore keeps
+// two register buffers and loads step s+1 while step s is scored, with a
+// scheduling barrier after each batch of loads -- left alone, the compiler
+// interleaves each load with its use to save registers and the block waits
+// out one full latency per 16-byte load.  The loads are raw buffer loads: the
+// K (V) rows of the block's KV head form one buffer resource whose size ends
+// at row e1, so an address needs one 32-bit VGPR and rows past the end read
+// as zero (and are scored as -inf) with no clamp or branch.
+template <int HD> struct ScanShape {
+    static constexpr int DPL = HD / 16;
+    static constexpr int P = HD == 64 ? 8 : HD == 128 ? 4 : 2;
+};
+
+struct ScanBufs {
+    __amdgpu_buffer_rsrc_t k, v;
+    uint32_t row_bytes;      // bytes between consecutive positions
+    uint32_t lane_bytes;     // this lane's byte offset inside a row
+};
+
+// kb/vb point at dim 0 of the KV head in row 0; rows [0, e1) are readable.
+// The caller guarantees e1 * row_bytes < 2^32.
+__device__ __forceinline__ float* uniform_ptr(const float* p) {
+    // the value is block-uniform; readfirstlane makes that visible to the
+    // compiler, which otherwise may keep it in VGPRs and wrap every buffer
+    // load in a waterfall loop
+    const uint64_t u = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (float*)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ ScanBufs scan_bufs(const float* kb, const float* vb, long kv_stride,
+                                              int e1, int lane_dims) {
+    ScanBufs b;
+    const uint32_t rb = __builtin_amdgcn_readfirstlane((uint32_t)(kv_stride * 4));
+    const int n = __builtin_amdgcn_readfirstlane((int)((uint32_t)e1 * rb));
+    b.k = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kb), (short)0, n, 0x00020000);
+    b.v = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(vb), (short)0, n, 0x00020000);
+    b.row_bytes = rb;
+    b.lane_bytes = (uint32_t)lane_dims * 4u;
+    return b;
+}
+
+template <int HD>
+__device__ __forceinline__ void scan_load(const ScanBufs& b, int t,
+                                          float (&kf)[ScanShape<HD>::P][HD / 16],
+                                          float (&vf)[ScanShape<HD>::P][HD / 16]) {
+    constexpr int P = ScanShape<HD>::P, DPL = HD / 16;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const uint32_t off = (uint32_t)(t + i) * b.row_bytes + b.lane_bytes;
+#pragma unroll
+        for (int d = 0; d < DPL; d += 4) {
+            const f32x4 kv = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(b.k, (int)(off + d * 4), 0, 0));
+            const f32x4 vv = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(b.v, (int)(off + d * 4), 0, 0));
+            kf[i][d] = kv.x; kf[i][d + 1] = kv.y; kf[i][d + 2] = kv.z; kf[i][d + 3] = kv.w;
+            vf[i][d] = vv.x; vf[i][d + 1] = vv.y; vf[i][d + 2] = vv.z; vf[i][d + 3] = vv.w;
+        }
+    }
+}
+
+// Online-softmax update of a group's state with positions t .. t+P-1 (those
+// >= end are masked).  q is pre-scaled by scale * log2(e).  A group may see
+// steps with no valid position (the scan loop is block-uniform); its state
+// then stays (m, l, o) = (-inf, 0, 0) with no NaN.
+template <int HD, int G>
+__device__ __forceinline__ void scan_update(const float (&q)[G][HD / 16], float (&m)[G],
+                                            float (&l)[G], float (&o)[G][HD / 16],
+                                            const float (&kf)[ScanShape<HD>::P][HD / 16],
+                                            const float (&vf)[ScanShape<HD>::P][HD / 16], int t,
+                                            int end) {
+    constexpr int P = ScanShape<HD>::P, DPL = HD / 16;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float s[P];
+        float smax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            float acc = 0.f;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) acc += q[h][d] * kf[i][d];
+            acc = row16_sum(acc);
+            s[i] = t + i < end ? acc : -INFINITY;
+            smax = fmaxf(smax, s[i]);
+        }
+        const float mn = fmaxf(m[h], smax);
+        const float corr = m[h] == -INFINITY ? 0.f : exp2f(m[h] - mn);
+        float psum = 0.f, p[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            p[i] = t + i < end ? exp2f(s[i] - mn) : 0.f;
+            psum += p[i];
+        }
+        l[h] = l[h] * corr + psum;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) {
+            float acc = o[h][d] * corr;
+#pragma unroll
+            for (int i = 0; i < P; ++i) acc += p[i] * vf[i][d];
+            o[h][d] = acc;
+        }
+        m[h] = mn;
+    }
+}
+
+// Scan cache rows [b0, e1) into the (wave, row) group's state.  kb/vb:
+// dim 0 of the KV head in row 0, lane_dims: the lane's first dim.
+template <int HD, int G>
+__device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long kv_stride,
+                                          int lane_dims, int b0, int e1, int group,
+                                          const float (&q)[G][HD / 16], float (&m)[G],
+                                          float (&l)[G], float (&o)[G][HD / 16]) {
+    constexpr int P = ScanShape<HD>::P, DPL = HD / 16, S = 16 * P;
+    // Block-uniform trip count and one exit, at the bottom of the loop: with a
+    // divergent or mid-body exit the compiler must assume the other buffer's
+    // loads may still be in flight at the loop head and waits for them there,
+    // serialising the two buffers again.
+    const int steps = __builtin_amdgcn_readfirstlane(e1 > b0 ? (e1 - b0 + S - 1) / S : 0);
+    if (steps == 0) return;
+    const ScanBufs b = scan_bufs(kb, vb, kv_stride, e1, lane_dims);
+    int t = b0 + group * P;
+    float ka[P][DPL], va[P][DPL], kn[P][DPL], vn[P][DPL];
+    scan_load<HD>(b, t, ka, va);
+    for (int pair = 0; pair < steps / 2; ++pair) {
+        scan_load<HD>(b, t + S, kn, vn);
+        __builtin_amdgcn_sched_barrier(0);
+        scan_update<HD, G>(q, m, l, o, ka, va, t, e1);
+        t += S;
+        scan_load<HD>(b, t + S, ka, va);       // past the end: zeros, no traffic
+        __builtin_amdgcn_sched_barrier(0);
+        scan_update<HD, G>(q, m, l, o, kn, vn, t, e1);
+        t += S;
+    }
+    if (steps & 1) scan_update<HD, G>(q, m, l, o, ka, va, t, e1);
+}
+
+template <int HD, int G>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;              // dims per lane
     constexpr float LOG2E = 1.4426950408889634f;
@@ -65,56 +211,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    const float* kbase = a.k_cache + (long)kvh * HD + dl * DPL;
-    const float* vbase = a.v_cache + (long)kvh * HD + dl * DPL;
-    // positions handled by (wave, row): t = b0 + 16*P*it + (wave*4 + row)*P + i
-    for (int t0 = b0 + (wave * 4 + row) * P; t0 < b1; t0 += 16 * P) {
-        float kf[P][DPL], vf[P][DPL];
-        bool valid[P];
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            const int t = t0 + i;
-            valid[i] = t < b1;
-            const long off = (long)(valid[i] ? t : t0) * kv_stride;
-#pragma unroll
-            for (int d = 0; d < DPL; d += 4) {
-                const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off + d);
-                const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off + d);
-                kf[i][d] = kv.x; kf[i][d + 1] = kv.y; kf[i][d + 2] = kv.z; kf[i][d + 3] = kv.w;
-                vf[i][d] = vv.x; vf[i][d + 1] = vv.y; vf[i][d + 2] = vv.z; vf[i][d + 3] = vv.w;
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float s[P];
-            float smax = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < P; ++i) {
-                float acc = 0.f;
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) acc += q[h][d] * kf[i][d];
-                acc = row16_sum(acc);
-                s[i] = valid[i] ? acc : -INFINITY;
-                smax = fmaxf(smax, s[i]);
-            }
-            const float mn = fmaxf(m[h], smax);
-            // mn is finite: position t0 is always valid
-            const float corr = exp2f(m[h] - mn);
-            float psum = 0.f;
-            float p[P];
-#pragma unroll
-            for (int i = 0; i < P; ++i) { p[i] = exp2f(s[i] - mn); psum += p[i]; }
-            l[h] = l[h] * corr + psum;
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) {
-                float acc = o[h][d] * corr;
-#pragma unroll
-                for (int i = 0; i < P; ++i) acc += p[i] * vf[i][d];
-                o[h][d] = acc;
-            }
-            m[h] = mn;
-        }
-    }
+    attn_scan<HD, G>(a.k_cache + (long)kvh * HD, a.v_cache + (long)kvh * HD, kv_stride, dl * DPL,
+                     b0, b1, wave * 4 + row, q, m, l, o);
 
     // ---- merge the 16 (wave,row) states of this block through LDS ---------
     __shared__ float s_m[16][G], s_l[16][G];
@@ -238,18 +336,24 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
 //    block that sees n_splits - 1 merges and resets the counter to 0 (no
 //    waiting anywhere, and the counters are clean for the next launch).
 // ---------------------------------------------------------------------------
-template <int HD, int G, int P>
+template <int HD, int G>
 __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
     constexpr int DPL = HD / 16;
     constexpr int EPL = HD / 64;              // head elements per lane in the prep
     constexpr float LOG2E = 1.4426950408889634f;
-    const int kvh = blockIdx.x, split = blockIdx.y, n_splits = gridDim.y, seq = blockIdx.z;
+    const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = lane >> 4, dl = lane & 15;
     const int pos = a.pos_dev[seq];
     const int slot = a.slot_dev ? a.slot_dev[seq] : 0;
     const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
     const int ctx = pos - t_lo + 1;
+    // active splits: all gridDim.y, or one per min_chunk positions of the live
+    // context (the grid is fixed when a decode step is captured once and
+    // replayed at every position; surplus blocks leave here)
+    int n_splits = gridDim.y;
+    if (a.min_chunk > 0) n_splits = min(n_splits, max(1, (ctx + a.min_chunk - 1) / a.min_chunk));
+    if (split >= n_splits) return;
     const int chunk = (ctx + n_splits - 1) / n_splits;
     const int b0 = t_lo + split * chunk;
     const int b1 = min(pos + 1, b0 + chunk);
@@ -325,71 +429,20 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    auto update = [&](const float (&kf)[P][DPL], const float (&vf)[P][DPL], const bool (&valid)[P]) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float s[P];
-            float smax = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < P; ++i) {
-                float acc = 0.f;
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) acc += q[h][d] * kf[i][d];
-                acc = row16_sum(acc);
-                s[i] = valid[i] ? acc : -INFINITY;
-                smax = fmaxf(smax, s[i]);
-            }
-            const float mn = fmaxf(m[h], smax);
-            const float corr = exp2f(m[h] - mn);
-            float psum = 0.f, p[P];
-#pragma unroll
-            for (int i = 0; i < P; ++i) { p[i] = exp2f(s[i] - mn); psum += p[i]; }
-            l[h] = l[h] * corr + psum;
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) {
-                float acc = o[h][d] * corr;
-#pragma unroll
-                for (int i = 0; i < P; ++i) acc += p[i] * vf[i][d];
-                o[h][d] = acc;
-            }
-            m[h] = mn;
-        }
-    };
-
-    const float* kbase = kc + (long)kvh * HD + dl * DPL;
-    const float* vbase = vc + (long)kvh * HD + dl * DPL;
-    for (int t0 = b0 + (wave * 4 + row) * P; t0 < e1; t0 += 16 * P) {
-        float kf[P][DPL], vf[P][DPL];
-        bool valid[P];
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            const int t = t0 + i;
-            valid[i] = t < e1;
-            const long off = (long)(valid[i] ? t : t0) * kv_stride;
-#pragma unroll
-            for (int d = 0; d < DPL; d += 4) {
-                const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off + d);
-                const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off + d);
-                kf[i][d] = kv.x; kf[i][d + 1] = kv.y; kf[i][d + 2] = kv.z; kf[i][d + 3] = kv.w;
-                vf[i][d] = vv.x; vf[i][d + 1] = vv.y; vf[i][d + 2] = vv.z; vf[i][d + 3] = vv.w;
-            }
-        }
-        update(kf, vf, valid);
-    }
+    attn_scan<HD, G>(kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, dl * DPL, b0, e1,
+                     wave * 4 + row, q, m, l, o);
     if (owner && wave == 0 && row == 0) {
         // position pos from LDS (the 16 lanes of row 0 of wave 0)
+        constexpr int P = ScanShape<HD>::P;
         float kf[P][DPL], vf[P][DPL];
-        bool valid[P];
 #pragma unroll
-        for (int i = 0; i < P; ++i) {
-            valid[i] = i == 0;
+        for (int i = 0; i < P; ++i)
 #pragma unroll
             for (int d = 0; d < DPL; ++d) {
                 kf[i][d] = sk[dl * DPL + d];
                 vf[i][d] = sv[dl * DPL + d];
             }
-        }
-        update(kf, vf, valid);
+        scan_update<HD, G>(q, m, l, o, kf, vf, 0, 1);
     }
 
     // ---- merge the 16 (wave,row) states of this block ------------------------
@@ -404,7 +457,9 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
         for (int d = 0; d < DPL; ++d) s_o[st][h][dl * DPL + d] = o[h][d];
     }
     __syncthreads();
-    const long pbase = (long)seq * a.n_heads * n_splits;
+    // each sequence owns n_heads * gridDim.y partial slots (its active split
+    // count may be smaller and differs between sequences)
+    const long pbase = (long)seq * a.n_heads * gridDim.y;
     for (int e = threadIdx.x; e < G * HD; e += 256) {
         const int h = e / HD, d = e % HD;
         float mx = -INFINITY;
@@ -461,7 +516,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
 
 template <int HD, int G>
 static int launch_fused(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st) {
-    hipLaunchKernelGGL((attn_fused_kernel<HD, G, 4>), dim3(a.n_kv, n_splits, n_seq), dim3(256), 0,
+    hipLaunchKernelGGL((attn_fused_kernel<HD, G>), dim3(a.n_kv, n_splits, n_seq), dim3(256), 0,
                        st, a);
     ATLAS_LAUNCH_CHECK("attn_fused");
     return ATLAS_OK;
@@ -482,6 +537,9 @@ int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream
     ATLAS_REQUIRE(n_splits == 1 || (a.part_m && a.part_l && a.part_o && a.counters),
                   "attention: split partials missing");
     ATLAS_REQUIRE(n_seq >= 1 && n_splits >= 1, "attention: empty grid");
+    ATLAS_REQUIRE(attn_rows_fit(a.max_rows, a.n_kv, a.head_dim),
+                  "attention: %d cache rows of %d x %d exceed 32-bit offsets", a.max_rows, a.n_kv,
+                  a.head_dim);
     const uintptr_t al = (uintptr_t)a.qkv | (uintptr_t)a.k_cache | (uintptr_t)a.v_cache;
     ATLAS_REQUIRE((al & 15) == 0 && a.qkv_stride % 4 == 0 && a.slot_stride % 4 == 0,
                   "attention: 16-byte alignment");
@@ -515,18 +573,26 @@ int attn_reserve(int n_heads, int head_dim, int n_splits) {
     return ATLAS_OK;
 }
 
+int attn_max_splits(int n_kv) {
+    // Measured on MI355X (7B shapes, ctx 64..8192): the merge's device-scope
+    // release (an L2 write-back per block) makes grids beyond ~128 blocks
+    // slower, whatever the context; 8 splits of a GQA head already stream
+    // at the scan's rate.
+    int s = 128 / (n_kv > 0 ? n_kv : 1);
+    return s < 1 ? 1 : (s > 8 ? 8 : s);
+}
+
 int attn_pick_splits(int n_kv, int max_ctx) {
-    // ~2 blocks per CU, each with at least 64 positions
-    int want = (2 * device_cu_count() + n_kv - 1) / n_kv;
-    int cap = (max_ctx + 63) / 64;
-    int s = want < cap ? want : cap;
-    if (s > 128) s = 128;
+    // one split per kAttnSplitChunk positions, within attn_max_splits
+    const int by_ctx = (max_ctx + kAttnSplitChunk - 1) / kAttnSplitChunk;
+    const int cap = attn_max_splits(n_kv);
+    const int s = by_ctx < cap ? by_ctx : cap;
     return s < 1 ? 1 : s;
 }
 
 template <int HD, int G>
 static int launch_split(AttnArgs a, int n_splits, hipStream_t st) {
-    hipLaunchKernelGGL((attn_split_kernel<HD, G, 4>), dim3(a.n_kv, n_splits), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_split_kernel<HD, G>), dim3(a.n_kv, n_splits), dim3(256), 0, st, a);
     ATLAS_LAUNCH_CHECK("attn_split");
     if (n_splits > 1) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_heads), dim3(HD < 256 ? HD : 256), 0, st,
@@ -546,7 +612,8 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
     const bool aligned =
         (((uintptr_t)a.q | (uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 15) == 0;
     const bool fast = aligned && (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) &&
-                      (G == 1 || G == 2 || G == 4 || G == 8);
+                      (G == 1 || G == 2 || G == 4 || G == 8) &&
+                      attn_rows_fit(a.max_rows, a.n_kv, a.head_dim);
     if (!fast) {
         hipLaunchKernelGGL(attn_generic_kernel, dim3(a.n_heads), dim3(256), 0, st, a, a.head_dim);
         ATLAS_LAUNCH_CHECK("attn_generic");

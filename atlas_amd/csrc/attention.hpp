@@ -17,6 +17,7 @@ struct AttnArgs {
     float* part_m;           // split partials (library scratch)
     float* part_l;
     float* part_o;
+    int max_rows;            // cache rows that may be read (max_seq), > 0
 };
 
 // Fused QK-norm + RoPE + KV write + split-K attention + split merge.
@@ -42,9 +43,21 @@ struct AttnFusedArgs {
     float* part_l;
     float* part_o;           // [n_seq][n_heads][n_splits][hd]
     int* counters;           // [n_seq][n_kv], zero before the first launch
+    int min_chunk;           // > 0: active splits = min(grid, ceil(ctx / min_chunk))
+    int max_rows;            // cache rows per slot (max_seq), > 0
 };
 
+// The scan addresses one KV head's rows with 32-bit byte offsets.
+inline bool attn_rows_fit(long max_rows, int n_kv, int head_dim) {
+    return max_rows > 0 && max_rows * (long)n_kv * head_dim * 4 <= 0xFFFFFFFFL;
+}
+
+// Positions per split below which another split costs more than it saves
+// (one pipelined block scans ~512 rows in the time a split merge takes).
+constexpr int kAttnSplitChunk = 512;
+
 bool attn_fused_supported(int n_heads, int n_kv, int head_dim);
+int attn_max_splits(int n_kv);
 int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st);
 int attn_pick_splits(int n_kv, int max_ctx);
 int attn_reserve(int n_heads, int head_dim, int n_splits);

@@ -99,6 +99,7 @@ ATLAS_API void atlas_decode_attention(const float* q, const float* k_cache, cons
     a.q = q; a.k_cache = k_cache; a.v_cache = v_cache; a.out = out;
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = head_dim;
     a.pos = pos; a.pos_dev = nullptr; a.scale = scale; a.window = window;
+    a.max_rows = pos + 1;
     const int ctx = (window > 0 && pos + 1 > window) ? window : pos + 1;
     attn_launch(a, attn_pick_splits(n_kv > 0 ? n_kv : 1, ctx), stream());
 }
@@ -202,7 +203,8 @@ ATLAS_API int atlas_attention_fused_f32(const float* qkv, const float* q_norm,
                                         const float* k_norm, float qk_eps, const float* cos_tab,
                                         const float* sin_tab, float* k_cache, float* v_cache,
                                         float* out, int n_heads, int n_kv, int head_dim, int pos,
-                                        float scale, int window, int n_splits) {
+                                        float scale, int window, int n_splits,
+                                        int min_chunk) {
     ATLAS_REQUIRE(pos >= 0, "attention_fused: pos < 0");
     ATLAS_REQUIRE(attn_fused_supported(n_heads, n_kv, head_dim), "attention_fused: shape");
     const int ctx = (window > 0 && pos + 1 > window) ? window : pos + 1;
@@ -240,6 +242,8 @@ ATLAS_API int atlas_attention_fused_f32(const float* qkv, const float* q_norm,
     a.part_l = d_part + (size_t)n_heads * n_splits;
     a.part_o = d_part + (size_t)2 * n_heads * n_splits;
     a.counters = d_cnt;
+    a.min_chunk = min_chunk > 0 ? min_chunk : 0;
+    a.max_rows = pos + 1;
     return attn_fused_launch(a, n_splits, 1, stream());
 }
 

@@ -95,12 +95,15 @@ struct atlas_model {
     float* attn_part = nullptr;
     int* attn_counters = nullptr;
     bool fused = false;
+    // fused step: SwiGLU in the gate/up epilogue (true) or in W_down's prologue
+    bool silu_epi = true;
     int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
     uint32_t *tok_dev = nullptr, *hist = nullptr, *suppress_dev = nullptr, *choice_dev = nullptr;
     int suppress_cap = 0;
     unsigned long long* argpart = nullptr;
     long slot_stride = 0;
-    int attn_splits = 1;
+    int attn_splits = 1;           // fused kernel: maximum (grid) split count
+    int attn_splits_unfused = 1;
     int pos = 0;
     hipStream_t st = nullptr;
     bool use_graph = true;
@@ -227,7 +230,8 @@ int layer_step(atlas_model* m, int li) {
     a.q = m->qkv; a.k_cache = L.kc; a.v_cache = L.vc; a.out = m->att;
     a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
     a.pos = 0; a.pos_dev = m->pos_dev; a.scale = m->scale; a.window = L.window;
-    TRY(attn_launch(a, m->attn_splits, m->st));
+    a.max_rows = c.max_seq;
+    TRY(attn_launch(a, m->attn_splits_unfused, m->st));
     TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
     if (c.post_norm) {
         TRY(residual_rmsnorm_launch(m->x, m->y, L.attn_norm, d, 1, d, c.rms_eps, m->st));
@@ -272,13 +276,29 @@ GemvArgs pro_args(const DevMat& w, const float* x, float* y, int pro, const floa
     return a;
 }
 
+// GU of the fused step: x'_l = x_l + rmsnorm(y1) * attn_norm_l materialised
+// into xb, then h = silu(gate) * up (silu_epi) or the raw (gate, up) pairs.
+int enqueue_gu_fused(atlas_model* m, const LayerW& L) {
+    GemvArgs gu = pro_args(L.gu, m->x, m->h, PRO_RESNORM, m->y, L.attn_norm, m->cfg.rms_eps, m->xb);
+    if (m->silu_epi) gu.epi = EPI_SILU_MUL;
+    return gemv_launch(gu, m->st);
+}
+
+// DOWN of the fused step: y2 = W_down h, or W_down (silu(gate) * up) with the
+// SwiGLU applied while staging the pairs when the epilogue did not.
+int enqueue_down_fused(atlas_model* m, const LayerW& L) {
+    if (m->silu_epi) return gemv(m, L.down, m->h, m->y2, EPI_STORE);
+    return gemv_launch(pro_args(L.down, nullptr, m->y2, PRO_SILU, m->h, nullptr, 0.f, nullptr), m->st);
+}
+
 // The post-norm decode step with the norms folded into the GEMV prologues
 // and one attention launch per layer (5 launches per layer):
 //   QKV    x_l = x'_{l-1} + rmsnorm(y2) * ffn_norm_{l-1}   (layer 0: embedding)
 //   ATTN   QK-norm + RoPE + KV write + split-K attention + merge
 //   WO     y1 = W_o att
-//   GU     x'_l = x_l + rmsnorm(y1) * attn_norm_l;  h = [gate | up](x'_l)
-//   DOWN   y2 = W_down (silu(gate) * up)
+//   GU     x'_l = x_l + rmsnorm(y1) * attn_norm_l;  h = silu(gate) * up
+//   DOWN   y2 = W_down h
+// (int8 moves the SwiGLU from GU's epilogue into DOWN's prologue).
 // x_l lives in m->x, x'_l in m->xb.
 int enqueue_step_fused(atlas_model* m, int mode) {
     const atlas_model_config& c = m->cfg;
@@ -305,12 +325,11 @@ int enqueue_step_fused(atlas_model* m, int mode) {
         a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
         a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
         a.counters = m->attn_counters;
+        a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
         TRY(attn_fused_launch(a, m->attn_splits, 1, m->st));
         TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
-        TRY(gemv_launch(pro_args(L.gu, m->x, m->h, PRO_RESNORM, m->y, L.attn_norm, eps, m->xb),
-                        m->st));
-        TRY(gemv_launch(pro_args(L.down, nullptr, m->y2, PRO_SILU, m->h, nullptr, 0.f, nullptr),
-                        m->st));
+        TRY(enqueue_gu_fused(m, L));
+        TRY(enqueue_down_fused(m, L));
     }
     // x_L = x'_{L-1} + rmsnorm(y2) * ffn_norm_{L-1}, in place in xb
     TRY(residual_rmsnorm_launch(m->xb, m->y2, m->L[c.n_layers - 1].ffn_norm, d, 1, d, eps, m->st));
@@ -695,6 +714,7 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
             a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
+            a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
             TRY(attn_fused_launch(a, m->attn_splits, n, m->st));
         }
         QkvPostArgs q{};
@@ -713,7 +733,8 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             a.out = m->att + (size_t)i * d;
             a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
             a.pos_dev = m->pos_dev + i; a.scale = m->scale; a.window = L.window;
-            TRY(attn_launch(a, m->attn_splits, m->st));
+            a.max_rows = c.max_seq;
+            TRY(attn_launch(a, m->attn_splits_unfused, m->st));
         }
         TRY(skinny(m, L.wo, m->att, m->y, n, EPI_STORE));
         if (c.post_norm) {
@@ -841,12 +862,22 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
             return fail(m);
         }
     }
+    // Split counts.  The fused kernel sizes its grid for the longest context
+    // and activates one split per kAttnSplitChunk positions of the live
+    // context, so short contexts run one block per KV head and merge nothing.
+    // The unfused kernel's count is fixed at launch.
     m->attn_splits = attn_pick_splits(c.n_kv_heads, c.max_seq);
-    if (attn_reserve(c.n_heads, hd, m->attn_splits)) return fail(m);
+    m->attn_splits_unfused = m->attn_splits;
+    if (attn_reserve(c.n_heads, hd, m->attn_splits_unfused)) return fail(m);
     // fused step: post-norm model whose attention shape the fused kernel
     // covers and whose GEMVs take the aligned fast path (d % 32 == 0)
     m->fused = c.post_norm && attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
-               d % 32 == 0 && c.ffn_hidden % 32 == 0;
+               attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && d % 32 == 0 &&
+               c.ffn_hidden % 32 == 0;
+    // the two-row int8 GEMV (a wave owns a (gate, up) pair) needs ~170 VGPRs
+    // and runs at half the one-row variant's rate: int8 stores gate/up and
+    // applies SwiGLU while staging W_down's input instead
+    m->silu_epi = c.weight_format != ATLAS_W_INT8;
     if (dalloc(m, (void**)&m->attn_part,
                (size_t)B * c.n_heads * m->attn_splits * (hd + 2) * 4) ||
         dalloc(m, (void**)&m->attn_counters, (size_t)B * c.n_kv_heads * 4))
@@ -1213,22 +1244,29 @@ ATLAS_API int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, in
 
 ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float* ms,
                                      int* launches, int64_t* bytes) {
-    ATLAS_REQUIRE(m && iters > 0 && ms && launches && bytes && which >= 0 && which <= 2,
+    ATLAS_REQUIRE(m && iters > 0 && ms && launches && bytes && which >= 0 && which <= 3,
                   "bench_gemv: bad arguments");
     const float eps = m->cfg.rms_eps;
     auto mat_bytes = [](const DevMat& w, int64_t out) {
         return (int64_t)w.data_bytes() + (int64_t)w.scale_count() * 4 + (int64_t)w.cols * 4 + out * 4;
     };
-    const bool k_set = which == 0 || which == 1, down_set = which == 0 || which == 2;
+    const bool k_set = which == 0 || which == 1, down_set = which == 0 || which == 2,
+               gu_set = which == 0 || which == 3;
+    const bool silu_in_gu = !m->fused || m->silu_epi;
     int64_t b = 0;
     int n = 0;
     for (const auto& L : m->L) {
         if (k_set) {
-            b += mat_bytes(L.qkv, L.qkv.rows) + mat_bytes(L.wo, L.wo.rows) + mat_bytes(L.gu, L.gu.rows);
-            n += 3;
+            b += mat_bytes(L.qkv, L.qkv.rows) + mat_bytes(L.wo, L.wo.rows);
+            n += 2;
+        }
+        if (gu_set) {
+            b += mat_bytes(L.gu, silu_in_gu ? L.gu.rows / 2 : L.gu.rows);
+            n += 1;
         }
         if (down_set) {
-            b += mat_bytes(L.down, L.down.rows) + (int64_t)L.down.cols * 4;   // pairs read twice as wide
+            // the SwiGLU prologue reads both halves of each (gate, up) pair
+            b += mat_bytes(L.down, L.down.rows) + (silu_in_gu ? 0 : (int64_t)L.down.cols * 4);
             n += 1;
         }
     }
@@ -1244,21 +1282,19 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
         for (size_t li = 0; li < m->L.size(); ++li) {
             LayerW& L = m->L[li];
             if (k_set) {
-                if (m->fused) {
+                if (m->fused)
                     TRY(gemv_launch(pro_args(L.qkv, m->xb, m->qkv, PRO_RESNORM, m->y2, L.ffn_norm, eps, m->x), m->st));
-                    TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
-                    TRY(gemv_launch(pro_args(L.gu, m->x, m->h, PRO_RESNORM, m->y, L.attn_norm, eps, m->xb), m->st));
-                } else {
+                else
                     TRY(gemv(m, L.qkv, m->x, m->qkv, EPI_STORE));
-                    TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
-                    TRY(gemv(m, L.gu, m->x, m->h, EPI_SILU_MUL));
-                }
+                TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
+            }
+            if (gu_set) {
+                if (m->fused) TRY(enqueue_gu_fused(m, L));
+                else TRY(gemv(m, L.gu, m->x, m->h, EPI_SILU_MUL));
             }
             if (down_set) {
-                if (m->fused)
-                    TRY(gemv_launch(pro_args(L.down, nullptr, m->y2, PRO_SILU, m->h, nullptr, 0.f, nullptr), m->st));
-                else
-                    TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
+                if (m->fused) TRY(enqueue_down_fused(m, L));
+                else TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
             }
         }
         if (k_set) {

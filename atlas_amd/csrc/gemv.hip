@@ -139,135 +139,11 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, f32x4* xs, int K) {
     }
 }
 
-// dot of one 16-byte weight chunk with its EPC x values held in registers
-template <int FMT>
-__device__ __forceinline__ float chunk_dot_r(const u32x4 w, const float* x, float acc) {
-    if constexpr (FMT == WF_F32) {
-        acc += __uint_as_float(w.x) * x[0];
-        acc += __uint_as_float(w.y) * x[1];
-        acc += __uint_as_float(w.z) * x[2];
-        acc += __uint_as_float(w.w) * x[3];
-    } else if constexpr (FMT == WF_BF16) {
-        acc += bf16_lo(w.x) * x[0];  acc += bf16_hi(w.x) * x[1];
-        acc += bf16_lo(w.y) * x[2];  acc += bf16_hi(w.y) * x[3];
-        acc += bf16_lo(w.z) * x[4];  acc += bf16_hi(w.z) * x[5];
-        acc += bf16_lo(w.w) * x[6];  acc += bf16_hi(w.w) * x[7];
-    } else if constexpr (FMT == WF_I8) {
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int b = 0; b < 4; ++b) acc += s8_at(ww[j], b) * x[4 * j + b];
-    } else {   // int4: sum of (16*q) * x
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t hi = ww[j] & 0xF0F0F0F0u;
-            const uint32_t lo = (ww[j] << 4) & 0xF0F0F0F0u;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                acc += s8_at(hi, b) * x[8 * j + 2 * b];
-                acc += s8_at(lo, b) * x[8 * j + 2 * b + 1];
-            }
-        }
-    }
-    return acc;
-}
-
 // ordered (value, index) key: larger value wins, ties keep the larger index
 __device__ __forceinline__ unsigned long long argkey_f(float v, int i) {
     uint32_t u = __float_as_uint(v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (uint32_t)i;
-}
-
-// ---------------------------------------------------------------------------
-// K <= 64*CPL*EPC: x lives in registers (each lane keeps the x values of its
-// CPL chunks for the whole kernel), weights stream through raw buffer loads
-// (32-bit offsets; offsets past the matrix return 0, which also serves the
-// per-row tail), one full row per wave with the next row prefetched.  No LDS
-// traffic in the loop and no barriers after the prologue.
-// ---------------------------------------------------------------------------
-#define ATLAS_BUF_DWORD3 0x00020000
-#define ATLAS_OOB 0x80000000u
-
-template <int FMT, int CPL>
-__global__ __launch_bounds__(256) void gemv_xreg_kernel(GemvArgs a) {
-    extern __shared__ f32x4 xs[];
-    constexpr int EPC = WT<FMT>::EPC;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int K = a.K, M = a.M;
-    const int chunks = K / EPC;
-    const uint32_t row_bytes = (uint32_t)chunks * 16u;
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(a.w), (short)0, (int)((uint64_t)M * row_bytes), ATLAS_BUF_DWORD3);
-    const int n_scales = FMT == WF_I4 ? M * a.bpr : M;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(a.scales), (short)0, (FMT == WF_I4 || FMT == WF_I8) ? n_scales * 4 : 0,
-        ATLAS_BUF_DWORD3);
-    int lcpb = 0;
-    while ((1 << lcpb) < a.cpb) ++lcpb;
-
-    auto load_row = [&](int r, u32x4 (&w)[CPL], float (&sc)[CPL]) {
-        const uint32_t base = (uint32_t)r * row_bytes;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = lane + 64 * j;
-            const uint32_t off = c < chunks ? base + (uint32_t)c * 16u : ATLAS_OOB;
-            w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 2));
-            if constexpr (FMT == WF_I4) {
-                const uint32_t bi = (uint32_t)r * (uint32_t)a.bpr + ((uint32_t)c >> lcpb);
-                const uint32_t so = c < chunks ? bi * 4u : ATLAS_OOB;
-                sc[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0)) *
-                        0.0625f;
-            }
-        }
-    };
-
-    const int S = gridDim.x * 4;
-    int row = blockIdx.x * 4 + wave;
-    u32x4 wa[CPL], wb[CPL];
-    float sa[CPL], sb[CPL];
-    if (row < M) load_row(row, wa, sa);      // first row in flight during the prologue
-    stage_x<false>(a, xs, K);
-    __syncthreads();
-    float xr[CPL][EPC];
-    const float* xf = reinterpret_cast<const float*>(xs);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) xr[j][e] = c < chunks ? xf[c * EPC + e] : 0.0f;
-    }
-
-    unsigned long long best = 0;
-    auto finish = [&](int r, const u32x4 (&w)[CPL], const float (&sc)[CPL]) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            if constexpr (FMT == WF_I4) acc += sc[j] * chunk_dot_r<FMT>(w[j], xr[j], 0.0f);
-            else acc = chunk_dot_r<FMT>(w[j], xr[j], acc);
-        }
-        acc = wave_sum(acc);
-        if constexpr (FMT == WF_I8) acc *= a.scales[r];
-        if (lane == 0) a.y[r] = acc;
-        if (a.epi == EPI_ARGMAX) {
-            const unsigned long long k = argkey_f(acc, r);
-            best = k > best ? k : best;
-        }
-    };
-
-    while (row < M) {
-        const int r1 = row + S;
-        if (r1 < M) load_row(r1, wb, sb);
-        finish(row, wa, sa);
-        if (r1 >= M) break;
-        const int r2 = r1 + S;
-        if (r2 < M) load_row(r2, wa, sa);
-        finish(r1, wb, sb);
-        row = r2;
-    }
-    if (a.epi == EPI_ARGMAX && lane == 0) a.arg_part[blockIdx.x * 4 + wave] = best;
 }
 
 template <int FMT, int ROWS, int UNROLL>
@@ -321,6 +197,7 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
     float acc[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+    unsigned long long best = 0;          // EPI_ARGMAX: best (logit, row) of this wave
 
     for (int it = 0; it < total; ++it) {
         u32x4 nxt[UNROLL][ROWS];
@@ -362,6 +239,14 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
 #pragma unroll
                 for (int r = 0; r < ROWS; ++r)
                     if (lane == r && r0 + r < M) a.y[r0 + r] = acc[r];
+                if (a.epi == EPI_ARGMAX) {
+#pragma unroll
+                    for (int r = 0; r < ROWS; ++r)
+                        if (r0 + r < M) {
+                            const unsigned long long k = argkey_f(acc[r], r0 + r);
+                            best = k > best ? k : best;
+                        }
+                }
             }
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
@@ -376,6 +261,7 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
                 }
         }
     }
+    if (a.epi == EPI_ARGMAX && lane == 0) a.arg_part[blockIdx.x * 4 + wave] = best;
 }
 
 // Any-shape fallback (K not a multiple of the chunk width, tiny matrices):
@@ -450,6 +336,19 @@ int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m,
 
 // ---------------------------------------------------------------------------
 
+// persistent grid of the LDS-staged kernel: LDS bounds the resident blocks
+// per CU, so never ask for more than fit
+static int n1_blocks(int M, int K, int rows, int blocks_per_cu) {
+    const int n_groups = (M + rows - 1) / rows;
+    int blocks = (n_groups + 3) / 4;
+    const size_t lds = (size_t)K * 4;
+    int fit = (int)((160 * 1024) / (lds ? lds : 1));
+    if (fit < 1) fit = 1;
+    const int bpc = blocks_per_cu < fit ? blocks_per_cu : fit;
+    const int cap = bpc * device_cu_count();
+    return blocks > cap ? cap : blocks;
+}
+
 template <int FMT, int ROWS, int UNROLL>
 int launch_n1(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
     const size_t lds = (size_t)a.K * 4;
@@ -464,14 +363,9 @@ int launch_n1(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
             raised = true;
         }
     }
-    const int n_groups = (a.M + ROWS - 1) / ROWS;
-    int blocks = (n_groups + 3) / 4;
-    // LDS bounds the resident blocks per CU; never ask for more than fit
-    int fit = (int)((160 * 1024) / (lds ? lds : 1));
-    if (fit < 1) fit = 1;
-    int bpc = blocks_per_cu < fit ? blocks_per_cu : fit;
-    const int cap = bpc * device_cu_count();
-    if (blocks > cap) blocks = cap;
+    const int blocks = n1_blocks(a.M, a.K, ROWS, blocks_per_cu);
+    if (a.epi == EPI_ARGMAX)
+        ATLAS_REQUIRE(blocks * 4 <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a);
     ATLAS_LAUNCH_CHECK("gemv_n1");
     return ATLAS_OK;
@@ -487,41 +381,25 @@ int gemv_fast_ok(int fmt, int K, int block) {
     return 0;
 }
 
-// resident blocks per CU of the register-x kernel (also fixes the number of
-// argmax partials it writes: 4 per block)
-constexpr int XREG_BPC = 2;
-
-template <int FMT, int CPL>
-static int launch_xreg(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
-    int blocks = (a.M + 3) / 4;
-    const int cap = blocks_per_cu * device_cu_count();
-    if (blocks > cap) blocks = cap;
-    if (a.epi == EPI_ARGMAX)
-        ATLAS_REQUIRE(blocks * 4 <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
-    hipLaunchKernelGGL((gemv_xreg_kernel<FMT, CPL>), dim3(blocks), dim3(256), (size_t)a.K * 4, st, a);
-    ATLAS_LAUNCH_CHECK("gemv_xreg");
-    return ATLAS_OK;
+// Launch shape per (format, K): rows per wave, chunk unroll, blocks per CU.
+// Chosen by sweeping the 7B decode shapes on MI355X over >= 1.1 GB of
+// rotating weights (rows = 1 wins: more waves in flight per CU).
+struct N1Shape { int rows, unroll, bpc; };
+static N1Shape n1_shape(int fmt, int M, int K, int epi) {
+    if (epi == EPI_SILU_MUL) return {2, fmt == WF_BF16 ? 4 : 2, 8};
+    const bool big_k = K > 4096;
+    switch (fmt) {
+    case WF_BF16: return big_k ? N1Shape{1, 8, 2} : N1Shape{1, 4, 8};
+    case WF_I8:   return big_k ? N1Shape{1, 8, 16} : (M >= 65536 ? N1Shape{1, 4, 4} : N1Shape{1, 2, 8});
+    case WF_I4:   return big_k ? N1Shape{2, 2, 8} : N1Shape{1, 2, 8};
+    default:      return {1, 4, 8};
+    }
 }
 
-// CPL is bounded so that a lane keeps at most 64 x values in registers
-template <int FMT>
-static int dispatch_xreg(const GemvArgs& a, hipStream_t st, int cpl, int bpc) {
-    constexpr int MAXC = 64 / WT<FMT>::EPC < 8 ? 64 / WT<FMT>::EPC : 8;
-    if (cpl <= 1) return launch_xreg<FMT, 1>(a, st, bpc);
-    if (cpl <= 2 || MAXC == 2) return launch_xreg<FMT, (MAXC < 2 ? MAXC : 2)>(a, st, bpc);
-    if (cpl <= 4 || MAXC == 4) return launch_xreg<FMT, (MAXC < 4 ? MAXC : 4)>(a, st, bpc);
-    return launch_xreg<FMT, MAXC>(a, st, bpc);
-}
-
-static int elem_per_chunk(int fmt) {
-    return fmt == WF_F32 ? 4 : fmt == WF_BF16 ? 8 : fmt == WF_I8 ? 16 : 32;
-}
-
-// number of persistent waves the batch-1 kernel launches (argmax partial count)
+// number of persistent waves gemv_launch uses (argmax partial count)
 int gemv_waves(const GemvArgs& a) {
-    const int blocks = (a.M + 3) / 4;
-    const int cap = XREG_BPC * device_cu_count();
-    return 4 * (blocks < cap ? blocks : cap);
+    const N1Shape sh = n1_shape(a.fmt, a.M, a.K, a.epi);
+    return 4 * n1_blocks(a.M, a.K, sh.rows, sh.bpc);
 }
 
 int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
@@ -549,38 +427,16 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     const bool fast = (align & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
                       (size_t)a.K * 4 <= 160 * 1024;
     if (fast) {
-        const int chunks = a.K / elem_per_chunk(a.fmt);
-        const uint64_t wbytes = (uint64_t)a.M * chunks * 16;
-        const bool pow2_cpb = (a.cpb & (a.cpb - 1)) == 0;
-        const bool xreg_ok = chunks <= 64 * (64 / elem_per_chunk(a.fmt) < 8 ? 64 / elem_per_chunk(a.fmt) : 8) &&
-                             wbytes < (1ull << 31) && a.epi != EPI_SILU_MUL &&
-                             (a.fmt != WF_I4 || (a.bpr > 0 && pow2_cpb &&
-                                                 (uint64_t)a.M * a.bpr * 4 < (1ull << 31)));
-        if (xreg_ok) {
-            const int need = (chunks + 63) / 64;
-            const int cpl = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
-            switch (a.fmt) {
-            case WF_F32:  return dispatch_xreg<WF_F32>(a, st, cpl, XREG_BPC);
-            case WF_BF16: return dispatch_xreg<WF_BF16>(a, st, cpl, XREG_BPC);
-            case WF_I8:   return dispatch_xreg<WF_I8>(a, st, cpl, 2);
-            case WF_I4:   return dispatch_xreg<WF_I4>(a, st, cpl, 2);
-            }
-        }
-        ATLAS_REQUIRE(a.epi != EPI_ARGMAX, "gemv: argmax epilogue needs K <= 4096 shapes");
-        if (a.epi == EPI_SILU_MUL) {
-            switch (a.fmt) {
-            case WF_F32:  return launch_n1<WF_F32, 2, 4>(a, st, 8);
-            case WF_BF16: return launch_n1<WF_BF16, 2, 4>(a, st, 8);
-            case WF_I8:   return launch_n1<WF_I8, 2, 4>(a, st, 8);
-            case WF_I4:   return launch_n1<WF_I4, 2, 2>(a, st, 8);
-            }
-        }
-        switch (a.fmt) {
-        case WF_F32:  return launch_n1<WF_F32, 1, 4>(a, st, 8);
-        case WF_BF16: return launch_n1<WF_BF16, 1, 8>(a, st, 2);
-        case WF_I8:   return launch_n1<WF_I8, 1, 8>(a, st, 16);
-        case WF_I4:   return launch_n1<WF_I4, 2, 2>(a, st, 8);
-        }
+        const N1Shape sh = n1_shape(a.fmt, a.M, a.K, a.epi);
+#define ATLAS_N1(F, R, U) \
+        if (a.fmt == F && sh.rows == R && sh.unroll == U) return launch_n1<F, R, U>(a, st, sh.bpc);
+        ATLAS_N1(WF_BF16, 1, 4) ATLAS_N1(WF_BF16, 1, 8) ATLAS_N1(WF_BF16, 2, 4)
+        ATLAS_N1(WF_I8, 1, 2) ATLAS_N1(WF_I8, 1, 4) ATLAS_N1(WF_I8, 1, 8) ATLAS_N1(WF_I8, 2, 2)
+        ATLAS_N1(WF_I4, 1, 2) ATLAS_N1(WF_I4, 2, 2)
+        ATLAS_N1(WF_F32, 1, 4) ATLAS_N1(WF_F32, 2, 4)
+#undef ATLAS_N1
+        set_error(ATLAS_EUNSUPPORTED, "gemv: no kernel for format %d", a.fmt);
+        return ATLAS_EUNSUPPORTED;
     }
     ATLAS_REQUIRE(a.epi == EPI_STORE && a.pro == PRO_X,
                   "gemv: fused prologue/epilogue needs an aligned fast-path shape");

@@ -29,6 +29,10 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of each bf16 decode GEMV kernel: rocprofv3 FETCH_SIZE x 2
+# + WRITE_SIZE x 1 (the factors a 1 GiB copy reads on this part), measured by
+# `bench.py --pmc-probe` (profiles/gemv_bf16_7b_hbm_traffic.md).
+TRAFFIC = {"gate_up": 180961176, "qkv_wo_lm_head": 79142423, "w_down": 90677966}
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
@@ -207,6 +211,9 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="fewer microbenchmark iterations")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="short program for rocprofv3 --pmc passes: a 1 GiB device copy "
+                         "(calibration), then one launch set of each bf16 decode GEMV kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -226,6 +233,8 @@ def main() -> int:
     lib.atlas_set_stream(C.c_void_p(torch.cuda.current_stream().cuda_stream))
     rng = np.random.default_rng(2026)
     prompt = rng.integers(0, 100278, 128)
+    if args.pmc_probe:
+        return pmc_probe(torch, lib, am)
 
     micro = {}
     attn = {}
@@ -241,8 +250,9 @@ def main() -> int:
     log(f"bf16 decode: {ms_step:.3f} ms/token, {tok_s:.1f} tok/s, "
         f"weights {wbytes / 1e9:.2f} GB -> {wbytes / (ms_step * 1e-3) / 1e9:.0f} GB/s")
 
-    # dominant kernel: the register-x bf16 GEMV (QKV, W_o, gate/up, lm_head:
-    # 79% of the step's weight bytes); W_down runs the LDS-staged kernel
+    # The step's bf16 GEMVs run as three kernel instances; the roofline is
+    # reported for the one that takes the most time per step (gate/up: 42% of
+    # the weight bytes), the other two beside it.
     def gemv_set(which, iters=8):
         ms, launches, nbytes = C.c_float(), C.c_int(), C.c_int64()
         assert lib.atlas_model_bench_gemv(m._h, 1, which, C.byref(ms), C.byref(launches),
@@ -253,16 +263,25 @@ def main() -> int:
         per_launch_bytes = nbytes.value / (launches.value / iters)
         return (per_launch_ms, per_launch_bytes, ms.value / iters, launches.value // iters)
 
-    k_ms, k_bytes, k_step_ms, k_n = gemv_set(1)
-    d_ms, d_bytes, d_step_ms, d_n = gemv_set(2)
-    gemv_gbs = k_bytes / (k_ms * 1e-3) / 1e9
-    down_gbs = d_bytes / (d_ms * 1e-3) / 1e9
-    step_gemv_ms = k_step_ms + d_step_ms
-    per_launch_ms, per_launch_bytes = k_ms, k_bytes
-    all_gbs = (k_bytes * k_n + d_bytes * d_n) / (step_gemv_ms * 1e-3) / 1e9
-    log(f"decode GEMVs (K=4096 kernel): {k_n} launches/step, {k_step_ms:.3f} ms, "
-        f"{gemv_gbs:.0f} GB/s ({gemv_gbs / HBM_PEAK_GBS:.1%}); W_down: {d_n} launches, "
-        f"{d_step_ms:.3f} ms, {down_gbs:.0f} GB/s; all GEMVs {all_gbs:.0f} GB/s")
+    kernels = {}
+    for which, name, kern in (
+            (3, "gate_up", "gemv_n1_kernel<bf16, rows 2, unroll 4> (RMSNorm+residual prologue, "
+                           "SwiGLU epilogue)"),
+            (1, "qkv_wo_lm_head", "gemv_n1_kernel<bf16, rows 1, unroll 4> (RMSNorm prologues)"),
+            (2, "w_down", "gemv_n1_kernel<bf16, rows 1, unroll 8>")):
+        per_ms, per_bytes, step_ms, n = gemv_set(which)
+        gbs = per_bytes / (per_ms * 1e-3) / 1e9
+        kernels[name] = {"kernel": kern, "launches_per_step": n, "ms_per_step": round(step_ms, 4),
+                         "traffic": TRAFFIC.get(name),
+                         "bytes_per_launch": int(per_bytes), "us_per_launch": round(per_ms * 1e3, 3),
+                         "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"decode GEMVs {name}: {n} launches/step, {step_ms:.3f} ms, {per_ms * 1e3:.2f} us and "
+            f"{per_bytes / 1e6:.2f} MB per launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+    step_gemv_ms = sum(k["ms_per_step"] for k in kernels.values())
+    all_gbs = sum(k["bytes_per_launch"] * k["launches_per_step"] for k in kernels.values()) / (
+        step_gemv_ms * 1e-3) / 1e9
+    dom = max(kernels.values(), key=lambda k: k["ms_per_step"])
+    log(f"decode GEMVs: {step_gemv_ms:.3f} ms/step, {all_gbs:.0f} GB/s")
 
     # roofline share of the whole step: weights + KV at 8 TB/s vs measured
     ctx_mid = len(prompt) + args.warmup + args.steps // 2
@@ -305,18 +324,17 @@ def main() -> int:
                                "(BASELINE.json configs[4])",
                    "global_batch": 1, "seq_len": len(prompt) + args.warmup + args.steps,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_xreg_kernel<bf16,8>: QKV, W_o, gate/up, lm_head GEMVs "
-                               "of one decode step (fused-prologue launches)",
-                     "bytes_per_launch": int(per_launch_bytes),
-                     "us_per_launch": round(per_launch_ms * 1e3, 3)},
+        "roofline": {"bound": "hbm", "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": dom["frac"], "traffic": dom["traffic"],
+                     "kernel": dom["kernel"],
+                     "bytes_per_launch": dom["bytes_per_launch"],
+                     "us_per_launch": dom["us_per_launch"]},
+        "gemv_kernels": kernels,
         "step_roofline": {"bytes_per_step": int(step_bytes),
                           "floor_ms": round(step_floor_ms, 4),
                           "frac_of_step_at_roofline": round(step_floor_ms / ms_step, 4),
                           "gemv_ms_per_step": round(step_gemv_ms, 4),
-                          "gemv_all_GB_s": round(all_gbs, 1),
-                          "w_down_GB_s": round(down_gbs, 1)},
+                          "gemv_all_GB_s": round(all_gbs, 1)},
         "int8": {"tok_s": round(tok_s8, 2), "ms_per_step": round(dt8 * 1e3 / args.steps, 4)},
         "gemv_microbench": micro,
         "attention_microbench": attn,
@@ -325,6 +343,33 @@ def main() -> int:
     if cpu:
         res["cpu_baseline"] = cpu
     print(json.dumps(res), flush=True)
+    return 0
+
+
+def pmc_probe(torch, lib, am) -> int:
+    """Dispatches whose HBM counters calibrate and measure `traffic`: three
+    copies of 1 GiB (2 GiB moved each: FETCH_SIZE and WRITE_SIZE of a plain
+    copy of known size), then the bf16 7B model's GEMV sets (bench_gemv which
+    = 3, 1, 2), one launch each."""
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc probe: copy of {n * 4} bytes x3 done")
+    del src, dst
+    m = am.OlmoModel(am.ModelConfig.olmo3_actual_7b(), weight_format=am.W_BF16, int4_block=32)
+    m.init_random(7)
+    m.reset()
+    m.forward_one(1)
+    ms, launches, nbytes = C.c_float(), C.c_int(), C.c_int64()
+    for which in (3, 1, 2):
+        assert lib.atlas_model_bench_gemv(m._h, 1, which, C.byref(ms), C.byref(launches),
+                                          C.byref(nbytes)) == 0
+        log(f"pmc probe: GEMV set {which}: {launches.value} launches, {nbytes.value} "
+            f"algorithmic bytes, {ms.value:.3f} ms")
+    m.close()
     return 0
 
 

@@ -139,10 +139,10 @@ int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, int n_steps,
 /* Benchmark helper: enqueue `iters` copies of the weight GEMV launches of one
  * decode step (same kernels, shapes, prologues and weights; activations from
  * the engine's scratch) and time them with HIP events on the engine stream.
- * which: 0 = all of them, 1 = the K = d_model GEMVs (QKV, W_o, gate/up,
- * lm_head: one kernel), 2 = the W_down GEMVs.  *ms = elapsed milliseconds,
- * *launches = GEMV launches issued, *bytes = algorithmic bytes of one copy
- * (weights + scales + x + y).                                                */
+ * which: 0 = all of them, 1 = QKV, W_o and lm_head, 2 = W_down, 3 = gate/up
+ * (for bf16 weights each of 1-3 is one kernel instance).  *ms = elapsed
+ * milliseconds, *launches = GEMV launches issued, *bytes = algorithmic bytes
+ * of one copy (weights + scales + x + y).                                    */
 int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float* ms, int* launches,
                            int64_t* bytes);
 /* 1 = capture the decode step in a HIP graph (default), 0 = plain launches */

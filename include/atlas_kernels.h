@@ -186,11 +186,14 @@ int atlas_qkv_post_f32(float* qkv, const float* q_norm, const float* k_norm, flo
  * pos, split-K GQA attention over [max(0, pos - window + 1), pos] and the
  * split merge, in one launch (atlas_qkv_post_f32 + atlas_decode_attention
  * semantics).  head_dim 64/128/256, n_heads / n_kv in {1, 2, 4, 8}.
- * n_splits <= 0 picks a split count for the context.                        */
+ * n_splits <= 0 picks a split count for the context.  min_chunk > 0 makes
+ * n_splits a maximum: the kernel uses min(n_splits, ceil(ctx / min_chunk))
+ * splits for the live context length ctx (as a captured decode step does).  */
 int atlas_attention_fused_f32(const float* qkv, const float* q_norm, const float* k_norm,
                               float qk_eps, const float* cos_tab, const float* sin_tab,
                               float* k_cache, float* v_cache, float* out, int n_heads, int n_kv,
-                              int head_dim, int pos, float scale, int window, int n_splits);
+                              int head_dim, int pos, float scale, int window, int n_splits,
+                              int min_chunk);
 
 /* Greedy choice: index of the last maximum of x[0..n) as u32 (device).      */
 int atlas_argmax_u32(const float* x, int n, uint32_t* out_idx);

@@ -393,13 +393,17 @@ def test_gemv_fused_prologues(orc, fmt, M, K):
     assert rel_err(out.get(), orc.linear(view, xs, threads=8)) <= GEMV_TOL
 
 
-@pytest.mark.parametrize("H,KVH,hd,ctx,window,splits", [
-    (32, 8, 128, 512, 0, 0), (32, 8, 128, 4096, 0, 0), (32, 8, 128, 16384, 0, 0),
-    (32, 8, 128, 16384, 4096, 0), (32, 8, 128, 1, 0, 0), (32, 8, 128, 300, 64, 7),
-    (32, 32, 128, 200, 0, 4), (8, 8, 64, 77, 0, 3), (4, 1, 64, 50, 16, 1), (8, 2, 256, 90, 0, 5),
-    (16, 2, 128, 1000, 0, 64)])
-def test_attention_fused(orc, H, KVH, hd, ctx, window, splits):
-    print(f"attention_fused H={H} KVH={KVH} hd={hd} ctx={ctx} w={window} s={splits}", flush=True)
+@pytest.mark.parametrize("H,KVH,hd,ctx,window,splits,chunk", [
+    (32, 8, 128, 512, 0, 0, 0), (32, 8, 128, 4096, 0, 0, 0), (32, 8, 128, 16384, 0, 0, 0),
+    (32, 8, 128, 16384, 4096, 0, 0), (32, 8, 128, 1, 0, 0, 0), (32, 8, 128, 300, 64, 7, 0),
+    (32, 32, 128, 200, 0, 4, 0), (8, 8, 64, 77, 0, 3, 0), (4, 1, 64, 50, 16, 1, 0),
+    (8, 2, 256, 90, 0, 5, 0), (16, 2, 128, 1000, 0, 64, 0),
+    # min_chunk: fewer active splits than the grid holds
+    (32, 8, 128, 4096, 0, 64, 1024), (32, 32, 128, 200, 0, 16, 64), (32, 8, 128, 1, 0, 16, 256),
+    (32, 32, 128, 700, 0, 16, 256), (8, 2, 256, 3000, 1000, 8, 300), (8, 8, 64, 129, 0, 4, 64)])
+def test_attention_fused(orc, H, KVH, hd, ctx, window, splits, chunk):
+    print(f"attention_fused H={H} KVH={KVH} hd={hd} ctx={ctx} w={window} s={splits} c={chunk}",
+          flush=True)
     rng = np.random.default_rng(ctx * 7 + hd)
     max_seq = ctx + 2
     yarn = dict(factor=8.0, orig_max_pos=8192, attn_factor=1.2079441541679836,
@@ -428,7 +432,7 @@ def test_attention_fused(orc, H, KVH, hd, ctx, window, splits):
     for rep in range(2):          # a second launch reuses the merge counters
         assert lib().atlas_attention_fused_f32(d_qkv.ptr, dqn.ptr, dkn.ptr, 1e-6, dc.ptr, ds.ptr,
                                                dk.ptr, dv.ptr, do.ptr, H, KVH, hd, pos, scale,
-                                               window, splits) == 0
+                                               window, splits, chunk) == 0
         assert rel_err(do.get(), ref) <= ATTN_TOL, rep
     assert np.max(np.abs(dk.get()[pos] - Kr[pos])) <= 1e-5 * np.max(np.abs(k))
     assert np.array_equal(dv.get()[pos], Vr[pos])
