@@ -95,8 +95,6 @@ struct atlas_model {
     float* attn_part = nullptr;
     int* attn_counters = nullptr;
     bool fused = false;
-    // fused step: SwiGLU in the gate/up epilogue (true) or in W_down's prologue
-    bool silu_epi = true;
     int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
     uint32_t *tok_dev = nullptr, *hist = nullptr, *suppress_dev = nullptr, *choice_dev = nullptr;
     int suppress_cap = 0;
@@ -277,18 +275,16 @@ GemvArgs pro_args(const DevMat& w, const float* x, float* y, int pro, const floa
 }
 
 // GU of the fused step: x'_l = x_l + rmsnorm(y1) * attn_norm_l materialised
-// into xb, then h = silu(gate) * up (silu_epi) or the raw (gate, up) pairs.
+// into xb, then h = silu(gate) * up in the epilogue.
 int enqueue_gu_fused(atlas_model* m, const LayerW& L) {
     GemvArgs gu = pro_args(L.gu, m->x, m->h, PRO_RESNORM, m->y, L.attn_norm, m->cfg.rms_eps, m->xb);
-    if (m->silu_epi) gu.epi = EPI_SILU_MUL;
+    gu.epi = EPI_SILU_MUL;
     return gemv_launch(gu, m->st);
 }
 
-// DOWN of the fused step: y2 = W_down h, or W_down (silu(gate) * up) with the
-// SwiGLU applied while staging the pairs when the epilogue did not.
+// DOWN of the fused step: y2 = W_down h.
 int enqueue_down_fused(atlas_model* m, const LayerW& L) {
-    if (m->silu_epi) return gemv(m, L.down, m->h, m->y2, EPI_STORE);
-    return gemv_launch(pro_args(L.down, nullptr, m->y2, PRO_SILU, m->h, nullptr, 0.f, nullptr), m->st);
+    return gemv(m, L.down, m->h, m->y2, EPI_STORE);
 }
 
 // The post-norm decode step with the norms folded into the GEMV prologues
@@ -298,7 +294,6 @@ int enqueue_down_fused(atlas_model* m, const LayerW& L) {
 //   WO     y1 = W_o att
 //   GU     x'_l = x_l + rmsnorm(y1) * attn_norm_l;  h = silu(gate) * up
 //   DOWN   y2 = W_down h
-// (int8 moves the SwiGLU from GU's epilogue into DOWN's prologue).
 // x_l lives in m->x, x'_l in m->xb.
 int enqueue_step_fused(atlas_model* m, int mode) {
     const atlas_model_config& c = m->cfg;
@@ -874,10 +869,6 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->fused = c.post_norm && attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
                attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && d % 32 == 0 &&
                c.ffn_hidden % 32 == 0;
-    // the two-row int8 GEMV (a wave owns a (gate, up) pair) needs ~170 VGPRs
-    // and runs at half the one-row variant's rate: int8 stores gate/up and
-    // applies SwiGLU while staging W_down's input instead
-    m->silu_epi = c.weight_format != ATLAS_W_INT8;
     if (dalloc(m, (void**)&m->attn_part,
                (size_t)B * c.n_heads * m->attn_splits * (hd + 2) * 4) ||
         dalloc(m, (void**)&m->attn_counters, (size_t)B * c.n_kv_heads * 4))
@@ -1252,7 +1243,6 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
     };
     const bool k_set = which == 0 || which == 1, down_set = which == 0 || which == 2,
                gu_set = which == 0 || which == 3;
-    const bool silu_in_gu = !m->fused || m->silu_epi;
     int64_t b = 0;
     int n = 0;
     for (const auto& L : m->L) {
@@ -1261,12 +1251,11 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
             n += 2;
         }
         if (gu_set) {
-            b += mat_bytes(L.gu, silu_in_gu ? L.gu.rows / 2 : L.gu.rows);
+            b += mat_bytes(L.gu, L.gu.rows / 2);
             n += 1;
         }
         if (down_set) {
-            // the SwiGLU prologue reads both halves of each (gate, up) pair
-            b += mat_bytes(L.down, L.down.rows) + (silu_in_gu ? 0 : (int64_t)L.down.cols * 4);
+            b += mat_bytes(L.down, L.down.rows);
             n += 1;
         }
     }

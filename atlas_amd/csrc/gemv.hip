@@ -20,6 +20,8 @@
 //    int4 uses the byte trick (byte & 0xF0) == 16*q_even and
 //    ((byte << 4) & 0xF0) == 16*q_odd, with 1/16 folded into the block scale;
 //  * wave reduction with DPP (row swaps, mirrors, row broadcasts).
+#include <mutex>
+
 #include "common.hpp"
 #include "gemv.hpp"
 
@@ -96,8 +98,65 @@ __device__ __forceinline__ float block_sum256(float v, float* red4) {
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
+// Every global read of the staging is issued before the first use, so a
+// norm prologue costs one round trip, not two (sum of squares, then x, w):
+// a thread owns the 16-byte pieces p = tid + 256 j, j < PPT, in registers.
+template <bool SWZ, int PPT>
+__device__ __forceinline__ void stage_x_regs(const GemvArgs& a, f32x4* xs, int K) {
+    __shared__ float red4[4];
+    const int np = K >> 2;
+    const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
+    const f32x4* yin = reinterpret_cast<const f32x4*>(a.pro_y);
+    const f32x4* win = reinterpret_cast<const f32x4*>(a.pro_w);
+    const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
+    f32x4 xv[PPT], yv[PPT], wv[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+        const int p = threadIdx.x + 256 * j;
+        if (p < np) {
+            xv[j] = xin[p];
+            if (res) yv[j] = yin[p];
+            if (norm) wv[j] = win[p];
+        }
+    }
+    float inv = 1.0f;
+    if (norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) {
+            if (threadIdx.x + 256 * j < np) {
+                const f32x4 t = res ? yv[j] : xv[j];
+                ss += t.x * t.x;
+                ss += t.y * t.y;
+                ss += t.z * t.z;
+                ss += t.w * t.w;
+            }
+        }
+        ss = block_sum256(ss, red4);
+        inv = 1.0f / sqrtf(ss / (float)K + a.pro_eps);
+    }
+    const bool write_out = a.pro_out && blockIdx.x == 0 && norm;
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+        const int p = threadIdx.x + 256 * j;
+        if (p < np) {
+            f32x4 r;
+            if (res) r = xv[j] + (yv[j] * inv) * wv[j];
+            else if (norm) r = (xv[j] * inv) * wv[j];
+            else r = xv[j];
+            xs[SWZ ? swz(p) : p] = r;
+            if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = r;
+        }
+    }
+}
+
+// General staging: any K the LDS holds, and the SwiGLU prologue.
 template <bool SWZ>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, f32x4* xs, int K) {
+    if (a.pro != PRO_SILU && K <= 256 * 4 * 4) {    // d_model <= 4096: 48 VGPRs
+        stage_x_regs<SWZ, 4>(a, xs, K);
+        return;
+    }
     __shared__ float red4[4];
     const int np = K >> 2;
     const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
@@ -157,17 +216,25 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
     const int wave = threadIdx.x >> 6;
     const int chunks = K / EPC;                   // 16-byte chunks per row
     const u32x4* W = reinterpret_cast<const u32x4*>(a.w);
-    const int n_groups = (M + ROWS - 1) / ROWS;
+    // One-row waves with the SwiGLU epilogue take a (gate, up) row pair one
+    // row after the other (SEQ = 2): the pair's epilogue stays in the wave
+    // without the registers of a two-row wave.
+    const int SEQ = (ROWS == 1 && a.epi == EPI_SILU_MUL) ? 2 : 1;
+    const int n_groups = ((M + ROWS - 1) / ROWS + SEQ - 1) / SEQ;
     // persistent waves: wave w of the grid takes row groups w, w + S, ...
     const int S = gridDim.x * 4;
     const int g0 = blockIdx.x * 4 + wave;
     const int iters = (chunks + STEP - 1) / STEP;
     const int my_groups = g0 < n_groups ? (n_groups - 1 - g0) / S + 1 : 0;
-    const int total = my_groups * iters;          // (group, k-slice) steps of this wave
+    const int total = my_groups * SEQ * iters;    // (group, row, k-slice) steps of this wave
+    // first row of step `it`
+    auto row_of = [&](int it) {
+        return ((g0 + (it / (iters * SEQ)) * S) * SEQ + (it / iters) % SEQ) * ROWS;
+    };
 
     // weights (and int4 block scales) of step `it` into registers
     auto load = [&](int it, u32x4 (&wb)[UNROLL][ROWS], float (&sb)[UNROLL][ROWS]) {
-        const int g = g0 + (it / iters) * S;
+        const int g = row_of(it) / ROWS;
         const int c0 = lane + (it % iters) * STEP;
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
@@ -198,6 +265,7 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
     unsigned long long best = 0;          // EPI_ARGMAX: best (logit, row) of this wave
+    float gate = 0.0f;                    // SEQ == 2: the pair's gate row
 
     for (int it = 0; it < total; ++it) {
         u32x4 nxt[UNROLL][ROWS];
@@ -220,7 +288,7 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
         }
         if (ks == iters - 1) {
             // end of this row group: reduce across the wave and store
-            const int r0 = (g0 + (it / iters) * S) * ROWS;
+            const int r0 = row_of(it);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
             if constexpr (FMT == WF_I8) {
@@ -234,6 +302,9 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
                     for (int r = 0; r < ROWS; r += 2)
                         if (lane == r && r0 + r + 1 < M)
                             a.y[(r0 + r) >> 1] = silu_f(acc[r]) * acc[r + 1];
+                } else if (ROWS == 1) {
+                    if ((r0 & 1) == 0) gate = acc[0];
+                    else if (lane == 0 && r0 < M) a.y[r0 >> 1] = silu_f(gate) * acc[0];
                 }
             } else {
 #pragma unroll
@@ -336,34 +407,65 @@ int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m,
 
 // ---------------------------------------------------------------------------
 
-// persistent grid of the LDS-staged kernel: LDS bounds the resident blocks
-// per CU, so never ask for more than fit
-static int n1_blocks(int M, int K, int rows, int blocks_per_cu) {
+// Allow `kern` up to 160 KB of dynamic LDS (once per kernel) and return the
+// blocks of it (256 threads, `lds` dynamic LDS bytes) one CU holds at once;
+// cached per (kernel, LDS size).
+static int resident_per_cu(const void* kern, size_t lds) {
+    struct Entry { const void* k; size_t lds; int n; };
+    static std::mutex mu;
+    static Entry cache[64];
+    static int used = 0;
+    static const void* raised[32];
+    static int n_raised = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+        if (cache[i].k == kern && cache[i].lds == lds) return cache[i].n;
+    if (lds > 64 * 1024) {
+        bool done = false;
+        for (int i = 0; i < n_raised; ++i) done = done || raised[i] == kern;
+        if (!done) {
+            if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    160 * 1024) != hipSuccess) {
+                (void)hipGetLastError();
+                return 0;
+            }
+            if (n_raised < 32) raised[n_raised++] = kern;
+        }
+    }
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    if (used < 64) cache[used++] = Entry{kern, lds, n};
+    return n;
+}
+
+// Persistent grid of the LDS-staged kernel: every block resident at once
+// (LDS and register occupancy bound the blocks per CU), at most
+// blocks_per_cu of them per CU.  0 if the kernel cannot run at this K.
+static int n1_blocks(const void* kern, int M, int K, int rows, int blocks_per_cu) {
     const int n_groups = (M + rows - 1) / rows;
-    int blocks = (n_groups + 3) / 4;
-    const size_t lds = (size_t)K * 4;
-    int fit = (int)((160 * 1024) / (lds ? lds : 1));
-    if (fit < 1) fit = 1;
+    const int blocks = (n_groups + 3) / 4;
+    const int fit = resident_per_cu(kern, (size_t)K * 4);
+    if (fit < 1) return 0;
     const int bpc = blocks_per_cu < fit ? blocks_per_cu : fit;
     const int cap = bpc * device_cu_count();
     return blocks > cap ? cap : blocks;
 }
 
+// rows one wave's group covers (the kernel's SEQ rule)
+static int n1_group_rows(const GemvArgs& a, int rows) {
+    return (rows == 1 && a.epi == EPI_SILU_MUL) ? 2 : rows;
+}
+
 template <int FMT, int ROWS, int UNROLL>
 int launch_n1(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
     const size_t lds = (size_t)a.K * 4;
+    ATLAS_REQUIRE(lds <= 160 * 1024, "gemv: K=%d exceeds the LDS-staged limit 40960", a.K);
     auto kern = gemv_n1_kernel<FMT, ROWS, UNROLL>;
-    if (lds > 64 * 1024) {
-        ATLAS_REQUIRE(lds <= 160 * 1024, "gemv: K=%d exceeds the LDS-staged limit 40960", a.K);
-        static bool raised = false;
-        if (!raised) {
-            ATLAS_HIP(hipFuncSetAttribute((const void*)kern,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          160 * 1024));
-            raised = true;
-        }
-    }
-    const int blocks = n1_blocks(a.M, a.K, ROWS, blocks_per_cu);
+    const int blocks = n1_blocks((const void*)kern, a.M, a.K, n1_group_rows(a, ROWS), blocks_per_cu);
+    ATLAS_REQUIRE(blocks > 0, "gemv: the kernel does not fit a CU at K=%d", a.K);
     if (a.epi == EPI_ARGMAX)
         ATLAS_REQUIRE(blocks * 4 <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a);
@@ -386,7 +488,10 @@ int gemv_fast_ok(int fmt, int K, int block) {
 // rotating weights (rows = 1 wins: more waves in flight per CU).
 struct N1Shape { int rows, unroll, bpc; };
 static N1Shape n1_shape(int fmt, int M, int K, int epi) {
-    if (epi == EPI_SILU_MUL) return {2, fmt == WF_BF16 ? 4 : 2, 8};
+    // SwiGLU epilogue: bf16 two-row waves; int8/int4 one-row waves taking
+    // the pair in sequence (their two-row variants need ~100-170 VGPRs)
+    if (epi == EPI_SILU_MUL)
+        return fmt == WF_BF16 ? N1Shape{2, 4, 8} : fmt == WF_I8 ? N1Shape{1, 4, 8} : N1Shape{1, 2, 8};
     const bool big_k = K > 4096;
     switch (fmt) {
     case WF_BF16: return big_k ? N1Shape{1, 8, 2} : N1Shape{1, 4, 8};
@@ -396,10 +501,26 @@ static N1Shape n1_shape(int fmt, int M, int K, int epi) {
     }
 }
 
+// The instantiations gemv_launch dispatches to.
+#define ATLAS_N1_LIST(X)                                                           \
+    X(WF_BF16, 1, 4) X(WF_BF16, 1, 8) X(WF_BF16, 2, 4)                             \
+    X(WF_I8, 1, 2) X(WF_I8, 1, 4) X(WF_I8, 1, 8)                    \
+    X(WF_I4, 1, 2) X(WF_I4, 2, 2)                                                  \
+    X(WF_F32, 1, 4) X(WF_F32, 2, 4)
+
+static const void* n1_kernel(int fmt, int rows, int unroll) {
+#define ATLAS_N1_PTR(F, R, U) \
+    if (fmt == F && rows == R && unroll == U) return (const void*)gemv_n1_kernel<F, R, U>;
+    ATLAS_N1_LIST(ATLAS_N1_PTR)
+#undef ATLAS_N1_PTR
+    return nullptr;
+}
+
 // number of persistent waves gemv_launch uses (argmax partial count)
 int gemv_waves(const GemvArgs& a) {
     const N1Shape sh = n1_shape(a.fmt, a.M, a.K, a.epi);
-    return 4 * n1_blocks(a.M, a.K, sh.rows, sh.bpc);
+    const void* kern = n1_kernel(a.fmt, sh.rows, sh.unroll);
+    return kern ? 4 * n1_blocks(kern, a.M, a.K, n1_group_rows(a, sh.rows), sh.bpc) : 0;
 }
 
 int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
@@ -430,10 +551,7 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
         const N1Shape sh = n1_shape(a.fmt, a.M, a.K, a.epi);
 #define ATLAS_N1(F, R, U) \
         if (a.fmt == F && sh.rows == R && sh.unroll == U) return launch_n1<F, R, U>(a, st, sh.bpc);
-        ATLAS_N1(WF_BF16, 1, 4) ATLAS_N1(WF_BF16, 1, 8) ATLAS_N1(WF_BF16, 2, 4)
-        ATLAS_N1(WF_I8, 1, 2) ATLAS_N1(WF_I8, 1, 4) ATLAS_N1(WF_I8, 1, 8) ATLAS_N1(WF_I8, 2, 2)
-        ATLAS_N1(WF_I4, 1, 2) ATLAS_N1(WF_I4, 2, 2)
-        ATLAS_N1(WF_F32, 1, 4) ATLAS_N1(WF_F32, 2, 4)
+        ATLAS_N1_LIST(ATLAS_N1)
 #undef ATLAS_N1
         set_error(ATLAS_EUNSUPPORTED, "gemv: no kernel for format %d", a.fmt);
         return ATLAS_EUNSUPPORTED;
