@@ -5,23 +5,27 @@
 // together the weights are still read once, and the N products per weight
 // go to the matrix cores: v_mfma_f32_16x16x32_bf16.
 //
-// Layout (per wave, per MFMA):
-//  * A operand = activations: lane (i = lane % 16, g = lane / 16) supplies 8
-//    values of activation column i for its k-set; column i = 2*s + part holds
-//    sequence s split into a bf16 "hi" (truncation) and "lo" (RNE of the
-//    exact remainder) part, so hi + lo carries 16 significant bits and the
-//    f32-accumulated product matches an f32 GEMV to ~2^-16;
-//  * B operand = weights: lane (r = lane % 16, g) supplies 8 values of weight
-//    row r (bf16 as stored; int8/int4 sign-extended to f32 by SDWA converts
-//    and truncated to bf16, which is exact for |16*q| <= 128);
-//  * D: lane (r, g) holds D[4g + v][r] -> rows of the output for sequences
-//    2g and 2g + 1, so every lane owns one weight row and a per-row or
-//    per-(row, block) scale is a single value per lane.
-//  * int4: one MFMA covers exactly one 32-element chunk of one row (lane
-//    group g takes the chunk's 4-byte word g), so the block scale applies to
-//    the MFMA result.
-//  * split-K across blocks writes fp32 partials; a second kernel sums them in
-//    a fixed order (deterministic) and applies the epilogue.
+// MFMA operands (lane = 16 g + i, g = lane / 16):
+//  * A = activations: lane (g, i) supplies k = 8g..8g+7 of a 32-k tile for
+//    A-row i = 2s + part: sequence s split into a bf16 "hi" (truncation) and
+//    "lo" (RNE of the exact remainder) part, so hi + lo carries 16
+//    significant bits and the f32-accumulated product matches an f32 GEMV
+//    to ~2^-16.  Rows i >= 2N are zero.
+//  * B = weights: lane (g, n) supplies the same 8 k of weight row n, as
+//    stored (bf16) or dequantised exactly to bf16 (int8 q and int4 16*q have
+//    at most 8 significant bits).  An int4 tile is one 32-element scale
+//    block of each row, so the block scale applies to the tile's product.
+//  * D: lane (g, n) holds D[4g + v][n]: sequences 2g, 2g+1 of row n.
+//
+// Work split: a 1024-thread block (16 waves) owns a K-slice of at most 128
+// tiles (4096 k); wave w owns a fixed run of <= 8 of its tiles and keeps
+// their A operands in registers, converted once.  The block walks 16-row
+// weight tiles (persistent over the grid) with the next tile's weights in
+// flight; the 16 waves' partial D meet in LDS (double-buffered, one barrier
+// per tile) and 128 threads apply the epilogue.  K > 4096 splits K across
+// blocks into fp32 partials summed by skinny_reduce_kernel in a fixed order.
+#include <type_traits>
+
 #include "common.hpp"
 #include "gemv.hpp"
 
@@ -29,167 +33,408 @@ namespace atlas {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+constexpr int SK_WAVES = 16;        // waves per block
+constexpr int SK_KTW = 8;           // max 32-k tiles per wave
+constexpr int SK_KT_BLOCK = SK_WAVES * SK_KTW;
+
 __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// bf16 bits (low 16) of the hi (part 0) or lo (part 1) component of v
-__device__ __forceinline__ uint32_t split_part(float v, int part) {
+// bf16 bits (low 16) of the hi (part 0) or lo (part 1) component of v;
+// branch-free (part differs between neighbouring lanes)
+__device__ __forceinline__ uint32_t split_part(float v, bool lo) {
     const uint32_t u = __float_as_uint(v);
-    if (part == 0) return u >> 16;
     const float hi = __uint_as_float(u & 0xFFFF0000u);
-    return bf16_rne_bits(v - hi);
+    const uint32_t lb = bf16_rne_bits(v - hi);
+    return lo ? lb : (u >> 16);
 }
 
 __device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) {
     return (lo16 & 0xFFFFu) | (hi16 << 16);
 }
 
-// exact f32 -> bf16 bits for values with <= 8 significant bits
+// two f32 with <= 8 significant bits -> packed bf16 pair (a low), exact
 __device__ __forceinline__ uint32_t pack_f32_pair(float a, float b) {
-    return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xFFFF0000u);
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
 }
 
-template <int FMT> struct SK;
-template <> struct SK<WF_BF16> { static constexpr int SEG = 32;  static constexpr int MF = 1; };
-template <> struct SK<WF_I8>   { static constexpr int SEG = 64;  static constexpr int MF = 2; };
-template <> struct SK<WF_I4>   { static constexpr int SEG = 128; static constexpr int MF = 4; };
+// one lane's weights of one 32-k tile
+template <int FMT> struct SkFrag;
+template <> struct SkFrag<WF_BF16> { u32x4 w; };
+template <> struct SkFrag<WF_I8>   { uint32_t w0, w1; };
+template <> struct SkFrag<WF_I4>   { uint32_t w; float s; };
 
-// k offset (within a segment) of lane group g's 8 values for MFMA m
+// A weight row's base addresses (data, and int4 block scales; K % block == 0
+// so every row starts a block).
+struct SkRow { const uint8_t* w; const float* s; };
+
 template <int FMT>
-__device__ __forceinline__ int kset(int g, int m) {
-    if constexpr (FMT == WF_BF16) return 8 * g;
-    else if constexpr (FMT == WF_I8) return 16 * g + 8 * m;
-    else return 32 * m + 8 * g;
+__device__ __forceinline__ SkRow sk_row(const GemvArgs& a, int row) {
+    SkRow r;
+    constexpr int NUM = FMT == WF_BF16 ? 2 : 1, DEN = FMT == WF_I4 ? 2 : 1;
+    r.w = reinterpret_cast<const uint8_t*>(a.w) + (long)row * a.K * NUM / DEN;
+    r.s = FMT == WF_I4 ? a.scales + (long)row * a.bpr : nullptr;
+    return r;
 }
 
-template <int FMT, int TILES>
-__global__ __launch_bounds__(256) void skinny_kernel(GemvArgs a, float* __restrict__ partial,
-                                                     int splitk) {
-    constexpr int SEG = SK<FMT>::SEG, MF = SK<FMT>::MF;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lr = lane & 15, g = lane >> 4;
-    const int row0 = (blockIdx.x * 4 + wave) * (TILES * 16);
-    if (row0 >= a.M) return;                       // wave-uniform
-    const int M = a.M, K = a.K, N = a.N;
-    const int nseg = K / SEG;
-    const int ks = blockIdx.y;
-    const int s0 = (int)((long)nseg * ks / splitk), s1 = (int)((long)nseg * (ks + 1) / splitk);
+// fragment of 32-k tile kt; cpb_shift: log2 of the int4 chunks per block
+template <int FMT>
+__device__ __forceinline__ void sk_load(const SkRow& r, int kt, int g, int cpb_shift,
+                                        SkFrag<FMT>& f) {
+    if constexpr (FMT == WF_BF16) {
+        f.w = ldg_stream(reinterpret_cast<const u32x4*>(r.w + (kt * 32 + 8 * g) * 2));
+    } else if constexpr (FMT == WF_I8) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x2*>(r.w + kt * 32 + 8 * g));
+        f.w0 = v.x;
+        f.w1 = v.y;
+    } else {
+        f.w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(r.w + kt * 16 + 4 * g));
+        f.s = r.s[kt >> cpb_shift] * 0.0625f;        // the tile holds 16 * q
+    }
+}
 
-    // activation column handled by this lane in the A operand
-    const int xs = lr >> 1, xpart = lr & 1;
-    const bool xvalid = xs < N;
-    const float* xrow = a.x + (xvalid ? (long)xs * a.x_stride_n : 0);
+template <int FMT>
+__device__ __forceinline__ bf16x8 sk_operand(const SkFrag<FMT>& f) {
+    u32x4 b;
+    if constexpr (FMT == WF_BF16) {
+        b = f.w;
+    } else if constexpr (FMT == WF_I8) {
+        b.x = pack_f32_pair(s8_at(f.w0, 0), s8_at(f.w0, 1));
+        b.y = pack_f32_pair(s8_at(f.w0, 2), s8_at(f.w0, 3));
+        b.z = pack_f32_pair(s8_at(f.w1, 0), s8_at(f.w1, 1));
+        b.w = pack_f32_pair(s8_at(f.w1, 2), s8_at(f.w1, 3));
+    } else {
+        const uint32_t hi = f.w & 0xF0F0F0F0u;            // 16 * even elements
+        const uint32_t lo = (f.w << 4) & 0xF0F0F0F0u;     // 16 * odd elements
+        b.x = pack_f32_pair(s8_at(hi, 0), s8_at(lo, 0));
+        b.y = pack_f32_pair(s8_at(hi, 1), s8_at(lo, 1));
+        b.z = pack_f32_pair(s8_at(hi, 2), s8_at(lo, 2));
+        b.w = pack_f32_pair(s8_at(hi, 3), s8_at(lo, 3));
+    }
+    return __builtin_bit_cast(bf16x8, b);
+}
 
-    int rows[TILES];
+// grid (tile blocks, K splits); block 1024 threads.  partial: [splits][N][M]
+// (used when gridDim.y > 1).  kt_split: 32-k tiles per K split (<= 128).
+template <int FMT>
+__global__ __launch_bounds__(1024) void skinny_kernel(GemvArgs a, float* __restrict__ partial,
+                                                      int kt_split, int cpb_shift) {
+    const int lane = threadIdx.x & 63;
+    // wave-uniform by construction; readfirstlane lets the compiler see it
+    // (per-lane branches around the loads would serialise them)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, li = lane & 15;
+    const int M = a.M, N = a.N;
+    const int kt_total = a.K / 32;
+    const int kt0 = blockIdx.y * kt_split;
+    const int kt1 = min(kt_total, kt0 + kt_split);
+    const int per = (kt1 - kt0 + SK_WAVES - 1) / SK_WAVES;      // <= SK_KTW
+    const int w0 = kt0 + wave * per;
+    const int nkt = max(0, min(per, kt1 - w0));                  // wave-uniform
+    const int n_tiles = (M + 15) / 16;
+    const int step = gridDim.x;
+    const int t0 = blockIdx.x;
+
+    // ---- x of this lane's A operands: every load issued before the
+    // weights', so the conversion waits for x alone
+    // (lanes of rows i >= 2N read sequence 0 and are zeroed at conversion,
+    // so no lane-divergent branch separates the loads from their use)
+    const int s = li >> 1;
+    const bool lo = li & 1, real = s < N;
+    const float* xr = a.x + (real ? (long)s * a.x_stride_n : 0);
+    float xv[SK_KTW][8];
+    // Every one of the SK_KTW slots is loaded and multiplied (straight-line
+    // code keeps the wait counts exact); slots j >= nkt re-read a valid tile
+    // and get a zero A operand.
+    auto ktile = [&](int j) { return min(w0 + j, kt1 - 1); };
+    if (a.x_vec) {
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-        const int r = row0 + t * 16 + lr;
-        rows[t] = r < M ? r : M - 1;
+        for (int j = 0; j < SK_KTW; ++j) {
+            const long k = (long)ktile(j) * 32 + 8 * g;
+            const f32x4 p0 = *reinterpret_cast<const f32x4*>(xr + k);
+            const f32x4 p1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
+            xv[j][0] = p0.x; xv[j][1] = p0.y; xv[j][2] = p0.z; xv[j][3] = p0.w;
+            xv[j][4] = p1.x; xv[j][5] = p1.y; xv[j][6] = p1.z; xv[j][7] = p1.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < SK_KTW; ++j) {
+            const long k = (long)ktile(j) * 32 + 8 * g;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[j][e] = xr[(k + e) * a.x_stride_k];
+        }
     }
 
-    f32x4 acc[TILES];
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_sched_barrier(0);
 
-    for (int seg = s0; seg < s1; ++seg) {
-        const int kb = seg * SEG;
-        // ---- weight fragments for every tile (issued first) --------------
-        u32x4 wraw[TILES];
-        uint32_t w4[TILES][MF];
-        if constexpr (FMT == WF_BF16 || FMT == WF_I8) {
-            const int eb = FMT == WF_BF16 ? 2 : 1;
+    // ---- weights of the first tile (one buffer, refilled in place)
+    SkFrag<FMT> cur[SK_KTW];
+    {
+        const SkRow r = sk_row<FMT>(a, min(t0 * 16 + li, M - 1));
 #pragma unroll
-            for (int t = 0; t < TILES; ++t) {
-                const char* base = reinterpret_cast<const char*>(a.w) +
-                                   ((long)rows[t] * K + kb + (FMT == WF_BF16 ? 8 : 16) * g) * eb;
-                wraw[t] = ldg_stream(reinterpret_cast<const u32x4*>(base));
-            }
-        } else {
+        for (int j = 0; j < SK_KTW; ++j) sk_load<FMT>(r, ktile(j), g, cpb_shift, cur[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- A operands, converted once (rows i >= 2N stay zero)
+    bf16x8 A[SK_KTW];
 #pragma unroll
-            for (int t = 0; t < TILES; ++t)
+    for (int j = 0; j < SK_KTW; ++j) {
+        if (!real || j >= nkt) {
 #pragma unroll
-                for (int m = 0; m < MF; ++m) {
-                    const uint32_t* base = reinterpret_cast<const uint32_t*>(
-                        reinterpret_cast<const uint8_t*>(a.w) + ((long)rows[t] * K + kb + 32 * m) / 2);
-                    w4[t][m] = __builtin_nontemporal_load(base + g);
-                }
+            for (int e = 0; e < 8; ++e) xv[j][e] = 0.f;
         }
-        // ---- per MFMA ------------------------------------------------------
+        u32x4 xa;
+        xa.x = pack2(split_part(xv[j][0], lo), split_part(xv[j][1], lo));
+        xa.y = pack2(split_part(xv[j][2], lo), split_part(xv[j][3], lo));
+        xa.z = pack2(split_part(xv[j][4], lo), split_part(xv[j][5], lo));
+        xa.w = pack2(split_part(xv[j][6], lo), split_part(xv[j][7], lo));
+        A[j] = __builtin_bit_cast(bf16x8, xa);
+    }
+
+    __shared__ f32x4 red[2][SK_WAVES][64];
+    const bool split_out = gridDim.y > 1;
+    int buf = 0;
+    const int my_tiles = t0 < n_tiles ? (n_tiles - 1 - t0) / step + 1 : 0;
+    int t = t0;
+    for (int i = 0; i < my_tiles; ++i, t += step) {      // block-uniform trip count
+        const SkRow rn = sk_row<FMT>(a, min((t + step) * 16 + li, M - 1));
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        // MFMAs over the tile; with REFILL each fragment's buffer takes the
+        // next tile's fragment as soon as it has become an operand (two
+        // straight-line versions keep the wait counts exact)
+        auto body = [&](auto refill) {
 #pragma unroll
-        for (int m = 0; m < MF; ++m) {
-            const int k0 = kb + kset<FMT>(g, m);
-            u32x4 xa = u32x4{0u, 0u, 0u, 0u};
-            if (xvalid) {
-                float v[8];
-                if (a.x_vec) {
-                    const f32x4 p0 = *reinterpret_cast<const f32x4*>(xrow + k0);
-                    const f32x4 p1 = *reinterpret_cast<const f32x4*>(xrow + k0 + 4);
-                    v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
-                    v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = xrow[(long)(k0 + j) * a.x_stride_k];
-                }
-                xa.x = pack2(split_part(v[0], xpart), split_part(v[1], xpart));
-                xa.y = pack2(split_part(v[2], xpart), split_part(v[3], xpart));
-                xa.z = pack2(split_part(v[4], xpart), split_part(v[5], xpart));
-                xa.w = pack2(split_part(v[6], xpart), split_part(v[7], xpart));
-            }
-            const bf16x8 A = __builtin_bit_cast(bf16x8, xa);
-#pragma unroll
-            for (int t = 0; t < TILES; ++t) {
-                u32x4 wb;
-                if constexpr (FMT == WF_BF16) {
-                    wb = wraw[t];
-                } else if constexpr (FMT == WF_I8) {
-                    const uint32_t w0 = m == 0 ? wraw[t].x : wraw[t].z;
-                    const uint32_t w1 = m == 0 ? wraw[t].y : wraw[t].w;
-                    wb.x = pack_f32_pair(s8_at(w0, 0), s8_at(w0, 1));
-                    wb.y = pack_f32_pair(s8_at(w0, 2), s8_at(w0, 3));
-                    wb.z = pack_f32_pair(s8_at(w1, 0), s8_at(w1, 1));
-                    wb.w = pack_f32_pair(s8_at(w1, 2), s8_at(w1, 3));
-                } else {
-                    const uint32_t hi = w4[t][m] & 0xF0F0F0F0u;          // 16 * even
-                    const uint32_t lo = (w4[t][m] << 4) & 0xF0F0F0F0u;   // 16 * odd
-                    wb.x = pack_f32_pair(s8_at(hi, 0), s8_at(lo, 0));
-                    wb.y = pack_f32_pair(s8_at(hi, 1), s8_at(lo, 1));
-                    wb.z = pack_f32_pair(s8_at(hi, 2), s8_at(lo, 2));
-                    wb.w = pack_f32_pair(s8_at(hi, 3), s8_at(lo, 3));
-                }
-                const bf16x8 B = __builtin_bit_cast(bf16x8, wb);
+            for (int j = 0; j < SK_KTW; ++j) {
+                bf16x8 B = sk_operand<FMT>(cur[j]);
+                if constexpr (FMT == WF_BF16) asm volatile("" : "+v"(B));
+                float sc = 1.0f;
+                if constexpr (FMT == WF_I4) sc = cur[j].s;
+                if constexpr (decltype(refill)::value) sk_load<FMT>(rn, ktile(j), g, cpb_shift, cur[j]);
                 if constexpr (FMT == WF_I4) {
                     const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        A, B, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    const int c = (kb >> 5) + m;              // chunk index in the row
-                    long bi;
-                    if (a.bpr > 0) bi = (long)rows[t] * a.bpr + (a.cpb == 1 ? c : c / a.cpb);
-                    else bi = ((long)rows[t] * K + (long)c * 32) / a.block;
-                    const float s = a.scales[bi] * 0.0625f;
-                    acc[t] += d * s;
+                        A[j], B, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    acc += d * sc;
                 } else {
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, acc[t], 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j], B, acc, 0, 0, 0);
                 }
             }
+        };
+        if (i + 1 < my_tiles) body(std::true_type{});
+        else body(std::false_type{});
+        red[buf][wave][lane] = acc;
+        __syncthreads();
+        if (threadIdx.x < 128) {
+            // thread (l, sp): sequence 2*(l/16) + sp of row 16 t + l % 16
+            const int l = threadIdx.x & 63, sp = threadIdx.x >> 6;
+            const int sq = 2 * (l >> 4) + sp, row = t * 16 + (l & 15);
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < SK_WAVES; ++w) {
+                const f32x4 pr = red[buf][w][l];
+                v += sp ? pr.z + pr.w : pr.x + pr.y;
+            }
+            if constexpr (FMT == WF_I8) v *= a.scales[min(row, M - 1)];
+            if (split_out) {
+                if (sq < N && row < M) partial[((long)blockIdx.y * N + sq) * M + row] = v;
+            } else if (a.epi == EPI_SILU_MUL) {
+                // rows (2i, 2i+1) = (gate_i, up_i) sit in adjacent lanes
+                const float up = __shfl_xor(v, 1, 64);
+                if ((row & 1) == 0 && sq < N && row + 1 < M)
+                    a.y[sq * a.y_stride_n + (long)(row >> 1) * a.y_stride_m] =
+                        v / (1.0f + expf(-v)) * up;
+            } else if (sq < N && row < M) {
+                a.y[sq * a.y_stride_n + (long)row * a.y_stride_m] = v;
+            }
+        }
+        buf ^= 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// int4 variant: a 16-row weight tile reaches LDS through contiguous 16-byte
+// loads (two tiles in flight in registers) -- the MFMA layout would read 4
+// bytes per lane scattered over 16 rows and as many scale words.  Rows are
+// padded by 16 bytes so the fragment reads (16 rows apart) hit distinct
+// banks.  The A operands, the wave's K range and the reduction are those of
+// skinny_kernel.
+constexpr int SKI4_MAX_ROWB = 2048;     // packed bytes of a row's K slice (4096 k)
+
+template <int PFN, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float* __restrict__ partial,
+                                                               int kt_split, int cpb_shift) {
+    constexpr int KTW = SK_KT_BLOCK / WAVES;                     // 32-k tiles per wave
+    constexpr int THREADS = 64 * WAVES;
+    constexpr int NPC = 16 * (SKI4_MAX_ROWB / 16) / THREADS;     // pieces per thread
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, li = lane & 15;
+    const int M = a.M, N = a.N;
+    const int kt_total = a.K / 32;
+    const int kt0 = blockIdx.y * kt_split;
+    const int kt1 = min(kt_total, kt0 + kt_split);
+    const int nks = kt1 - kt0;                                   // chunks of the slice
+    const int per = (nks + WAVES - 1) / WAVES;
+    const int w0 = wave * per;                                   // slice-relative
+    const int nkt = max(0, min(per, nks - w0));
+    const int n_tiles = (M + 15) / 16;
+    const int step = gridDim.x;
+    const int t0 = blockIdx.x;
+    const int rowb = nks * 16;                                   // slice bytes per row
+    constexpr int ROWP = SKI4_MAX_ROWB + 16;                     // padded LDS row
+    // scale words of the slice per row (block index range)
+    const int sb0 = kt0 >> cpb_shift;
+    const int nsc = ((kt1 - 1) >> cpb_shift) - sb0 + 1;
+
+    __shared__ __align__(16) uint8_t wt[2][16 * ROWP];           // 2 x 33 KB
+    __shared__ __align__(16) float sct[2][16][SKI4_MAX_ROWB / 16 + 4];
+    __shared__ f32x4 red[2][WAVES][64];
+
+    // ---- this thread's pieces of every tile (fixed): 16-byte data pieces
+    // q = 0, 1 and scale words q = 0, 1 as (row in tile, byte/word column);
+    // pieces past the tile re-read its last piece and are not stored
+    const int dpr = rowb >> 4;                                   // 16-B pieces per row
+    int drow[NPC], dcol[NPC], srow[NPC], scol[NPC];
+    bool dok[NPC], sok[NPC];
+#pragma unroll
+    for (int q = 0; q < NPC; ++q) {
+        const int pd = (int)threadIdx.x + THREADS * q, ps = pd;
+        dok[q] = pd < 16 * dpr;
+        sok[q] = ps < 16 * nsc;
+        const int cd = min(pd, 16 * dpr - 1), cs = min(ps, 16 * nsc - 1);
+        drow[q] = cd / dpr;
+        dcol[q] = (cd % dpr) * 16;
+        srow[q] = cs / nsc;
+        scol[q] = cs % nsc;
+    }
+    struct Pf { u32x4 d[NPC]; float s[NPC]; };
+    const uint8_t* wbase = reinterpret_cast<const uint8_t*>(a.w) + kt0 * 16;
+    const long wstride = a.K / 2;
+    auto fetch = [&](int t, Pf& f) {
+#pragma unroll
+        for (int q = 0; q < NPC; ++q) {
+            const int r = min(t * 16 + drow[q], M - 1);
+            f.d[q] = ldg_stream(reinterpret_cast<const u32x4*>(wbase + (long)r * wstride + dcol[q]));
+        }
+#pragma unroll
+        for (int q = 0; q < NPC; ++q) {
+            const int r = min(t * 16 + srow[q], M - 1);
+            f.s[q] = a.scales[(long)r * a.bpr + sb0 + scol[q]] * 0.0625f;
+        }
+    };
+    auto stash = [&](const Pf& f, int b) {
+#pragma unroll
+        for (int q = 0; q < NPC; ++q)
+            if (dok[q]) *reinterpret_cast<u32x4*>(&wt[b][drow[q] * ROWP + dcol[q]]) = f.d[q];
+#pragma unroll
+        for (int q = 0; q < NPC; ++q)
+            if (sok[q]) sct[b][srow[q]][scol[q]] = f.s[q];
+    };
+
+    // ---- the first PFN tiles' weights, then x in two halves of four A
+    // operands (the staging overlaps the weights' latency and holds 32 VGPRs
+    // of x at a time)
+    Pf pf[PFN];
+#pragma unroll
+    for (int p = 0; p < PFN; ++p) fetch(min(t0 + p * step, n_tiles - 1), pf[p]);
+    __builtin_amdgcn_sched_barrier(0);
+    const int s = li >> 1;
+    const bool lo = li & 1, real = s < N;
+    const float* xr = a.x + (real ? (long)s * a.x_stride_n : 0);
+    auto ktile = [&](int j) { return kt0 + min(w0 + j, nks - 1); };
+    bf16x8 A[KTW];
+#pragma unroll
+    for (int h = 0; h < KTW; h += KTW / 2) {
+        float xv[KTW / 2][8];
+#pragma unroll
+        for (int j = 0; j < KTW / 2; ++j) {
+            const long k = (long)ktile(h + j) * 32 + 8 * g;
+            if (a.x_vec) {
+                const f32x4 p0 = *reinterpret_cast<const f32x4*>(xr + k);
+                const f32x4 p1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
+                xv[j][0] = p0.x; xv[j][1] = p0.y; xv[j][2] = p0.z; xv[j][3] = p0.w;
+                xv[j][4] = p1.x; xv[j][5] = p1.y; xv[j][6] = p1.z; xv[j][7] = p1.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[j][e] = xr[(k + e) * a.x_stride_k];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KTW / 2; ++j) {
+            if (!real || h + j >= nkt) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[j][e] = 0.f;
+            }
+            u32x4 xa;
+            xa.x = pack2(split_part(xv[j][0], lo), split_part(xv[j][1], lo));
+            xa.y = pack2(split_part(xv[j][2], lo), split_part(xv[j][3], lo));
+            xa.z = pack2(split_part(xv[j][4], lo), split_part(xv[j][5], lo));
+            xa.w = pack2(split_part(xv[j][6], lo), split_part(xv[j][7], lo));
+            A[h + j] = __builtin_bit_cast(bf16x8, xa);
         }
     }
 
-    // ---- epilogue: lane (r, g) owns row r, sequences 2g and 2g+1 -----------
+    const bool split_out = gridDim.y > 1;
+    const int my_tiles = t0 < n_tiles ? (n_tiles - 1 - t0) / step + 1 : 0;
+    // the LDS buffer b = i & 1 holds tile i; registers pf[i % PFN] hold tile
+    // i until stashed, then take tile i + PFN
+    auto tile = [&](int i, Pf& f) {
+        const int t = t0 + i * step, b = i & 1;
+        stash(f, b);
+        if (i + PFN < my_tiles) fetch(t0 + (i + PFN) * step, f);
+        __syncthreads();
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-        const int r = row0 + t * 16 + lr;
-        if (r >= M) continue;
-        float y0 = acc[t].x + acc[t].y, y1 = acc[t].z + acc[t].w;
-        if constexpr (FMT == WF_I8) {
-            const float s = a.scales[r];
-            y0 *= s;
-            y1 *= s;
+        for (int j = 0; j < KTW; ++j) {
+            const int c = min(w0 + j, nks - 1);                 // slice chunk
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(&wt[b][li * ROWP + c * 16 + 4 * g]);
+            const float sc = sct[b][li][((kt0 + c) >> cpb_shift) - sb0];
+            const uint32_t hi = w & 0xF0F0F0F0u;
+            const uint32_t lw = (w << 4) & 0xF0F0F0F0u;
+            u32x4 bb;
+            bb.x = pack_f32_pair(s8_at(hi, 0), s8_at(lw, 0));
+            bb.y = pack_f32_pair(s8_at(hi, 1), s8_at(lw, 1));
+            bb.z = pack_f32_pair(s8_at(hi, 2), s8_at(lw, 2));
+            bb.w = pack_f32_pair(s8_at(hi, 3), s8_at(lw, 3));
+            const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                A[j], __builtin_bit_cast(bf16x8, bb), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            acc += d * sc;
         }
-        const int n0 = 2 * g, n1 = 2 * g + 1;
-        if (n0 < N) partial[((long)ks * N + n0) * M + r] = y0;
-        if (n1 < N) partial[((long)ks * N + n1) * M + r] = y1;
+        red[b][wave][lane] = acc;
+        __syncthreads();
+        if (threadIdx.x < 128) {
+            const int l = threadIdx.x & 63, sp = threadIdx.x >> 6;
+            const int sq = 2 * (l >> 4) + sp, row = t * 16 + (l & 15);
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const f32x4 pr = red[b][w][l];
+                v += sp ? pr.z + pr.w : pr.x + pr.y;
+            }
+            if (split_out) {
+                if (sq < N && row < M) partial[((long)blockIdx.y * N + sq) * M + row] = v;
+            } else if (a.epi == EPI_SILU_MUL) {
+                const float up = __shfl_xor(v, 1, 64);
+                if ((row & 1) == 0 && sq < N && row + 1 < M)
+                    a.y[sq * a.y_stride_n + (long)(row >> 1) * a.y_stride_m] =
+                        v / (1.0f + expf(-v)) * up;
+            } else if (sq < N && row < M) {
+                a.y[sq * a.y_stride_n + (long)row * a.y_stride_m] = v;
+            }
+        }
+    };
+    int i = 0;
+    for (; i + PFN <= my_tiles; i += PFN) {
+#pragma unroll
+        for (int p = 0; p < PFN; ++p) tile(i + p, pf[p]);
     }
+#pragma unroll
+    for (int p = 0; p < PFN - 1; ++p)
+        if (i + p < my_tiles) tile(i + p, pf[p]);
 }
 
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemvArgs a, const float* __restrict__ partial,
@@ -235,28 +480,47 @@ int skinny_reserve(int M, int N, int K) {
     return ensure_partial((size_t)64 * N * M * sizeof(float));
 }
 
-template <int FMT, int TILES>
+template <int FMT>
 static int launch_skinny(const GemvArgs& a, hipStream_t st) {
-    constexpr int SEG = SK<FMT>::SEG;
-    const int rows_per_block = 4 * TILES * 16;
-    const int bx = (a.M + rows_per_block - 1) / rows_per_block;
-    const int nseg = a.K / SEG;
-    const int waves = bx * 4;
-    int splitk = (4 * device_cu_count() * 4 + waves - 1) / waves;   // >= 4 waves per SIMD
-    if (splitk > nseg) splitk = nseg;
-    if (splitk > 64) splitk = 64;
-    if (splitk < 1) splitk = 1;
-    int rc = ensure_partial((size_t)splitk * a.N * a.M * sizeof(float));
-    if (rc) return rc;
-    hipLaunchKernelGGL((skinny_kernel<FMT, TILES>), dim3(bx, splitk), dim3(256), 0, st, a,
-                       g_partial, splitk);
+    const int kt_total = a.K / 32;
+    const int splits = (kt_total + SK_KT_BLOCK - 1) / SK_KT_BLOCK;
+    const int kt_split = (kt_total + splits - 1) / splits;
+    const int n_tiles = (a.M + 15) / 16;
+    static int resident = 0;     // blocks of 1024 threads one CU holds
+    if (resident == 0) {
+        int n = 0;
+        const void* kern = FMT == WF_I4 ? (const void*)skinny_i4_kernel<1, 16>
+                                        : (const void*)skinny_kernel<FMT>;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 1024, 0) != hipSuccess ||
+            n < 1) {
+            (void)hipGetLastError();
+            n = 1;
+        }
+        resident = n;
+    }
+    int bx = resident * device_cu_count();
+    if (bx > n_tiles) bx = n_tiles;
+    if (splits > 1) {
+        int rc = ensure_partial((size_t)splits * a.N * a.M * sizeof(float));
+        if (rc) return rc;
+    }
+    int cpb_shift = 0;
+    while ((1 << cpb_shift) < a.cpb) ++cpb_shift;
+    if constexpr (FMT == WF_I4)
+        hipLaunchKernelGGL((skinny_i4_kernel<1, 16>), dim3(bx, splits), dim3(1024), 0, st, a,
+                           g_partial, kt_split, cpb_shift);
+    else
+        hipLaunchKernelGGL((skinny_kernel<FMT>), dim3(bx, splits), dim3(1024), 0, st, a,
+                           g_partial, kt_split, cpb_shift);
     ATLAS_LAUNCH_CHECK("skinny");
-    const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
-    long rb = ((long)a.N * m_out + 255) / 256;
-    if (rb > 4096) rb = 4096;
-    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, g_partial,
-                       splitk);
-    ATLAS_LAUNCH_CHECK("skinny_reduce");
+    if (splits > 1) {
+        const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
+        long rb = ((long)a.N * m_out + 255) / 256;
+        if (rb > 4096) rb = 4096;
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a,
+                           g_partial, splits);
+        ATLAS_LAUNCH_CHECK("skinny_reduce");
+    }
     return ATLAS_OK;
 }
 
@@ -269,16 +533,20 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     ATLAS_REQUIRE(a.fmt == WF_BF16 || a.scales, "skinny: null scales");
     if (a.epi == EPI_SILU_MUL) ATLAS_REQUIRE(a.M % 2 == 0, "skinny: silu-mul needs even rows");
     if (a.M == 0) return ATLAS_OK;
+    ATLAS_REQUIRE(a.K % 32 == 0 && a.K > 0, "skinny: K %% 32 != 0");
+    const uintptr_t al = (uintptr_t)a.w;
     switch (a.fmt) {
     case WF_BF16:
-        ATLAS_REQUIRE(a.K % 32 == 0, "skinny bf16: K %% 32 != 0");
-        return launch_skinny<WF_BF16, 2>(a, st);
+        ATLAS_REQUIRE((al & 15) == 0, "skinny bf16: weights not 16-byte aligned");
+        return launch_skinny<WF_BF16>(a, st);
     case WF_I8:
-        ATLAS_REQUIRE(a.K % 64 == 0, "skinny int8: K %% 64 != 0");
-        return launch_skinny<WF_I8, 2>(a, st);
+        ATLAS_REQUIRE((al & 7) == 0, "skinny int8: weights not 8-byte aligned");
+        return launch_skinny<WF_I8>(a, st);
     case WF_I4:
-        ATLAS_REQUIRE(a.K % 128 == 0 && a.block % 32 == 0, "skinny int4: K %% 128 or block %% 32");
-        return launch_skinny<WF_I4, 2>(a, st);
+        ATLAS_REQUIRE((al & 3) == 0, "skinny int4: weights not 4-byte aligned");
+        ATLAS_REQUIRE(a.block % 32 == 0 && (a.cpb & (a.cpb - 1)) == 0 && a.bpr > 0,
+                      "skinny int4: block %d must be 32 * 2^j and divide K", a.block);
+        return launch_skinny<WF_I4>(a, st);
     }
     set_error(ATLAS_EUNSUPPORTED, "skinny: weight format %d", a.fmt);
     return ATLAS_EUNSUPPORTED;
