@@ -145,14 +145,15 @@ __device__ __forceinline__ void scan_update(const float (&q)[G][HD / 16], float 
     }
 }
 
-// Scan cache rows [b0, e1) into the (wave, row) group's state.  kb/vb:
-// dim 0 of the KV head in row 0, lane_dims: the lane's first dim.
-template <int HD, int G>
+// Scan cache rows [b0, e1) into the (wave, row) group's state (NG groups per
+// block).  kb/vb: dim 0 of the KV head in row 0, lane_dims: the lane's
+// first dim.
+template <int HD, int G, int NG>
 __device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long kv_stride,
                                           int lane_dims, int b0, int e1, int group,
                                           const float (&q)[G][HD / 16], float (&m)[G],
                                           float (&l)[G], float (&o)[G][HD / 16]) {
-    constexpr int P = ScanShape<HD>::P, DPL = HD / 16, S = 16 * P;
+    constexpr int P = ScanShape<HD>::P, DPL = HD / 16, S = NG * P;
     // Block-uniform trip count and one exit, at the bottom of the loop: with a
     // divergent or mid-body exit the compiler must assume the other buffer's
     // loads may still be in flight at the loop head and waits for them there,
@@ -176,8 +177,8 @@ __device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long
     if (steps & 1) scan_update<HD, G>(q, m, l, o, ka, va, t, e1);
 }
 
-template <int HD, int G>
-__global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+template <int HD, int G, int W>
+__global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;              // dims per lane
     constexpr float LOG2E = 1.4426950408889634f;
     const int kvh = blockIdx.x, split = blockIdx.y, n_splits = gridDim.y;
@@ -211,12 +212,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    attn_scan<HD, G>(a.k_cache + (long)kvh * HD, a.v_cache + (long)kvh * HD, kv_stride, dl * DPL,
-                     b0, b1, wave * 4 + row, q, m, l, o);
+    attn_scan<HD, G, 4 * W>(a.k_cache + (long)kvh * HD, a.v_cache + (long)kvh * HD, kv_stride,
+                            dl * DPL, b0, b1, wave * 4 + row, q, m, l, o);
 
     // ---- merge the 16 (wave,row) states of this block through LDS ---------
-    __shared__ float s_m[16][G], s_l[16][G];
-    __shared__ float s_o[16][G][HD];
+    __shared__ float s_m[4 * W][G], s_l[4 * W][G];
+    __shared__ float s_o[4 * W][G][HD];
     const int st = wave * 4 + row;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -226,15 +227,15 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     }
     __syncthreads();
     // thread -> (head, dim) pairs
-    for (int e = threadIdx.x; e < G * HD; e += 256) {
+    for (int e = threadIdx.x; e < G * HD; e += 64 * W) {
         const int h = e / HD, d = e % HD;
         float mx = -INFINITY;
 #pragma unroll
-        for (int s2 = 0; s2 < 16; ++s2) mx = fmaxf(mx, s_m[s2][h]);
+        for (int s2 = 0; s2 < 4 * W; ++s2) mx = fmaxf(mx, s_m[s2][h]);
         float lsum = 0.f, osum = 0.f;
         if (mx != -INFINITY) {
 #pragma unroll
-            for (int s2 = 0; s2 < 16; ++s2) {
+            for (int s2 = 0; s2 < 4 * W; ++s2) {
                 const float w = exp2f(s_m[s2][h] - mx);   // 0 for empty states
                 lsum += s_l[s2][h] * w;
                 osum += s_o[s2][h][d] * w;
@@ -336,8 +337,8 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
 //    block that sees n_splits - 1 merges and resets the counter to 0 (no
 //    waiting anywhere, and the counters are clean for the next launch).
 // ---------------------------------------------------------------------------
-template <int HD, int G>
-__global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
+template <int HD, int G, int W>
+__global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     constexpr int DPL = HD / 16;
     constexpr int EPL = HD / 64;              // head elements per lane in the prep
     constexpr float LOG2E = 1.4426950408889634f;
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
     // ---- prep: QK-norm + RoPE of the G q heads and k, wave per vector -----
     const float* cr = a.cos_tab + (long)pos * (HD / 2);
     const float* sr = a.sin_tab + (long)pos * (HD / 2);
-    for (int vi = wave; vi < G + 1; vi += 4) {
+    for (int vi = wave; vi < G + 1; vi += W) {
         const bool isq = vi < G;
         const int head = isq ? kvh * G + vi : kvh;
         const float* src = qkv + (isq ? (long)head * HD : (long)(a.n_heads + kvh) * HD);
@@ -407,10 +408,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
             else sk[e] = r[j];
         }
     }
-    for (int e = threadIdx.x; e < HD; e += 256) sv[e] = qkv[(long)(a.n_heads + a.n_kv + kvh) * HD + e];
+    for (int e = threadIdx.x; e < HD; e += 64 * W) sv[e] = qkv[(long)(a.n_heads + a.n_kv + kvh) * HD + e];
     __syncthreads();
     if (owner) {
-        for (int e = threadIdx.x; e < HD; e += 256) {
+        for (int e = threadIdx.x; e < HD; e += 64 * W) {
             kc[(long)pos * kv_stride + (long)kvh * HD + e] = sk[e];
             vc[(long)pos * kv_stride + (long)kvh * HD + e] = sv[e];
         }
@@ -429,8 +430,8 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    attn_scan<HD, G>(kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, dl * DPL, b0, e1,
-                     wave * 4 + row, q, m, l, o);
+    attn_scan<HD, G, 4 * W>(kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, dl * DPL, b0,
+                            e1, wave * 4 + row, q, m, l, o);
     if (owner && wave == 0 && row == 0) {
         // position pos from LDS (the 16 lanes of row 0 of wave 0)
         constexpr int P = ScanShape<HD>::P;
@@ -446,8 +447,8 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
     }
 
     // ---- merge the 16 (wave,row) states of this block ------------------------
-    __shared__ float s_m[16][G], s_l[16][G];
-    __shared__ float s_o[16][G][HD];
+    __shared__ float s_m[4 * W][G], s_l[4 * W][G];
+    __shared__ float s_o[4 * W][G][HD];
     __shared__ int s_last;
     const int st = wave * 4 + row;
 #pragma unroll
@@ -460,15 +461,15 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
     // each sequence owns n_heads * gridDim.y partial slots (its active split
     // count may be smaller and differs between sequences)
     const long pbase = (long)seq * a.n_heads * gridDim.y;
-    for (int e = threadIdx.x; e < G * HD; e += 256) {
+    for (int e = threadIdx.x; e < G * HD; e += 64 * W) {
         const int h = e / HD, d = e % HD;
         float mx = -INFINITY;
 #pragma unroll
-        for (int s2 = 0; s2 < 16; ++s2) mx = fmaxf(mx, s_m[s2][h]);
+        for (int s2 = 0; s2 < 4 * W; ++s2) mx = fmaxf(mx, s_m[s2][h]);
         float lsum = 0.f, osum = 0.f;
         if (mx != -INFINITY) {
 #pragma unroll
-            for (int s2 = 0; s2 < 16; ++s2) {
+            for (int s2 = 0; s2 < 4 * W; ++s2) {
                 const float w = exp2f(s_m[s2][h] - mx);
                 lsum += s_l[s2][h] * w;
                 osum += s_o[s2][h][d] * w;
@@ -494,7 +495,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
     __syncthreads();
     if (!s_last) return;
     __threadfence();
-    for (int e = threadIdx.x; e < G * HD; e += 256) {
+    for (int e = threadIdx.x; e < G * HD; e += 64 * W) {
         const int h = e / HD, d = e % HD;
         const int qh = kvh * G + h;
         const long p0 = pbase + (long)qh * n_splits;
@@ -514,10 +515,16 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnFusedArgs a) {
     if (threadIdx.x == 0) atomicExch(&a.counters[seq * a.n_kv + kvh], 0);
 }
 
+// Waves per block.  Measured on MI355X at the 7B and GQA-32/8 shapes, ctx
+// 128..16384: 8-wave blocks (twice the K/V rows in flight per block) run
+// 10-35% slower than 4-wave blocks at every split count, so 4 it is.
+template <int HD, int G> constexpr int attn_waves() { return 4; }
+
 template <int HD, int G>
 static int launch_fused(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st) {
-    hipLaunchKernelGGL((attn_fused_kernel<HD, G>), dim3(a.n_kv, n_splits, n_seq), dim3(256), 0,
-                       st, a);
+    constexpr int W = attn_waves<HD, G>();
+    hipLaunchKernelGGL((attn_fused_kernel<HD, G, W>), dim3(a.n_kv, n_splits, n_seq), dim3(64 * W),
+                       0, st, a);
     ATLAS_LAUNCH_CHECK("attn_fused");
     return ATLAS_OK;
 }
@@ -592,7 +599,9 @@ int attn_pick_splits(int n_kv, int max_ctx) {
 
 template <int HD, int G>
 static int launch_split(AttnArgs a, int n_splits, hipStream_t st) {
-    hipLaunchKernelGGL((attn_split_kernel<HD, G>), dim3(a.n_kv, n_splits), dim3(256), 0, st, a);
+    constexpr int W = attn_waves<HD, G>();
+    hipLaunchKernelGGL((attn_split_kernel<HD, G, W>), dim3(a.n_kv, n_splits), dim3(64 * W), 0, st,
+                       a);
     ATLAS_LAUNCH_CHECK("attn_split");
     if (n_splits > 1) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_heads), dim3(HD < 256 ? HD : 256), 0, st,

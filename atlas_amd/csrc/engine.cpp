@@ -106,6 +106,13 @@ struct atlas_model {
     hipStream_t st = nullptr;
     bool use_graph = true;
     hipGraphExec_t gexec[2] = {nullptr, nullptr};
+    hipGraphExec_t bgexec[9] = {};   // ragged batch step per batch size 1..8
+    // pinned staging ring for the batch step's tokens / positions / slots:
+    // entry k is rewritten only after its event (the copies) completed
+    static constexpr int kRing = 8;
+    int* ring = nullptr;             // [kRing][3][8]
+    hipEvent_t ring_ev[kRing] = {};
+    bool ring_used[kRing] = {};
     // greedy choice settings baked into the captured graph
     float g_theta = 1.f;
     int g_window = 0, g_nsup = 0;
@@ -367,6 +374,11 @@ int enqueue_step(atlas_model* m, int mode) {
 
 void drop_graphs(atlas_model* m) {
     for (auto& g : m->gexec)
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
+    for (auto& g : m->bgexec)
         if (g) {
             (void)hipGraphExecDestroy(g);
             g = nullptr;
@@ -682,6 +694,13 @@ int tensor_io(atlas_model* m, int kind, int layer, void* data, float* scales, bo
 }
 
 // ---- the ragged batch step ----------------------------------------------------
+// n rows of activations through w: the batch-1 GEMV for one row, the skinny
+// MFMA GEMM for 2..8
+int bmm(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int epi) {
+    if (n == 1) return gemv(m, w, x, y, epi);
+    return skinny(m, w, x, y, n, epi);
+}
+
 int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
     const atlas_model_config& c = m->cfg;
     const int d = c.d_model;
@@ -693,7 +712,7 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             TRY(rmsnorm_launch(m->x, L.attn_norm, m->xn, d, n, d, c.rms_eps, m->st));
             xin = m->xn;
         }
-        TRY(skinny(m, L.qkv, xin, m->qkv, n, EPI_STORE));
+        TRY(bmm(m, L.qkv, xin, m->qkv, n, EPI_STORE));
         if (m->fused) {
             // one launch: every sequence's QK-norm/RoPE/KV write and attention
             AttnFusedArgs a{};
@@ -731,22 +750,58 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             a.max_rows = c.max_seq;
             TRY(attn_launch(a, m->attn_splits_unfused, m->st));
         }
-        TRY(skinny(m, L.wo, m->att, m->y, n, EPI_STORE));
+        TRY(bmm(m, L.wo, m->att, m->y, n, EPI_STORE));
         if (c.post_norm) {
             TRY(residual_rmsnorm_launch(m->x, m->y, L.attn_norm, d, n, d, c.rms_eps, m->st));
-            TRY(skinny(m, L.gu, m->x, m->h, n, EPI_SILU_MUL));
-            TRY(skinny(m, L.down, m->h, m->y, n, EPI_STORE));
+            TRY(bmm(m, L.gu, m->x, m->h, n, EPI_SILU_MUL));
+            TRY(bmm(m, L.down, m->h, m->y, n, EPI_STORE));
             TRY(residual_rmsnorm_launch(m->x, m->y, L.ffn_norm, d, n, d, c.rms_eps, m->st));
         } else {
             TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, (long)n * d, m->st));
             TRY(rmsnorm_launch(m->x, L.ffn_norm, m->xn, d, n, d, c.rms_eps, m->st));
-            TRY(skinny(m, L.gu, m->xn, m->h, n, EPI_SILU_MUL));
-            TRY(skinny(m, L.down, m->h, m->y, n, EPI_STORE));
+            TRY(bmm(m, L.gu, m->xn, m->h, n, EPI_SILU_MUL));
+            TRY(bmm(m, L.down, m->h, m->y, n, EPI_STORE));
             TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, (long)n * d, m->st));
         }
     }
     TRY(rmsnorm_launch(m->x, m->final_norm, m->xn, d, n, d, c.rms_eps, m->st));
-    TRY(skinny(m, m->lm_head, m->xn, m->logits, n, EPI_STORE));
+    TRY(bmm(m, m->lm_head, m->xn, m->logits, n, EPI_STORE));
+    // greedy choice of every row into choice_dev (last maximum wins)
+    for (int j = 0; j < n; ++j) {
+        ArgmaxArgs g{};
+        g.x = m->logits + (size_t)j * c.vocab; g.n = c.vocab; g.part = m->argpart;
+        g.out_u32 = m->choice_dev + j; g.theta = 1.0f;
+        TRY(argmax_launch(g, m->st));
+    }
+    return ATLAS_OK;
+}
+
+// batch_step replayed from a graph captured per batch size (fused models:
+// tokens, positions and slots are read from device memory)
+int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
+    if (!m->use_graph || !m->fused) return batch_step(m, n, slots);
+    if (!m->bgexec[n]) {
+        hipGraph_t g = nullptr;
+        ATLAS_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
+        int rc = batch_step(m, n, slots);
+        hipError_t e = hipStreamEndCapture(m->st, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) {
+            set_error(ATLAS_EHIP, "graph capture: %s", hipGetErrorString(e));
+            return ATLAS_EHIP;
+        }
+        e = hipGraphInstantiate(&m->bgexec[n], g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            m->bgexec[n] = nullptr;
+            set_error(ATLAS_EHIP, "graph instantiate: %s", hipGetErrorString(e));
+            return ATLAS_EHIP;
+        }
+    }
+    ATLAS_HIP(hipGraphLaunch(m->bgexec[n], m->st));
     return ATLAS_OK;
 }
 
@@ -864,6 +919,15 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->attn_splits = attn_pick_splits(c.n_kv_heads, c.max_seq);
     m->attn_splits_unfused = m->attn_splits;
     if (attn_reserve(c.n_heads, hd, m->attn_splits_unfused)) return fail(m);
+    // split-K partials of the ragged batch's skinny GEMMs, allocated now so
+    // that no later launch (graph capture included) allocates
+    if (m->B > 1) {
+        const int nb = m->B < 8 ? m->B : 8;
+        const int shapes[5][2] = {{m->qkv_rows, d}, {d, c.n_heads * hd}, {2 * c.ffn_hidden, d},
+                                  {d, c.ffn_hidden}, {c.vocab, d}};
+        for (const auto& sh : shapes)
+            if (sh[1] % 32 == 0 && skinny_reserve(sh[0], nb, sh[1])) return fail(m);
+    }
     // fused step: post-norm model whose attention shape the fused kernel
     // covers and whose GEMVs take the aligned fast path (d % 32 == 0)
     m->fused = c.post_norm && attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
@@ -886,6 +950,9 @@ ATLAS_API void atlas_model_destroy(atlas_model* m) {
     if (m->st) (void)hipStreamSynchronize(m->st);
     drop_graphs(m);
     for (void* p : m->allocs) (void)hipFree(p);
+    for (auto& e : m->ring_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (m->ring) (void)hipHostFree(m->ring);
     if (m->st) (void)hipStreamDestroy(m->st);
     delete m;
 }
@@ -1345,6 +1412,11 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
     std::vector<uint32_t> toks(n_seqs), choice(n_seqs);
     std::vector<int> slots(n_seqs), poss(n_seqs), idx(n_seqs);
     std::vector<float> lg;
+    if (!m->ring) {
+        ATLAS_HIP(hipHostMalloc((void**)&m->ring, sizeof(int) * 24 * atlas_model::kRing));
+        for (auto& e : m->ring_ev) ATLAS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    int ring_next = 0;
     while (true) {
         int n = 0;
         for (int i = 0; i < n_seqs; ++i) {
@@ -1360,21 +1432,38 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
             ++n;
         }
         if (n == 0) break;
-        ATLAS_HIP(hipMemcpyAsync(m->tok_dev, toks.data(), (size_t)n * 4, hipMemcpyHostToDevice, m->st));
-        ATLAS_HIP(hipMemcpyAsync(m->pos_dev, poss.data(), (size_t)n * 4, hipMemcpyHostToDevice, m->st));
-        ATLAS_HIP(hipMemcpyAsync(m->slot_dev, slots.data(), (size_t)n * 4, hipMemcpyHostToDevice, m->st));
-        std::vector<int> sl(slots.begin(), slots.begin() + n);
-        TRY(batch_step(m, n, sl));
-        if (!host_path) {
+        {
+            // stage through the pinned ring: steps without a host round trip
+            // may still be queued when the next step's values are written
+            const int k = ring_next++ % atlas_model::kRing;
+            if (m->ring_used[k]) ATLAS_HIP(hipEventSynchronize(m->ring_ev[k]));
+            int* e = m->ring + (size_t)k * 24;
             for (int j = 0; j < n; ++j) {
-                ArgmaxArgs g{};
-                g.x = m->logits + (size_t)j * V; g.n = V; g.part = m->argpart + 0;
-                g.out_u32 = m->choice_dev + j; g.theta = 1.0f;
-                TRY(argmax_launch(g, m->st));
+                e[j] = (int)toks[j];
+                e[8 + j] = poss[j];
+                e[16 + j] = slots[j];
             }
-            ATLAS_HIP(hipMemcpyAsync(choice.data(), m->choice_dev, (size_t)n * 4, hipMemcpyDeviceToHost,
-                                     m->st));
-            ATLAS_HIP(hipStreamSynchronize(m->st));
+            ATLAS_HIP(hipMemcpyAsync(m->tok_dev, e, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+            ATLAS_HIP(hipMemcpyAsync(m->pos_dev, e + 8, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+            ATLAS_HIP(hipMemcpyAsync(m->slot_dev, e + 16, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+            ATLAS_HIP(hipEventRecord(m->ring_ev[k], m->st));
+            m->ring_used[k] = true;
+        }
+        std::vector<int> sl(slots.begin(), slots.begin() + n);
+        TRY(run_batch_step(m, n, sl));
+        // a row chooses a token when it consumes its last prompt token or
+        // generates; steps inside every row's prompt need no host round trip
+        bool any_choice = false;
+        for (int j = 0; j < n; ++j) {
+            const int i = idx[j];
+            any_choice = any_choice || cursor[i] + 1 >= prompt_lens[i];
+        }
+        if (!host_path) {
+            if (any_choice) {
+                ATLAS_HIP(hipMemcpyAsync(choice.data(), m->choice_dev, (size_t)n * 4,
+                                         hipMemcpyDeviceToHost, m->st));
+                ATLAS_HIP(hipStreamSynchronize(m->st));
+            }
         } else {
             lg.resize((size_t)n * V);
             ATLAS_HIP(hipMemcpyAsync(lg.data(), m->logits, (size_t)n * V * 4, hipMemcpyDeviceToHost,

@@ -476,14 +476,24 @@ static int ensure_partial(size_t bytes) {
     return ATLAS_OK;
 }
 
+// K splits launch_skinny uses for this K
+static int skinny_splits(int K) {
+    const int kt_total = K / 32;
+    return (kt_total + SK_KT_BLOCK - 1) / SK_KT_BLOCK;
+}
+
+// Allocate the split-K partials an (M, N, K) launch needs, so that later
+// launches (e.g. under graph capture) allocate nothing.
 int skinny_reserve(int M, int N, int K) {
-    return ensure_partial((size_t)64 * N * M * sizeof(float));
+    const int splits = skinny_splits(K);
+    if (splits <= 1) return ATLAS_OK;
+    return ensure_partial((size_t)splits * N * M * sizeof(float));
 }
 
 template <int FMT>
 static int launch_skinny(const GemvArgs& a, hipStream_t st) {
     const int kt_total = a.K / 32;
-    const int splits = (kt_total + SK_KT_BLOCK - 1) / SK_KT_BLOCK;
+    const int splits = skinny_splits(a.K);
     const int kt_split = (kt_total + splits - 1) / splits;
     const int n_tiles = (a.M + 15) / 16;
     static int resident = 0;     // blocks of 1024 threads one CU holds

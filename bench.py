@@ -211,6 +211,7 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="fewer microbenchmark iterations")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the ragged batch of config 5")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="short program for rocprofv3 --pmc passes: a 1 GiB device copy "
                          "(calibration), then one launch set of each bf16 decode GEMV kernel")
@@ -299,12 +300,23 @@ def main() -> int:
     m.close()
     del m
 
-    # ---- int8 model ------------------------------------------------------------
-    m8, dt8 = decode_bench(am, am.W_INT8, prompt, args.steps, args.warmup, seed=7)
-    tok_s8 = args.steps / dt8
-    log(f"int8 decode: {dt8 * 1e3 / args.steps:.3f} ms/token, {tok_s8:.1f} tok/s")
-    m8.close()
-    del m8
+    # ---- int8 and int4 models ------------------------------------------------
+    quant = {}
+    for fmt, name in ((am.W_INT8, "int8"), (am.W_INT4, "int4")):
+        mq, dtq = decode_bench(am, fmt, prompt, args.steps, args.warmup, seed=7)
+        wq = mq.weight_bytes()
+        quant[name] = {"tok_s": round(args.steps / dtq, 2),
+                       "ms_per_step": round(dtq * 1e3 / args.steps, 4),
+                       "weight_bytes": int(wq),
+                       "weight_GB_s": round(wq / (dtq / args.steps) / 1e9, 1)}
+        log(f"{name} decode: {dtq * 1e3 / args.steps:.3f} ms/token, {args.steps / dtq:.1f} tok/s, "
+            f"weights {wq / 1e9:.2f} GB")
+        mq.close()
+        del mq
+
+    ragged = None
+    if not args.no_ragged:
+        ragged = ragged_bench(am, rng, args.quick)
 
     res = {
         "metric": "decode GEMV HBM GB/s (% of peak) + tok/s, 7B OLMo-shape bf16/int8/int4",
@@ -335,7 +347,9 @@ def main() -> int:
                           "frac_of_step_at_roofline": round(step_floor_ms / ms_step, 4),
                           "gemv_ms_per_step": round(step_gemv_ms, 4),
                           "gemv_all_GB_s": round(all_gbs, 1)},
-        "int8": {"tok_s": round(tok_s8, 2), "ms_per_step": round(dt8 * 1e3 / args.steps, 4)},
+        "int8": quant["int8"],
+        "int4": quant["int4"],
+        "ragged_batch": ragged,
         "gemv_microbench": micro,
         "attention_microbench": attn,
         "reference_published": {"olmo3_7b_bf16_tok_s": 61.7, "hardware": "A100-SXM4-40GB"},
@@ -344,6 +358,34 @@ def main() -> int:
         res["cpu_baseline"] = cpu
     print(json.dumps(res), flush=True)
     return 0
+
+
+def ragged_bench(am, rng, quick: bool) -> dict:
+    """Config 5's ragged batch: 8 greedy sequences with prompts of 16..2048
+    random ids decoded together (one skinny-GEMM step per position; prompts
+    are fed token by token, as the reference does), bf16 weights."""
+    import dataclasses
+    lens = [16, 64, 128, 256, 512, 1024, 1536, 2048]
+    max_new = 64 if quick else 256
+    cfg = dataclasses.replace(am.ModelConfig.olmo3_actual_7b(),
+                              max_seq_len=max(lens) + max_new + 8)
+    m = am.OlmoModel(cfg, weight_format=am.W_BF16, int4_block=32, max_batch=len(lens))
+    m.init_random(7)
+    prompts = [[int(t) for t in rng.integers(0, 100278, n)] for n in lens]
+    t0 = time.perf_counter()
+    out = m.generate_batch(prompts, max_new)
+    dt = time.perf_counter() - t0
+    gen = sum(len(o) for o in out)
+    total = sum(lens) + gen
+    steps = max(lens) + max_new
+    res = {"sequences": len(lens), "prompt_lens": lens, "max_new": max_new,
+           "generated_tokens": gen, "tokens_processed": total, "seconds": round(dt, 3),
+           "tok_s_processed": round(total / dt, 1), "tok_s_generated": round(gen / dt, 1),
+           "batch_steps": steps, "ms_per_batch_step": round(dt * 1e3 / steps, 3)}
+    log(f"ragged batch: {len(lens)} sequences, {total} tokens ({gen} generated) in {dt:.2f} s "
+        f"-> {total / dt:.0f} tok/s processed, {dt * 1e3 / steps:.2f} ms per batch step")
+    m.close()
+    return res
 
 
 def pmc_probe(torch, lib, am) -> int:
