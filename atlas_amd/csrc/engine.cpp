@@ -499,10 +499,10 @@ int host_argmax(const float* x, int n) {
     return n > 0 ? best : 0;
 }
 
-void rep_penalty(std::vector<float>& lg, const std::vector<uint32_t>& hist, int window,
+void rep_penalty(std::vector<float>& lg, const uint32_t* hist, size_t n_hist, int window,
                  float theta) {
-    const size_t start = hist.size() > (size_t)window ? hist.size() - window : 0;
-    for (size_t i = start; i < hist.size(); ++i) {
+    const size_t start = n_hist > (size_t)window ? n_hist - window : 0;
+    for (size_t i = start; i < n_hist; ++i) {
         const uint32_t t = hist[i];
         if (t < lg.size()) {
             if (lg[t] > 0.0f) lg[t] /= theta;
@@ -574,19 +574,20 @@ void softmax_host(std::vector<float>& x) {
     for (float& v : x) v *= inv;
 }
 
-uint32_t host_choose(atlas_model* m, const float* logits, int step,
-                     const std::vector<uint32_t>& hist, const atlas_sampling* s) {
-    const int V = m->cfg.vocab;
+// One token choice over `logits` given the generated history (lib.rs:1623-1711).
+uint32_t choose_token(const float* logits, int V, int step, const uint32_t* hist,
+                      size_t n_hist, const atlas_sampling* s, Rng& rng) {
     std::vector<float> lg(logits, logits + V);
     if (s && step == 0)
         for (int i = 0; i < s->n_suppress; ++i)
             if (s->suppress_initial_tokens[i] < (uint32_t)V) lg[s->suppress_initial_tokens[i]] = -INFINITY;
-    if (s && s->repetition_penalty != 1.0f && !hist.empty())
-        rep_penalty(lg, hist, s->repetition_window, s->repetition_penalty);
+    if (s && s->repetition_penalty != 1.0f && n_hist)
+        rep_penalty(lg, hist, n_hist, s->repetition_window, s->repetition_penalty);
     if (is_greedy(s)) return (uint32_t)host_argmax(lg.data(), V);
-    if (s->frequency_penalty != 0.0f && !hist.empty()) {
+    if (s->frequency_penalty != 0.0f && n_hist) {
         std::vector<std::pair<uint32_t, size_t>> counts;
-        for (uint32_t t : hist) {
+        for (size_t j = 0; j < n_hist; ++j) {
+            const uint32_t t = hist[j];
             auto it = std::find_if(counts.begin(), counts.end(),
                                    [t](const auto& e) { return e.first == t; });
             if (it != counts.end()) ++it->second;
@@ -595,8 +596,8 @@ uint32_t host_choose(atlas_model* m, const float* logits, int step,
         for (auto& e : counts)
             if (e.first < (uint32_t)V) lg[e.first] -= s->frequency_penalty * (float)e.second;
     }
-    if (s->presence_penalty != 0.0f && !hist.empty()) {
-        std::vector<uint32_t> seen(hist);
+    if (s->presence_penalty != 0.0f && n_hist) {
+        std::vector<uint32_t> seen(hist, hist + n_hist);
         std::sort(seen.begin(), seen.end());
         seen.erase(std::unique(seen.begin(), seen.end()), seen.end());
         for (uint32_t t : seen)
@@ -607,13 +608,18 @@ uint32_t host_choose(atlas_model* m, const float* logits, int step,
     if (s->top_p < 1.0f) top_p(lg, s->top_p);
     if (s->min_p > 0.0f) min_p(lg, s->min_p);
     softmax_host(lg);
-    const float r = m->rng.next_f32();
+    const float r = rng.next_f32();
     float cum = 0.f;
     for (int i = 0; i < V; ++i) {
         cum += lg[i];
         if (r < cum) return (uint32_t)i;
     }
     return (uint32_t)(V - 1);
+}
+
+uint32_t host_choose(atlas_model* m, const float* logits, int step,
+                     const std::vector<uint32_t>& hist, const atlas_sampling* s) {
+    return choose_token(logits, m->cfg.vocab, step, hist.data(), hist.size(), s, m->rng);
 }
 
 void seed_rng(atlas_model* m, const atlas_sampling* s) {
@@ -1369,6 +1375,18 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
     *ms = t;
     *launches = n * iters;
     *bytes = b;
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_sample_host(const float* logits, int vocab, const uint32_t* hist, int n_hist,
+                                int step, const atlas_sampling* s, uint64_t* rng_state,
+                                uint32_t* token) {
+    if (!logits || vocab <= 0 || n_hist < 0 || (n_hist && !hist) || !rng_state || !token ||
+        (s && s->n_suppress > 0 && !s->suppress_initial_tokens))
+        return ATLAS_EINVAL;
+    Rng rng{*rng_state};
+    *token = choose_token(logits, vocab, step, hist, (size_t)n_hist, s, rng);
+    *rng_state = rng.s;
     return ATLAS_OK;
 }
 

@@ -102,6 +102,24 @@ class SamplingConfig:
                               top_p=0.95, top_k=50, min_p=0.05, suppress_initial_tokens=[14023])
 
 
+def sample_host(logits, hist: Sequence[int], step: int, cfg: SamplingConfig,
+                rng_state: int):
+    """One token choice of generate_with_sampling (lib.rs:1623-1711) on the
+    host: returns (token, new XorShift64 state).  ``rng_state`` is the raw
+    state (Rng::from_seed stores seed | 1, lib.rs:1203-1206)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    h = np.ascontiguousarray(list(hist) or [0], np.uint32)
+    sup = np.ascontiguousarray(cfg.suppress_initial_tokens or [0], np.uint32)
+    s = SamplingC(cfg.temperature, cfg.repetition_penalty, cfg.repetition_window,
+                  cfg.frequency_penalty, cfg.presence_penalty, cfg.top_p, cfg.top_k, cfg.min_p,
+                  sup.ctypes.data, len(cfg.suppress_initial_tokens), -1, None, 0, 0)
+    st = C.c_uint64(rng_state & (2**64 - 1))
+    tok = C.c_uint32(0)
+    check(load().atlas_sample_host(_p(lg), lg.size, _p(h), len(hist), step, C.byref(s),
+                                   C.byref(st), C.byref(tok)))
+    return int(tok.value), int(st.value)
+
+
 class OlmoModel:
     """Decode engine handle: weights in HBM, one captured step per token."""
 

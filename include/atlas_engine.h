@@ -131,6 +131,16 @@ int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts, const in
                                int n_seqs, int max_new, const atlas_sampling* s, uint32_t* out,
                                int* n_out);
 
+/* One token choice of generate_with_sampling's loop on the host
+ * (crates/atlas-model/src/lib.rs:1623-1711): step-0 suppression, repetition
+ * penalty over the last repetition_window of hist, greedy argmax, or
+ * frequency / presence penalties, temperature, top-k, top-p, min-p, softmax
+ * and one draw of the XorShift64 Rng (lib.rs:1190-1214) whose state is
+ * *rng_state (advanced in place).  The eos / stop / rng_seed fields are not
+ * read.  Needs no device.                                                   */
+int atlas_sample_host(const float* logits, int vocab, const uint32_t* hist, int n_hist, int step,
+                      const atlas_sampling* s, uint64_t* rng_state, uint32_t* token);
+
 /* Benchmark helper: greedy decode of n_steps tokens continuing from the
  * current state, replaying the captured step with no host synchronisation
  * in between.  tokens (host, may be NULL) receives the chosen ids.          */

@@ -68,6 +68,23 @@ class Layer(C.Structure):
                 ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
 
 
+class Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("repetition_penalty", C.c_float),
+                ("repetition_window", C.c_int), ("frequency_penalty", C.c_float),
+                ("presence_penalty", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int),
+                ("min_p", C.c_float), ("suppress", C.c_void_p), ("n_suppress", C.c_int)]
+
+
+def sampling(temperature=1.0, top_p=1.0, top_k=0, min_p=0.0, repetition_penalty=1.0,
+             repetition_window=64, frequency_penalty=0.0, presence_penalty=0.0, suppress=()):
+    """A Sampling struct; the suppress array is kept alive on the struct."""
+    su = np.ascontiguousarray(list(suppress) or [0], np.uint32)
+    s = Sampling(temperature, repetition_penalty, repetition_window, frequency_penalty,
+                 presence_penalty, top_p, top_k, min_p, su.ctypes.data, len(suppress))
+    s._keep = su
+    return s
+
+
 def _declare(L):
     P, I, I64, F, U64, SZ = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_uint64, C.c_size_t
     sig = {
@@ -104,6 +121,15 @@ def _declare(L):
         "orc_argmax": (I, [P, I]),
         "orc_repetition_penalty": (None, [P, I, P, I, F]),
         "orc_generate_greedy": (I, [P, P, I, I, P, I, F, I, I64, P, I, P]),
+        "orc_rng_next": (F, [C.POINTER(U64)]),
+        "orc_frequency_penalty": (None, [P, I, P, P, I, F]),
+        "orc_presence_penalty": (None, [P, I, P, I, F]),
+        "orc_top_k": (None, [P, I, I]),
+        "orc_top_p": (None, [P, I, F]),
+        "orc_min_p": (None, [P, I, F]),
+        "orc_sample_from_probs": (I, [P, I, F]),
+        "orc_sample_step": (I, [P, I, P, I, I, C.POINTER(Sampling), C.POINTER(U64)]),
+        "orc_generate_sampled": (I, [P, P, I, I, C.POINTER(Sampling), U64, I64, P, I, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -290,6 +316,63 @@ def repetition_penalty(logits, toks, theta):
     return logits
 
 
+# ---- sampling ----------------------------------------------------------------
+
+class Rng:
+    """Rng::from_seed / next_f32 (XorShift64), lib.rs:1203-1214."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64((seed | 1) & (2**64 - 1))
+
+    def next_f32(self) -> float:
+        return lib().orc_rng_next(C.byref(self.state))
+
+
+def frequency_penalty(logits, toks, counts, penalty):
+    logits = np.array(logits, np.float32, copy=True)
+    t = np.ascontiguousarray(toks, np.uint32)
+    c = np.ascontiguousarray(counts, np.uint32)
+    lib().orc_frequency_penalty(_p(logits), logits.size, _p(t), _p(c), t.size, penalty)
+    return logits
+
+
+def presence_penalty(logits, toks, penalty):
+    logits = np.array(logits, np.float32, copy=True)
+    t = np.ascontiguousarray(toks, np.uint32)
+    lib().orc_presence_penalty(_p(logits), logits.size, _p(t), t.size, penalty)
+    return logits
+
+
+def _filter(fn, logits, arg):
+    logits = np.array(logits, np.float32, copy=True)
+    getattr(lib(), fn)(_p(logits), logits.size, arg)
+    return logits
+
+
+def top_k(logits, k):
+    return _filter("orc_top_k", logits, k)
+
+
+def top_p(logits, p):
+    return _filter("orc_top_p", logits, p)
+
+
+def min_p(logits, mp):
+    return _filter("orc_min_p", logits, mp)
+
+
+def sample_from_probs(probs, rand) -> int:
+    p = np.ascontiguousarray(probs, np.float32)
+    return lib().orc_sample_from_probs(_p(p), p.size, rand)
+
+
+def sample_step(logits, hist, step, s: Sampling, rng: Rng) -> int:
+    lg = np.ascontiguousarray(logits, np.float32)
+    h = np.ascontiguousarray(list(hist) or [0], np.uint32)
+    return lib().orc_sample_step(_p(lg), lg.size, _p(h), len(hist), step, C.byref(s),
+                                 C.byref(rng.state))
+
+
 # ---- model ---------------------------------------------------------------------
 
 class Model:
@@ -376,4 +459,14 @@ class Model:
         n = lib().orc_generate_greedy(self.h, _p(pr), pr.size, max_new, _p(su), len(suppress),
                                       rep_penalty, rep_window, -1 if eos is None else eos,
                                       _p(ex), len(extra_stop), _p(out))
+        return [int(t) for t in out[:n]]
+
+    def generate_sampled(self, prompt, max_new, s: Sampling, seed: int, eos=None,
+                         extra_stop=()):
+        pr = np.ascontiguousarray(prompt, np.uint32)
+        ex = np.ascontiguousarray(list(extra_stop) or [0], np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = lib().orc_generate_sampled(self.h, _p(pr), pr.size, max_new, C.byref(s), seed,
+                                       -1 if eos is None else eos, _p(ex), len(extra_stop),
+                                       _p(out))
         return [int(t) for t in out[:n]]

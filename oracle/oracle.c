@@ -570,3 +570,181 @@ int orc_generate_greedy(orc_model* m, const uint32_t* prompt, int n_prompt,
     free(last); free(logits);
     return n_out;
 }
+
+
+/* ---- temperature sampling ------------------------------------------------ */
+float orc_rng_next(uint64_t* state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return (float)(x >> 33) / (float)(1ULL << 31);
+}
+
+void orc_frequency_penalty(float* logits, int n, const uint32_t* toks,
+                           const uint32_t* counts, int n_toks, float penalty) {
+    for (int i = 0; i < n_toks; ++i)
+        if (toks[i] < (uint32_t)n) logits[toks[i]] -= penalty * (float)counts[i];
+}
+
+void orc_presence_penalty(float* logits, int n, const uint32_t* toks, int n_toks,
+                          float penalty) {
+    for (int i = 0; i < n_toks; ++i)
+        if (toks[i] < (uint32_t)n) logits[toks[i]] -= penalty;
+}
+
+static int cmp_desc_f32(const void* a, const void* b) {
+    float x = *(const float*)a, y = *(const float*)b;
+    return (x < y) - (x > y);
+}
+
+void orc_top_k(float* logits, int n, int k) {
+    if (k <= 0 || k >= n) return;
+    float* sorted = (float*)malloc((size_t)n * 4);
+    memcpy(sorted, logits, (size_t)n * 4);
+    qsort(sorted, (size_t)n, 4, cmp_desc_f32);
+    float th = sorted[k - 1];
+    free(sorted);
+    int at_or_above = 0, above = 0;
+    for (int i = 0; i < n; ++i) {
+        if (logits[i] >= th) ++at_or_above;
+        if (logits[i] > th) ++above;
+    }
+    if (at_or_above <= k) {
+        for (int i = 0; i < n; ++i) if (logits[i] < th) logits[i] = -INFINITY;
+    } else {
+        int need = k - above, kept = 0;
+        for (int i = 0; i < n; ++i) {
+            if (logits[i] > th) continue;
+            if (logits[i] == th && kept < need) { ++kept; continue; }
+            logits[i] = -INFINITY;
+        }
+    }
+}
+
+typedef struct { int idx; float p; } orc_ip;
+
+/* probability descending; equal probabilities keep index order */
+static int cmp_ip(const void* a, const void* b) {
+    const orc_ip* x = (const orc_ip*)a;
+    const orc_ip* y = (const orc_ip*)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return (x->idx > y->idx) - (x->idx < y->idx);
+}
+
+void orc_top_p(float* logits, int n, float p) {
+    if (n <= 0) return;
+    float mx = -INFINITY;
+    for (int i = 0; i < n; ++i) mx = rmax(mx, logits[i]);
+    orc_ip* pr = (orc_ip*)malloc((size_t)n * sizeof(orc_ip));
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i) { pr[i].idx = i; pr[i].p = expf(logits[i] - mx); }
+    for (int i = 0; i < n; ++i) sum += pr[i].p;
+    if (sum <= 0.0f) { free(pr); return; }
+    for (int i = 0; i < n; ++i) pr[i].p /= sum;
+    qsort(pr, (size_t)n, sizeof(orc_ip), cmp_ip);
+    float cum = 0.0f;
+    int cut = n;
+    for (int i = 0; i < n; ++i) {
+        cum += pr[i].p;
+        if (cum >= p) { cut = i + 1; break; }
+    }
+    for (int i = cut; i < n; ++i) logits[pr[i].idx] = -INFINITY;
+    free(pr);
+}
+
+void orc_min_p(float* logits, int n, float min_p) {
+    if (min_p <= 0.0f) return;
+    float mx = -INFINITY;
+    for (int i = 0; i < n; ++i) mx = rmax(mx, logits[i]);
+    float th = mx + logf(min_p);
+    for (int i = 0; i < n; ++i) if (logits[i] < th) logits[i] = -INFINITY;
+}
+
+int orc_sample_from_probs(const float* probs, int n, float rand) {
+    float cum = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        cum += probs[i];
+        if (rand < cum) return i;
+    }
+    return n - 1;
+}
+
+int orc_sample_step(const float* logits_in, int n, const uint32_t* hist, int n_hist, int step,
+                    const orc_sampling* s, uint64_t* rng) {
+    float* lg = (float*)malloc((size_t)n * 4);
+    memcpy(lg, logits_in, (size_t)n * 4);
+    /* step-0 suppression and the repetition penalty: lib.rs:1627-1644, 1649-1666 */
+    if (step == 0)
+        for (int i = 0; i < s->n_suppress; ++i)
+            if (s->suppress[i] < (uint32_t)n) lg[s->suppress[i]] = -INFINITY;
+    if (s->repetition_penalty != 1.0f && n_hist > 0) {
+        int start = n_hist > s->repetition_window ? n_hist - s->repetition_window : 0;
+        orc_repetition_penalty(lg, n, hist + start, n_hist - start, s->repetition_penalty);
+    }
+    int tok;
+    if (s->temperature <= 0.0f || s->temperature < 1e-6f) {
+        tok = orc_argmax(lg, n);                       /* lib.rs:1646 */
+    } else {
+        /* frequency penalty over (token, count) in first-seen order: lib.rs:1669-1680 */
+        if (s->frequency_penalty != 0.0f && n_hist > 0) {
+            uint32_t* tk = (uint32_t*)malloc((size_t)n_hist * 4);
+            uint32_t* ct = (uint32_t*)malloc((size_t)n_hist * 4);
+            int nu = 0;
+            for (int i = 0; i < n_hist; ++i) {
+                int j = 0;
+                while (j < nu && tk[j] != hist[i]) ++j;
+                if (j < nu) ++ct[j];
+                else { tk[nu] = hist[i]; ct[nu] = 1; ++nu; }
+            }
+            orc_frequency_penalty(lg, n, tk, ct, nu, s->frequency_penalty);
+            free(tk); free(ct);
+        }
+        /* presence penalty over the sorted, deduplicated history: lib.rs:1683-1688 */
+        if (s->presence_penalty != 0.0f && n_hist > 0) {
+            uint32_t* seen = (uint32_t*)malloc((size_t)n_hist * 4);
+            memcpy(seen, hist, (size_t)n_hist * 4);
+            for (int i = 1; i < n_hist; ++i)                 /* insertion sort */
+                for (int j = i; j > 0 && seen[j - 1] > seen[j]; --j) {
+                    uint32_t t = seen[j]; seen[j] = seen[j - 1]; seen[j - 1] = t;
+                }
+            int nu = 0;
+            for (int i = 0; i < n_hist; ++i)
+                if (nu == 0 || seen[nu - 1] != seen[i]) seen[nu++] = seen[i];
+            orc_presence_penalty(lg, n, seen, nu, s->presence_penalty);
+            free(seen);
+        }
+        for (int i = 0; i < n; ++i) lg[i] /= s->temperature;   /* lib.rs:1691-1693 */
+        if (s->top_k > 0) orc_top_k(lg, n, s->top_k);             /* lib.rs:1696-1698 */
+        if (s->top_p < 1.0f) orc_top_p(lg, n, s->top_p);          /* lib.rs:1701-1703 */
+        if (s->min_p > 0.0f) orc_min_p(lg, n, s->min_p);          /* lib.rs:1706-1708 */
+        orc_softmax(lg, n);                                      /* lib.rs:1711 */
+        tok = orc_sample_from_probs(lg, n, orc_rng_next(rng));
+    }
+    free(lg);
+    return tok;
+}
+
+int orc_generate_sampled(orc_model* m, const uint32_t* prompt, int n_prompt, int max_new,
+                         const orc_sampling* s, uint64_t seed, int64_t eos,
+                         const uint32_t* extra_stop, int n_extra, uint32_t* out) {
+    int V = m->cfg.vocab;
+    uint64_t rng = seed | 1ULL;
+    float* last = (float*)calloc((size_t)V, 4);
+    orc_model_reset(m);
+    for (int i = 0; i < n_prompt; ++i) orc_model_forward_one(m, prompt[i], last, NULL);
+    int n_out = 0;
+    for (int step = 0; step < max_new; ++step) {
+        uint32_t tok = (uint32_t)orc_sample_step(last, V, out, n_out, step, s, &rng);
+        if (eos >= 0 && (int64_t)tok == eos) break;              /* lib.rs:1713-1718 */
+        int stop = 0;
+        for (int i = 0; i < n_extra; ++i) if (extra_stop[i] == tok) stop = 1;
+        if (stop) break;
+        out[n_out++] = tok;
+        orc_model_forward_one(m, tok, last, NULL);
+    }
+    free(last);
+    return n_out;
+}

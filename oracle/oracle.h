@@ -157,6 +157,47 @@ int   orc_generate_greedy(orc_model* m, const uint32_t* prompt, int n_prompt,
                           const uint32_t* extra_stop, int n_extra,
                           uint32_t* out);
 
+/* ---- temperature sampling (generate_with_sampling's sampled branch) ----- */
+/* Rng::next_f32, XorShift64: lib.rs:1208-1214 (state seeded as seed | 1,
+ * Rng::from_seed lib.rs:1203-1206)                                          */
+float orc_rng_next(uint64_t* state);
+/* apply_frequency_penalty lib.rs:2598-2605 (counts in first-seen order),
+ * apply_presence_penalty lib.rs:2610-2617                                    */
+void  orc_frequency_penalty(float* logits, int n, const uint32_t* toks,
+                            const uint32_t* counts, int n_toks, float penalty);
+void  orc_presence_penalty(float* logits, int n, const uint32_t* toks, int n_toks,
+                           float penalty);
+/* apply_top_k lib.rs:2658-2689, apply_top_p lib.rs:2625-2655 (the
+ * reference's unstable sort leaves the order of exactly equal
+ * probabilities unspecified; this one keeps index order), apply_min_p
+ * lib.rs:2692-2699, sample_from_probs lib.rs:2710-2717                      */
+void  orc_top_k(float* logits, int n, int k);
+void  orc_top_p(float* logits, int n, float p);
+void  orc_min_p(float* logits, int n, float min_p);
+int   orc_sample_from_probs(const float* probs, int n, float rand);
+
+typedef struct {
+    float temperature, repetition_penalty;
+    int repetition_window;
+    float frequency_penalty, presence_penalty, top_p;
+    int top_k;
+    float min_p;
+    const uint32_t* suppress;
+    int n_suppress;
+} orc_sampling;
+
+/* One token choice of generate_with_sampling (lib.rs:1623-1711): step-0
+ * suppression, repetition / frequency / presence penalties over `hist`,
+ * greedy argmax when temperature <= 0 or < 1e-6, else temperature, top-k,
+ * top-p, min-p, softmax and a draw from *rng.  logits is copied.            */
+int   orc_sample_step(const float* logits, int n, const uint32_t* hist, int n_hist, int step,
+                      const orc_sampling* s, uint64_t* rng);
+/* The whole loop (lib.rs:1599-1732) with an explicit RNG seed (state =
+ * seed | 1); returns the generated count (EOS / stop tokens end it).        */
+int   orc_generate_sampled(orc_model* m, const uint32_t* prompt, int n_prompt, int max_new,
+                           const orc_sampling* s, uint64_t seed, int64_t eos,
+                           const uint32_t* extra_stop, int n_extra, uint32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

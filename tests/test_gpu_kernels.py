@@ -311,18 +311,20 @@ def test_device_quantisers_bit_exact(orc):
     w[3] = 0.0                                      # all-zero row -> scale 1
     w[5, :10] = [127 * 0.01, 2.5 * 0.01, -2.5 * 0.01, 0, 0, 0, 0, 0, 0, 0]
     q_ref, s_ref = orc.int8_quantize(w)
-    dq, ds = Dev.empty(w.shape, np.int8), Dev.empty(257)
-    assert lib().atlas_quantize_int8_dev(Dev(w).ptr, 0, 257, 192, dq.ptr, ds.ptr) == 0
+    # every device buffer stays referenced until the results are read back
+    dw, dq, ds = Dev(w), Dev.empty(w.shape, np.int8), Dev.empty(257)
+    assert lib().atlas_quantize_int8_dev(dw.ptr, 0, 257, 192, dq.ptr, ds.ptr) == 0
     assert np.array_equal(dq.get(), q_ref) and np.array_equal(ds.get(), s_ref)
     for bs in (32, 64, 50):
         q4, s4 = orc.int4_quantize(w, bs)
         d4, d4s = Dev.empty(q4.shape, np.uint8), Dev.empty(s4.shape)
-        assert lib().atlas_quantize_int4_dev(Dev(w).ptr, 0, w.size, bs, d4.ptr, d4s.ptr) == 0
+        assert lib().atlas_quantize_int4_dev(dw.ptr, 0, w.size, bs, d4.ptr, d4s.ptr) == 0
         assert np.array_equal(d4.get(), q4) and np.array_equal(d4s.get(), s4), bs
     # bf16-bits input quantises the widened values
     bits = orc.bf16_from_f32(w)
     q_ref, s_ref = orc.int8_quantize(orc.bf16_to_f32(bits))
-    assert lib().atlas_quantize_int8_dev(Dev(bits).ptr, 1, 257, 192, dq.ptr, ds.ptr) == 0
+    dbits = Dev(bits)
+    assert lib().atlas_quantize_int8_dev(dbits.ptr, 1, 257, 192, dq.ptr, ds.ptr) == 0
     assert np.array_equal(dq.get(), q_ref) and np.array_equal(ds.get(), s_ref)
 
 
