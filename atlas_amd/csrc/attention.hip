@@ -59,16 +59,6 @@ struct ScanBufs {
 
 // kb/vb point at dim 0 of the KV head in row 0; rows [0, e1) are readable.
 // The caller guarantees e1 * row_bytes < 2^32.
-__device__ __forceinline__ float* uniform_ptr(const float* p) {
-    // the value is block-uniform; readfirstlane makes that visible to the
-    // compiler, which otherwise may keep it in VGPRs and wrap every buffer
-    // load in a waterfall loop
-    const uint64_t u = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-    return (float*)(((uint64_t)hi << 32) | lo);
-}
-
 __device__ __forceinline__ ScanBufs scan_bufs(const float* kb, const float* vb, long kv_stride,
                                               int e1, int lane_dims) {
     ScanBufs b;

@@ -114,4 +114,15 @@ __device__ __forceinline__ u32x4 ldg_stream(const u32x4* p) {
     return __builtin_nontemporal_load(p);
 }
 
+// A block-uniform pointer made visible as uniform (readfirstlane of both
+// halves).  Buffer descriptors built from it live in SGPRs; built from a
+// VGPR pointer, every buffer load would be wrapped in a waterfall loop.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(const T* p) {
+    const uint64_t u = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (T*)(((uint64_t)hi << 32) | lo);
+}
+
 }  // namespace atlas

@@ -40,6 +40,8 @@ struct DevMat {
     void* w = nullptr;
     float* scales = nullptr;
     int rows = 0, cols = 0, block = 0;
+    size_t pitch = 0;        // bytes between rows in HBM; 0 = packed (row_bytes)
+    size_t row_pitch() const { return pitch ? pitch : row_bytes(); }
     size_t row_bytes() const {
         switch (fmt) {
         case WF_F32: return (size_t)cols * 4;
@@ -53,7 +55,8 @@ struct DevMat {
         if (fmt == WF_I4) return (size_t)cols / block;
         return 0;
     }
-    size_t data_bytes() const { return row_bytes() * rows; }
+    size_t data_bytes() const { return row_bytes() * rows; }     // algorithmic bytes
+    size_t alloc_bytes() const { return row_pitch() * rows; }
     size_t scale_count() const { return scales_per_row() * rows; }
 };
 
@@ -141,12 +144,23 @@ int dalloc(atlas_model* m, void** p, size_t bytes) {
         if (rc_) return rc_;      \
     } while (0)
 
+// Row pitch in HBM.  bf16 rows longer than 8 KB whose length is not a
+// multiple of 4 KB (the 7B W_down: 22016 B) stream ~10% faster with one
+// extra 256-byte gap per row; other rows are stored packed.
+size_t pad_pitch(int fmt, int cols) {
+    if (fmt != WF_BF16 || cols <= 4096) return 0;
+    const size_t rb = (size_t)cols * 2;
+    if (rb % 4096 == 0) return 0;
+    return (rb + 255) / 256 * 256 + 256;
+}
+
 int alloc_mat(atlas_model* m, DevMat& d, int fmt, int rows, int cols, int block) {
     d.fmt = fmt;
     d.rows = rows;
     d.cols = cols;
     d.block = block;
-    TRY(dalloc(m, &d.w, d.data_bytes()));
+    d.pitch = pad_pitch(fmt, cols);
+    TRY(dalloc(m, &d.w, d.alloc_bytes()));
     if (d.scale_count()) TRY(dalloc(m, (void**)&d.scales, d.scale_count() * 4));
     return ATLAS_OK;
 }
@@ -163,6 +177,7 @@ GemvArgs gemv_args(const DevMat& w, const float* x, float* y, int epi) {
     a.K = w.cols;
     a.epi = epi;
     a.N = 1;
+    a.ldw = (long)w.pitch;
     return a;
 }
 
@@ -638,14 +653,14 @@ void seed_rng(atlas_model* m, const atlas_sampling* s) {
 // row index is base + r * stride (stride 2 interleaves gate/up).
 int place_rows(atlas_model* m, DevMat& dst, int base, int stride, int rows, const void* data,
                const float* scales, bool upload) {
-    const size_t rb = dst.row_bytes();
+    const size_t rb = dst.row_bytes(), rp = dst.row_pitch();
     const size_t spr = dst.scales_per_row();
     const hipMemcpyKind kind = upload ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
-    char* dptr = (char*)dst.w + (size_t)base * rb;
+    char* dptr = (char*)dst.w + (size_t)base * rp;
     if (upload)
-        ATLAS_HIP(hipMemcpy2DAsync(dptr, rb * stride, data, rb, rb, rows, kind, m->st));
+        ATLAS_HIP(hipMemcpy2DAsync(dptr, rp * stride, data, rb, rb, rows, kind, m->st));
     else
-        ATLAS_HIP(hipMemcpy2DAsync((void*)data, rb, dptr, rb * stride, rb, rows, kind, m->st));
+        ATLAS_HIP(hipMemcpy2DAsync((void*)data, rb, dptr, rp * stride, rb, rows, kind, m->st));
     if (spr) {
         ATLAS_REQUIRE(scales, "tensor needs scales for format %d", dst.fmt);
         float* sptr = dst.scales + (size_t)base * spr;
@@ -1007,15 +1022,15 @@ ATLAS_API int atlas_model_init_random(atlas_model* m, uint64_t seed) {
         const long n = (long)rows * dst.cols;
         if (fmt == WF_BF16) {
             TRY(init_launch(INIT_NORMAL_BF16, tmp, n, sub(kind, layer), 0.f, 0.02f, m->st));
-            const size_t rb = dst.row_bytes();
-            ATLAS_HIP(hipMemcpy2DAsync((char*)dst.w + (size_t)base * rb, rb * stride, tmp, rb, rb, rows,
+            const size_t rb = dst.row_bytes(), rp = dst.row_pitch();
+            ATLAS_HIP(hipMemcpy2DAsync((char*)dst.w + (size_t)base * rp, rp * stride, tmp, rb, rb, rows,
                                        hipMemcpyDeviceToDevice, m->st));
         } else {
             TRY(init_launch(INIT_NORMAL_F32, tmp, n, sub(kind, layer), 0.f, 0.02f, m->st));
             if (fmt == WF_I8) TRY(quant_i8_launch(tmp, 0, rows, dst.cols, (int8_t*)qd, qs, m->st));
             else TRY(quant_i4_launch(tmp, 0, n, dst.block, (uint8_t*)qd, qs, m->st));
-            const size_t rb = dst.row_bytes(), spr = dst.scales_per_row();
-            ATLAS_HIP(hipMemcpy2DAsync((char*)dst.w + (size_t)base * rb, rb * stride, qd, rb, rb, rows,
+            const size_t rb = dst.row_bytes(), rp = dst.row_pitch(), spr = dst.scales_per_row();
+            ATLAS_HIP(hipMemcpy2DAsync((char*)dst.w + (size_t)base * rp, rp * stride, qd, rb, rb, rows,
                                        hipMemcpyDeviceToDevice, m->st));
             ATLAS_HIP(hipMemcpy2DAsync(dst.scales + (size_t)base * spr, spr * 4 * stride, qs, spr * 4,
                                        spr * 4, rows, hipMemcpyDeviceToDevice, m->st));

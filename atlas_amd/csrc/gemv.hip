@@ -150,11 +150,37 @@ __device__ __forceinline__ void stage_x_regs(const GemvArgs& a, f32x4* xs, int K
     }
 }
 
+// Plain x (no prologue) of up to 256 * PPT pieces: every load is issued
+// before the first LDS write, so staging costs one round trip for any K the
+// registers hold (PPT = 12: K <= 12288).  Buffer loads address all pieces
+// from one VGPR offset (the piece stride goes in the SGPR offset), and reads
+// past the end of x return zeros that are never stored.
+template <bool SWZ, int PPT>
+__device__ __forceinline__ void stage_x_plain(const GemvArgs& a, f32x4* xs, int K) {
+    const int np = K >> 2;
+    const __amdgpu_buffer_rsrc_t xb =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.x), (short)0, K * 4, 0x00020000);
+    f32x4 xv[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j)
+        xv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              xb, (int)threadIdx.x * 16, 4096 * j, 0));
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+        const int p = threadIdx.x + 256 * j;
+        if (p < np) xs[SWZ ? swz(p) : p] = xv[j];
+    }
+}
+
 // General staging: any K the LDS holds, and the SwiGLU prologue.
 template <bool SWZ>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, f32x4* xs, int K) {
     if (a.pro != PRO_SILU && K <= 256 * 4 * 4) {    // d_model <= 4096: 48 VGPRs
         stage_x_regs<SWZ, 4>(a, xs, K);
+        return;
+    }
+    if (a.pro == PRO_X && K <= 256 * 4 * 12) {      // e.g. the W_down input
+        stage_x_plain<SWZ, 12>(a, xs, K);
         return;
     }
     __shared__ float red4[4];
@@ -215,6 +241,7 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int chunks = K / EPC;                   // 16-byte chunks per row
+    const long ldc = a.ldw > 0 ? a.ldw / 16 : chunks;   // chunks between rows
     const u32x4* W = reinterpret_cast<const u32x4*>(a.w);
     // One-row waves with the SwiGLU epilogue take a (gate, up) row pair one
     // row after the other (SEQ = 2): the pair's epilogue stays in the wave
@@ -242,7 +269,7 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const int row = g * ROWS + r < M ? g * ROWS + r : M - 1;
-                wb[u][r] = c < chunks ? ldg_stream(W + (long)row * chunks + c)
+                wb[u][r] = c < chunks ? ldg_stream(W + (long)row * ldc + c)
                                       : u32x4{0u, 0u, 0u, 0u};
                 if constexpr (FMT == WF_I4) {
                     long bi;
@@ -343,14 +370,18 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(GemvArgs a) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.M) return;
     float acc = 0.0f;
+    // rows start ldw bytes apart when ldw is set (f32 / bf16 / int8 only)
+    constexpr int ESZ = FMT == WF_F32 ? 4 : FMT == WF_BF16 ? 2 : 1;
+    const long rs = (FMT != WF_I4 && a.ldw > 0) ? a.ldw / ESZ : a.K;
     for (int k = lane; k < a.K; k += 64) {
         const long e = (long)row * a.K + k;
         float w;
-        if constexpr (FMT == WF_F32) w = reinterpret_cast<const float*>(a.w)[e];
+        if constexpr (FMT == WF_F32) w = reinterpret_cast<const float*>(a.w)[(long)row * rs + k];
         else if constexpr (FMT == WF_BF16)
-            w = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.w)[e] << 16);
+            w = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.w)[(long)row * rs + k]
+                                << 16);
         else if constexpr (FMT == WF_I8)
-            w = (float)reinterpret_cast<const int8_t*>(a.w)[e] * a.scales[row];
+            w = (float)reinterpret_cast<const int8_t*>(a.w)[(long)row * rs + k] * a.scales[row];
         else {
             const uint8_t b = reinterpret_cast<const uint8_t*>(a.w)[e >> 1];
             const int nib = (e & 1) ? (b & 0x0F) : (b >> 4);
@@ -485,7 +516,8 @@ int gemv_fast_ok(int fmt, int K, int block) {
 
 // Launch shape per (format, K): rows per wave, chunk unroll, blocks per CU.
 // Chosen by sweeping the 7B decode shapes on MI355X over >= 1.1 GB of
-// rotating weights (rows = 1 wins: more waves in flight per CU).
+// rotating weights (rows = 1 wins at K = 4096: more waves in flight per CU;
+// the bf16 W_down, 4096 x 11008 with padded rows, prefers two-row waves).
 struct N1Shape { int rows, unroll, bpc; };
 static N1Shape n1_shape(int fmt, int M, int K, int epi) {
     // SwiGLU epilogue: bf16 two-row waves; int8/int4 one-row waves taking
@@ -494,7 +526,7 @@ static N1Shape n1_shape(int fmt, int M, int K, int epi) {
         return fmt == WF_BF16 ? N1Shape{2, 4, 8} : fmt == WF_I8 ? N1Shape{1, 4, 8} : N1Shape{1, 2, 8};
     const bool big_k = K > 4096;
     switch (fmt) {
-    case WF_BF16: return big_k ? N1Shape{1, 8, 2} : N1Shape{1, 4, 8};
+    case WF_BF16: return big_k ? N1Shape{2, 4, 3} : N1Shape{1, 4, 8};
     case WF_I8:   return big_k ? N1Shape{1, 8, 16} : (M >= 65536 ? N1Shape{1, 4, 4} : N1Shape{1, 2, 8});
     case WF_I4:   return big_k ? N1Shape{2, 2, 8} : N1Shape{1, 2, 8};
     default:      return {1, 4, 8};
@@ -503,7 +535,7 @@ static N1Shape n1_shape(int fmt, int M, int K, int epi) {
 
 // The instantiations gemv_launch dispatches to.
 #define ATLAS_N1_LIST(X)                                                           \
-    X(WF_BF16, 1, 4) X(WF_BF16, 1, 8) X(WF_BF16, 2, 4)                             \
+    X(WF_BF16, 1, 4) X(WF_BF16, 2, 4)                                              \
     X(WF_I8, 1, 2) X(WF_I8, 1, 4) X(WF_I8, 1, 8)                    \
     X(WF_I4, 1, 2) X(WF_I4, 2, 2)                                                  \
     X(WF_F32, 1, 4) X(WF_F32, 2, 4)
@@ -543,6 +575,7 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
         set_error(ATLAS_EUNSUPPORTED, "gemv: K == 0");
         return ATLAS_EUNSUPPORTED;
     }
+    ATLAS_REQUIRE(gemv_pitch_ok(a), "gemv: row pitch %ld bytes for K %d", a.ldw, a.K);
     const uintptr_t align = (uintptr_t)a.w | (uintptr_t)a.x | (uintptr_t)a.pro_y |
                             (uintptr_t)a.pro_w | (uintptr_t)a.pro_out;
     const bool fast = (align & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
@@ -558,6 +591,7 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     }
     ATLAS_REQUIRE(a.epi == EPI_STORE && a.pro == PRO_X,
                   "gemv: fused prologue/epilogue needs an aligned fast-path shape");
+    ATLAS_REQUIRE(a.fmt != WF_I4 || a.ldw == 0, "gemv: int4 row pitch needs the fast path");
     const int blocks = (a.M + 3) / 4;
     switch (a.fmt) {
     case WF_F32:  hipLaunchKernelGGL(gemv_generic_kernel<WF_F32>, dim3(blocks), dim3(256), 0, st, a); break;

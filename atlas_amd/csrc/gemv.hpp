@@ -35,6 +35,7 @@ struct GemvArgs {
     float pro_eps;
     float* pro_out;          // RESNORM / RMSNORM: x written out by block 0 (nullable)
     unsigned long long* arg_part;   // EPI_ARGMAX: per-wave (value, index) keys
+    long ldw;                // bytes between weight rows (multiple of 16); 0 = packed rows
 };
 
 enum { GEMV_MAX_WAVES = 16384 };    // bound on persistent waves (argmax partials)
@@ -46,6 +47,17 @@ int skinny_launch(const GemvArgs& a, hipStream_t st);   // 1 <= N <= 8
 int skinny_reserve(int M, int N, int K);
 int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,
                         hipStream_t st);
+
+// packed bytes of one weight row
+inline long gemv_row_bytes(int fmt, int K) {
+    return fmt == WF_F32 ? 4L * K : fmt == WF_BF16 ? 2L * K : fmt == WF_I8 ? (long)K : K / 2;
+}
+
+// a row pitch is 0 (packed) or a multiple of 16 bytes that holds the row
+inline bool gemv_pitch_ok(const GemvArgs& a) {
+    return a.ldw == 0 || (a.ldw % 16 == 0 && a.ldw >= gemv_row_bytes(a.fmt, a.K) &&
+                          (a.fmt != WF_I4 || a.K % 2 == 0));
+}
 
 inline void gemv_fill_int4_index(GemvArgs& a) {
     a.bpr = 0;

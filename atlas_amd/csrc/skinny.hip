@@ -74,7 +74,7 @@ template <int FMT>
 __device__ __forceinline__ SkRow sk_row(const GemvArgs& a, int row) {
     SkRow r;
     constexpr int NUM = FMT == WF_BF16 ? 2 : 1, DEN = FMT == WF_I4 ? 2 : 1;
-    r.w = reinterpret_cast<const uint8_t*>(a.w) + (long)row * a.K * NUM / DEN;
+    r.w = reinterpret_cast<const uint8_t*>(a.w) + (long)row * (a.ldw > 0 ? a.ldw : (long)a.K * NUM / DEN);
     r.s = FMT == WF_I4 ? a.scales + (long)row * a.bpr : nullptr;
     return r;
 }
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float
     }
     struct Pf { u32x4 d[NPC]; float s[NPC]; };
     const uint8_t* wbase = reinterpret_cast<const uint8_t*>(a.w) + kt0 * 16;
-    const long wstride = a.K / 2;
+    const long wstride = a.ldw > 0 ? a.ldw : a.K / 2;
     auto fetch = [&](int t, Pf& f) {
 #pragma unroll
         for (int q = 0; q < NPC; ++q) {
@@ -544,6 +544,7 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     if (a.epi == EPI_SILU_MUL) ATLAS_REQUIRE(a.M % 2 == 0, "skinny: silu-mul needs even rows");
     if (a.M == 0) return ATLAS_OK;
     ATLAS_REQUIRE(a.K % 32 == 0 && a.K > 0, "skinny: K %% 32 != 0");
+    ATLAS_REQUIRE(gemv_pitch_ok(a), "skinny: row pitch %ld bytes for K %d", a.ldw, a.K);
     const uintptr_t al = (uintptr_t)a.w;
     switch (a.fmt) {
     case WF_BF16:

@@ -201,6 +201,26 @@ def test_ragged_batch_matches_single(orc):
     assert len(m.generate_with_sampling(prompts[0], 8, SamplingConfig.greedy())) == 8
 
 
+def test_padded_rows_wide_ffn(orc):
+    # ffn_hidden 4352: the bf16 W_down rows (8704 B, not a multiple of 4 KB)
+    # are stored with a padded pitch; decode, tensor download and the ragged
+    # batch (skinny GEMM) must all read through the pitch
+    cfg = modelgen.olmo3_small_config(n_layers=2, ffn_hidden=4352, max_seq=64)
+    W = modelgen.make_weights(cfg, seed=31, fmt="bf16")
+    toks = np.random.default_rng(2).integers(0, cfg["vocab"], 12)
+    assert _teacher_forced(W, toks) <= LOGIT_TOL
+    from atlas_amd import model as am
+    m = modelgen.engine_model(W, max_batch=4)
+    want = W["layers"][1]["w_down_stored"][1][0]
+    got = m.get_tensor(am.T_W_DOWN, 1, want.shape, np.uint16)
+    assert np.array_equal(got, want)
+    prompts = [[1, 2, 3], [7], [9, 8, 7, 6, 5]]
+    batch = m.generate_batch(prompts, 6)
+    for p, b in zip(prompts, batch):
+        m2 = modelgen.engine_model(W)
+        assert b == m2.generate_with_sampling(p, 6, am.SamplingConfig.greedy()), p
+
+
 def test_init_random_weights_roundtrip(orc):
     from atlas_amd import model as am
     cfg = am.ModelConfig(vocab_size=300, d_model=128, n_layers=2, n_heads=2, n_kv_heads=1,
