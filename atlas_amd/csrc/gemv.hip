@@ -27,7 +27,12 @@
 
 namespace atlas {
 
-__device__ __forceinline__ int swz(int p) { return p ^ ((p >> 3) & 7); }
+// x lives in LDS as 16-byte pieces with one empty piece after every 16
+// (piece p at p + p / 16).  A lane's chunk reads PPC <= 8 consecutive pieces
+// starting at a multiple of PPC, which never straddle a gap, so the reads
+// take immediate offsets from one base address; the gaps spread the lanes
+// of a 16-lane group over distinct banks for every PPC in {1, 2, 4, 8}.
+__device__ __forceinline__ int xpad(int p) { return p + (p >> 4); }
 
 template <int FMT> struct WT;
 template <> struct WT<WF_F32>  { static constexpr int EPC = 4;  };   // elems per 16 B
@@ -35,18 +40,22 @@ template <> struct WT<WF_BF16> { static constexpr int EPC = 8;  };
 template <> struct WT<WF_I8>   { static constexpr int EPC = 16; };
 template <> struct WT<WF_I4>   { static constexpr int EPC = 32; };
 
-// dot of one 16-byte weight chunk with its EPC x values (from swizzled LDS).
+// dot of one 16-byte weight chunk with its EPC x values (padded LDS layout;
+// p0 is the chunk's first piece, a multiple of the pieces per chunk).
 template <int FMT>
-__device__ __forceinline__ float chunk_dot(const u32x4 w, const f32x4* __restrict__ xs,
+__device__ __forceinline__ float chunk_dot(const u32x4 w, const f32x4* __restrict__ xs_all,
                                            int p0, float acc) {
+    int b = xpad(p0);
+    asm volatile("" : "+v"(b));    // one base address; the pieces take immediate offsets
+    const f32x4* __restrict__ xs = xs_all + b;
     if constexpr (FMT == WF_F32) {
-        f32x4 x = xs[swz(p0)];
+        f32x4 x = xs[0];
         acc += __uint_as_float(w.x) * x.x;
         acc += __uint_as_float(w.y) * x.y;
         acc += __uint_as_float(w.z) * x.z;
         acc += __uint_as_float(w.w) * x.w;
     } else if constexpr (FMT == WF_BF16) {
-        f32x4 x0 = xs[swz(p0)], x1 = xs[swz(p0 + 1)];
+        f32x4 x0 = xs[0], x1 = xs[1];
         acc += bf16_lo(w.x) * x0.x;  acc += bf16_hi(w.x) * x0.y;
         acc += bf16_lo(w.y) * x0.z;  acc += bf16_hi(w.y) * x0.w;
         acc += bf16_lo(w.z) * x1.x;  acc += bf16_hi(w.z) * x1.y;
@@ -55,7 +64,7 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const f32x4* __restric
         const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            f32x4 x = xs[swz(p0 + j)];
+            f32x4 x = xs[j];
             acc += s8_at(ww[j], 0) * x.x;
             acc += s8_at(ww[j], 1) * x.y;
             acc += s8_at(ww[j], 2) * x.z;
@@ -67,7 +76,7 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const f32x4* __restric
         for (int j = 0; j < 4; ++j) {
             const uint32_t hi = ww[j] & 0xF0F0F0F0u;          // even elements * 16
             const uint32_t lo = (ww[j] << 4) & 0xF0F0F0F0u;   // odd elements * 16
-            f32x4 xa = xs[swz(p0 + 2 * j)], xb = xs[swz(p0 + 2 * j + 1)];
+            f32x4 xa = xs[2 * j], xb = xs[2 * j + 1];
             acc += s8_at(hi, 0) * xa.x;
             acc += s8_at(lo, 0) * xa.y;
             acc += s8_at(hi, 1) * xa.z;
@@ -144,7 +153,7 @@ __device__ __forceinline__ void stage_x_regs(const GemvArgs& a, f32x4* xs, int K
             if (res) r = xv[j] + (yv[j] * inv) * wv[j];
             else if (norm) r = (xv[j] * inv) * wv[j];
             else r = xv[j];
-            xs[SWZ ? swz(p) : p] = r;
+            xs[SWZ ? xpad(p) : p] = r;
             if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = r;
         }
     }
@@ -168,7 +177,7 @@ __device__ __forceinline__ void stage_x_plain(const GemvArgs& a, f32x4* xs, int 
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
         const int p = threadIdx.x + 256 * j;
-        if (p < np) xs[SWZ ? swz(p) : p] = xv[j];
+        if (p < np) xs[SWZ ? xpad(p) : p] = xv[j];
     }
 }
 
@@ -219,7 +228,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, f32x4* xs, int K) {
             r = f32x4{silu_f(g0.x) * g0.y, silu_f(g0.z) * g0.w, silu_f(g1.x) * g1.y,
                       silu_f(g1.z) * g1.w};
         }
-        xs[SWZ ? swz(p) : p] = r;
+        xs[SWZ ? xpad(p) : p] = r;
         if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = r;
     }
 }
@@ -478,7 +487,7 @@ static int resident_per_cu(const void* kern, size_t lds) {
 static int n1_blocks(const void* kern, int M, int K, int rows, int blocks_per_cu) {
     const int n_groups = (M + rows - 1) / rows;
     const int blocks = (n_groups + 3) / 4;
-    const int fit = resident_per_cu(kern, (size_t)K * 4);
+    const int fit = resident_per_cu(kern, gemv_x_lds_bytes(K));
     if (fit < 1) return 0;
     const int bpc = blocks_per_cu < fit ? blocks_per_cu : fit;
     const int cap = bpc * device_cu_count();
@@ -492,8 +501,8 @@ static int n1_group_rows(const GemvArgs& a, int rows) {
 
 template <int FMT, int ROWS, int UNROLL>
 int launch_n1(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
-    const size_t lds = (size_t)a.K * 4;
-    ATLAS_REQUIRE(lds <= 160 * 1024, "gemv: K=%d exceeds the LDS-staged limit 40960", a.K);
+    const size_t lds = gemv_x_lds_bytes(a.K);
+    ATLAS_REQUIRE(lds <= 160 * 1024, "gemv: K=%d exceeds the LDS-staged limit", a.K);
     auto kern = gemv_n1_kernel<FMT, ROWS, UNROLL>;
     const int blocks = n1_blocks((const void*)kern, a.M, a.K, n1_group_rows(a, ROWS), blocks_per_cu);
     ATLAS_REQUIRE(blocks > 0, "gemv: the kernel does not fit a CU at K=%d", a.K);
@@ -579,7 +588,7 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     const uintptr_t align = (uintptr_t)a.w | (uintptr_t)a.x | (uintptr_t)a.pro_y |
                             (uintptr_t)a.pro_w | (uintptr_t)a.pro_out;
     const bool fast = (align & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
-                      (size_t)a.K * 4 <= 160 * 1024;
+                      gemv_x_lds_bytes(a.K) <= 160 * 1024;
     if (fast) {
         const N1Shape sh = n1_shape(a.fmt, a.M, a.K, a.epi);
 #define ATLAS_N1(F, R, U) \

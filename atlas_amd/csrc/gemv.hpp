@@ -48,6 +48,13 @@ int skinny_reserve(int M, int N, int K);
 int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,
                         hipStream_t st);
 
+// LDS bytes of the batch-1 GEMV's staged x: K / 4 pieces of 16 bytes plus
+// one gap piece per 16
+inline size_t gemv_x_lds_bytes(int K) {
+    const size_t np = (size_t)K / 4;
+    return (np + (np + 15) / 16) * 16;
+}
+
 // packed bytes of one weight row
 inline long gemv_row_bytes(int fmt, int K) {
     return fmt == WF_F32 ? 4L * K : fmt == WF_BF16 ? 2L * K : fmt == WF_I8 ? (long)K : K / 2;
