@@ -268,23 +268,25 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
         return ((g0 + (it / (iters * SEQ)) * S) * SEQ + (it / iters) % SEQ) * ROWS;
     };
 
-    // weights (and int4 block scales) of step `it` into registers
+    // Weights (and raw int4 block scales) of step `it` into registers.  The
+    // loads are unconditional (chunk and row clamped into the matrix; the
+    // compute skips lanes past the row end) and nothing consumes them here,
+    // so the prefetch never forces a wait on the loads in flight.
     auto load = [&](int it, u32x4 (&wb)[UNROLL][ROWS], float (&sb)[UNROLL][ROWS]) {
         const int g = row_of(it) / ROWS;
         const int c0 = lane + (it % iters) * STEP;
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            const int c = c0 + 64 * u;
+            const int c = min(c0 + 64 * u, chunks - 1);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const int row = g * ROWS + r < M ? g * ROWS + r : M - 1;
-                wb[u][r] = c < chunks ? ldg_stream(W + (long)row * ldc + c)
-                                      : u32x4{0u, 0u, 0u, 0u};
+                wb[u][r] = ldg_stream(W + (long)row * ldc + c);
                 if constexpr (FMT == WF_I4) {
                     long bi;
                     if (a.bpr > 0) bi = (long)row * a.bpr + (a.cpb == 1 ? c : c / a.cpb);
                     else bi = ((long)row * K + (long)c * EPC) / a.block;
-                    sb[u][r] = c < chunks ? a.scales[bi] * 0.0625f : 0.0f;
+                    sb[u][r] = a.scales[bi];
                 }
             }
         }
@@ -327,6 +329,11 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
             const int r0 = row_of(it);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
+            if constexpr (FMT == WF_I4) {
+                // the chunks hold 16 * q: one exact power-of-two rescale per row
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) acc[r] *= 0.0625f;
+            }
             if constexpr (FMT == WF_I8) {
 #pragma unroll
                 for (int r = 0; r < ROWS; ++r) acc[r] *= a.scales[r0 + r < M ? r0 + r : M - 1];
@@ -529,15 +536,17 @@ int gemv_fast_ok(int fmt, int K, int block) {
 // the bf16 W_down, 4096 x 11008 with padded rows, prefers two-row waves).
 struct N1Shape { int rows, unroll, bpc; };
 static N1Shape n1_shape(int fmt, int M, int K, int epi) {
-    // SwiGLU epilogue: bf16 two-row waves; int8/int4 one-row waves taking
-    // the pair in sequence (their two-row variants need ~100-170 VGPRs)
+    (void)M;
+    // SwiGLU epilogue: bf16 and int4 two-row waves hold the (gate, up) pair;
+    // int8 one-row waves take the pair in sequence (its two-row variant
+    // needs ~170 VGPRs)
     if (epi == EPI_SILU_MUL)
-        return fmt == WF_BF16 ? N1Shape{2, 4, 8} : fmt == WF_I8 ? N1Shape{1, 4, 8} : N1Shape{1, 2, 8};
+        return fmt == WF_BF16 ? N1Shape{2, 4, 8} : fmt == WF_I8 ? N1Shape{1, 4, 8} : N1Shape{2, 2, 4};
     const bool big_k = K > 4096;
     switch (fmt) {
     case WF_BF16: return big_k ? N1Shape{2, 4, 3} : N1Shape{1, 4, 8};
-    case WF_I8:   return big_k ? N1Shape{1, 8, 16} : (M >= 65536 ? N1Shape{1, 4, 4} : N1Shape{1, 2, 8});
-    case WF_I4:   return big_k ? N1Shape{2, 2, 8} : N1Shape{1, 2, 8};
+    case WF_I8:   return big_k ? N1Shape{1, 4, 8} : N1Shape{1, 2, 8};
+    case WF_I4:   return N1Shape{2, 2, 8};
     default:      return {1, 4, 8};
     }
 }
@@ -545,8 +554,8 @@ static N1Shape n1_shape(int fmt, int M, int K, int epi) {
 // The instantiations gemv_launch dispatches to.
 #define ATLAS_N1_LIST(X)                                                           \
     X(WF_BF16, 1, 4) X(WF_BF16, 2, 4)                                              \
-    X(WF_I8, 1, 2) X(WF_I8, 1, 4) X(WF_I8, 1, 8)                    \
-    X(WF_I4, 1, 2) X(WF_I4, 2, 2)                                                  \
+    X(WF_I8, 1, 2) X(WF_I8, 1, 4)                                                  \
+    X(WF_I4, 2, 2)                                                                 \
     X(WF_F32, 1, 4) X(WF_F32, 2, 4)
 
 static const void* n1_kernel(int fmt, int rows, int unroll) {
