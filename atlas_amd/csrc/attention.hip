@@ -22,6 +22,8 @@
 //    (m, l, o) per head and split; attn_combine merges the splits.
 //  * the split count is fixed at launch and `pos` may come from device
 //    memory, so the same launch can be captured once and replayed per token.
+#include <algorithm>
+
 #include "common.hpp"
 #include "attention.hpp"
 
@@ -242,20 +244,34 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     }
 }
 
+// Split merge of the reference-ABI path: one block per query head.  The
+// split maxima and weights go through LDS once; every (split, dim) partial is
+// then an independent load, so the sum streams instead of waiting on each
+// split in turn.  Empty splits carry (m, l, o) = (-inf, 0, 0) and weigh 0.
+constexpr int kAttnMaxSplits = 256;
+
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int n_splits, int hd) {
+    __shared__ float s_w[kAttnMaxSplits];
+    __shared__ float s_red[4];
     const int qh = blockIdx.x;
+    const long base = (long)qh * n_splits;
+    float mx = -INFINITY;
+    for (int s = threadIdx.x; s < n_splits; s += blockDim.x) mx = fmaxf(mx, a.part_m[base + s]);
+    mx = wave_max(mx);
+    const int nw = (blockDim.x + 63) >> 6;
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = s_red[0];
+    for (int w = 1; w < nw; ++w) mx = fmaxf(mx, s_red[w]);
+    for (int s = threadIdx.x; s < n_splits; s += blockDim.x)
+        s_w[s] = exp2f(a.part_m[base + s] - mx);
+    __syncthreads();
+    float lsum = 0.f;
+    for (int s = 0; s < n_splits; ++s) lsum += a.part_l[base + s] * s_w[s];
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float mx = -INFINITY;
-        for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, a.part_m[(long)qh * n_splits + s]);
-        float lsum = 0.f, osum = 0.f;
-        for (int s = 0; s < n_splits; ++s) {
-            const long pi = (long)qh * n_splits + s;
-            const float mm = a.part_m[pi];
-            if (mm == -INFINITY) continue;
-            const float w = exp2f(mm - mx);
-            lsum += a.part_l[pi] * w;
-            osum += a.part_o[pi * hd + d] * w;
-        }
+        float osum = 0.f;
+#pragma unroll 8
+        for (int s = 0; s < n_splits; ++s) osum += a.part_o[(base + s) * hd + d] * s_w[s];
         a.out[(long)qh * hd + d] = osum / lsum;
     }
 }
@@ -579,6 +595,19 @@ int attn_max_splits(int n_kv) {
     return s < 1 ? 1 : (s > 8 ? 8 : s);
 }
 
+int attn_pick_splits_unfused(int n_kv, int ctx) {
+    // split + combine kernels (no cross-block merge): at least ~128 blocks
+    // while splits keep >= 32 positions, at most 512 positions per split,
+    // and at most 256 blocks (measured at the GQA 32/8/128 shape, ctx
+    // 512..16384: 32..512 positions per split stream fastest)
+    const int nkv = n_kv > 0 ? n_kv : 1;
+    int s = (ctx + kAttnSplitChunk - 1) / kAttnSplitChunk;
+    const int wide = std::min(128 / nkv, (ctx + 31) / 32);
+    s = std::max(s, wide);
+    s = std::min(s, std::max(1, 256 / nkv));
+    return std::max(1, std::min(s, kAttnMaxSplits));
+}
+
 int attn_pick_splits(int n_kv, int max_ctx) {
     // one split per kAttnSplitChunk positions, within attn_max_splits
     const int by_ctx = (max_ctx + kAttnSplitChunk - 1) / kAttnSplitChunk;
@@ -619,6 +648,7 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
         return ATLAS_OK;
     }
     if (n_splits < 1) n_splits = 1;
+    if (n_splits > kAttnMaxSplits) n_splits = kAttnMaxSplits;
     if (n_splits > 1) {
         int rc = attn_reserve(a.n_heads, a.head_dim, n_splits);
         if (rc) return rc;

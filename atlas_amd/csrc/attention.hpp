@@ -60,6 +60,8 @@ bool attn_fused_supported(int n_heads, int n_kv, int head_dim);
 int attn_max_splits(int n_kv);
 int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st);
 int attn_pick_splits(int n_kv, int max_ctx);
+// split count of the two-kernel path (attn_launch) for a live context
+int attn_pick_splits_unfused(int n_kv, int ctx);
 int attn_reserve(int n_heads, int head_dim, int n_splits);
 int attn_launch(AttnArgs a, int n_splits, hipStream_t st);
 

@@ -101,7 +101,7 @@ ATLAS_API void atlas_decode_attention(const float* q, const float* k_cache, cons
     a.pos = pos; a.pos_dev = nullptr; a.scale = scale; a.window = window;
     a.max_rows = pos + 1;
     const int ctx = (window > 0 && pos + 1 > window) ? window : pos + 1;
-    attn_launch(a, attn_pick_splits(n_kv > 0 ? n_kv : 1, ctx), stream());
+    attn_launch(a, attn_pick_splits_unfused(n_kv, ctx), stream());
 }
 
 static unsigned long long* argmax_scratch() {
