@@ -248,7 +248,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
 // split maxima and weights go through LDS once; every (split, dim) partial is
 // then an independent load, so the sum streams instead of waiting on each
 // split in turn.  Empty splits carry (m, l, o) = (-inf, 0, 0) and weigh 0.
-constexpr int kAttnMaxSplits = 256;
+
 
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int n_splits, int hd) {
     __shared__ float s_w[kAttnMaxSplits];
@@ -501,22 +501,37 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     __syncthreads();
     if (!s_last) return;
     __threadfence();
+    // Split weights of the G heads through LDS first; every (split, dim)
+    // partial is then an independent load.  Empty splits carry m = -inf and
+    // weigh exp2(-inf) = 0.
+    __shared__ float s_wt[G][kAttnFusedMaxSplits];
+    __shared__ float s_mx[G];
+    const long ph = pbase + (long)kvh * G * n_splits;     // head kvh*G, split 0
+    for (int i = threadIdx.x; i < G * n_splits; i += 64 * W)
+        s_wt[i / n_splits][i % n_splits] =
+            __hip_atomic_load(&a.part_m[ph + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (threadIdx.x < G) {
+        float mx = -INFINITY;
+        for (int s2 = 0; s2 < n_splits; ++s2) mx = fmaxf(mx, s_wt[threadIdx.x][s2]);
+        s_mx[threadIdx.x] = mx;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * n_splits; i += 64 * W) {
+        const int h = i / n_splits, s2 = i % n_splits;
+        s_wt[h][s2] = exp2f(s_wt[h][s2] - s_mx[h]);
+    }
+    __syncthreads();
     for (int e = threadIdx.x; e < G * HD; e += 64 * W) {
         const int h = e / HD, d = e % HD;
-        const int qh = kvh * G + h;
-        const long p0 = pbase + (long)qh * n_splits;
-        float mx = -INFINITY;
-        for (int s2 = 0; s2 < n_splits; ++s2)
-            mx = fmaxf(mx, __hip_atomic_load(&a.part_m[p0 + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const long p0 = ph + (long)h * n_splits;
         float lsum = 0.f, osum = 0.f;
         for (int s2 = 0; s2 < n_splits; ++s2) {
-            const float mm = __hip_atomic_load(&a.part_m[p0 + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (mm == -INFINITY) continue;
-            const float w = exp2f(mm - mx);
+            const float w = s_wt[h][s2];
             lsum += __hip_atomic_load(&a.part_l[p0 + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * w;
             osum += __hip_atomic_load(&a.part_o[(p0 + s2) * HD + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * w;
         }
-        a.out[(long)seq * a.out_stride + (long)qh * HD + d] = osum / lsum;
+        a.out[(long)seq * a.out_stride + (long)(kvh * G + h) * HD + d] = osum / lsum;
     }
     if (threadIdx.x == 0) atomicExch(&a.counters[seq * a.n_kv + kvh], 0);
 }
@@ -550,6 +565,8 @@ int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream
     ATLAS_REQUIRE(n_splits == 1 || (a.part_m && a.part_l && a.part_o && a.counters),
                   "attention: split partials missing");
     ATLAS_REQUIRE(n_seq >= 1 && n_splits >= 1, "attention: empty grid");
+    ATLAS_REQUIRE(n_splits <= kAttnFusedMaxSplits, "attention: %d splits > %d", n_splits,
+                  kAttnFusedMaxSplits);
     ATLAS_REQUIRE(attn_rows_fit(a.max_rows, a.n_kv, a.head_dim),
                   "attention: %d cache rows of %d x %d exceed 32-bit offsets", a.max_rows, a.n_kv,
                   a.head_dim);

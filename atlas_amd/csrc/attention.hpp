@@ -56,6 +56,11 @@ inline bool attn_rows_fit(long max_rows, int n_kv, int head_dim) {
 // (one pipelined block scans ~512 rows in the time a split merge takes).
 constexpr int kAttnSplitChunk = 512;
 
+// split-count bounds: the two-kernel path's merge, and the fused kernel's
+// in-kernel merge (its split weights live in LDS)
+constexpr int kAttnMaxSplits = 256;
+constexpr int kAttnFusedMaxSplits = 64;
+
 bool attn_fused_supported(int n_heads, int n_kv, int head_dim);
 int attn_max_splits(int n_kv);
 int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st);
