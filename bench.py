@@ -32,7 +32,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of each bf16 decode GEMV kernel: rocprofv3 FETCH_SIZE x 2
 # + WRITE_SIZE x 1 (the factors a 1 GiB copy reads on this part), measured by
 # `bench.py --pmc-probe` (profiles/gemv_bf16_7b_hbm_traffic.md).
-TRAFFIC = {"gate_up": 180981370, "qkv_wo_lm_head": 79176539, "w_down": 90696356}
+TRAFFIC = {"gate_up": 180976635, "qkv_wo_lm_head": 79177037, "w_down": 90670047}
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
