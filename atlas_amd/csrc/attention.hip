@@ -53,6 +53,12 @@ template <int HD> struct ScanShape {
     static constexpr int P = HD == 64 ? 8 : HD == 128 ? 4 : 2;
 };
 
+// A lane of a 16-lane position group owns DPL = HD/16 dims in chunks of 4:
+// chunk c holds dims c*64 + dl*4 .. +3.  One 16-byte load per chunk then
+// covers 256 contiguous bytes of the row across the group (whole cache
+// lines), where contiguous per-lane dims would touch each line twice.
+__device__ __forceinline__ int lane_dim(int dl, int d) { return (d >> 2) * 64 + dl * 4 + (d & 3); }
+
 struct ScanBufs {
     __amdgpu_buffer_rsrc_t k, v;
     uint32_t row_bytes;      // bytes between consecutive positions
@@ -84,9 +90,9 @@ __device__ __forceinline__ void scan_load(const ScanBufs& b, int t,
 #pragma unroll
         for (int d = 0; d < DPL; d += 4) {
             const f32x4 kv = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(b.k, (int)(off + d * 4), 0, 0));
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(b.k, (int)(off + (d >> 2) * 256), 0, 0));
             const f32x4 vv = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(b.v, (int)(off + d * 4), 0, 0));
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(b.v, (int)(off + (d >> 2) * 256), 0, 0));
             kf[i][d] = kv.x; kf[i][d + 1] = kv.y; kf[i][d + 2] = kv.z; kf[i][d + 3] = kv.w;
             vf[i][d] = vv.x; vf[i][d + 1] = vv.y; vf[i][d + 2] = vv.z; vf[i][d + 3] = vv.w;
         }
@@ -139,7 +145,7 @@ __device__ __forceinline__ void scan_update(const float (&q)[G][HD / 16], float 
 
 // Scan cache rows [b0, e1) into the (wave, row) group's state (NG groups per
 // block).  kb/vb: dim 0 of the KV head in row 0, lane_dims: the lane's
-// first dim.
+// first dim (lane_dim(dl, 0)).
 template <int HD, int G, int NG>
 __device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long kv_stride,
                                           int lane_dims, int b0, int e1, int group,
@@ -189,10 +195,10 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     float q[G][DPL];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const float* qh = a.q + (long)(kvh * G + h) * HD + dl * DPL;
+        const float* qh = a.q + (long)(kvh * G + h) * HD;
 #pragma unroll
         for (int d = 0; d < DPL; d += 4) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(qh + d);
+            const f32x4 v = *reinterpret_cast<const f32x4*>(qh + lane_dim(dl, d));
             q[h][d] = v.x * sc; q[h][d + 1] = v.y * sc; q[h][d + 2] = v.z * sc; q[h][d + 3] = v.w * sc;
         }
     }
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     }
 
     attn_scan<HD, G, 4 * W>(a.k_cache + (long)kvh * HD, a.v_cache + (long)kvh * HD, kv_stride,
-                            dl * DPL, b0, b1, wave * 4 + row, q, m, l, o);
+                            lane_dim(dl, 0), b0, b1, wave * 4 + row, q, m, l, o);
 
     // ---- merge the 16 (wave,row) states of this block through LDS ---------
     __shared__ float s_m[4 * W][G], s_l[4 * W][G];
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     for (int h = 0; h < G; ++h) {
         if (dl == 0) { s_m[st][h] = m[h]; s_l[st][h] = l[h]; }
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) s_o[st][h][dl * DPL + d] = o[h][d];
+        for (int d = 0; d < DPL; ++d) s_o[st][h][lane_dim(dl, d)] = o[h][d];
     }
     __syncthreads();
     // thread -> (head, dim) pairs
@@ -427,7 +433,7 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) q[h][d] = sq[h][dl * DPL + d];
+        for (int d = 0; d < DPL; ++d) q[h][d] = sq[h][lane_dim(dl, d)];
     float m[G], l[G], o[G][DPL];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -436,7 +442,7 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    attn_scan<HD, G, 4 * W>(kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, dl * DPL, b0,
+    attn_scan<HD, G, 4 * W>(kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, lane_dim(dl, 0), b0,
                             e1, wave * 4 + row, q, m, l, o);
     if (owner && wave == 0 && row == 0) {
         // position pos from LDS (the 16 lanes of row 0 of wave 0)
@@ -446,8 +452,8 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         for (int i = 0; i < P; ++i)
 #pragma unroll
             for (int d = 0; d < DPL; ++d) {
-                kf[i][d] = sk[dl * DPL + d];
-                vf[i][d] = sv[dl * DPL + d];
+                kf[i][d] = sk[lane_dim(dl, d)];
+                vf[i][d] = sv[lane_dim(dl, d)];
             }
         scan_update<HD, G>(q, m, l, o, kf, vf, 0, 1);
     }
@@ -461,7 +467,7 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     for (int h = 0; h < G; ++h) {
         if (dl == 0) { s_m[st][h] = m[h]; s_l[st][h] = l[h]; }
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) s_o[st][h][dl * DPL + d] = o[h][d];
+        for (int d = 0; d < DPL; ++d) s_o[st][h][lane_dim(dl, d)] = o[h][d];
     }
     __syncthreads();
     // each sequence owns n_heads * gridDim.y partial slots (its active split
