@@ -125,6 +125,7 @@ SIGNATURES = {
                                            C.POINTER(C.c_int)]),
     "atlas_model_generate_batch": (I, [P, P, P, I, I, C.POINTER(SamplingC), P, P]),
     "atlas_model_decode_greedy": (I, [P, U32, I, P]),
+    "atlas_model_set_long_context": (I, [P, I]),
     "atlas_sample_host": (I, [P, I, P, I, I, C.POINTER(SamplingC), C.POINTER(C.c_uint64), P]),
     "atlas_model_bench_gemv": (I, [P, I, I, P, P, P]),
     "atlas_model_use_graph": (I, [P, I]),

@@ -179,12 +179,14 @@ template <int HD, int G, int W>
 __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;              // dims per lane
     constexpr float LOG2E = 1.4426950408889634f;
-    const int kvh = blockIdx.x, split = blockIdx.y, n_splits = gridDim.y;
+    const int kvh = blockIdx.x, split = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = lane >> 4, dl = lane & 15;     // position row, dim group
     const int pos = load_pos(a.pos_dev, a.pos);
     const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
     const int ctx = pos - t_lo + 1;
+    const int n_splits = a.adaptive ? min((int)gridDim.y, attn_splits_for(a.n_kv, ctx)) : gridDim.y;
+    if (split >= n_splits) return;
     const int chunk = (ctx + n_splits - 1) / n_splits;
     const int b0 = t_lo + split * chunk;
     const int b1 = min(pos + 1, b0 + chunk);
@@ -260,6 +262,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int n_spl
     __shared__ float s_w[kAttnMaxSplits];
     __shared__ float s_red[4];
     const int qh = blockIdx.x;
+    if (a.adaptive) {
+        // the split kernel's active count for this launch's live context
+        const int pos = load_pos(a.pos_dev, a.pos);
+        const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
+        n_splits = min(n_splits, attn_splits_for(a.n_kv, pos - t_lo + 1));
+        if (n_splits == 1) return;             // the split kernel wrote out
+    }
     const long base = (long)qh * n_splits;
     float mx = -INFINITY;
     for (int s = threadIdx.x; s < n_splits; s += blockDim.x) mx = fmaxf(mx, a.part_m[base + s]);
@@ -618,18 +627,7 @@ int attn_max_splits(int n_kv) {
     return s < 1 ? 1 : (s > 8 ? 8 : s);
 }
 
-int attn_pick_splits_unfused(int n_kv, int ctx) {
-    // split + combine kernels (no cross-block merge): at least ~128 blocks
-    // while splits keep >= 32 positions, at most 512 positions per split,
-    // and at most 256 blocks (measured at the GQA 32/8/128 shape, ctx
-    // 512..16384: 32..512 positions per split stream fastest)
-    const int nkv = n_kv > 0 ? n_kv : 1;
-    int s = (ctx + kAttnSplitChunk - 1) / kAttnSplitChunk;
-    const int wide = std::min(128 / nkv, (ctx + 31) / 32);
-    s = std::max(s, wide);
-    s = std::min(s, std::max(1, 256 / nkv));
-    return std::max(1, std::min(s, kAttnMaxSplits));
-}
+int attn_pick_splits_unfused(int n_kv, int ctx) { return attn_splits_for(n_kv, ctx); }
 
 int attn_pick_splits(int n_kv, int max_ctx) {
     // one split per kAttnSplitChunk positions, within attn_max_splits
@@ -672,13 +670,14 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
     }
     if (n_splits < 1) n_splits = 1;
     if (n_splits > kAttnMaxSplits) n_splits = kAttnMaxSplits;
-    if (n_splits > 1) {
+    if (n_splits > 1 && !a.part_m) {
         int rc = attn_reserve(a.n_heads, a.head_dim, n_splits);
         if (rc) return rc;
         a.part_m = g_part;
         a.part_l = g_part + (size_t)a.n_heads * n_splits;
         a.part_o = g_part + (size_t)2 * a.n_heads * n_splits;
     }
+    ATLAS_REQUIRE(n_splits == 1 || (a.part_l && a.part_o), "attention: partial buffers missing");
 #define ATLAS_ATTN_CASE(HDV, GV) \
     if (a.head_dim == HDV && G == GV) return launch_split<HDV, GV>(a, n_splits, st);
     ATLAS_ATTN_CASE(128, 1) ATLAS_ATTN_CASE(128, 2) ATLAS_ATTN_CASE(128, 4) ATLAS_ATTN_CASE(128, 8)

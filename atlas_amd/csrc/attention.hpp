@@ -14,10 +14,12 @@ struct AttnArgs {
     const int* pos_dev;      // device-resident position (graph replay)
     float scale;
     int window;              // 0 = full attention
-    float* part_m;           // split partials (library scratch)
+    float* part_m;           // split partials: the caller's, or null for library scratch
     float* part_l;
     float* part_o;
     int max_rows;            // cache rows that may be read (max_seq), > 0
+    int adaptive;            // 1: active splits = min(grid, attn_splits_for(n_kv, ctx)) of
+                             // the live context (a captured step replayed at any pos)
 };
 
 // Fused QK-norm + RoPE + KV write + split-K attention + split merge.
@@ -60,6 +62,20 @@ constexpr int kAttnSplitChunk = 512;
 // in-kernel merge (its split weights live in LDS)
 constexpr int kAttnMaxSplits = 256;
 constexpr int kAttnFusedMaxSplits = 64;
+
+// Split count of the two-kernel path for a live context ctx: at least ~128
+// blocks while splits keep >= 32 positions, at most 512 positions per split,
+// and at most 256 blocks (measured at the GQA 32/8/128 shape, ctx 512..16384).
+__host__ __device__ inline int attn_splits_for(int n_kv, int ctx) {
+    const int nkv = n_kv > 0 ? n_kv : 1;
+    int s = (ctx + kAttnSplitChunk - 1) / kAttnSplitChunk;
+    const int wide = 128 / nkv < (ctx + 31) / 32 ? 128 / nkv : (ctx + 31) / 32;
+    if (wide > s) s = wide;
+    const int cap = 256 / nkv > 1 ? 256 / nkv : 1;
+    if (s > cap) s = cap;
+    if (s > kAttnMaxSplits) s = kAttnMaxSplits;
+    return s < 1 ? 1 : s;
+}
 
 bool attn_fused_supported(int n_heads, int n_kv, int head_dim);
 int attn_max_splits(int n_kv);

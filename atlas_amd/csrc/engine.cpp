@@ -35,6 +35,12 @@ using namespace atlas;
 
 namespace {
 
+// Context length from which the fused step's attention (one launch per layer,
+// at most 128 blocks because of its in-kernel split merge) gives way to three
+// launches: QK-norm/RoPE/KV write, the split kernel over up to 256 blocks, and
+// the split merge (the two-kernel path of atlas_decode_attention).
+constexpr int kLongAttnFrom = 1024;
+
 struct DevMat {
     int fmt = WF_BF16;
     void* w = nullptr;
@@ -105,10 +111,13 @@ struct atlas_model {
     long slot_stride = 0;
     int attn_splits = 1;           // fused kernel: maximum (grid) split count
     int attn_splits_unfused = 1;
+    int attn_splits_long = 1;      // long-context step: split kernel grid (adaptive)
+    int long_from = kLongAttnFrom; // positions >= this replay the long-context step
     int pos = 0;
     hipStream_t st = nullptr;
     bool use_graph = true;
     hipGraphExec_t gexec[2] = {nullptr, nullptr};
+    hipGraphExec_t gexec_long[2] = {nullptr, nullptr};
     hipGraphExec_t bgexec[9] = {};   // ragged batch step per batch size 1..8
     // pinned staging ring for the batch step's tokens / positions / slots:
     // entry k is rewritten only after its event (the copies) completed
@@ -251,6 +260,10 @@ int layer_step(atlas_model* m, int li) {
     a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
     a.pos = 0; a.pos_dev = m->pos_dev; a.scale = m->scale; a.window = L.window;
     a.max_rows = c.max_seq;
+    // the model's own partials: a captured step must not point at library
+    // scratch that another model's reservation may reallocate
+    const size_t np = (size_t)c.n_heads * m->attn_splits_unfused;
+    a.part_m = m->attn_part; a.part_l = m->attn_part + np; a.part_o = m->attn_part + 2 * np;
     TRY(attn_launch(a, m->attn_splits_unfused, m->st));
     TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
     if (c.post_norm) {
@@ -296,6 +309,32 @@ GemvArgs pro_args(const DevMat& w, const float* x, float* y, int pro, const floa
     return a;
 }
 
+// Attention of the long-context step: QK-norm + RoPE in place and the K/V
+// cache write, then split kernel + merge with the split count of the live
+// context (read on the device, so one captured step serves every position).
+int enqueue_attn_long(atlas_model* m, const LayerW& L) {
+    const atlas_model_config& c = m->cfg;
+    QkvPostArgs q{};
+    q.qkv = m->qkv; q.qkv_stride = m->qkv_rows;
+    q.q_norm = L.q_norm; q.k_norm = L.k_norm; q.qk_eps = 1e-6f;
+    q.cos_tab = m->cos_tab; q.sin_tab = m->sin_tab;
+    q.k_cache = L.kc; q.v_cache = L.vc; q.slot_stride = m->slot_stride;
+    q.slot_dev = nullptr; q.pos_dev = m->pos_dev; q.pos = 0;
+    q.n_heads = c.n_heads; q.n_kv = c.n_kv_heads; q.head_dim = m->hd;
+    TRY(qkv_post_launch(q, 1, m->st));
+    AttnArgs a{};
+    a.q = m->qkv; a.k_cache = L.kc; a.v_cache = L.vc; a.out = m->att;
+    a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
+    a.pos = 0; a.pos_dev = m->pos_dev; a.scale = m->scale; a.window = L.window;
+    a.max_rows = c.max_seq;
+    a.adaptive = 1;
+    const size_t np = (size_t)c.n_heads * m->attn_splits_long;
+    a.part_m = m->attn_part;
+    a.part_l = m->attn_part + np;
+    a.part_o = m->attn_part + 2 * np;
+    return attn_launch(a, m->attn_splits_long, m->st);
+}
+
 // GU of the fused step: x'_l = x_l + rmsnorm(y1) * attn_norm_l materialised
 // into xb, then h = silu(gate) * up in the epilogue.
 int enqueue_gu_fused(atlas_model* m, const LayerW& L) {
@@ -317,7 +356,7 @@ int enqueue_down_fused(atlas_model* m, const LayerW& L) {
 //   GU     x'_l = x_l + rmsnorm(y1) * attn_norm_l;  h = silu(gate) * up
 //   DOWN   y2 = W_down h
 // x_l lives in m->x, x'_l in m->xb.
-int enqueue_step_fused(atlas_model* m, int mode) {
+int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
     const atlas_model_config& c = m->cfg;
     const int d = c.d_model;
     const float eps = c.rms_eps;
@@ -329,21 +368,25 @@ int enqueue_step_fused(atlas_model* m, int mode) {
         else
             TRY(gemv_launch(pro_args(L.qkv, m->xb, m->qkv, PRO_RESNORM, m->y2, m->L[li - 1].ffn_norm,
                                      eps, m->x), m->st));
-        AttnFusedArgs a{};
-        a.qkv = m->qkv; a.qkv_stride = m->qkv_rows;
-        a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.qk_eps = 1e-6f;
-        a.cos_tab = m->cos_tab; a.sin_tab = m->sin_tab;
-        a.k_cache = L.kc; a.v_cache = L.vc; a.slot_stride = m->slot_stride;
-        a.slot_dev = nullptr; a.pos_dev = m->pos_dev;
-        a.out = m->att; a.out_stride = d;
-        a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
-        a.scale = m->scale; a.window = L.window;
-        a.part_m = m->attn_part;
-        a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
-        a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
-        a.counters = m->attn_counters;
-        a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
-        TRY(attn_fused_launch(a, m->attn_splits, 1, m->st));
+        if (long_ctx) {
+            TRY(enqueue_attn_long(m, L));
+        } else {
+            AttnFusedArgs a{};
+            a.qkv = m->qkv; a.qkv_stride = m->qkv_rows;
+            a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.qk_eps = 1e-6f;
+            a.cos_tab = m->cos_tab; a.sin_tab = m->sin_tab;
+            a.k_cache = L.kc; a.v_cache = L.vc; a.slot_stride = m->slot_stride;
+            a.slot_dev = nullptr; a.pos_dev = m->pos_dev;
+            a.out = m->att; a.out_stride = d;
+            a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
+            a.scale = m->scale; a.window = L.window;
+            a.part_m = m->attn_part;
+            a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
+            a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
+            a.counters = m->attn_counters;
+            a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
+            TRY(attn_fused_launch(a, m->attn_splits, 1, m->st));
+        }
         TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
         TRY(enqueue_gu_fused(m, L));
         TRY(enqueue_down_fused(m, L));
@@ -376,8 +419,8 @@ int enqueue_step_fused(atlas_model* m, int mode) {
 }
 
 // mode 0: forward only; mode 1: forward + greedy choice into tok_dev/hist
-int enqueue_step(atlas_model* m, int mode) {
-    if (m->fused) return enqueue_step_fused(m, mode);
+int enqueue_step(atlas_model* m, int mode, bool long_ctx) {
+    if (m->fused) return enqueue_step_fused(m, mode, long_ctx);
     const atlas_model_config& c = m->cfg;
     TRY(embed_launch(m->embed, c.vocab, c.d_model, m->tok_dev, 0, m->x, c.d_model, 1, m->st));
     for (int li = 0; li < c.n_layers; ++li) TRY(layer_step(m, li));
@@ -393,6 +436,11 @@ void drop_graphs(atlas_model* m) {
             (void)hipGraphExecDestroy(g);
             g = nullptr;
         }
+    for (auto& g : m->gexec_long)
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
     for (auto& g : m->bgexec)
         if (g) {
             (void)hipGraphExecDestroy(g);
@@ -403,13 +451,17 @@ void drop_graphs(atlas_model* m) {
 int run_step(atlas_model* m, int mode) {
     ATLAS_REQUIRE(m->pos < m->cfg.max_seq, "position %d reaches max_seq %d", m->pos,
                   m->cfg.max_seq);
+    // the host knows the position this step runs at: long contexts replay the
+    // long-context step
+    const bool long_ctx = m->fused && m->pos >= m->long_from;
     if (!m->use_graph) {
-        TRY(enqueue_step(m, mode));
+        TRY(enqueue_step(m, mode, long_ctx));
     } else {
-        if (!m->gexec[mode]) {
+        hipGraphExec_t& gx = long_ctx ? m->gexec_long[mode] : m->gexec[mode];
+        if (!gx) {
             hipGraph_t g = nullptr;
             ATLAS_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
-            int rc = enqueue_step(m, mode);
+            int rc = enqueue_step(m, mode, long_ctx);
             hipError_t e = hipStreamEndCapture(m->st, &g);
             if (rc) {
                 if (g) (void)hipGraphDestroy(g);
@@ -419,15 +471,15 @@ int run_step(atlas_model* m, int mode) {
                 set_error(ATLAS_EHIP, "graph capture: %s", hipGetErrorString(e));
                 return ATLAS_EHIP;
             }
-            e = hipGraphInstantiate(&m->gexec[mode], g, nullptr, nullptr, 0);
+            e = hipGraphInstantiate(&gx, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             if (e != hipSuccess) {
-                m->gexec[mode] = nullptr;
+                gx = nullptr;
                 set_error(ATLAS_EHIP, "graph instantiate: %s", hipGetErrorString(e));
                 return ATLAS_EHIP;
             }
         }
-        ATLAS_HIP(hipGraphLaunch(m->gexec[mode], m->st));
+        ATLAS_HIP(hipGraphLaunch(gx, m->st));
     }
     m->pos += 1;
     return ATLAS_OK;
@@ -474,10 +526,11 @@ int set_greedy_cfg(atlas_model* m, const atlas_sampling* s) {
         m->g_theta = theta;
         m->g_window = window;
         m->g_nsup = nsup;
-        if (m->gexec[1]) {
-            (void)hipGraphExecDestroy(m->gexec[1]);
-            m->gexec[1] = nullptr;
-        }
+        for (hipGraphExec_t* g : {&m->gexec[1], &m->gexec_long[1]})
+            if (*g) {
+                (void)hipGraphExecDestroy(*g);
+                *g = nullptr;
+            }
     }
     return ATLAS_OK;
 }
@@ -769,6 +822,8 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
             a.pos_dev = m->pos_dev + i; a.scale = m->scale; a.window = L.window;
             a.max_rows = c.max_seq;
+            const size_t np = (size_t)c.n_heads * m->attn_splits_unfused;
+            a.part_m = m->attn_part; a.part_l = m->attn_part + np; a.part_o = m->attn_part + 2 * np;
             TRY(attn_launch(a, m->attn_splits_unfused, m->st));
         }
         TRY(bmm(m, L.wo, m->att, m->y, n, EPI_STORE));
@@ -939,6 +994,7 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     // The unfused kernel's count is fixed at launch.
     m->attn_splits = attn_pick_splits(c.n_kv_heads, c.max_seq);
     m->attn_splits_unfused = m->attn_splits;
+    m->attn_splits_long = attn_splits_for(c.n_kv_heads, c.max_seq);
     if (attn_reserve(c.n_heads, hd, m->attn_splits_unfused)) return fail(m);
     // split-K partials of the ragged batch's skinny GEMMs, allocated now so
     // that no later launch (graph capture included) allocates
@@ -954,8 +1010,11 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->fused = c.post_norm && attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
                attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && d % 32 == 0 &&
                c.ffn_hidden % 32 == 0;
-    if (dalloc(m, (void**)&m->attn_part,
-               (size_t)B * c.n_heads * m->attn_splits * (hd + 2) * 4) ||
+    // split partials: the fused kernel's B x n_heads x attn_splits, or the
+    // long-context step's n_heads x attn_splits_long
+    const size_t part_slots = std::max((size_t)B * c.n_heads * m->attn_splits,
+                                       (size_t)c.n_heads * m->attn_splits_long);
+    if (dalloc(m, (void**)&m->attn_part, part_slots * (hd + 2) * 4) ||
         dalloc(m, (void**)&m->attn_counters, (size_t)B * c.n_kv_heads * 4))
         return fail(m);
     if (hipMemset(m->attn_counters, 0, (size_t)B * c.n_kv_heads * 4) != hipSuccess) {
@@ -1081,6 +1140,13 @@ ATLAS_API int atlas_model_pos(const atlas_model* m) { return m ? m->pos : -1; }
 ATLAS_API float atlas_model_attn_scale(const atlas_model* m) { return m ? m->scale : 0.f; }
 ATLAS_API void* atlas_model_stream(atlas_model* m) { return m ? (void*)m->st : nullptr; }
 ATLAS_API const float* atlas_model_logits_dev(atlas_model* m) { return m ? m->logits : nullptr; }
+
+ATLAS_API int atlas_model_set_long_context(atlas_model* m, int from_pos) {
+    ATLAS_REQUIRE(m, "set_long_context: null model");
+    ATLAS_REQUIRE(from_pos >= 0, "set_long_context: from_pos %d < 0", from_pos);
+    m->long_from = from_pos;
+    return ATLAS_OK;
+}
 
 ATLAS_API int atlas_model_use_graph(atlas_model* m, int enable) {
     ATLAS_REQUIRE(m, "use_graph: null model");

@@ -193,6 +193,11 @@ class OlmoModel:
         """lib.rs:1961-1963; used by the next generate call."""
         self._rng_seed = seed
 
+    def set_long_context(self, from_pos: int) -> None:
+        """Position from which decode steps use the long-context attention
+        path (extension; default 1024)."""
+        check(load().atlas_model_set_long_context(self._h, from_pos))
+
     def use_graph(self, enable: bool) -> None:
         check(load().atlas_model_use_graph(self._h, 1 if enable else 0))
 

@@ -141,6 +141,12 @@ int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts, const in
 int atlas_sample_host(const float* logits, int vocab, const uint32_t* hist, int n_hist, int step,
                       const atlas_sampling* s, uint64_t* rng_state, uint32_t* token);
 
+/* Extension: position from which decode steps run the long-context attention
+ * (QK-norm/RoPE/KV-write kernel, split kernel over up to 256 blocks, split
+ * merge) instead of the one-launch fused attention; default 1024.  Each path
+ * is captured in its own graph; the choice is made per step on the host.  */
+int atlas_model_set_long_context(atlas_model* m, int from_pos);
+
 /* Benchmark helper: greedy decode of n_steps tokens continuing from the
  * current state, replaying the captured step with no host synchronisation
  * in between.  tokens (host, may be NULL) receives the chosen ids.          */

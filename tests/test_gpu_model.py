@@ -201,6 +201,41 @@ def test_ragged_batch_matches_single(orc):
     assert len(m.generate_with_sampling(prompts[0], 8, SamplingConfig.greedy())) == 8
 
 
+def test_long_context_attention_path(orc):
+    # positions >= from_pos replay the long-context step (QK-norm/RoPE/KV-write
+    # kernel, adaptive split kernel, split merge); forcing it from position 8
+    # covers its windowed and full layers, the switch between the two captured
+    # graphs, and the eager path
+    cfg = modelgen.olmo3_small_config(max_seq=320)
+    W = modelgen.make_weights(cfg, seed=37)
+    toks = np.random.default_rng(4).integers(0, cfg["vocab"], 300)
+    for graph in (True, False):
+        m = modelgen.engine_model(W, use_graph=graph)
+        m.set_long_context(8)
+        o = modelgen.oracle_model(W, threads=8)
+        worst = 0.0
+        for i, t in enumerate(toks):
+            lg, ref = m.forward_one(int(t)), o.forward_one(int(t))
+            if i % 7 == 0 or i > 280:
+                worst = max(worst, _rel(lg, ref))
+        print(f"long-context path (graph={graph}): worst rel logit err {worst:.2e}")
+        assert worst <= LOGIT_TOL
+    # greedy generation agrees between the two paths
+    from atlas_amd.model import SamplingConfig
+    a, b = modelgen.engine_model(W), modelgen.engine_model(W)
+    b.set_long_context(4)
+    prompt = [int(t) for t in toks[:20]]
+    ga = a.generate_with_sampling(prompt, 24, SamplingConfig.greedy())
+    gb = b.generate_with_sampling(prompt, 24, SamplingConfig.greedy())
+    if ga != gb:
+        k = next(i for i in range(min(len(ga), len(gb))) if ga[i] != gb[i])
+        o = modelgen.oracle_model(W)
+        lg = None
+        for t in prompt + ga[:k]:
+            lg = o.forward_one(int(t))
+        assert _top2_margin(lg) <= 2 * LOGIT_TOL * np.max(np.abs(lg)), k
+
+
 def test_padded_rows_wide_ffn(orc):
     # ffn_hidden 4352: the bf16 W_down rows (8704 B, not a multiple of 4 KB)
     # are stored with a padded pitch; decode, tensor download and the ragged
