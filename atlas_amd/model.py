@@ -195,7 +195,7 @@ class OlmoModel:
 
     def set_long_context(self, from_pos: int) -> None:
         """Position from which decode steps use the long-context attention
-        path (extension; default 1024)."""
+        path (extension; default 512)."""
         check(load().atlas_model_set_long_context(self._h, from_pos))
 
     def use_graph(self, enable: bool) -> None:

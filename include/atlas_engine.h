@@ -143,7 +143,7 @@ int atlas_sample_host(const float* logits, int vocab, const uint32_t* hist, int 
 
 /* Extension: position from which decode steps run the long-context attention
  * (QK-norm/RoPE/KV-write kernel, split kernel over up to 256 blocks, split
- * merge) instead of the one-launch fused attention; default 1024.  Each path
+ * merge) instead of the one-launch fused attention; default 512.  Each path
  * is captured in its own graph; the choice is made per step on the host.  */
 int atlas_model_set_long_context(atlas_model* m, int from_pos);
 
