@@ -535,8 +535,7 @@ int gemv_fast_ok(int fmt, int K, int block) {
 // rotating weights (rows = 1 wins at K = 4096: more waves in flight per CU;
 // the bf16 W_down, 4096 x 11008 with padded rows, prefers two-row waves).
 struct N1Shape { int rows, unroll, bpc; };
-static N1Shape n1_shape(int fmt, int M, int K, int epi) {
-    (void)M;
+static N1Shape n1_shape(int fmt, int K, int epi) {
     // SwiGLU epilogue: bf16 and int4 two-row waves hold the (gate, up) pair;
     // int8 one-row waves take the pair in sequence (its two-row variant
     // needs ~170 VGPRs)
@@ -568,7 +567,7 @@ static const void* n1_kernel(int fmt, int rows, int unroll) {
 
 // number of persistent waves gemv_launch uses (argmax partial count)
 int gemv_waves(const GemvArgs& a) {
-    const N1Shape sh = n1_shape(a.fmt, a.M, a.K, a.epi);
+    const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
     const void* kern = n1_kernel(a.fmt, sh.rows, sh.unroll);
     return kern ? 4 * n1_blocks(kern, a.M, a.K, n1_group_rows(a, sh.rows), sh.bpc) : 0;
 }
@@ -599,7 +598,7 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     const bool fast = (align & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
                       gemv_x_lds_bytes(a.K) <= 160 * 1024;
     if (fast) {
-        const N1Shape sh = n1_shape(a.fmt, a.M, a.K, a.epi);
+        const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
 #define ATLAS_N1(F, R, U) \
         if (a.fmt == F && sh.rows == R && sh.unroll == U) return launch_n1<F, R, U>(a, st, sh.bpc);
         ATLAS_N1_LIST(ATLAS_N1)
