@@ -184,13 +184,18 @@ template <int HD, int G, int W>
 __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;              // dims per lane
     constexpr float LOG2E = 1.4426950408889634f;
-    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = lane >> 4, dl = lane & 15;     // position row, dim group
-    const int pos = load_pos(a.pos_dev, a.pos);
+    const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos;
+    const long cache0 = a.slot_dev ? (long)a.slot_dev[seq] * a.slot_stride : 0;
+    const float* qs = a.q + (long)seq * a.q_stride;
+    float* out = a.out + (long)seq * a.out_stride;
+    const long pbase = (long)seq * a.n_heads * gridDim.y;
     const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
     const int ctx = pos - t_lo + 1;
-    const int n_splits = a.adaptive ? min((int)gridDim.y, attn_splits_for(a.n_kv, ctx)) : gridDim.y;
+    const int n_splits = a.adaptive
+        ? min((int)gridDim.y, attn_batch_splits_for(a.n_kv, gridDim.z, ctx)) : gridDim.y;
     if (split >= n_splits) return;
     const int chunk = (ctx + n_splits - 1) / n_splits;
     const int b0 = t_lo + split * chunk;
@@ -202,7 +207,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     float q[G][DPL];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const float* qh = a.q + (long)(kvh * G + h) * HD;
+        const float* qh = qs + (long)(kvh * G + h) * HD;
 #pragma unroll
         for (int d = 0; d < DPL; d += 4) {
             const f32x4 v = *reinterpret_cast<const f32x4*>(qh + lane_dim(dl, d));
@@ -217,8 +222,8 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    attn_scan<HD, G, 4 * W>(a.k_cache + (long)kvh * HD, a.v_cache + (long)kvh * HD, kv_stride,
-                            lane_dim(dl, 0), b0, b1, wave * 4 + row, q, m, l, o);
+    attn_scan<HD, G, 4 * W>(a.k_cache + cache0 + (long)kvh * HD, a.v_cache + cache0 + (long)kvh * HD,
+                            kv_stride, lane_dim(dl, 0), b0, b1, wave * 4 + row, q, m, l, o);
 
     // ---- merge the 16 (wave,row) states of this block through LDS ---------
     __shared__ float s_m[4 * W][G], s_l[4 * W][G];
@@ -248,9 +253,9 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
         }
         const int qh = kvh * G + h;
         if (n_splits == 1) {
-            a.out[(long)qh * HD + d] = osum / lsum;
+            out[(long)qh * HD + d] = osum / lsum;
         } else {
-            const long pi = (long)qh * n_splits + split;
+            const long pi = pbase + (long)qh * n_splits + split;
             a.part_o[pi * HD + d] = osum;
             if (d == 0) { a.part_m[pi] = mx; a.part_l[pi] = lsum; }
         }
@@ -266,15 +271,17 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int n_splits, int hd) {
     __shared__ float s_w[kAttnMaxSplits];
     __shared__ float s_red[4];
-    const int qh = blockIdx.x;
+    const int qh = blockIdx.x, seq = blockIdx.y;
+    const long pbase = (long)seq * a.n_heads * n_splits;   // n_splits: the split grid
+    float* out = a.out + (long)seq * a.out_stride;
     if (a.adaptive) {
-        // the split kernel's active count for this launch's live context
-        const int pos = load_pos(a.pos_dev, a.pos);
+        // the split kernel's active count for this sequence's live context
+        const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos;
         const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
-        n_splits = min(n_splits, attn_splits_for(a.n_kv, pos - t_lo + 1));
+        n_splits = min(n_splits, attn_batch_splits_for(a.n_kv, gridDim.y, pos - t_lo + 1));
         if (n_splits == 1) return;             // the split kernel wrote out
     }
-    const long base = (long)qh * n_splits;
+    const long base = pbase + (long)qh * n_splits;
     float mx = -INFINITY;
     for (int s = threadIdx.x; s < n_splits; s += blockDim.x) mx = fmaxf(mx, a.part_m[base + s]);
     mx = wave_max(mx);
@@ -292,7 +299,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int n_spl
         float osum = 0.f;
 #pragma unroll 8
         for (int s = 0; s < n_splits; ++s) osum += a.part_o[(base + s) * hd + d] * s_w[s];
-        a.out[(long)qh * hd + d] = osum / lsum;
+        out[(long)qh * hd + d] = osum / lsum;
     }
 }
 
@@ -643,13 +650,13 @@ int attn_pick_splits(int n_kv, int max_ctx) {
 }
 
 template <int HD, int G>
-static int launch_split(AttnArgs a, int n_splits, hipStream_t st) {
+static int launch_split(AttnArgs a, int n_splits, hipStream_t st, int n_seq = 1) {
     constexpr int W = attn_waves<HD, G>();
-    hipLaunchKernelGGL((attn_split_kernel<HD, G, W>), dim3(a.n_kv, n_splits), dim3(64 * W), 0, st,
-                       a);
+    hipLaunchKernelGGL((attn_split_kernel<HD, G, W>), dim3(a.n_kv, n_splits, n_seq), dim3(64 * W),
+                       0, st, a);
     ATLAS_LAUNCH_CHECK("attn_split");
     if (n_splits > 1) {
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_heads), dim3(HD < 256 ? HD : 256), 0, st,
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_heads, n_seq), dim3(HD < 256 ? HD : 256), 0, st,
                            a, n_splits, HD);
         ATLAS_LAUNCH_CHECK("attn_combine");
     }
@@ -692,6 +699,31 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
     hipLaunchKernelGGL(attn_generic_kernel, dim3(a.n_heads), dim3(256), 0, st, a, a.head_dim);
     ATLAS_LAUNCH_CHECK("attn_generic");
     return ATLAS_OK;
+}
+
+int attn_batch_launch(const AttnArgs& a, int n_splits, int n_seq, hipStream_t st) {
+    ATLAS_REQUIRE(attn_fused_supported(a.n_heads, a.n_kv, a.head_dim),
+                  "attention: batch path needs head_dim 64/128/256 and group 1/2/4/8");
+    ATLAS_REQUIRE(a.q && a.k_cache && a.v_cache && a.out && a.pos_dev, "attention: null pointer");
+    ATLAS_REQUIRE(n_seq >= 1 && n_splits >= 1 && n_splits <= kAttnMaxSplits,
+                  "attention: %d sequences x %d splits", n_seq, n_splits);
+    ATLAS_REQUIRE(n_splits == 1 || (a.part_m && a.part_l && a.part_o),
+                  "attention: split partials missing");
+    ATLAS_REQUIRE(attn_rows_fit(a.max_rows, a.n_kv, a.head_dim),
+                  "attention: %d cache rows of %d x %d exceed 32-bit offsets", a.max_rows, a.n_kv,
+                  a.head_dim);
+    const uintptr_t al = (uintptr_t)a.q | (uintptr_t)a.k_cache | (uintptr_t)a.v_cache;
+    ATLAS_REQUIRE((al & 15) == 0 && a.q_stride % 4 == 0 && a.slot_stride % 4 == 0,
+                  "attention: 16-byte alignment");
+    const int G = a.n_heads / a.n_kv;
+#define ATLAS_BATCH_CASE(HDV, GV) \
+    if (a.head_dim == HDV && G == GV) return launch_split<HDV, GV>(a, n_splits, st, n_seq);
+    ATLAS_BATCH_CASE(128, 1) ATLAS_BATCH_CASE(128, 2) ATLAS_BATCH_CASE(128, 4) ATLAS_BATCH_CASE(128, 8)
+    ATLAS_BATCH_CASE(64, 1)  ATLAS_BATCH_CASE(64, 2)  ATLAS_BATCH_CASE(64, 4)  ATLAS_BATCH_CASE(64, 8)
+    ATLAS_BATCH_CASE(256, 1) ATLAS_BATCH_CASE(256, 2) ATLAS_BATCH_CASE(256, 4)
+#undef ATLAS_BATCH_CASE
+    set_error(ATLAS_EUNSUPPORTED, "attention: batch shape");
+    return ATLAS_EUNSUPPORTED;
 }
 
 }  // namespace atlas

@@ -18,8 +18,16 @@ struct AttnArgs {
     float* part_l;
     float* part_o;
     int max_rows;            // cache rows that may be read (max_seq), > 0
-    int adaptive;            // 1: active splits = min(grid, attn_splits_for(n_kv, ctx)) of
-                             // the live context (a captured step replayed at any pos)
+    int adaptive;            // 1: active splits = min(grid, attn_batch_splits_for(n_kv,
+                             // n_seq, ctx)) of the live context (a captured step
+                             // replayed at any pos)
+    // Batch (attn_batch_launch): sequence s reads q at q + s * q_stride, the
+    // cache slot slot_dev[s] (k_cache + slot * slot_stride), position
+    // pos_dev[s], and writes out + s * out_stride; its partials follow the
+    // previous sequences' n_heads * n_splits slots.
+    const int* slot_dev;
+    long slot_stride;
+    long q_stride, out_stride;
 };
 
 // Fused QK-norm + RoPE + KV write + split-K attention + split merge.
@@ -77,6 +85,16 @@ __host__ __device__ inline int attn_splits_for(int n_kv, int ctx) {
     return s < 1 ? 1 : s;
 }
 
+// Split count of n_seq sequences of one batch step: one split per
+// (sequence, KV head) once they make >= 128 blocks (then every extra split
+// only adds merge work: measured at the 7B shape, 2..8 sequences, ctx
+// 256..2048), else the single-sequence rule over the n_seq * n_kv streams.
+__host__ __device__ inline int attn_batch_splits_for(int n_kv, int n_seq, int ctx) {
+    if (n_seq <= 1) return attn_splits_for(n_kv, ctx);
+    const int streams = n_kv * n_seq;
+    return streams >= 128 ? 1 : attn_splits_for(streams, ctx);
+}
+
 bool attn_fused_supported(int n_heads, int n_kv, int head_dim);
 int attn_max_splits(int n_kv);
 int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st);
@@ -85,5 +103,9 @@ int attn_pick_splits(int n_kv, int max_ctx);
 int attn_pick_splits_unfused(int n_kv, int ctx);
 int attn_reserve(int n_heads, int head_dim, int n_splits);
 int attn_launch(AttnArgs a, int n_splits, hipStream_t st);
+// n_seq sequences of one batch step: split kernel (grid n_kv x n_splits x
+// n_seq) and split merge, no generic fallback; partials are the caller's,
+// [n_seq][n_heads][n_splits] (+ head_dim for part_o)
+int attn_batch_launch(const AttnArgs& a, int n_splits, int n_seq, hipStream_t st);
 
 }  // namespace atlas

@@ -114,6 +114,7 @@ struct atlas_model {
     int attn_splits = 1;           // fused kernel: maximum (grid) split count
     int attn_splits_unfused = 1;
     int attn_splits_long = 1;      // long-context step: split kernel grid (adaptive)
+    int attn_splits_batch[9] = {}; // long-context batch step of n sequences: split grid
     int long_from = kLongAttnFrom; // positions >= this replay the long-context step
     int pos = 0;
     hipStream_t st = nullptr;
@@ -121,6 +122,7 @@ struct atlas_model {
     hipGraphExec_t gexec[2] = {nullptr, nullptr};
     hipGraphExec_t gexec_long[2] = {nullptr, nullptr};
     hipGraphExec_t bgexec[9] = {};   // ragged batch step per batch size 1..8
+    hipGraphExec_t bgexec_long[9] = {};   // ... its long-context variant
     // pinned staging ring for the batch step's tokens / positions / slots:
     // entry k is rewritten only after its event (the copies) completed
     static constexpr int kRing = 8;
@@ -448,6 +450,11 @@ void drop_graphs(atlas_model* m) {
             (void)hipGraphExecDestroy(g);
             g = nullptr;
         }
+    for (auto& g : m->bgexec_long)
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
 }
 
 int run_step(atlas_model* m, int mode) {
@@ -771,13 +778,13 @@ int tensor_io(atlas_model* m, int kind, int layer, void* data, float* scales, bo
 
 // ---- the ragged batch step ----------------------------------------------------
 // n rows of activations through w: the batch-1 GEMV for one row, the skinny
-// MFMA GEMM for 2..8
+// launcher for 2..8 (the multi-row GEMV for 2-3 rows, MFMA tiles above)
 int bmm(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int epi) {
     if (n == 1) return gemv(m, w, x, y, epi);
     return skinny(m, w, x, y, n, epi);
 }
 
-int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
+int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx) {
     const atlas_model_config& c = m->cfg;
     const int d = c.d_model;
     TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, n, m->st));
@@ -789,7 +796,32 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             xin = m->xn;
         }
         TRY(bmm(m, L.qkv, xin, m->qkv, n, EPI_STORE));
-        if (m->fused) {
+        QkvPostArgs q{};
+        q.qkv = m->qkv; q.qkv_stride = m->qkv_rows;
+        q.q_norm = L.q_norm; q.k_norm = L.k_norm; q.qk_eps = 1e-6f;
+        q.cos_tab = m->cos_tab; q.sin_tab = m->sin_tab;
+        q.k_cache = L.kc; q.v_cache = L.vc; q.slot_stride = m->slot_stride;
+        q.slot_dev = m->slot_dev; q.pos_dev = m->pos_dev;
+        q.n_heads = c.n_heads; q.n_kv = c.n_kv_heads; q.head_dim = m->hd;
+        if (m->fused && long_ctx) {
+            // long contexts: QK-norm/RoPE/KV write, then the split kernel over
+            // (KV head, split, sequence) and the split merge as a second
+            // kernel (no per-block device-scope fence)
+            TRY(qkv_post_launch(q, n, m->st));
+            AttnArgs a{};
+            a.q = m->qkv; a.q_stride = m->qkv_rows;
+            a.k_cache = L.kc; a.v_cache = L.vc;
+            a.slot_dev = m->slot_dev; a.slot_stride = m->slot_stride;
+            a.pos_dev = m->pos_dev;
+            a.out = m->att; a.out_stride = d;
+            a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
+            a.scale = m->scale; a.window = L.window; a.max_rows = c.max_seq;
+            a.adaptive = 1;
+            const int sp = m->attn_splits_batch[n];
+            const size_t np = (size_t)n * c.n_heads * sp;
+            a.part_m = m->attn_part; a.part_l = m->attn_part + np; a.part_o = m->attn_part + 2 * np;
+            TRY(attn_batch_launch(a, sp, n, m->st));
+        } else if (m->fused) {
             // one launch: every sequence's QK-norm/RoPE/KV write and attention
             AttnFusedArgs a{};
             a.qkv = m->qkv; a.qkv_stride = m->qkv_rows;
@@ -807,13 +839,6 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
             TRY(attn_fused_launch(a, m->attn_splits, n, m->st));
         }
-        QkvPostArgs q{};
-        q.qkv = m->qkv; q.qkv_stride = m->qkv_rows;
-        q.q_norm = L.q_norm; q.k_norm = L.k_norm; q.qk_eps = 1e-6f;
-        q.cos_tab = m->cos_tab; q.sin_tab = m->sin_tab;
-        q.k_cache = L.kc; q.v_cache = L.vc; q.slot_stride = m->slot_stride;
-        q.slot_dev = m->slot_dev; q.pos_dev = m->pos_dev;
-        q.n_heads = c.n_heads; q.n_kv = c.n_kv_heads; q.head_dim = m->hd;
         if (!m->fused) TRY(qkv_post_launch(q, n, m->st));
         for (int i = 0; i < n && !m->fused; ++i) {
             AttnArgs a{};
@@ -854,14 +879,17 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
     return ATLAS_OK;
 }
 
-// batch_step replayed from a graph captured per batch size (fused models:
-// tokens, positions and slots are read from device memory)
-int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
-    if (!m->use_graph || !m->fused) return batch_step(m, n, slots);
-    if (!m->bgexec[n]) {
+// batch_step replayed from a graph captured per batch size and attention
+// variant (fused models: tokens, positions and slots are read from device
+// memory); long_ctx picks the long-context variant
+int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx) {
+    long_ctx = long_ctx && m->fused;
+    if (!m->use_graph || !m->fused) return batch_step(m, n, slots, long_ctx);
+    hipGraphExec_t& ge = long_ctx ? m->bgexec_long[n] : m->bgexec[n];
+    if (!ge) {
         hipGraph_t g = nullptr;
         ATLAS_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
-        int rc = batch_step(m, n, slots);
+        int rc = batch_step(m, n, slots, long_ctx);
         hipError_t e = hipStreamEndCapture(m->st, &g);
         if (rc) {
             if (g) (void)hipGraphDestroy(g);
@@ -871,15 +899,15 @@ int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots) {
             set_error(ATLAS_EHIP, "graph capture: %s", hipGetErrorString(e));
             return ATLAS_EHIP;
         }
-        e = hipGraphInstantiate(&m->bgexec[n], g, nullptr, nullptr, 0);
+        e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         if (e != hipSuccess) {
-            m->bgexec[n] = nullptr;
+            ge = nullptr;
             set_error(ATLAS_EHIP, "graph instantiate: %s", hipGetErrorString(e));
             return ATLAS_EHIP;
         }
     }
-    ATLAS_HIP(hipGraphLaunch(m->bgexec[n], m->st));
+    ATLAS_HIP(hipGraphLaunch(ge, m->st));
     return ATLAS_OK;
 }
 
@@ -1012,10 +1040,15 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->fused = c.post_norm && attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
                attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && d % 32 == 0 &&
                c.ffn_hidden % 32 == 0;
-    // split partials: the fused kernel's B x n_heads x attn_splits, or the
-    // long-context step's n_heads x attn_splits_long
-    const size_t part_slots = std::max((size_t)B * c.n_heads * m->attn_splits,
-                                       (size_t)c.n_heads * m->attn_splits_long);
+    // split partials: the fused kernel's B x n_heads x attn_splits, the
+    // long-context step's n_heads x attn_splits_long, or the long-context
+    // batch step's n x n_heads x attn_splits_batch[n]
+    size_t part_slots = std::max((size_t)B * c.n_heads * m->attn_splits,
+                                 (size_t)c.n_heads * m->attn_splits_long);
+    for (int n = 1; n <= B && n <= 8; ++n) {
+        m->attn_splits_batch[n] = attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
+        part_slots = std::max(part_slots, (size_t)n * c.n_heads * m->attn_splits_batch[n]);
+    }
     if (dalloc(m, (void**)&m->attn_part, part_slots * (hd + 2) * 4) ||
         dalloc(m, (void**)&m->attn_counters, (size_t)B * c.n_kv_heads * 4))
         return fail(m);
@@ -1551,7 +1584,9 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
             m->ring_used[k] = true;
         }
         std::vector<int> sl(slots.begin(), slots.begin() + n);
-        TRY(run_batch_step(m, n, sl));
+        int max_pos = 0;
+        for (int j = 0; j < n; ++j) max_pos = std::max(max_pos, poss[j]);
+        TRY(run_batch_step(m, n, sl, max_pos >= m->long_from));
         // a row chooses a token when it consumes its last prompt token or
         // generates; steps inside every row's prompt need no host round trip
         bool any_choice = false;

@@ -233,6 +233,79 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, f32x4* xs, int K) {
     }
 }
 
+// NX dot products of one 16-byte weight chunk with NX staged x vectors (the
+// weights are dequantised once): acc[n] += sum_e w_e * x_n[e], x vector n at
+// xs_all + n * npad.  The int4 path returns sums of 16 * q like chunk_dot.
+template <int FMT, int NX>
+__device__ __forceinline__ void chunk_dot_nx(const u32x4 w, const f32x4* __restrict__ xs_all,
+                                             int npad, int p0, float (&acc)[NX]) {
+    constexpr int EPC = WT<FMT>::EPC;
+    float v[EPC];
+    if constexpr (FMT == WF_F32) {
+        v[0] = __uint_as_float(w.x); v[1] = __uint_as_float(w.y);
+        v[2] = __uint_as_float(w.z); v[3] = __uint_as_float(w.w);
+    } else if constexpr (FMT == WF_BF16) {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { v[2 * j] = bf16_lo(ww[j]); v[2 * j + 1] = bf16_hi(ww[j]); }
+    } else if constexpr (FMT == WF_I8) {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) v[4 * j + b] = s8_at(ww[j], b);
+    } else {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t hi = ww[j] & 0xF0F0F0F0u;          // even elements * 16
+            const uint32_t lo = (ww[j] << 4) & 0xF0F0F0F0u;   // odd elements * 16
+#pragma unroll
+            for (int b = 0; b < 4; ++b) { v[8 * j + 2 * b] = s8_at(hi, b); v[8 * j + 2 * b + 1] = s8_at(lo, b); }
+        }
+    }
+    int base = xpad(p0);
+    asm volatile("" : "+v"(base));
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        const f32x4* __restrict__ xs = xs_all + n * npad + base;
+        float t = acc[n];
+#pragma unroll
+        for (int j = 0; j < EPC / 4; ++j) {
+            const f32x4 x = xs[j];
+            t += v[4 * j] * x.x;
+            t += v[4 * j + 1] * x.y;
+            t += v[4 * j + 2] * x.z;
+            t += v[4 * j + 3] * x.w;
+        }
+        acc[n] = t;
+    }
+}
+
+// Plain staging of NX x rows (row n at a.x + n * x_stride_n, 16-byte aligned)
+// into the padded layout, row n at xs + n * npad.  One row's loads are all in
+// flight before its stores.
+template <int NX>
+__device__ __forceinline__ void stage_xn(const GemvArgs& a, f32x4* xs, int K, int npad) {
+    const int np = K >> 2;
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr(a.x + (long)n * a.x_stride_n), (short)0, K * 4, 0x00020000);
+        f32x4 xv[12];
+#pragma unroll
+        for (int j = 0; j < 12; ++j)
+            if (256 * j < np)
+                xv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      xb, (int)threadIdx.x * 16, 4096 * j, 0));
+#pragma unroll
+        for (int j = 0; j < 12; ++j) {
+            const int p = threadIdx.x + 256 * j;
+            if (256 * j < np && p < np) xs[n * npad + xpad(p)] = xv[j];
+        }
+    }
+}
+
 // ordered (value, index) key: larger value wins, ties keep the larger index
 __device__ __forceinline__ unsigned long long argkey_f(float v, int i) {
     uint32_t u = __float_as_uint(v);
@@ -240,8 +313,10 @@ __device__ __forceinline__ unsigned long long argkey_f(float v, int i) {
     return ((unsigned long long)u << 32) | (uint32_t)i;
 }
 
-template <int FMT, int ROWS, int UNROLL>
+template <int FMT, int ROWS, int UNROLL, int NX = 1>
 __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
+    // NX > 1: NX activation rows share every weight load (a small ragged
+    // batch); plain x only, store / SwiGLU epilogues, y[n] at n * y_stride_n
     extern __shared__ f32x4 xs[];
     constexpr int EPC = WT<FMT>::EPC;
     constexpr int PPC = EPC / 4;                  // 16-byte x pieces per chunk
@@ -295,15 +370,21 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
     u32x4 cur[UNROLL][ROWS];
     float scur[UNROLL][ROWS];
     // the first weight loads go out before x is staged, hiding the staging
+    const int npad = (K >> 2) + ((K >> 2) + 15) / 16;     // padded pieces per x row
     if (total > 0) load(0, cur, scur);
-    stage_x<true>(a, xs, K);
+    if constexpr (NX == 1) stage_x<true>(a, xs, K);
+    else stage_xn<NX>(a, xs, K, npad);
     __syncthreads();
 
-    float acc[ROWS];
+    float acc[ROWS][NX];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int n = 0; n < NX; ++n) acc[r][n] = 0.0f;
     unsigned long long best = 0;          // EPI_ARGMAX: best (logit, row) of this wave
-    float gate = 0.0f;                    // SEQ == 2: the pair's gate row
+    float gate[NX];                       // SEQ == 2: the pair's gate row
+#pragma unroll
+    for (int n = 0; n < NX; ++n) gate[n] = 0.0f;
 
     for (int it = 0; it < total; ++it) {
         u32x4 nxt[UNROLL][ROWS];
@@ -317,10 +398,21 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
             if (c < chunks) {
 #pragma unroll
                 for (int r = 0; r < ROWS; ++r) {
-                    if constexpr (FMT == WF_I4)
-                        acc[r] += scur[u][r] * chunk_dot<FMT>(cur[u][r], xs, c * PPC, 0.0f);
-                    else
-                        acc[r] = chunk_dot<FMT>(cur[u][r], xs, c * PPC, acc[r]);
+                    if constexpr (NX == 1) {
+                        if constexpr (FMT == WF_I4)
+                            acc[r][0] += scur[u][r] * chunk_dot<FMT>(cur[u][r], xs, c * PPC, 0.0f);
+                        else
+                            acc[r][0] = chunk_dot<FMT>(cur[u][r], xs, c * PPC, acc[r][0]);
+                    } else if constexpr (FMT == WF_I4) {
+                        float t[NX];
+#pragma unroll
+                        for (int n = 0; n < NX; ++n) t[n] = 0.0f;
+                        chunk_dot_nx<FMT, NX>(cur[u][r], xs, npad, c * PPC, t);
+#pragma unroll
+                        for (int n = 0; n < NX; ++n) acc[r][n] += scur[u][r] * t[n];
+                    } else {
+                        chunk_dot_nx<FMT, NX>(cur[u][r], xs, npad, c * PPC, acc[r]);
+                    }
                 }
             }
         }
@@ -328,42 +420,82 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
             // end of this row group: reduce across the wave and store
             const int r0 = row_of(it);
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int n = 0; n < NX; ++n) acc[r][n] = wave_sum(acc[r][n]);
             if constexpr (FMT == WF_I4) {
                 // the chunks hold 16 * q: one exact power-of-two rescale per row
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r) acc[r] *= 0.0625f;
+                for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                    for (int n = 0; n < NX; ++n) acc[r][n] *= 0.0625f;
             }
             if constexpr (FMT == WF_I8) {
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r) acc[r] *= a.scales[r0 + r < M ? r0 + r : M - 1];
-            }
-            if (a.epi == EPI_SILU_MUL) {
-                // rows (2i, 2i+1) = (gate_i, up_i): y[i] = silu(gate) * up
-                if constexpr (ROWS % 2 == 0) {
+                for (int r = 0; r < ROWS; ++r) {
+                    const float sc = a.scales[r0 + r < M ? r0 + r : M - 1];
 #pragma unroll
-                    for (int r = 0; r < ROWS; r += 2)
-                        if (lane == r && r0 + r + 1 < M)
-                            a.y[(r0 + r) >> 1] = silu_f(acc[r]) * acc[r + 1];
-                } else if (ROWS == 1) {
-                    if ((r0 & 1) == 0) gate = acc[0];
-                    else if (lane == 0 && r0 < M) a.y[r0 >> 1] = silu_f(gate) * acc[0];
+                    for (int n = 0; n < NX; ++n) acc[r][n] *= sc;
                 }
-            } else {
+            }
+            if constexpr (NX == 1) {
+                if (a.epi == EPI_SILU_MUL) {
+                    // rows (2i, 2i+1) = (gate_i, up_i): y[i] = silu(gate) * up
+                    if constexpr (ROWS % 2 == 0) {
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r)
-                    if (lane == r && r0 + r < M) a.y[r0 + r] = acc[r];
-                if (a.epi == EPI_ARGMAX) {
+                        for (int r = 0; r < ROWS; r += 2)
+                            if (lane == r && r0 + r + 1 < M)
+                                a.y[(r0 + r) >> 1] = silu_f(acc[r][0]) * acc[r + 1][0];
+                    } else if (ROWS == 1) {
+                        if ((r0 & 1) == 0) gate[0] = acc[0][0];
+                        else if (lane == 0 && r0 < M) a.y[r0 >> 1] = silu_f(gate[0]) * acc[0][0];
+                    }
+                } else {
 #pragma unroll
                     for (int r = 0; r < ROWS; ++r)
-                        if (r0 + r < M) {
-                            const unsigned long long k = argkey_f(acc[r], r0 + r);
-                            best = k > best ? k : best;
+                        if (lane == r && r0 + r < M) a.y[r0 + r] = acc[r][0];
+                    if (a.epi == EPI_ARGMAX) {
+#pragma unroll
+                        for (int r = 0; r < ROWS; ++r)
+                            if (r0 + r < M) {
+                                const unsigned long long k = argkey_f(acc[r][0], r0 + r);
+                                best = k > best ? k : best;
+                            }
+                    }
+                }
+            } else {
+                // lane n * ROWS + r stores (row r0 + r, sequence n)
+                if (a.epi == EPI_SILU_MUL) {
+                    if constexpr (ROWS % 2 == 0) {
+#pragma unroll
+                        for (int n = 0; n < NX; ++n)
+#pragma unroll
+                            for (int r = 0; r < ROWS; r += 2)
+                                if (lane == n * ROWS + r && r0 + r + 1 < M)
+                                    a.y[n * a.y_stride_n + (long)((r0 + r) >> 1) * a.y_stride_m] =
+                                        silu_f(acc[r][n]) * acc[r + 1][n];
+                    } else if (ROWS == 1) {
+#pragma unroll
+                        for (int n = 0; n < NX; ++n) {
+                            if ((r0 & 1) == 0) gate[n] = acc[0][n];
+                            else if (lane == n && r0 < M)
+                                a.y[n * a.y_stride_n + (long)(r0 >> 1) * a.y_stride_m] =
+                                    silu_f(gate[n]) * acc[0][n];
                         }
+                    }
+                } else {
+#pragma unroll
+                    for (int n = 0; n < NX; ++n)
+#pragma unroll
+                        for (int r = 0; r < ROWS; ++r)
+                            if (lane == n * ROWS + r && r0 + r < M)
+                                a.y[n * a.y_stride_n + (long)(r0 + r) * a.y_stride_m] = acc[r][n];
                 }
             }
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int n = 0; n < NX; ++n) acc[r][n] = 0.0f;
         }
         if (it + 1 < total) {
 #pragma unroll
@@ -491,10 +623,10 @@ static int resident_per_cu(const void* kern, size_t lds) {
 // Persistent grid of the LDS-staged kernel: every block resident at once
 // (LDS and register occupancy bound the blocks per CU), at most
 // blocks_per_cu of them per CU.  0 if the kernel cannot run at this K.
-static int n1_blocks(const void* kern, int M, int K, int rows, int blocks_per_cu) {
+static int n1_blocks(const void* kern, int M, size_t lds, int rows, int blocks_per_cu) {
     const int n_groups = (M + rows - 1) / rows;
     const int blocks = (n_groups + 3) / 4;
-    const int fit = resident_per_cu(kern, gemv_x_lds_bytes(K));
+    const int fit = resident_per_cu(kern, lds);
     if (fit < 1) return 0;
     const int bpc = blocks_per_cu < fit ? blocks_per_cu : fit;
     const int cap = bpc * device_cu_count();
@@ -511,7 +643,7 @@ int launch_n1(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
     const size_t lds = gemv_x_lds_bytes(a.K);
     ATLAS_REQUIRE(lds <= 160 * 1024, "gemv: K=%d exceeds the LDS-staged limit", a.K);
     auto kern = gemv_n1_kernel<FMT, ROWS, UNROLL>;
-    const int blocks = n1_blocks((const void*)kern, a.M, a.K, n1_group_rows(a, ROWS), blocks_per_cu);
+    const int blocks = n1_blocks((const void*)kern, a.M, lds, n1_group_rows(a, ROWS), blocks_per_cu);
     ATLAS_REQUIRE(blocks > 0, "gemv: the kernel does not fit a CU at K=%d", a.K);
     if (a.epi == EPI_ARGMAX)
         ATLAS_REQUIRE(blocks * 4 <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
@@ -569,7 +701,8 @@ static const void* n1_kernel(int fmt, int rows, int unroll) {
 int gemv_waves(const GemvArgs& a) {
     const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
     const void* kern = n1_kernel(a.fmt, sh.rows, sh.unroll);
-    return kern ? 4 * n1_blocks(kern, a.M, a.K, n1_group_rows(a, sh.rows), sh.bpc) : 0;
+    return kern ? 4 * n1_blocks(kern, a.M, gemv_x_lds_bytes(a.K), n1_group_rows(a, sh.rows), sh.bpc)
+                : 0;
 }
 
 int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
@@ -619,6 +752,51 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     }
     ATLAS_LAUNCH_CHECK("gemv_generic");
     return ATLAS_OK;
+}
+
+// ---- small ragged batch: N = 2..4 activation rows per weight load ----------
+template <int FMT, int ROWS, int UNROLL, int NX>
+static int launch_nx(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
+    const size_t lds = (size_t)NX * gemv_x_lds_bytes(a.K);
+    ATLAS_REQUIRE(lds <= 160 * 1024, "gemv: %d rows of K=%d exceed LDS", NX, a.K);
+    auto kern = gemv_n1_kernel<FMT, ROWS, UNROLL, NX>;
+    const int blocks = n1_blocks((const void*)kern, a.M, lds, n1_group_rows(a, ROWS), blocks_per_cu);
+    ATLAS_REQUIRE(blocks > 0, "gemv: the kernel does not fit a CU at K=%d", a.K);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a);
+    ATLAS_LAUNCH_CHECK("gemv_nx");
+    return ATLAS_OK;
+}
+
+bool gemv_multi_ok(const GemvArgs& a) {
+    const uintptr_t al = (uintptr_t)a.w | (uintptr_t)a.x;
+    return a.N >= 2 && a.N <= kGemvMaxNx && a.M > 0 && a.K > 0 && (al & 15) == 0 &&
+           a.pro == PRO_X && (a.epi == EPI_STORE || a.epi == EPI_SILU_MUL) &&
+           a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && a.K % 4 == 0 &&
+           a.K <= 256 * 4 * 12 &&    // stage_xn: twelve 16-byte pieces per thread
+           gemv_fast_ok(a.fmt, a.K, a.block) && gemv_pitch_ok(a) &&
+           (size_t)a.N * gemv_x_lds_bytes(a.K) <= 160 * 1024 &&
+           (a.epi != EPI_SILU_MUL || a.M % 2 == 0);
+}
+
+int gemv_multi_launch(const GemvArgs& a_in, hipStream_t st) {
+    GemvArgs a = a_in;
+    gemv_fill_int4_index(a);
+    ATLAS_REQUIRE(a.w && a.x && a.y, "gemv: null pointer");
+    ATLAS_REQUIRE(a.fmt == WF_F32 || a.fmt == WF_BF16 || a.scales, "gemv: null scales");
+    ATLAS_REQUIRE(gemv_multi_ok(a), "gemv: %d rows need the aligned fast path", a.N);
+    const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
+#define ATLAS_NX(F, R, U)                                                            \
+    if (a.fmt == F && sh.rows == R && sh.unroll == U) {                              \
+        switch (a.N) {                                                               \
+        case 2: return launch_nx<F, R, U, 2>(a, st, sh.bpc);                         \
+        case 3: return launch_nx<F, R, U, 3>(a, st, sh.bpc);                         \
+        case 4: return launch_nx<F, R, U, 4>(a, st, sh.bpc);                         \
+        }                                                                            \
+    }
+    ATLAS_N1_LIST(ATLAS_NX)
+#undef ATLAS_NX
+    set_error(ATLAS_EUNSUPPORTED, "gemv: no %d-row kernel for format %d", a.N, a.fmt);
+    return ATLAS_EUNSUPPORTED;
 }
 
 }  // namespace atlas

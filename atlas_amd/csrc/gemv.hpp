@@ -44,6 +44,11 @@ int gemv_fast_ok(int fmt, int K, int block);
 int gemv_launch(const GemvArgs& a, hipStream_t st);     // N == 1
 int gemv_waves(const GemvArgs& a);                       // persistent waves of gemv_launch
 int skinny_launch(const GemvArgs& a, hipStream_t st);   // 1 <= N <= 8
+// N = 2..kGemvMaxNx rows through the batch-1 GEMV (every weight load feeds
+// all N rows); plain x, store / SwiGLU epilogues
+constexpr int kGemvMaxNx = 4;
+bool gemv_multi_ok(const GemvArgs& a);
+int gemv_multi_launch(const GemvArgs& a, hipStream_t st);
 int skinny_reserve(int M, int N, int K);
 int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,
                         hipStream_t st);

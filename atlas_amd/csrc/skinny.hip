@@ -545,6 +545,12 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     if (a.M == 0) return ATLAS_OK;
     ATLAS_REQUIRE(a.K % 32 == 0 && a.K > 0, "skinny: K %% 32 != 0");
     ATLAS_REQUIRE(gemv_pitch_ok(a), "skinny: row pitch %ld bytes for K %d", a.ldw, a.K);
+    // Two or three rows stream the weights once through the multi-row GEMV:
+    // at the 7B shapes on MI355X it takes 0.55-0.75x the MFMA kernel's time
+    // for two rows and 0.65-0.9x for three (int4 11008 x 4096 at three rows
+    // is within 3%); from four rows on, the LDS reads of the x rows per
+    // weight chunk make it no faster than the MFMA kernel.
+    if (a.N <= 3 && gemv_multi_ok(a)) return gemv_multi_launch(a, st);
     const uintptr_t al = (uintptr_t)a.w;
     switch (a.fmt) {
     case WF_BF16:

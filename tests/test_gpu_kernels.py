@@ -114,25 +114,26 @@ def test_gemv_swiglu(orc, fmt):
 
 
 # ---------------------------------------------------------------------------
-# skinny ragged batch (MFMA)
+# skinny ragged batch: multi-row GEMV (2-3 rows) and MFMA tiles (4-8 rows)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n", [1, 3, 5, 8])
-@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
-def test_skinny(orc, fmt, n):
-    M, K = (4096, 4096) if n in (1, 8) else (1000, 512)
-    print(f"skinny {fmt} n={n} M={M} K={K}", flush=True)
-    w = _w((M, K), 21 + n)
-    x = np.random.default_rng(n).standard_normal((n, K)).astype(np.float32)
+def _stored(orc, fmt, w, block=32):
+    """(oracle view, device weights, device scales, format id, block) of w."""
+    M, K = w.shape
     if fmt == "bf16":
         b = orc.bf16_from_f32(w)
-        view, dw, ds, fid, bs = orc.MatView.bf16(b, M, K), Dev(b), None, 1, 0
-    elif fmt == "int8":
+        return orc.MatView.bf16(b, M, K), Dev(b), None, 1, 0
+    if fmt == "int8":
         q, s = orc.int8_quantize(w)
-        view, dw, ds, fid, bs = orc.MatView.int8(q, s), Dev(q), Dev(s), 2, 0
-    else:
-        q, s = orc.int4_quantize(w, 32)
-        view, dw, ds, fid, bs = orc.MatView.int4(q, s, M, K, 32), Dev(q), Dev(s), 3, 32
+        return orc.MatView.int8(q, s), Dev(q), Dev(s), 2, 0
+    q, s = orc.int4_quantize(w, block)
+    return orc.MatView.int4(q, s, M, K, block), Dev(q), Dev(s), 3, block
+
+
+def _skinny_check(orc, fmt, n, M, K, block=32, seed=0):
+    w = _w((M, K), 21 + n + seed)
+    x = np.random.default_rng(n + seed).standard_normal((n, K)).astype(np.float32)
+    view, dw, ds, fid, bs = _stored(orc, fmt, w, block)
     ref = orc.linear_batch(view, x)
     dx, dy = Dev(x), Dev.empty((n, M))
     assert lib().atlas_gemm_skinny_f32(fid, dw.ptr, ds.ptr if ds else None, bs, dx.ptr, dy.ptr,
@@ -140,6 +141,27 @@ def test_skinny(orc, fmt, n):
     y = dy.get()
     for i in range(n):
         assert rel_err(y[i], ref[i]) <= GEMV_TOL, i
+
+
+@pytest.mark.parametrize("n", [1, 3, 5, 8])
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
+def test_skinny(orc, fmt, n):
+    M, K = (4096, 4096) if n in (1, 8) else (1000, 512)
+    print(f"skinny {fmt} n={n} M={M} K={K}", flush=True)
+    _skinny_check(orc, fmt, n, M, K)
+
+
+# Two and three rows take the multi-row GEMV: the 7B shapes (three rows of
+# K = 11008 fill 132 KB of LDS), odd row counts, K not a multiple of one
+# wave step, int4 blocks of 128, and a 3 x 32 matrix.
+@pytest.mark.parametrize("fmt,n,M,K,block", [
+    ("bf16", 2, 11008, 4096, 32), ("bf16", 3, 4096, 11008, 32), ("bf16", 2, 3, 32, 32),
+    ("int8", 2, 4096, 11008, 32), ("int8", 3, 1001, 544, 32), ("int8", 3, 12288, 4096, 32),
+    ("int4", 2, 11008, 4096, 32), ("int4", 3, 4096, 11008, 32), ("int4", 3, 777, 1024, 128),
+    ("int4", 2, 64, 12288, 64)])
+def test_skinny_multi_row(orc, fmt, n, M, K, block):
+    print(f"skinny multi-row {fmt} n={n} M={M} K={K} block={block}", flush=True)
+    _skinny_check(orc, fmt, n, M, K, block, seed=7)
 
 
 def test_sgemm_bf16_reference_layout(orc):

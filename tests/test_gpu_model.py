@@ -201,6 +201,54 @@ def test_ragged_batch_matches_single(orc):
     assert len(m.generate_with_sampling(prompts[0], 8, SamplingConfig.greedy())) == 8
 
 
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_ragged_batch_quantised(orc, fmt):
+    # three sequences of different prompt lengths: the batch narrows from
+    # three rows to two to one, so the multi-row GEMV runs its store and
+    # SwiGLU epilogues (int8: one-row waves taking the gate/up pair in turn)
+    cfg = modelgen.olmo3_small_config(max_seq=96)
+    W = modelgen.make_weights(cfg, seed=41, fmt=fmt)
+    m = modelgen.engine_model(W, max_batch=4)
+    rng = np.random.default_rng(9)
+    prompts = [list(rng.integers(0, cfg["vocab"], n)) for n in (2, 11, 25)]
+    batch = m.generate_batch(prompts, 16)
+    o = modelgen.oracle_model(W, threads=8)
+    for p, got in zip(prompts, batch):
+        want = o.generate_greedy(p, 16)
+        if got != want:
+            k = next(i for i in range(min(len(got), len(want))) if got[i] != want[i])
+            o2 = modelgen.oracle_model(W)
+            lg = None
+            for t in list(p) + want[:k]:
+                lg = o2.forward_one(int(t))
+            assert _top2_margin(lg) <= 2 * LOGIT_TOL * np.max(np.abs(lg)), (len(p), k)
+
+
+def test_ragged_batch_long_context(orc):
+    # positions >= 8 replay the batch step's long-context variant: QK-norm /
+    # RoPE / KV write for every sequence, the split kernel over (KV head,
+    # split, sequence) with each sequence's own adaptive split count, and the
+    # split merge; windowed and full layers, graph and eager
+    cfg = modelgen.olmo3_small_config(max_seq=200)
+    W = modelgen.make_weights(cfg, seed=43)
+    rng = np.random.default_rng(11)
+    prompts = [list(rng.integers(0, cfg["vocab"], n)) for n in (1, 5, 30, 70)]
+    o = modelgen.oracle_model(W, threads=8)
+    want = [o.generate_greedy(p, 24) for p in prompts]
+    for graph in (True, False):
+        m = modelgen.engine_model(W, max_batch=4, use_graph=graph)
+        m.set_long_context(8)
+        batch = m.generate_batch(prompts, 24)
+        for p, got, w in zip(prompts, batch, want):
+            if got != w:
+                k = next(i for i in range(min(len(got), len(w))) if got[i] != w[i])
+                o2 = modelgen.oracle_model(W)
+                lg = None
+                for t in list(p) + w[:k]:
+                    lg = o2.forward_one(int(t))
+                assert _top2_margin(lg) <= 2 * LOGIT_TOL * np.max(np.abs(lg)), (graph, len(p), k)
+
+
 def test_long_context_attention_path(orc):
     # positions >= from_pos replay the long-context step (QK-norm/RoPE/KV-write
     # kernel, adaptive split kernel, split merge); forcing it from position 8
