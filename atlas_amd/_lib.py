@@ -126,6 +126,23 @@ SIGNATURES = {
     "atlas_model_generate_batch": (I, [P, P, P, I, I, C.POINTER(SamplingC), P, P]),
     "atlas_model_decode_greedy": (I, [P, U32, I, P]),
     "atlas_model_set_long_context": (I, [P, I]),
+    "atlas_model_get_config": (I, [P, C.POINTER(ModelConfigC)]),
+    "atlas_model_set_tensor_dev": (I, [P, I, I, P, I, I64, P]),
+    "atlas_load_scratch_create": (P, []),
+    "atlas_load_scratch_destroy": (None, [P]),
+    # include/atlas_loader.h (crates/atlas-model/src/lib.rs:2048-2570)
+    "atlas_st_open": (I, [C.c_char_p, P]),
+    "atlas_st_from_bytes": (I, [P, SZ, P]),
+    "atlas_st_close": (None, [P]),
+    "atlas_st_count": (I, [P]),
+    "atlas_st_find": (I, [P, C.c_char_p]),
+    "atlas_st_desc": (I, [P, I, P, P, P, P, P]),
+    "atlas_st_get_f32": (I, [P, C.c_char_p, P, SZ, P]),
+    "atlas_st_get_bf16": (I, [P, C.c_char_p, P, SZ, P]),
+    "atlas_f16_to_f32": (F, [C.c_uint16]),
+    "atlas_config_patch_hf_json": (I, [C.c_char_p, C.POINTER(ModelConfigC), P, I, P, P]),
+    "atlas_model_load_safetensors": (I, [C.c_char_p, C.POINTER(ModelConfigC), P]),
+    "atlas_model_load_dir": (I, [C.c_char_p, C.POINTER(ModelConfigC), P, P]),
     "atlas_sample_host": (I, [P, I, P, I, I, C.POINTER(SamplingC), C.POINTER(C.c_uint64), P]),
     "atlas_model_bench_gemv": (I, [P, I, I, P, P, P]),
     "atlas_model_use_graph": (I, [P, I]),

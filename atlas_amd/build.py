@@ -22,7 +22,7 @@ OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libatlas_kernels.so")
 
 SOURCES = ["gemv.hip", "skinny.hip", "attention.hip", "fused.hip", "runtime.cpp", "capi.cpp",
-           "engine.cpp"]
+           "engine.cpp", "loader.cpp"]
 
 
 def hipcc() -> str:

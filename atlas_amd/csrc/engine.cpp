@@ -776,6 +776,132 @@ int tensor_io(atlas_model* m, int kind, int layer, void* data, float* scales, bo
     return ATLAS_EINVAL;
 }
 
+// ---- tensors from device memory (the safetensors loader) ---------------------
+// Where a tensor kind lives: rows [base, base + rows * stride) step stride of a
+// matrix, a float vector, or the bf16 embedding.
+struct TensorTarget {
+    DevMat* mat = nullptr;
+    int base = 0, stride = 1, rows = 0;
+    float* vec = nullptr;
+    size_t n = 0;                  // elements of the tensor
+    bool embed = false;
+};
+
+int tensor_target(atlas_model* m, int kind, int layer, TensorTarget& t) {
+    const atlas_model_config& c = m->cfg;
+    const int d = c.d_model;
+    auto mat = [&](DevMat& w, int base, int stride, int rows) {
+        t.mat = &w; t.base = base; t.stride = stride; t.rows = rows;
+        t.n = (size_t)rows * w.cols;
+        return ATLAS_OK;
+    };
+    auto vec = [&](float* v, size_t n) {
+        ATLAS_REQUIRE(v, "tensor kind %d is not present in this model", kind);
+        t.vec = v; t.n = n;
+        return ATLAS_OK;
+    };
+    switch (kind) {
+    case ATLAS_T_EMBED: t.embed = true; t.n = (size_t)c.vocab * d; return ATLAS_OK;
+    case ATLAS_T_LM_HEAD: return mat(m->lm_head, 0, 1, c.vocab);
+    case ATLAS_T_FINAL_NORM: return vec(m->final_norm, d);
+    }
+    ATLAS_REQUIRE(layer >= 0 && layer < c.n_layers, "layer %d out of range", layer);
+    LayerW& L = m->L[layer];
+    switch (kind) {
+    case ATLAS_T_WQ: return mat(L.qkv, 0, 1, d);
+    case ATLAS_T_WK: return mat(L.qkv, d, 1, m->kvd);
+    case ATLAS_T_WV: return mat(L.qkv, d + m->kvd, 1, m->kvd);
+    case ATLAS_T_WO: return mat(L.wo, 0, 1, d);
+    case ATLAS_T_W_GATE: return mat(L.gu, 0, 2, c.ffn_hidden);
+    case ATLAS_T_W_UP: return mat(L.gu, 1, 2, c.ffn_hidden);
+    case ATLAS_T_W_DOWN: return mat(L.down, 0, 1, d);
+    case ATLAS_T_ATTN_NORM: return vec(L.attn_norm, d);
+    case ATLAS_T_FFN_NORM: return vec(L.ffn_norm, d);
+    case ATLAS_T_Q_NORM: return vec(L.q_norm, (size_t)c.n_heads * m->hd);
+    case ATLAS_T_K_NORM: return vec(L.k_norm, (size_t)m->kvd);
+    }
+    set_error(ATLAS_EINVAL, "unknown tensor kind %d", kind);
+    return ATLAS_EINVAL;
+}
+
+}  // namespace
+
+// Device temporaries of set_tensor_dev, grown on demand.
+struct atlas_load_scratch {
+    void* conv = nullptr;          // bf16 conversion of an f32 matrix
+    void* qdata = nullptr;         // quantised rows
+    float* qscales = nullptr;
+    size_t conv_bytes = 0, qdata_bytes = 0, qscale_bytes = 0;
+};
+
+namespace {
+
+int grow(void** p, size_t* have, size_t need) {
+    if (need <= *have) return ATLAS_OK;
+    if (*p) {
+        ATLAS_HIP(hipDeviceSynchronize());
+        ATLAS_HIP(hipFree(*p));
+        *p = nullptr;
+        *have = 0;
+    }
+    if (hipMalloc(p, need) != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        set_error(ATLAS_ENOMEM, "load scratch: %zu bytes", need);
+        return ATLAS_ENOMEM;
+    }
+    *have = need;
+    return ATLAS_OK;
+}
+
+// Converts a device tensor (f32 or bf16 elements) into the model's format and
+// layout, on the model's stream, without waiting for it.
+int set_tensor_dev(atlas_model* m, int kind, int layer, const void* src, int src_dtype, size_t n,
+                   atlas_load_scratch& s) {
+    ATLAS_REQUIRE(src, "set_tensor_dev: null source");
+    ATLAS_REQUIRE(src_dtype == WF_F32 || src_dtype == WF_BF16,
+                  "set_tensor_dev: source dtype %d (f32 or bf16)", src_dtype);
+    TensorTarget t;
+    TRY(tensor_target(m, kind, layer, t));
+    ATLAS_REQUIRE(n == t.n, "set_tensor_dev: tensor kind %d has %zu elements, expected %zu", kind, n,
+                  t.n);
+    const bool bf16 = src_dtype == WF_BF16;
+    if (t.vec) {
+        if (bf16) return cvt_launch(CVT_BF16_F32, src, t.vec, (long)n, m->st);
+        ATLAS_HIP(hipMemcpyAsync(t.vec, src, n * 4, hipMemcpyDeviceToDevice, m->st));
+        return ATLAS_OK;
+    }
+    if (t.embed) {
+        if (!bf16) return cvt_launch(CVT_F32_BF16, src, m->embed, (long)n, m->st);
+        ATLAS_HIP(hipMemcpyAsync(m->embed, src, n * 2, hipMemcpyDeviceToDevice, m->st));
+        return ATLAS_OK;
+    }
+    DevMat& w = *t.mat;
+    const size_t rb = w.row_bytes(), rp = w.row_pitch(), spr = w.scales_per_row();
+    char* dst = (char*)w.w + (size_t)t.base * rp;
+    const void* rows_src = src;
+    if (w.fmt == WF_BF16) {
+        if (!bf16) {
+            TRY(grow(&s.conv, &s.conv_bytes, n * 2));
+            TRY(cvt_launch(CVT_F32_BF16, src, s.conv, (long)n, m->st));
+            rows_src = s.conv;
+        }
+    } else {
+        TRY(grow(&s.qdata, &s.qdata_bytes, rb * t.rows));
+        TRY(grow((void**)&s.qscales, &s.qscale_bytes, spr * t.rows * 4));
+        if (w.fmt == WF_I8)
+            TRY(quant_i8_launch(src, bf16, t.rows, w.cols, (int8_t*)s.qdata, s.qscales, m->st));
+        else
+            TRY(quant_i4_launch(src, bf16, (long)n, w.block, (uint8_t*)s.qdata, s.qscales, m->st));
+        rows_src = s.qdata;
+        ATLAS_HIP(hipMemcpy2DAsync(w.scales + (size_t)t.base * spr, spr * 4 * t.stride, s.qscales,
+                                   spr * 4, spr * 4, t.rows, hipMemcpyDeviceToDevice, m->st));
+    }
+    ATLAS_HIP(hipMemcpy2DAsync(dst, rp * t.stride, rows_src, rb, rb, t.rows, hipMemcpyDeviceToDevice,
+                               m->st));
+    return ATLAS_OK;
+}
+
 // ---- the ragged batch step ----------------------------------------------------
 // n rows of activations through w: the batch-1 GEMV for one row, the skinny
 // launcher for 2..8 (the multi-row GEMV for 2-3 rows, MFMA tiles above)
@@ -1078,6 +1204,34 @@ ATLAS_API int atlas_model_set_tensor(atlas_model* m, int kind, int layer, const 
     return tensor_io(m, kind, layer, const_cast<void*>(data), const_cast<float*>(scales), true);
 }
 
+ATLAS_API atlas_load_scratch* atlas_load_scratch_create(void) { return new atlas_load_scratch(); }
+
+ATLAS_API void atlas_load_scratch_destroy(atlas_load_scratch* s) {
+    if (!s) return;
+    if (s->conv || s->qdata || s->qscales) (void)hipDeviceSynchronize();
+    if (s->conv) (void)hipFree(s->conv);
+    if (s->qdata) (void)hipFree(s->qdata);
+    if (s->qscales) (void)hipFree(s->qscales);
+    delete s;
+}
+
+ATLAS_API int atlas_model_set_tensor_dev(atlas_model* m, int kind, int layer, const void* src,
+                                         int src_dtype, int64_t numel, atlas_load_scratch* scratch) {
+    ATLAS_REQUIRE(m, "set_tensor_dev: null model");
+    ATLAS_REQUIRE(numel >= 0, "set_tensor_dev: numel < 0");
+    if (scratch) return set_tensor_dev(m, kind, layer, src, src_dtype, (size_t)numel, *scratch);
+    atlas_load_scratch s;
+    int rc = set_tensor_dev(m, kind, layer, src, src_dtype, (size_t)numel, s);
+    if (hipStreamSynchronize(m->st) != hipSuccess && rc == ATLAS_OK) {
+        set_error(ATLAS_EHIP, "set_tensor_dev: stream synchronisation failed");
+        rc = ATLAS_EHIP;
+    }
+    if (s.conv) (void)hipFree(s.conv);
+    if (s.qdata) (void)hipFree(s.qdata);
+    if (s.qscales) (void)hipFree(s.qscales);
+    return rc;
+}
+
 ATLAS_API int atlas_model_get_tensor(atlas_model* m, int kind, int layer, void* data,
                                      float* scales) {
     ATLAS_REQUIRE(m && data, "get_tensor: null argument");
@@ -1168,6 +1322,12 @@ ATLAS_API int atlas_model_reset(atlas_model* m) {
     ATLAS_REQUIRE(m, "reset: null model");
     TRY(reset_state(m));
     ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_get_config(const atlas_model* m, atlas_model_config* out) {
+    ATLAS_REQUIRE(m && out, "get_config: null argument");
+    *out = m->cfg;
     return ATLAS_OK;
 }
 

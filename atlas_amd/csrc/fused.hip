@@ -499,6 +499,49 @@ int init_launch(int kind, void* out, long n, unsigned long long seed, float a, f
     return ATLAS_OK;
 }
 
+// ---- element conversions of the safetensors loader ------------------------------
+// F16 -> F32 follows f16_to_f32 (crates/atlas-model/src/lib.rs:2243-2263): zero
+// and subnormals as (mant / 1024) * 2^-14 (exact), exponent 31 as +-inf or the
+// canonical quiet NaN, else the rebiased bits.  F32 -> BF16 truncates
+// (bits >> 16, lib.rs:2274); BF16 -> F32 shifts (bits << 16).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    const uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1Fu, mant = h & 0x3FFu;
+    if (ex == 0) {
+        const float m = (float)mant * 5.9604644775390625e-8f;     // mant * 2^-24
+        return sign ? -m : m;
+    }
+    if (ex == 31) {
+        if (mant) return __uint_as_float(0x7FC00000u);
+        return __uint_as_float(sign ? 0xFF800000u : 0x7F800000u);
+    }
+    return __uint_as_float((sign << 31) | ((ex + 112u) << 23) | (mant << 13));
+}
+
+__global__ void cvt_kernel(int kind, const void* __restrict__ src, void* __restrict__ dst, long n) {
+    for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        if (kind == CVT_F16_F32)
+            reinterpret_cast<float*>(dst)[i] =
+                f16_bits_to_f32(reinterpret_cast<const uint16_t*>(src)[i]);
+        else if (kind == CVT_F32_BF16)
+            reinterpret_cast<uint16_t*>(dst)[i] =
+                (uint16_t)(reinterpret_cast<const uint32_t*>(src)[i] >> 16);
+        else
+            reinterpret_cast<uint32_t*>(dst)[i] =
+                (uint32_t)reinterpret_cast<const uint16_t*>(src)[i] << 16;
+    }
+}
+
+int cvt_launch(int kind, const void* src, void* dst, long n, hipStream_t st) {
+    ATLAS_REQUIRE(src && dst && n >= 0 && kind >= CVT_F16_F32 && kind <= CVT_BF16_F32,
+                  "convert: bad arguments");
+    if (n == 0) return ATLAS_OK;
+    long blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(cvt_kernel, dim3((unsigned)blocks), dim3(256), 0, st, kind, src, dst, n);
+    ATLAS_LAUNCH_CHECK("convert");
+    return ATLAS_OK;
+}
+
 // ---- device quantisers, bit-exact to crates/atlas-quant/src/lib.rs:43-145 -------
 // Rust `(v * inv).clamp(lo, hi).round() as i8`: clamp, round half away from zero.
 __device__ __forceinline__ int clamp_round(float v, float lo, float hi) {

@@ -7,6 +7,7 @@ namespace atlas {
 enum { EW_ADD = 0, EW_SCALE = 1, EW_RELU = 2, EW_SILU_MUL = 3, EW_COPY = 4, EW_FILL = 5 };
 enum { INIT_NORMAL_F32 = 0, INIT_NORMAL_BF16 = 1, INIT_UNIFORM_F32 = 2 };
 enum { ARGMAX_MAX_PARTS = 16384 };
+enum { CVT_F16_F32 = 0, CVT_F32_BF16 = 1, CVT_BF16_F32 = 2 };
 
 struct QkvPostArgs {
     float* qkv;              // per sequence: [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)]
@@ -68,5 +69,7 @@ int quant_i8_launch(const void* src, int src_bf16, int rows, int cols, int8_t* d
                     hipStream_t st);
 int quant_i4_launch(const void* src, int src_bf16, long n, int block, uint8_t* data, float* scales,
                     hipStream_t st);
+// element conversion (CVT_*): f16 -> f32, f32 -> bf16 (truncation), bf16 -> f32
+int cvt_launch(int kind, const void* src, void* dst, long n, hipStream_t st);
 
 }  // namespace atlas

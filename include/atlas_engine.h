@@ -89,6 +89,24 @@ int atlas_model_set_tensor(atlas_model* m, int kind, int layer, const void* data
                            const float* scales);
 /* Download one tensor in the same layout. */
 int atlas_model_get_tensor(atlas_model* m, int kind, int layer, void* data, float* scales);
+
+/* Upload one tensor from device memory: numel f32 (ATLAS_W_F32) or bf16
+ * (ATLAS_W_BF16) elements in the reference's row-major layout, converted on
+ * the device to the model's weight_format (bf16 by truncation, lib.rs:2274;
+ * int8 / int4 by the atlas-quant rules) and placed into the model's layout.
+ * The checkpoint loader's building block; no reference counterpart (the
+ * reference converts on the host, lib.rs:2271-2279).  With a scratch the
+ * work is only enqueued on the model's stream (atlas_model_stream) and the
+ * source must stay valid until it completes; with scratch == NULL the call
+ * allocates its temporaries and waits.                                      */
+typedef struct atlas_load_scratch atlas_load_scratch;
+atlas_load_scratch* atlas_load_scratch_create(void);
+void atlas_load_scratch_destroy(atlas_load_scratch* s);
+int atlas_model_set_tensor_dev(atlas_model* m, int kind, int layer, const void* src,
+                               int src_dtype, int64_t numel, atlas_load_scratch* scratch);
+/* The model's configuration (after creation or loading); layer_sliding
+ * points into the model and lives as long as it.                           */
+int atlas_model_get_config(const atlas_model* m, atlas_model_config* out);
 /* Random init on the device: projections, embedding and lm_head N(0, 0.02)
  * (bf16 by truncation, or quantised by the atlas-quant rules), norm and
  * QK-norm weights U(0.5, 1.5).                                               */

@@ -94,7 +94,8 @@ enum {
     ATLAS_EINVAL = -1,
     ATLAS_EHIP = -2,
     ATLAS_ENOMEM = -3,
-    ATLAS_EUNSUPPORTED = -4
+    ATLAS_EUNSUPPORTED = -4,
+    ATLAS_EIO = -5              /* file open / read / map failed (loader)      */
 };
 
 int atlas_last_error_code(void);
