@@ -212,6 +212,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
     ap.add_argument("--no-ragged", action="store_true", help="skip the ragged batch of config 5")
+    ap.add_argument("--loader", action="store_true",
+                    help="also time the checkpoint loader on a 7B-shaped 4-layer bf16 "
+                         "safetensors checkpoint (writes ~3.3 GB to a temporary directory)")
+    ap.add_argument("--loader-only", action="store_true", help="only the loader measurement")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="short program for rocprofv3 --pmc passes: a 1 GiB device copy "
                          "(calibration), then one launch set of each bf16 decode GEMV kernel")
@@ -236,6 +240,9 @@ def main() -> int:
     prompt = rng.integers(0, 100278, 128)
     if args.pmc_probe:
         return pmc_probe(torch, lib, am)
+    if args.loader_only:
+        print(json.dumps({"checkpoint_load": loader_bench(torch, am)}), flush=True)
+        return 0
 
     micro = {}
     attn = {}
@@ -317,6 +324,7 @@ def main() -> int:
     ragged = None
     if not args.no_ragged:
         ragged = ragged_bench(am, rng, args.quick)
+    load_res = loader_bench(torch, am) if args.loader else None
 
     res = {
         "metric": "decode GEMV HBM GB/s (% of peak) + tok/s, 7B OLMo-shape bf16/int8/int4",
@@ -350,6 +358,7 @@ def main() -> int:
         "int8": quant["int8"],
         "int4": quant["int4"],
         "ragged_batch": ragged,
+        "checkpoint_load": load_res,
         "gemv_microbench": micro,
         "attention_microbench": attn,
         "reference_published": {"olmo3_7b_bf16_tok_s": 61.7, "hardware": "A100-SXM4-40GB"},
@@ -385,6 +394,98 @@ def ragged_bench(am, rng, quick: bool) -> dict:
     log(f"ragged batch: {len(lens)} sequences, {total} tokens ({gen} generated) in {dt:.2f} s "
         f"-> {total / dt:.0f} tok/s processed, {dt * 1e3 / steps:.2f} ms per batch step")
     m.close()
+    return res
+
+
+def loader_bench(torch, am, n_layers: int = 4) -> dict:
+    """The checkpoint loader (load_model_from_dir) on a 7B-shaped bf16
+    safetensors checkpoint cut to n_layers layers (embedding, lm_head and the
+    layers' matrices at their real shapes) plus an OLMo-3 config.json,
+    written to local disk first, so the load reads from the page cache.
+    Roofline: the pinned host-to-device copy rate measured in the same run."""
+    import dataclasses
+    import json
+    import shutil
+    import struct
+    import tempfile
+    from atlas_amd import loader
+    d, f, V = 4096, 11008, 100278
+    cfg7 = am.ModelConfig.olmo3_actual_7b()
+    cfg = dataclasses.replace(cfg7, n_layers=n_layers, layer_types=cfg7.layer_types[:n_layers],
+                              max_seq_len=256)
+    tensors = [("model.embed_tokens.weight", (V, d))]
+    for li in range(n_layers):
+        p = f"model.layers.{li}."
+        tensors += [(p + "self_attn.q_proj.weight", (d, d)), (p + "self_attn.k_proj.weight", (d, d)),
+                    (p + "self_attn.v_proj.weight", (d, d)), (p + "self_attn.o_proj.weight", (d, d)),
+                    (p + "mlp.gate_proj.weight", (f, d)), (p + "mlp.up_proj.weight", (f, d)),
+                    (p + "mlp.down_proj.weight", (d, f)),
+                    (p + "post_attention_layernorm.weight", (d,)),
+                    (p + "post_feedforward_layernorm.weight", (d,)),
+                    (p + "self_attn.q_norm.weight", (d,)), (p + "self_attn.k_norm.weight", (d,))]
+    tensors += [("model.norm.weight", (d,)), ("lm_head.weight", (V, d))]
+    # one 64 MiB block of N(0, 0.02) bf16 values, repeated through every tensor
+    blk = (np.random.default_rng(1).standard_normal(32 << 20) * 0.02).astype(np.float32)
+    blk = (blk.view(np.uint32) >> 16).astype(np.uint16)
+    hdr, off = {}, 0
+    for name, shape in tensors:
+        nb = int(np.prod(shape)) * 2
+        hdr[name] = {"dtype": "BF16", "shape": list(shape), "data_offsets": [off, off + nb]}
+        off += nb
+    tmp = tempfile.mkdtemp(prefix="atlas_ckpt_")
+    res = {}
+    try:
+        t0 = time.perf_counter()
+        h = json.dumps(hdr).encode()
+        with open(os.path.join(tmp, "model.safetensors"), "wb") as fo:
+            fo.write(struct.pack("<Q", len(h)) + h)
+            for name, shape in tensors:
+                n = int(np.prod(shape))
+                while n > 0:
+                    k = min(n, blk.size)
+                    fo.write(blk[:k].tobytes())
+                    n -= k
+        with open(os.path.join(tmp, "config.json"), "w") as fo:
+            json.dump({"layer_types": ["sliding_attention" if t == "sliding" else "full_attention"
+                                       for t in cfg.layer_types],
+                       "sliding_window": 4096, "rope_theta": 500000.0, "rms_norm_eps": 1e-6,
+                       "rope_scaling": {"rope_type": "yarn", "factor": 8.0,
+                                        "original_max_position_embeddings": 8192,
+                                        "attention_factor": 1.2079441541679836,
+                                        "beta_fast": 32.0, "beta_slow": 1.0},
+                       "eos_token_id": 100257}, fo)
+        file_bytes = os.path.getsize(os.path.join(tmp, "model.safetensors"))
+        log(f"loader: wrote {file_bytes / 1e9:.2f} GB checkpoint in {time.perf_counter() - t0:.1f} s")
+        # pinned host -> device copy rate (the transfer roofline)
+        src = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+        dst = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(4):
+            dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        h2d = 4 * (1 << 30) / (time.perf_counter() - t0) / 1e9
+        del src, dst
+        res = {"file_bytes": file_bytes, "layers": n_layers, "h2d_pinned_GB_s": round(h2d, 1)}
+        log(f"loader: pinned host-to-device copy {h2d:.1f} GB/s")
+        t0 = time.perf_counter()
+        am.OlmoModel(cfg, weight_format=am.W_BF16).close()
+        res["create_seconds"] = round(time.perf_counter() - t0, 3)
+        log(f"loader: creating the model alone {res['create_seconds']:.3f} s")
+        for fmt, name in ((am.W_BF16, "bf16"), (am.W_BF16, "bf16_again"), (am.W_INT8, "int8"),
+                          (am.W_INT4, "int4")):
+            t0 = time.perf_counter()
+            m = loader.load_model_from_dir(tmp, cfg, weight_format=fmt)
+            dt = time.perf_counter() - t0
+            assert m.eos_token_id == 100257 and m.config.post_norm and m.config.qk_norm
+            m.close()
+            gbs = file_bytes / dt / 1e9
+            res[name] = {"seconds": round(dt, 3), "GB_s": round(gbs, 2),
+                         "frac_of_h2d": round(gbs / h2d, 3)}
+            log(f"loader: {name} residency {dt:.2f} s, {gbs:.2f} GB/s ({gbs / h2d:.0%} of H2D)")
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
     return res
 
 
