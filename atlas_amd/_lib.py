@@ -144,6 +144,7 @@ SIGNATURES = {
     "atlas_model_load_safetensors": (I, [C.c_char_p, C.POINTER(ModelConfigC), P]),
     "atlas_model_load_dir": (I, [C.c_char_p, C.POINTER(ModelConfigC), P, P]),
     "atlas_sample_host": (I, [P, I, P, I, I, C.POINTER(SamplingC), C.POINTER(C.c_uint64), P]),
+    "atlas_sample_device": (I, [P, I, P, I, I, C.POINTER(SamplingC), C.POINTER(C.c_uint64), P]),
     "atlas_model_bench_gemv": (I, [P, I, I, P, P, P]),
     "atlas_model_use_graph": (I, [P, I]),
     "atlas_model_stream": (P, [P]),

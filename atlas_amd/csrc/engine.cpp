@@ -109,6 +109,8 @@ struct atlas_model {
     int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
     uint32_t *tok_dev = nullptr, *hist = nullptr, *suppress_dev = nullptr, *choice_dev = nullptr;
     int suppress_cap = 0;
+    SampleCfg* samp_cfg = nullptr;       // device sampling settings (mode 2)
+    unsigned long long* rng_dev = nullptr;   // device XorShift64 state (mode 2)
     unsigned long long* argpart = nullptr;
     long slot_stride = 0;
     int attn_splits = 1;           // fused kernel: maximum (grid) split count
@@ -119,8 +121,9 @@ struct atlas_model {
     int pos = 0;
     hipStream_t st = nullptr;
     bool use_graph = true;
-    hipGraphExec_t gexec[2] = {nullptr, nullptr};
-    hipGraphExec_t gexec_long[2] = {nullptr, nullptr};
+    // captured decode steps per mode: 0 forward, 1 + greedy choice, 2 + sampled choice
+    hipGraphExec_t gexec[3] = {nullptr, nullptr, nullptr};
+    hipGraphExec_t gexec_long[3] = {nullptr, nullptr, nullptr};
     hipGraphExec_t bgexec[9] = {};   // ragged batch step per batch size 1..8
     hipGraphExec_t bgexec_long[9] = {};   // ... its long-context variant
     // pinned staging ring for the batch step's tokens / positions / slots:
@@ -292,6 +295,15 @@ int head_step(atlas_model* m) {
     return ATLAS_OK;
 }
 
+SampleArgs sample_args(atlas_model* m, int* pos_inc) {
+    SampleArgs a{};
+    a.x = m->logits; a.n = m->cfg.vocab; a.cfg = m->samp_cfg;
+    a.suppress = m->suppress_dev;
+    a.hist = m->hist; a.hist_len = m->hist_len; a.step = m->step_dev; a.pos_inc = pos_inc;
+    a.rng = m->rng_dev; a.out_u32 = m->tok_dev; a.record = 1;
+    return a;
+}
+
 int choose_step(atlas_model* m) {
     ArgmaxArgs g{};
     g.x = m->logits; g.n = m->cfg.vocab; g.part = m->argpart;
@@ -416,6 +428,8 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
         g.n_parts = fused_choice ? gemv_waves(h) : 0;
         g.pos_inc = m->pos_dev;
         TRY(argmax_launch(g, m->st));
+    } else if (mode == 2) {
+        TRY(sample_launch(sample_args(m, m->pos_dev), m->st));
     } else {
         TRY(add_int_launch(m->pos_dev, 1, 1, m->st));
     }
@@ -430,6 +444,7 @@ int enqueue_step(atlas_model* m, int mode, bool long_ctx) {
     for (int li = 0; li < c.n_layers; ++li) TRY(layer_step(m, li));
     TRY(head_step(m));
     if (mode == 1) TRY(choose_step(m));
+    if (mode == 2) TRY(sample_launch(sample_args(m, nullptr), m->st));
     TRY(add_int_launch(m->pos_dev, 1, 1, m->st));
     return ATLAS_OK;
 }
@@ -512,15 +527,9 @@ int download_logits(atlas_model* m, float* host) {
     return ATLAS_OK;
 }
 
-// ---- greedy settings baked into the graph --------------------------------
-int set_greedy_cfg(atlas_model* m, const atlas_sampling* s) {
-    float theta = 1.f;
-    int window = 0, nsup = 0;
-    if (s) {
-        theta = s->repetition_penalty;
-        window = s->repetition_window;
-        nsup = s->n_suppress > 0 && s->suppress_initial_tokens ? s->n_suppress : 0;
-    }
+// the step-0 suppression list on the device (a captured step holds the
+// pointer, so growing it drops the graphs)
+int upload_suppress(atlas_model* m, const atlas_sampling* s, int nsup) {
     if (nsup > m->suppress_cap) {
         void* p = nullptr;
         TRY(dalloc(m, &p, (size_t)nsup * 4));
@@ -531,6 +540,60 @@ int set_greedy_cfg(atlas_model* m, const atlas_sampling* s) {
     if (nsup)
         ATLAS_HIP(hipMemcpyAsync(m->suppress_dev, s->suppress_initial_tokens, (size_t)nsup * 4,
                                  hipMemcpyHostToDevice, m->st));
+    return ATLAS_OK;
+}
+
+// ---- device sampling: which configurations the sampler kernel takes ----------
+// temperature > 0 with 1 <= top_k <= SAMPLE_MAX_K (all of the vocabulary when
+// it is smaller), at most SAMPLE_MAX_HIST generated tokens when the frequency
+// or presence penalty is on, and a repetition window of at most SAMPLE_MAX_HIST
+// tokens.  Other configurations sample on the host.
+bool sample_dev_ok(const atlas_sampling* s, int V, int max_hist) {
+    if (!s || s->temperature <= 0.0f || s->temperature < 1e-6f) return false;
+    if (s->top_k < 1 || s->top_k > SAMPLE_MAX_K || (s->top_k >= V && V > SAMPLE_MAX_K)) return false;
+    if ((s->frequency_penalty != 0.0f || s->presence_penalty != 0.0f) && max_hist > SAMPLE_MAX_HIST)
+        return false;
+    if (s->repetition_penalty != 1.0f && std::min(s->repetition_window, max_hist) > SAMPLE_MAX_HIST)
+        return false;
+    return true;
+}
+
+SampleCfg sample_cfg_of(const atlas_sampling* s) {
+    SampleCfg c{};
+    c.temperature = s->temperature;
+    c.theta = s->repetition_penalty;
+    c.freq = s->frequency_penalty;
+    c.presence = s->presence_penalty;
+    c.top_p = s->top_p;
+    c.min_p = s->min_p;
+    c.log_min_p = s->min_p > 0.0f ? logf(s->min_p) : 0.0f;     // the host's logf, as min_p's
+    c.window = s->repetition_window;
+    c.top_k = s->top_k;
+    c.n_suppress = s->n_suppress > 0 && s->suppress_initial_tokens ? s->n_suppress : 0;
+    return c;
+}
+
+// settings, suppression list and RNG state of the sampled step (mode 2): the
+// captured step reads them from device memory
+int set_sample_cfg(atlas_model* m, const atlas_sampling* s) {
+    const SampleCfg c = sample_cfg_of(s);
+    TRY(upload_suppress(m, s, c.n_suppress));
+    ATLAS_HIP(hipMemcpyAsync(m->samp_cfg, &c, sizeof c, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipMemcpyAsync(m->rng_dev, &m->rng.s, 8, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipStreamSynchronize(m->st));     // c and the RNG state live on this frame
+    return ATLAS_OK;
+}
+
+// ---- greedy settings baked into the graph --------------------------------
+int set_greedy_cfg(atlas_model* m, const atlas_sampling* s) {
+    float theta = 1.f;
+    int window = 0, nsup = 0;
+    if (s) {
+        theta = s->repetition_penalty;
+        window = s->repetition_window;
+        nsup = s->n_suppress > 0 && s->suppress_initial_tokens ? s->n_suppress : 0;
+    }
+    TRY(upload_suppress(m, s, nsup));
     if (theta != m->g_theta || window != m->g_window || nsup != m->g_nsup) {
         m->g_theta = theta;
         m->g_window = window;
@@ -1129,8 +1192,11 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         dalloc(m, (void**)&m->hist_len, 4) ||
         dalloc(m, (void**)&m->hist, (size_t)(c.max_seq + 2) * 4) ||
         dalloc(m, (void**)&m->choice_dev, (size_t)B * 4) ||
-        dalloc(m, (void**)&m->argpart, (size_t)ARGMAX_MAX_PARTS * 8))
+        dalloc(m, (void**)&m->argpart, (size_t)ARGMAX_MAX_PARTS * 8) ||
+        dalloc(m, (void**)&m->samp_cfg, sizeof(SampleCfg)) || dalloc(m, (void**)&m->rng_dev, 8) ||
+        dalloc(m, (void**)&m->suppress_dev, 64 * 4))
         return fail(m);
+    m->suppress_cap = 64;     // a captured step holds the pointer: never null
     // RoPE tables
     {
         std::vector<float> cs, sn;
@@ -1417,8 +1483,10 @@ int generate_impl(atlas_model* m, const uint32_t* prompt, int n_prompt, int max_
     std::vector<uint32_t> gen;
     std::vector<float> logits((size_t)V, 0.0f);
     const bool greedy = is_greedy(s);
-    const bool device_choice = greedy && !on_token;
-    if (device_choice) TRY(set_greedy_cfg(m, s));
+    const bool device_sample = !greedy && !on_token && sample_dev_ok(s, V, max_new);
+    const bool device_choice = (greedy && !on_token) || device_sample;
+    const int choose_mode = greedy ? 1 : 2;
+    if (greedy && device_choice) TRY(set_greedy_cfg(m, s));
 
     // prompt: forward all but the last token without choosing
     for (int i = 0; i + 1 < n_prompt; ++i) {
@@ -1435,10 +1503,12 @@ int generate_impl(atlas_model* m, const uint32_t* prompt, int n_prompt, int max_
     }
 
     if (device_choice && n_prompt > 0) {
-        // greedy on the device: each replay forwards the last choice and
-        // chooses the next; check for stop tokens every `chunk` replays.
+        // choice on the device (greedy, or sampled from the device RNG state):
+        // each replay forwards the last choice and chooses the next; check for
+        // stop tokens every `chunk` replays.
+        if (device_sample) TRY(set_sample_cfg(m, s));
         TRY(set_token(m, prompt[n_prompt - 1]));
-        TRY(run_step(m, 1));                        // chooses t_1
+        TRY(run_step(m, choose_mode));              // chooses t_1
         int issued = 1;                              // tokens chosen so far
         int forwarded = 0;                           // generated tokens forwarded
         std::vector<uint32_t> h;
@@ -1464,7 +1534,7 @@ int generate_impl(atlas_model* m, const uint32_t* prompt, int n_prompt, int max_
             // each replay forwards the latest choice and chooses the next; the
             // forward of t_k is the reference's final forward (lib.rs:1725-1729)
             const int want = determined ? k - forwarded : std::min(chunk, max_new - forwarded);
-            for (int r = 0; r < want; ++r) TRY(run_step(m, 1));
+            for (int r = 0; r < want; ++r) TRY(run_step(m, choose_mode));
             issued += want;
             forwarded += want;
         }
@@ -1664,6 +1734,60 @@ ATLAS_API int atlas_sample_host(const float* logits, int vocab, const uint32_t* 
     *token = choose_token(logits, vocab, step, hist, (size_t)n_hist, s, rng);
     *rng_state = rng.s;
     return ATLAS_OK;
+}
+
+ATLAS_API int atlas_sample_device(const float* logits, int vocab, const uint32_t* hist,
+                                  int n_hist, int step, const atlas_sampling* s,
+                                  uint64_t* rng_state, uint32_t* token) {
+    ATLAS_REQUIRE(logits && vocab > 0 && n_hist >= 0 && (n_hist == 0 || hist) && s && rng_state &&
+                  token && step >= 0 && (s->n_suppress <= 0 || s->suppress_initial_tokens),
+                  "sample_device: bad arguments");
+    if (!sample_dev_ok(s, vocab, n_hist)) {
+        set_error(ATLAS_EUNSUPPORTED, "sample_device: temperature %g, top_k %d, %d history tokens: "
+                  "the device sampler needs temperature > 0 and 1 <= top_k <= %d", s->temperature,
+                  s->top_k, n_hist, (int)SAMPLE_MAX_K);
+        return ATLAS_EUNSUPPORTED;
+    }
+    const SampleCfg c = sample_cfg_of(s);
+    hipStream_t st = stream();
+    // one device block: logits copy | history | suppression | settings | counters
+    const size_t nh = (size_t)n_hist + 1, ns = (size_t)std::max(c.n_suppress, 1);
+    const size_t off_h = (size_t)vocab * 4, off_s = off_h + nh * 4, off_c = off_s + ns * 4;
+    const size_t off_i = (off_c + sizeof(SampleCfg) + 7) & ~(size_t)7;
+    const size_t bytes = off_i + 32;
+    char* d = nullptr;
+    ATLAS_HIP(hipMalloc((void**)&d, bytes));
+    int rc = ATLAS_OK;
+    const int ints[4] = {n_hist, step, 0, 0};
+    if (hipMemcpyAsync(d, logits, (size_t)vocab * 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+        (n_hist && hipMemcpyAsync(d + off_h, hist, (size_t)n_hist * 4, hipMemcpyHostToDevice, st) != hipSuccess) ||
+        (c.n_suppress && hipMemcpyAsync(d + off_s, s->suppress_initial_tokens, (size_t)c.n_suppress * 4,
+                                        hipMemcpyHostToDevice, st) != hipSuccess) ||
+        hipMemcpyAsync(d + off_c, &c, sizeof c, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(d + off_i, rng_state, 8, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(d + off_i + 8, ints, 16, hipMemcpyHostToDevice, st) != hipSuccess) {
+        set_error(ATLAS_EHIP, "sample_device: upload failed");
+        rc = ATLAS_EHIP;
+    }
+    if (!rc) {
+        SampleArgs a{};
+        a.x = (float*)d; a.n = vocab; a.cfg = (const SampleCfg*)(d + off_c);
+        a.suppress = (const uint32_t*)(d + off_s);
+        a.hist = (uint32_t*)(d + off_h); a.hist_len = (int*)(d + off_i + 8);
+        a.step = (int*)(d + off_i + 12); a.pos_inc = nullptr;
+        a.rng = (unsigned long long*)(d + off_i); a.out_u32 = (uint32_t*)(d + off_i + 16);
+        a.record = 0;
+        rc = sample_launch(a, st);
+    }
+    if (!rc && (hipMemcpyAsync(rng_state, d + off_i, 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
+                hipMemcpyAsync(token, d + off_i + 16, 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+                hipStreamSynchronize(st) != hipSuccess)) {
+        set_error(ATLAS_EHIP, "sample_device: download failed");
+        rc = ATLAS_EHIP;
+    }
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(d);
+    return rc;
 }
 
 ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts,

@@ -415,6 +415,496 @@ int argmax_launch(const ArgmaxArgs& a, hipStream_t st) {
     return ATLAS_OK;
 }
 
+// ---- device sampling: one token of generate_with_sampling (lib.rs:1623-1711) ------
+// One block of 1024 threads.  After the penalties, every stage works on the
+// top-k survivors compacted in index order: the reference's sums over the whole
+// vocabulary add exact zeros for the other entries (expf(-inf) = 0), so the
+// sequential loops here over the survivors give the same sums bit for bit.
+// The one difference is expf: the reference calls glibc's, which is not
+// correctly rounded for ~1e-4 of arguments; this computes exp in double and
+// rounds once (correctly rounded up to double's own error).
+
+// larger float -> larger key
+__device__ __forceinline__ uint32_t sample_key(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float sample_exp(float x) { return (float)exp((double)x); }
+
+__device__ float block_max1024(float v, float* sh) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int i = 1; i < 16; ++i) r = fmaxf(r, sh[i]);
+    __syncthreads();
+    return r;
+}
+
+// exclusive prefix sum of v over the 1024 threads; *total receives the sum
+__device__ int block_excl_scan1024(int v, int* sh, int* total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int incl = v;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
+    }
+    if (lane == 63) sh[w] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int i = 0; i < 16; ++i) {
+            const int t = sh[i];
+            sh[i] = acc;
+            acc += t;
+        }
+        sh[16] = acc;
+    }
+    __syncthreads();
+    const int r = sh[w] + incl - v;
+    *total = sh[16];
+    __syncthreads();
+    return r;
+}
+
+// Wave 0: the bin of `bins` (counts, nb of them, top bin first in rank order)
+// holding rank kk from the top, and the rank left inside that bin.
+__device__ void radix_pick(const int* bins, int nb, int kk, int* out_bin, int* out_kk) {
+    const int lane = threadIdx.x & 63;
+    const int per = nb / 64;
+    int sum = 0;
+    for (int j = 0; j < per; ++j) sum += bins[nb - 1 - (lane * per + j)];
+    int incl = sum;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
+    }
+    const unsigned long long ball = __ballot(incl >= kk);
+    const int first = ball ? __ffsll((long long)ball) - 1 : 63;
+    if (lane == first) {
+        int acc = incl - sum;
+        int b = nb - 1 - lane * per - (per - 1), k2 = kk - acc;
+        for (int j = 0; j < per; ++j) {
+            const int bb = nb - 1 - (lane * per + j);
+            if (acc + bins[bb] >= kk) {
+                b = bb;
+                k2 = kk - acc;
+                break;
+            }
+            acc += bins[bb];
+        }
+        *out_bin = b;
+        *out_kk = k2;
+    }
+}
+
+__device__ __forceinline__ float sample_unkey(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+// The kk-th largest (1-based) of keys[0..cnt) in LDS, and how many entries
+// equal to it rank within the first kk: radix select, 11 + 11 + 10 bits.
+__device__ void lds_select(const uint32_t* keys, int cnt, int kk, int* bins, int* pick,
+                           uint32_t* th, int* need) {
+    uint32_t prefix = 0, mask = 0;
+    for (int pass = 0; pass < 3; ++pass) {
+        const int shift = pass == 0 ? 21 : pass == 1 ? 10 : 0;
+        const int nb = pass == 2 ? 1024 : 2048;
+        for (int i = threadIdx.x; i < nb; i += 1024) bins[i] = 0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < cnt; i += 1024) {
+            const uint32_t key = keys[i];
+            if ((key & mask) == prefix) atomicAdd(&bins[(key >> shift) & (uint32_t)(nb - 1)], 1);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) radix_pick(bins, nb, kk, &pick[0], &pick[1]);
+        __syncthreads();
+        prefix |= (uint32_t)pick[0] << shift;
+        mask |= (uint32_t)(nb - 1) << shift;
+        kk = pick[1];
+        __syncthreads();
+    }
+    *th = prefix;
+    *need = kk;
+}
+
+// ascending bitonic sort of s[0..np2) (np2 a power of two), all 1024 threads
+__device__ void bitonic_u32(uint32_t* s, int np2) {
+    for (int k2 = 2; k2 <= np2; k2 <<= 1)
+        for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
+            for (int i = threadIdx.x; i < np2; i += 1024) {
+                const int p = i ^ j2;
+                if (p > i) {
+                    const bool up = (i & k2) == 0;
+                    const uint32_t u = s[i], v = s[p];
+                    if ((u > v) == up) { s[i] = v; s[p] = u; }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// hist[lo, hi) into s sorted ascending (padding 0xFFFFFFFF up to a power of two)
+__device__ int sorted_tokens(const uint32_t* hist, int lo, int hi, uint32_t* s) {
+    const int len = hi - lo;
+    int np2 = 1;
+    while (np2 < len) np2 <<= 1;
+    for (int i = threadIdx.x; i < np2; i += 1024) s[i] = i < len ? hist[lo + i] : 0xFFFFFFFFu;
+    __syncthreads();
+    bitonic_u32(s, np2);
+    return len;
+}
+
+__global__ __launch_bounds__(1024) void sample_kernel(SampleArgs a) {
+#pragma clang fp contract(off)
+    __shared__ uint32_t s_hist[SAMPLE_MAX_HIST];
+    __shared__ int s_bins[2048];
+    __shared__ int s_idx[SAMPLE_MAX_K];
+    __shared__ float s_val[SAMPLE_MAX_K];
+    __shared__ float s_p[SAMPLE_MAX_K];
+    __shared__ int s_ord[SAMPLE_MAX_K];
+    __shared__ int s_scan[17];
+    __shared__ uint32_t s_ck[SAMPLE_CAND];      // top-k candidates: keys, index order
+    __shared__ int s_ci[SAMPLE_CAND];           // and their indices
+    __shared__ int s_wbase[17];
+    __shared__ float s_red[16];
+    __shared__ int s_pick[2];
+    __shared__ float s_sum;
+    const SampleCfg c = *a.cfg;
+    const int tid = threadIdx.x, n = a.n;
+    float* x = a.x;
+    const int step = a.step ? *a.step : 0;
+    const int len = (a.hist && a.hist_len) ? *a.hist_len : 0;
+
+    // ---- step-0 suppression, then the repetition penalty in history order
+    if (step == 0 && a.suppress)
+        for (int i = tid; i < c.n_suppress; i += 1024)
+            if (a.suppress[i] < (uint32_t)n) x[a.suppress[i]] = -INFINITY;
+    __syncthreads();
+    // A token seen r times in the window is penalised r times in a row (the
+    // reference's loop in history order); distinct tokens are independent, so
+    // one thread per distinct token of the sorted window gives the same values.
+    // The host admits windows of at most SAMPLE_MAX_HIST tokens on this path.
+    if (c.theta != 1.0f && len > 0) {
+        int start = len > c.window ? len - c.window : 0;
+        if (len - start > SAMPLE_MAX_HIST) start = len - SAMPLE_MAX_HIST;
+        const int wl = sorted_tokens(a.hist, start, len, s_hist);
+        for (int i = tid; i < wl; i += 1024) {
+            const uint32_t t = s_hist[i];
+            if (i > 0 && s_hist[i - 1] == t) continue;
+            int j = i + 1;
+            while (j < wl && s_hist[j] == t) ++j;
+            if (t < (uint32_t)n) {
+                float v = x[t];
+                for (int r = i; r < j; ++r) v = v > 0.0f ? v / c.theta : v * c.theta;
+                x[t] = v;
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- frequency (times seen) and presence penalties per distinct token; the
+    // host admits at most SAMPLE_MAX_HIST history entries on this path
+    const int hl = len < SAMPLE_MAX_HIST ? len : SAMPLE_MAX_HIST;
+    if ((c.freq != 0.0f || c.presence != 0.0f) && hl > 0) {
+        sorted_tokens(a.hist, 0, hl, s_hist);
+        for (int i = tid; i < hl; i += 1024) {
+            const uint32_t t = s_hist[i];
+            if (i > 0 && s_hist[i - 1] == t) continue;
+            int j = i + 1;
+            while (j < hl && s_hist[j] == t) ++j;
+            if (t < (uint32_t)n) {
+                float v = x[t];
+                if (c.freq != 0.0f) v -= c.freq * (float)(j - i);
+                if (c.presence != 0.0f) v -= c.presence;
+                x[t] = v;
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- top-k (x / T): threshold key th = the k-th largest, ties at th kept
+    // first by index; survivors compacted in index order into s_idx / s_val
+    const float T = c.temperature;
+    int k = c.top_k < 1 ? 1 : c.top_k;
+    if (k > SAMPLE_MAX_K) k = SAMPLE_MAX_K;
+    if (k > n) k = n;
+    const int lane = tid & 63, wv = tid >> 6;
+    // (a) The k-th largest of the 1024 per-thread maxima is a lower bound L of
+    // th: those k maxima are k distinct entries >= it.
+    uint32_t kmax = 0;
+    for (int base = tid; base < n; base += 1024 * 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int i = base + u * 1024;
+            v[u] = x[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const uint32_t key = sample_key(v[u] / T);
+            if (base + u * 1024 < n && key > kmax) kmax = key;
+        }
+    }
+    s_hist[tid] = kmax;                          // the penalties are done with s_hist
+    __syncthreads();
+    uint32_t L, th;
+    int need, m;
+    lds_select(s_hist, 1024, k, s_bins, s_pick, &L, &need);
+    // (b) entries with key >= L, counted then written in index order: wave wv
+    // owns a contiguous range and takes 4 x 64 consecutive entries per step
+    const int chunk = ((n + 15) / 16 + 255) & ~255;
+    const int c_lo = wv * chunk < n ? wv * chunk : n;
+    const int c_hi = c_lo + chunk < n ? c_lo + chunk : n;
+    int wcount = 0;
+    for (int b = c_lo; b < c_hi; b += 256) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = b + u * 64 + lane;
+            v[u] = x[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = b + u * 64 + lane;
+            wcount += __popcll(__ballot(i < c_hi && sample_key(v[u] / T) >= L));
+        }
+    }
+    if (lane == 0) s_wbase[wv] = wcount;
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int w = 0; w < 16; ++w) {
+            const int t = s_wbase[w];
+            s_wbase[w] = acc;
+            acc += t;
+        }
+        s_wbase[16] = acc;
+    }
+    __syncthreads();
+    const int n_cand = s_wbase[16];
+    if (n_cand <= SAMPLE_CAND) {
+        int pos = s_wbase[wv];
+        for (int b = c_lo; b < c_hi; b += 256) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = b + u * 64 + lane;
+                v[u] = x[i < n ? i : n - 1];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = b + u * 64 + lane;
+                const uint32_t key = sample_key(v[u] / T);
+                const bool in = i < c_hi && key >= L;
+                const unsigned long long bal = __ballot(in);
+                if (in) {
+                    const int at = pos + __popcll(bal & ((1ull << lane) - 1));
+                    s_ck[at] = key;
+                    s_ci[at] = i;
+                }
+                pos += __popcll(bal);
+            }
+        }
+        __syncthreads();
+        lds_select(s_ck, n_cand, k, s_bins, s_pick, &th, &need);
+        // (c) survivors among the candidates (index order), one segment each
+        const int seg = (n_cand + 1023) / 1024;
+        const int lo = tid * seg < n_cand ? tid * seg : n_cand;
+        const int hi = lo + seg < n_cand ? lo + seg : n_cand;
+        int gt = 0, eq = 0;
+        for (int i = lo; i < hi; ++i) {
+            gt += s_ck[i] > th;
+            eq += s_ck[i] == th;
+        }
+        int tot;
+        const int eq_base = block_excl_scan1024(eq, s_scan, &tot);
+        int keep_eq = need - eq_base;
+        keep_eq = keep_eq < 0 ? 0 : (keep_eq > eq ? eq : keep_eq);
+        int o = block_excl_scan1024(gt + keep_eq, s_scan, &m);
+        int tie = eq_base;
+        for (int i = lo; i < hi; ++i) {
+            const uint32_t key = s_ck[i];
+            bool keep = key > th;
+            if (key == th) keep = tie++ < need;
+            if (keep && o < SAMPLE_MAX_K) {
+                s_idx[o] = s_ci[i];
+                s_val[o] = sample_unkey(key);
+                ++o;
+            }
+        }
+    } else {
+        // more candidates than LDS holds (long runs of equal logits): radix
+        // select and survivors over the whole vocabulary
+        uint32_t prefix = 0, mask = 0;
+        int kk = k;
+        for (int pass = 0; pass < 3; ++pass) {
+            const int shift = pass == 0 ? 21 : pass == 1 ? 10 : 0;
+            const int nb = pass == 2 ? 1024 : 2048;
+            for (int i = tid; i < nb; i += 1024) s_bins[i] = 0;
+            __syncthreads();
+            // 16 independent loads per thread in flight, then their keys
+            for (int base = tid; base < n; base += 1024 * 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const int i = base + u * 1024;
+                    v[u] = x[i < n ? i : n - 1];
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const uint32_t key = sample_key(v[u] / T);
+                    if (base + u * 1024 < n && (key & mask) == prefix)
+                        atomicAdd(&s_bins[(key >> shift) & (uint32_t)(nb - 1)], 1);
+                }
+            }
+            __syncthreads();
+            if (tid < 64) radix_pick(s_bins, nb, kk, &s_pick[0], &s_pick[1]);
+            __syncthreads();
+            prefix |= (uint32_t)s_pick[0] << shift;
+            mask |= (uint32_t)(nb - 1) << shift;
+            kk = s_pick[1];
+            __syncthreads();
+        }
+        th = prefix;
+        need = kk;                                   // ties at th kept, first by index
+
+        // ---- survivors in index order (each thread one contiguous segment)
+        const int seg = (n + 1023) / 1024;
+        const int lo = tid * seg < n ? tid * seg : n;
+        const int hi = lo + seg < n ? lo + seg : n;
+        int gt = 0, eq = 0;
+        for (int b = lo; b < hi; b += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = x[b + u < hi ? b + u : hi - 1];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const uint32_t key = sample_key(v[u] / T);
+                if (b + u < hi) {
+                    gt += key > th;
+                    eq += key == th;
+                }
+            }
+        }
+        int tot;
+        const int eq_base = block_excl_scan1024(eq, s_scan, &tot);
+        int keep_eq = need - eq_base;
+        keep_eq = keep_eq < 0 ? 0 : (keep_eq > eq ? eq : keep_eq);
+        int o = block_excl_scan1024(gt + keep_eq, s_scan, &m);
+        int tie = eq_base;
+        for (int b = lo; b < hi; b += 16) {
+            float w[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) w[u] = x[b + u < hi ? b + u : hi - 1];
+            for (int u = 0; u < 16 && b + u < hi; ++u) {
+                const float v = w[u] / T;
+                const uint32_t key = sample_key(v);
+                bool keep = key > th;
+                if (key == th) keep = tie++ < need;
+                if (keep && o < SAMPLE_MAX_K) {
+                    s_idx[o] = b + u;
+                    s_val[o] = v;
+                    ++o;
+                }
+            }
+        }
+    }
+    if (m > SAMPLE_MAX_K) m = SAMPLE_MAX_K;
+    __syncthreads();
+
+    // ---- top-p: probabilities of the survivors, ordered by (p desc, index),
+    // cut where the running sum first reaches top_p
+    if (c.top_p < 1.0f) {
+        const float mx = block_max1024(tid < m ? s_val[tid] : -INFINITY, s_red);
+        if (tid < m) s_p[tid] = sample_exp(s_val[tid] - mx);
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
+            for (int i = 0; i < m; ++i) sum += s_p[i];
+            s_sum = sum;
+        }
+        __syncthreads();
+        const float sum = s_sum;
+        if (sum > 0.0f) {
+            if (tid < m) s_p[tid] = s_p[tid] / sum;
+            int np2 = 1;
+            while (np2 < m) np2 <<= 1;
+            s_ord[tid] = tid;                       // np2 <= 1024 positions
+            __syncthreads();
+            for (int k2 = 2; k2 <= np2; k2 <<= 1)
+                for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
+                    const int i = tid, p = i ^ j2;
+                    if (i < np2 && p > i) {
+                        const int u = s_ord[i], v = s_ord[p];
+                        // u before v: larger p first, then lower index; padding last
+                        const float pu = u < m ? s_p[u] : -1.0f, pv = v < m ? s_p[v] : -1.0f;
+                        const int iu = u < m ? s_idx[u] : 0x7FFFFFFF, iv = v < m ? s_idx[v] : 0x7FFFFFFF;
+                        const bool u_first = pu > pv || (pu == pv && iu < iv);
+                        const bool up = (i & k2) == 0;
+                        if (u_first != up) { s_ord[i] = v; s_ord[p] = u; }
+                    }
+                    __syncthreads();
+                }
+            if (tid == 0) {
+                float cum = 0.0f;
+                int cut = m;
+                for (int r = 0; r < m; ++r) {
+                    cum += s_p[s_ord[r]];
+                    if (cum >= c.top_p) { cut = r + 1; break; }
+                }
+                s_pick[0] = cut;
+            }
+            __syncthreads();
+            if (tid < m && tid >= s_pick[0]) s_val[s_ord[tid]] = -INFINITY;
+            __syncthreads();
+        }
+    }
+
+    // ---- min-p: drop logits below max + ln(min_p)
+    if (c.min_p > 0.0f) {
+        const float mx = block_max1024(tid < m ? s_val[tid] : -INFINITY, s_red);
+        const float th2 = mx + c.log_min_p;
+        if (tid < m && s_val[tid] < th2) s_val[tid] = -INFINITY;
+        __syncthreads();
+    }
+
+    // ---- softmax and the inverse CDF in index order (sample_from_probs)
+    const float mx = block_max1024(tid < m ? s_val[tid] : -INFINITY, s_red);
+    if (tid < m) s_p[tid] = sample_exp(s_val[tid] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < m; ++i) sum += s_p[i];
+        const float inv = 1.0f / sum;
+        unsigned long long r = *a.rng;
+        r ^= r << 13;
+        r ^= r >> 7;
+        r ^= r << 17;
+        const float u = (float)(uint32_t)(r >> 33) / 2147483648.0f;
+        float cum = 0.0f;
+        uint32_t tok = (uint32_t)(n - 1);
+        for (int i = 0; i < m; ++i) {
+            const float p = s_p[i] * inv;
+            cum += p;
+            if (u < cum) { tok = (uint32_t)s_idx[i]; break; }
+        }
+        *a.rng = r;
+        if (a.out_u32) *a.out_u32 = tok;
+        if (a.record && a.hist && a.hist_len) { a.hist[len] = tok; *a.hist_len = len + 1; }
+        if (a.step) *a.step = step + 1;
+        if (a.pos_inc) *a.pos_inc += 1;
+    }
+}
+
+int sample_launch(const SampleArgs& a, hipStream_t st) {
+    ATLAS_REQUIRE(a.x && a.n > 0 && a.cfg && a.rng && a.out_u32, "sample: bad arguments");
+    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(1024), 0, st, a);
+    ATLAS_LAUNCH_CHECK("sample");
+    return ATLAS_OK;
+}
+
 // ---- embedding gather -----------------------------------------------------------
 __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__ table, int vocab,
                                                     int d, const uint32_t* tok_dev, uint32_t tok,

@@ -44,6 +44,33 @@ struct ArgmaxArgs {
     int* pos_inc;                  // device position bumped after the choice, or null
 };
 
+// Device-resident sampling settings (SamplingConfig, lib.rs:1223-1295).
+struct SampleCfg {
+    float temperature;             // > 0
+    float theta;                   // repetition penalty (1 = off)
+    float freq, presence;          // frequency / presence penalties (0 = off)
+    float top_p;                   // 1 = off
+    float min_p, log_min_p;        // min_p > 0: threshold max + logf(min_p) (host logf)
+    int window;                    // repetition window
+    int top_k;                     // 1 .. SAMPLE_MAX_K
+    int n_suppress;                // step-0 suppression list length
+};
+enum { SAMPLE_MAX_K = 1024, SAMPLE_MAX_HIST = 4096, SAMPLE_CAND = 4096 };
+
+struct SampleArgs {
+    float* x;                      // logits [n] (modified in place by the penalties)
+    int n;
+    const SampleCfg* cfg;          // device
+    const uint32_t* suppress;      // device [cfg->n_suppress] or null
+    uint32_t* hist;                // generated-token history (device)
+    int* hist_len;                 // its length (device)
+    int* step;                     // device step counter (step 0 = first token)
+    int* pos_inc;                  // device position bumped after the choice, or null
+    unsigned long long* rng;       // device XorShift64 state
+    uint32_t* out_u32;             // the chosen token
+    int record;                    // append the choice to hist and bump hist_len
+};
+
 int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, long ld, float eps,
                    hipStream_t st);
 int residual_rmsnorm_launch(float* x, const float* y, const float* w, int n, int rows, long ld,
@@ -60,6 +87,8 @@ int softmax_rows_launch(const float* x, float* out, int rows, int cols, hipStrea
 int adamw_launch(float* p, float* m, float* v, const float* g, float lr, float b1, float b2,
                  float eps, float wd, float bc1, float bc2, int n, hipStream_t st);
 int argmax_launch(const ArgmaxArgs& a, hipStream_t st);
+// one token of generate_with_sampling (temperature > 0, 1 <= top_k <= 1024)
+int sample_launch(const SampleArgs& a, hipStream_t st);
 int embed_launch(const uint16_t* table, int vocab, int d, const uint32_t* tok_dev, uint32_t tok,
                  float* out, long ld, int n_seq, hipStream_t st);
 int add_int_launch(int* p, int n, int v, hipStream_t st);

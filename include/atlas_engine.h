@@ -158,6 +158,16 @@ int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts, const in
  * read.  Needs no device.                                                   */
 int atlas_sample_host(const float* logits, int vocab, const uint32_t* hist, int n_hist, int step,
                       const atlas_sampling* s, uint64_t* rng_state, uint32_t* token);
+/* The same token choice on the device, from device-resident logits (copied,
+ * not modified): the sampler kernel the engine's generate loop replays for
+ * temperature > 0 with 1 <= top_k <= 1024 (SamplingConfig::olmo3() among
+ * them).  Every sum runs in the reference's order, so the choice equals the
+ * host's except where glibc's expf and a correctly rounded exp differ (about
+ * 1e-4 of arguments, 1 ulp) and that ulp moves a cumulative-probability
+ * boundary across the random draw.  ATLAS_EUNSUPPORTED for other settings.
+ * No reference counterpart (the reference samples on the host).             */
+int atlas_sample_device(const float* logits, int vocab, const uint32_t* hist, int n_hist,
+                        int step, const atlas_sampling* s, uint64_t* rng_state, uint32_t* token);
 
 /* Extension: position from which decode steps run the long-context attention
  * (QK-norm/RoPE/KV-write kernel, split kernel over up to 256 blocks, split
