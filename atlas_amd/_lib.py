@@ -126,6 +126,8 @@ SIGNATURES = {
     "atlas_model_generate_batch": (I, [P, P, P, I, I, C.POINTER(SamplingC), P, P]),
     "atlas_model_decode_greedy": (I, [P, U32, I, P]),
     "atlas_model_set_long_context": (I, [P, I]),
+    "atlas_model_prefill": (I, [P, P, I]),
+    "atlas_model_set_prefill_chunk": (I, [P, I]),
     "atlas_model_get_config": (I, [P, C.POINTER(ModelConfigC)]),
     "atlas_model_set_tensor_dev": (I, [P, I, I, P, I, I64, P]),
     "atlas_load_scratch_create": (P, []),

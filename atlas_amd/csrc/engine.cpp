@@ -42,6 +42,9 @@ namespace {
 // on the 7B bf16 decode: 2.86 vs 2.99 ms/token at ctx 400, 3.12 vs 3.04 at
 // 656, 3.66 vs 3.34 at 2192 and 4.23 vs 3.65 at 4240 (fused vs long).
 constexpr int kLongAttnFrom = 512;
+// Prompt tokens per prefill step: the multi-row step's rows (the multi-row
+// GEMV for 2-3 rows, MFMA tiles up to 8).
+constexpr int kPrefillChunk = 8;
 
 struct DevMat {
     int fmt = WF_BF16;
@@ -92,6 +95,8 @@ struct atlas_model {
     atlas_model_config cfg{};
     std::vector<uint8_t> sliding;
     int hd = 0, kvd = 0, qkv_rows = 0, B = 1;
+    int R = 1;                       // rows of the multi-row step buffers: max(B, prefill chunk)
+    int prefill_chunk = kPrefillChunk;   // prompt tokens per prefill step (1: token by token)
     float scale = 1.f;
     std::vector<LayerW> L;
     uint16_t* embed = nullptr;
@@ -126,6 +131,8 @@ struct atlas_model {
     hipGraphExec_t gexec_long[3] = {nullptr, nullptr, nullptr};
     hipGraphExec_t bgexec[9] = {};   // ragged batch step per batch size 1..8
     hipGraphExec_t bgexec_long[9] = {};   // ... its long-context variant
+    hipGraphExec_t pgexec[9] = {};        // prefill step (no lm_head) per row count
+    hipGraphExec_t pgexec_long[9] = {};
     // pinned staging ring for the batch step's tokens / positions / slots:
     // entry k is rewritten only after its event (the copies) completed
     static constexpr int kRing = 8;
@@ -397,8 +404,8 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
             a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
             a.scale = m->scale; a.window = L.window;
             a.part_m = m->attn_part;
-            a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
-            a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
+            a.part_l = m->attn_part + (size_t)m->R * c.n_heads * m->attn_splits;
+            a.part_o = m->attn_part + (size_t)2 * m->R * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
             a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
             TRY(attn_fused_launch(a, m->attn_splits, 1, m->st));
@@ -470,6 +477,12 @@ void drop_graphs(atlas_model* m) {
             (void)hipGraphExecDestroy(g);
             g = nullptr;
         }
+    for (auto* arr : {m->pgexec, m->pgexec_long})
+        for (int k = 0; k < 9; ++k)
+            if (arr[k]) {
+                (void)hipGraphExecDestroy(arr[k]);
+                arr[k] = nullptr;
+            }
 }
 
 int run_step(atlas_model* m, int mode) {
@@ -973,7 +986,9 @@ int bmm(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int ep
     return skinny(m, w, x, y, n, epi);
 }
 
-int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx) {
+// with_head = false: a prefill chunk, no final norm / lm_head / choice
+int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx,
+               bool with_head = true) {
     const atlas_model_config& c = m->cfg;
     const int d = c.d_model;
     TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, n, m->st));
@@ -1022,8 +1037,8 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
             a.scale = m->scale; a.window = L.window;
             a.part_m = m->attn_part;
-            a.part_l = m->attn_part + (size_t)m->B * c.n_heads * m->attn_splits;
-            a.part_o = m->attn_part + (size_t)2 * m->B * c.n_heads * m->attn_splits;
+            a.part_l = m->attn_part + (size_t)m->R * c.n_heads * m->attn_splits;
+            a.part_o = m->attn_part + (size_t)2 * m->R * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
             a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
             TRY(attn_fused_launch(a, m->attn_splits, n, m->st));
@@ -1056,6 +1071,7 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, (long)n * d, m->st));
         }
     }
+    if (!with_head) return ATLAS_OK;
     TRY(rmsnorm_launch(m->x, m->final_norm, m->xn, d, n, d, c.rms_eps, m->st));
     TRY(bmm(m, m->lm_head, m->xn, m->logits, n, EPI_STORE));
     // greedy choice of every row into choice_dev (last maximum wins)
@@ -1071,14 +1087,16 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
 // batch_step replayed from a graph captured per batch size and attention
 // variant (fused models: tokens, positions and slots are read from device
 // memory); long_ctx picks the long-context variant
-int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx) {
+int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx,
+                   bool with_head = true) {
     long_ctx = long_ctx && m->fused;
-    if (!m->use_graph || !m->fused) return batch_step(m, n, slots, long_ctx);
-    hipGraphExec_t& ge = long_ctx ? m->bgexec_long[n] : m->bgexec[n];
+    if (!m->use_graph || !m->fused) return batch_step(m, n, slots, long_ctx, with_head);
+    hipGraphExec_t& ge = with_head ? (long_ctx ? m->bgexec_long[n] : m->bgexec[n])
+                                   : (long_ctx ? m->pgexec_long[n] : m->pgexec[n]);
     if (!ge) {
         hipGraph_t g = nullptr;
         ATLAS_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
-        int rc = batch_step(m, n, slots, long_ctx);
+        int rc = batch_step(m, n, slots, long_ctx, with_head);
         hipError_t e = hipStreamEndCapture(m->st, &g);
         if (rc) {
             if (g) (void)hipGraphDestroy(g);
@@ -1098,6 +1116,45 @@ int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool lo
     }
     ATLAS_HIP(hipGraphLaunch(ge, m->st));
     return ATLAS_OK;
+}
+
+// Prompt tokens through the multi-row step, up to prefill_chunk at a time, at
+// the single sequence's positions m->pos.. in KV slot 0 (fused models; others
+// and lone tokens take the decode step).  Always the step's two-kernel
+// attention variant: its QK-norm / RoPE / KV-write kernel stores every row's K
+// and V before the split kernel's row j reads cache rows up to m->pos + j.
+// (The fused attention kernel writes a row's K/V in the same launch that
+// other rows read; the rows of a ragged batch live in different slots, the
+// rows of a prefill chunk in one.)
+int prefill(atlas_model* m, const uint32_t* toks, int n) {
+    const int chunk = m->fused ? std::min(m->prefill_chunk, std::min(m->R, kPrefillChunk)) : 1;
+    int done = 0;
+    while (done < n) {
+        const int k = std::min(chunk, n - done);
+        ATLAS_REQUIRE(m->pos + k <= m->cfg.max_seq, "prefill: position %d + %d exceeds max_seq %d",
+                      m->pos, k, m->cfg.max_seq);
+        if (k == 1) {
+            TRY(sync_pos(m));
+            TRY(set_token(m, toks[done]));
+            TRY(run_step(m, 0));
+            ++done;
+            continue;
+        }
+        int host[3][kPrefillChunk];
+        for (int j = 0; j < k; ++j) {
+            host[0][j] = (int)toks[done + j];
+            host[1][j] = m->pos + j;
+            host[2][j] = 0;
+        }
+        ATLAS_HIP(hipMemcpyAsync(m->tok_dev, host[0], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
+        ATLAS_HIP(hipMemcpyAsync(m->pos_dev, host[1], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
+        ATLAS_HIP(hipMemcpyAsync(m->slot_dev, host[2], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
+        TRY(run_batch_step(m, k, std::vector<int>(k, 0), true, false));
+        ATLAS_HIP(hipStreamSynchronize(m->st));      // host[] lives on this frame
+        m->pos += k;
+        done += k;
+    }
+    return sync_pos(m);                               // pos_dev[0] for the decode step
 }
 
 }  // namespace
@@ -1142,6 +1199,7 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->kvd = c.n_kv_heads * hd;
     m->qkv_rows = c.d_model + 2 * m->kvd;
     m->B = c.max_batch < 1 ? 1 : c.max_batch;
+    m->R = std::max(m->B, kPrefillChunk);
     // scale = attn_factor / sqrt(head_dim) (lib.rs:632, 1331-1335)
     m->scale = 1.0f / sqrtf((float)hd);
     const float af = c.yarn ? c.yarn_attn_factor : 1.0f;
@@ -1179,19 +1237,20 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         dalloc(m, (void**)&m->final_norm, (size_t)d * 4))
         return fail(m);
     // scratch
-    const int big = std::max(c.ffn_hidden, d);
-    if (dalloc(m, (void**)&m->x, (size_t)B * d * 4) || dalloc(m, (void**)&m->xn, (size_t)B * d * 4) ||
-        dalloc(m, (void**)&m->y, (size_t)B * d * 4) ||
-        dalloc(m, (void**)&m->qkv, (size_t)B * m->qkv_rows * 4) ||
-        dalloc(m, (void**)&m->att, (size_t)B * d * 4) ||
-        dalloc(m, (void**)&m->h, (size_t)B * 2 * big * 4) ||
-        dalloc(m, (void**)&m->xb, (size_t)B * d * 4) || dalloc(m, (void**)&m->y2, (size_t)B * d * 4) ||
-        dalloc(m, (void**)&m->logits, (size_t)B * c.vocab * 4) ||
-        dalloc(m, (void**)&m->pos_dev, (size_t)B * 4) || dalloc(m, (void**)&m->slot_dev, (size_t)B * 4) ||
-        dalloc(m, (void**)&m->tok_dev, (size_t)B * 4) || dalloc(m, (void**)&m->step_dev, 4) ||
+    // activations of up to R rows (a ragged batch or a prefill chunk)
+    const int big = std::max(c.ffn_hidden, d), R = m->R;
+    if (dalloc(m, (void**)&m->x, (size_t)R * d * 4) || dalloc(m, (void**)&m->xn, (size_t)R * d * 4) ||
+        dalloc(m, (void**)&m->y, (size_t)R * d * 4) ||
+        dalloc(m, (void**)&m->qkv, (size_t)R * m->qkv_rows * 4) ||
+        dalloc(m, (void**)&m->att, (size_t)R * d * 4) ||
+        dalloc(m, (void**)&m->h, (size_t)R * 2 * big * 4) ||
+        dalloc(m, (void**)&m->xb, (size_t)R * d * 4) || dalloc(m, (void**)&m->y2, (size_t)R * d * 4) ||
+        dalloc(m, (void**)&m->logits, (size_t)R * c.vocab * 4) ||
+        dalloc(m, (void**)&m->pos_dev, (size_t)R * 4) || dalloc(m, (void**)&m->slot_dev, (size_t)R * 4) ||
+        dalloc(m, (void**)&m->tok_dev, (size_t)R * 4) || dalloc(m, (void**)&m->step_dev, 4) ||
         dalloc(m, (void**)&m->hist_len, 4) ||
         dalloc(m, (void**)&m->hist, (size_t)(c.max_seq + 2) * 4) ||
-        dalloc(m, (void**)&m->choice_dev, (size_t)B * 4) ||
+        dalloc(m, (void**)&m->choice_dev, (size_t)R * 4) ||
         dalloc(m, (void**)&m->argpart, (size_t)ARGMAX_MAX_PARTS * 8) ||
         dalloc(m, (void**)&m->samp_cfg, sizeof(SampleCfg)) || dalloc(m, (void**)&m->rng_dev, 8) ||
         dalloc(m, (void**)&m->suppress_dev, 64 * 4))
@@ -1220,8 +1279,8 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     if (attn_reserve(c.n_heads, hd, m->attn_splits_unfused)) return fail(m);
     // split-K partials of the ragged batch's skinny GEMMs, allocated now so
     // that no later launch (graph capture included) allocates
-    if (m->B > 1) {
-        const int nb = m->B < 8 ? m->B : 8;
+    {
+        const int nb = R < 8 ? R : 8;
         const int shapes[5][2] = {{m->qkv_rows, d}, {d, c.n_heads * hd}, {2 * c.ffn_hidden, d},
                                   {d, c.ffn_hidden}, {c.vocab, d}};
         for (const auto& sh : shapes)
@@ -1235,16 +1294,16 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     // split partials: the fused kernel's B x n_heads x attn_splits, the
     // long-context step's n_heads x attn_splits_long, or the long-context
     // batch step's n x n_heads x attn_splits_batch[n]
-    size_t part_slots = std::max((size_t)B * c.n_heads * m->attn_splits,
+    size_t part_slots = std::max((size_t)R * c.n_heads * m->attn_splits,
                                  (size_t)c.n_heads * m->attn_splits_long);
-    for (int n = 1; n <= B && n <= 8; ++n) {
+    for (int n = 1; n <= R && n <= 8; ++n) {
         m->attn_splits_batch[n] = attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
         part_slots = std::max(part_slots, (size_t)n * c.n_heads * m->attn_splits_batch[n]);
     }
     if (dalloc(m, (void**)&m->attn_part, part_slots * (hd + 2) * 4) ||
-        dalloc(m, (void**)&m->attn_counters, (size_t)B * c.n_kv_heads * 4))
+        dalloc(m, (void**)&m->attn_counters, (size_t)R * c.n_kv_heads * 4))
         return fail(m);
-    if (hipMemset(m->attn_counters, 0, (size_t)B * c.n_kv_heads * 4) != hipSuccess) {
+    if (hipMemset(m->attn_counters, 0, (size_t)R * c.n_kv_heads * 4) != hipSuccess) {
         set_error(ATLAS_EHIP, "counter init failed");
         return fail(m);
     }
@@ -1409,6 +1468,21 @@ ATLAS_API int atlas_model_set_long_context(atlas_model* m, int from_pos) {
     return ATLAS_OK;
 }
 
+ATLAS_API int atlas_model_set_prefill_chunk(atlas_model* m, int chunk) {
+    ATLAS_REQUIRE(m, "set_prefill_chunk: null model");
+    ATLAS_REQUIRE(chunk >= 1 && chunk <= kPrefillChunk, "set_prefill_chunk: %d outside 1..%d", chunk,
+                  kPrefillChunk);
+    m->prefill_chunk = chunk;
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_prefill(atlas_model* m, const uint32_t* tokens, int n) {
+    ATLAS_REQUIRE(m && n >= 0 && (n == 0 || tokens), "prefill: bad arguments");
+    TRY(prefill(m, tokens, n));
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
 ATLAS_API int atlas_model_use_graph(atlas_model* m, int enable) {
     ATLAS_REQUIRE(m, "use_graph: null model");
     m->use_graph = enable != 0;
@@ -1489,10 +1563,7 @@ int generate_impl(atlas_model* m, const uint32_t* prompt, int n_prompt, int max_
     if (greedy && device_choice) TRY(set_greedy_cfg(m, s));
 
     // prompt: forward all but the last token without choosing
-    for (int i = 0; i + 1 < n_prompt; ++i) {
-        TRY(set_token(m, prompt[i]));
-        TRY(run_step(m, 0));
-    }
+    if (n_prompt > 1) TRY(prefill(m, prompt, n_prompt - 1));
     if (max_new == 0) {
         if (n_prompt > 0) {
             TRY(set_token(m, prompt[n_prompt - 1]));

@@ -198,6 +198,16 @@ class OlmoModel:
         path (extension; default 512)."""
         check(load().atlas_model_set_long_context(self._h, from_pos))
 
+    def prefill(self, tokens: Sequence[int]) -> None:
+        """Feed tokens at the current position without choosing, several per
+        step (extension; the reference feeds one per forward)."""
+        t = np.ascontiguousarray(list(tokens) or [0], np.uint32)
+        check(load().atlas_model_prefill(self._h, _p(t), len(tokens)))
+
+    def set_prefill_chunk(self, chunk: int) -> None:
+        """Tokens per prefill step, 1..8 (1 = token by token)."""
+        check(load().atlas_model_set_prefill_chunk(self._h, chunk))
+
     def use_graph(self, enable: bool) -> None:
         check(load().atlas_model_use_graph(self._h, 1 if enable else 0))
 

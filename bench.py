@@ -181,6 +181,9 @@ def attention_bench(torch, lib, rng, quick: bool) -> dict:
     return out
 
 
+PREFILL = {}      # weight format -> prompt prefill timings of decode_bench
+
+
 def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int):
     import dataclasses
     cfg = dataclasses.replace(model_mod.ModelConfig.olmo3_actual_7b(),
@@ -190,11 +193,23 @@ def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int
     m.init_random(seed)
     log(f"fmt {fmt}: random init {time.perf_counter() - t0:.1f}s, "
         f"{m.weight_bytes() / 1e9:.2f} GB of weights in HBM")
-    m.reset()
-    t0 = time.perf_counter()
-    for t in prompt[:-1]:
-        m.forward_one(int(t))
-    log(f"fmt {fmt}: prompt of {len(prompt)} fed in {time.perf_counter() - t0:.2f}s")
+    # the prompt: token by token (the reference's loop), then through the
+    # multi-row prefill step; the second leaves the state the decode continues
+    pre = {}
+    for chunk in (1, 8):
+        m.reset()
+        m.set_prefill_chunk(chunk)
+        m.prefill([int(t) for t in prompt[:4]])          # capture the step graphs
+        m.reset()
+        t0 = time.perf_counter()
+        m.prefill([int(t) for t in prompt[:-1]])
+        dt_p = time.perf_counter() - t0
+        pre["token_by_token_s" if chunk == 1 else "chunk8_s"] = round(dt_p, 4)
+        log(f"fmt {fmt}: prompt of {len(prompt) - 1} tokens prefilled {chunk} per step in "
+            f"{dt_p * 1e3:.1f} ms ({(len(prompt) - 1) / dt_p:.0f} tok/s)")
+    pre["tokens"] = len(prompt) - 1
+    pre["chunk8_tok_s"] = round((len(prompt) - 1) / pre["chunk8_s"], 1)
+    PREFILL[fmt] = pre
     toks = m.decode_greedy(int(prompt[-1]), warmup)
     t0 = time.perf_counter()
     toks2 = m.decode_greedy(int(toks[-1]) if warmup else int(prompt[-1]), steps)
@@ -358,6 +373,7 @@ def main() -> int:
         "int8": quant["int8"],
         "int4": quant["int4"],
         "ragged_batch": ragged,
+        "prefill_bf16": PREFILL.get(am.W_BF16),
         "checkpoint_load": load_res,
         "gemv_microbench": micro,
         "attention_microbench": attn,

@@ -124,7 +124,16 @@ int atlas_model_forward_one(atlas_model* m, uint32_t token, float* logits);
 int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits, float* hidden,
                                    atlas_hook_fn hook, void* user);
 
-/* generate_with_sampling: resets, feeds the prompt token by token, then
+/* Feed n tokens at the current position without choosing (the prompt part of
+ * generate): up to `chunk` tokens per step through the multi-row step, whose
+ * per-row causal attention reads exactly the cache rows the reference's
+ * token-by-token loop (lib.rs:1612-1618) would.  Extension: the reference
+ * feeds one token per forward.                                              */
+int atlas_model_prefill(atlas_model* m, const uint32_t* tokens, int n);
+/* Tokens per prefill step, 1..8 (default 8; 1 = token by token). */
+int atlas_model_set_prefill_chunk(atlas_model* m, int chunk);
+
+/* generate_with_sampling: resets, feeds the prompt (atlas_model_prefill), then
  * generates up to max_new tokens (EOS / stop tokens end it and are not
  * emitted).  out: [max_new]; *n_out receives the count.                     */
 int atlas_model_generate(atlas_model* m, const uint32_t* prompt, int n_prompt, int max_new,

@@ -249,6 +249,45 @@ def test_ragged_batch_long_context(orc):
                 assert _top2_margin(lg) <= 2 * LOGIT_TOL * np.max(np.abs(lg)), (graph, len(p), k)
 
 
+def test_prefill_chunks_match_token_by_token(orc):
+    # the prompt through the multi-row step (8 tokens per step: multi-row GEMV
+    # for the 2-3 token remainders, MFMA tiles above, per-row causal
+    # attention) leaves the same state as the reference's token-by-token loop:
+    # the next token's logits agree with the oracle and with chunk size 1, for
+    # remainders of every size and a prompt that crosses the long-context
+    # threshold (512) inside a chunk
+    cfg = modelgen.olmo3_small_config(max_seq=640)
+    W = modelgen.make_weights(cfg, seed=71)
+    toks = [int(t) for t in np.random.default_rng(12).integers(0, cfg["vocab"], 604)]
+    chunked, single = modelgen.engine_model(W), modelgen.engine_model(W)
+    single.set_prefill_chunk(1)
+    o = modelgen.oracle_model(W, threads=8)
+    ref_logits = {}
+    o.reset()
+    for i, t in enumerate(toks):
+        lg = o.forward_one(t)
+        if i + 1 in (2, 3, 4, 10, 18, 604):
+            ref_logits[i + 1] = lg
+    for n, ref in ref_logits.items():
+        for m in (chunked, single):
+            m.reset()
+            m.prefill(toks[:n - 1])
+            assert m.pos == n - 1
+            lg = m.forward_one(toks[n - 1])
+            assert _rel(lg, ref) <= LOGIT_TOL, (n, m is chunked)
+    # generate uses the chunked prefill; greedy tokens agree with token by token
+    from atlas_amd.model import SamplingConfig
+    a = chunked.generate_with_sampling(toks[:37], 12, SamplingConfig.greedy())
+    b = single.generate_with_sampling(toks[:37], 12, SamplingConfig.greedy())
+    if a != b:
+        k = next(i for i in range(min(len(a), len(b))) if a[i] != b[i])
+        o2 = modelgen.oracle_model(W)
+        lg = None
+        for t in toks[:37] + b[:k]:
+            lg = o2.forward_one(int(t))
+        assert _top2_margin(lg) <= 2 * LOGIT_TOL * np.max(np.abs(lg)), k
+
+
 def test_long_context_attention_path(orc):
     # positions >= from_pos replay the long-context step (QK-norm/RoPE/KV-write
     # kernel, adaptive split kernel, split merge); forcing it from position 8
