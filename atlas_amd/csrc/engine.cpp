@@ -1898,17 +1898,27 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
             if ((int)gen[i].size() >= max_new) done[i] = true;
         }
     }
-    std::vector<uint32_t> toks(n_seqs), choice(n_seqs);
-    std::vector<int> slots(n_seqs), poss(n_seqs), idx(n_seqs);
+    std::vector<uint32_t> toks(kPrefillChunk), choice(kPrefillChunk);
+    std::vector<int> slots(kPrefillChunk), poss(kPrefillChunk), idx(kPrefillChunk);
+    std::vector<int> rows_of(n_seqs);
     std::vector<float> lg;
     if (!m->ring) {
         ATLAS_HIP(hipHostMalloc((void**)&m->ring, sizeof(int) * 24 * atlas_model::kRing));
         for (auto& e : m->ring_ev) ATLAS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     int ring_next = 0;
+    // Rows per step: one per live sequence (its pending token or next prompt
+    // token); rows left over take further prompt tokens of the sequences with
+    // the most prompt left, at consecutive positions of their own slot (up to
+    // prefill_chunk rows per sequence).  Such a step takes the two-kernel
+    // attention variant, which writes every row's K/V before any row attends.
+    const int cap = std::min(kPrefillChunk, m->R);
+    bool any_choice_row = false;
     while (true) {
         int n = 0;
+        any_choice_row = false;
         for (int i = 0; i < n_seqs; ++i) {
+            rows_of[i] = 0;
             if (done[i]) continue;
             uint32_t t;
             if (cursor[i] < prompt_lens[i]) t = prompts[off[i] + cursor[i]];
@@ -1918,9 +1928,30 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
             slots[n] = i;
             poss[n] = pos[i];
             idx[n] = i;
+            any_choice_row = any_choice_row || cursor[i] + 1 >= prompt_lens[i];
+            rows_of[i] = 1;
             ++n;
         }
         if (n == 0) break;
+        bool multi = false;
+        while (n < cap && m->prefill_chunk > 1) {
+            int best = -1, best_rem = 0;
+            for (int i = 0; i < n_seqs; ++i) {
+                if (done[i] || rows_of[i] == 0 || rows_of[i] >= m->prefill_chunk) continue;
+                const int rem = prompt_lens[i] - cursor[i] - rows_of[i];
+                if (rem > best_rem) { best = i; best_rem = rem; }
+            }
+            if (best < 0) break;
+            const int r = rows_of[best];
+            toks[n] = prompts[off[best] + cursor[best] + r];
+            slots[n] = best;
+            poss[n] = pos[best] + r;
+            idx[n] = best;
+            any_choice_row = any_choice_row || cursor[best] + r + 1 >= prompt_lens[best];
+            rows_of[best] = r + 1;
+            multi = true;
+            ++n;
+        }
         {
             // stage through the pinned ring: steps without a host round trip
             // may still be queued when the next step's values are written
@@ -1941,14 +1972,10 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
         std::vector<int> sl(slots.begin(), slots.begin() + n);
         int max_pos = 0;
         for (int j = 0; j < n; ++j) max_pos = std::max(max_pos, poss[j]);
-        TRY(run_batch_step(m, n, sl, max_pos >= m->long_from));
+        TRY(run_batch_step(m, n, sl, multi || max_pos >= m->long_from));
         // a row chooses a token when it consumes its last prompt token or
         // generates; steps inside every row's prompt need no host round trip
-        bool any_choice = false;
-        for (int j = 0; j < n; ++j) {
-            const int i = idx[j];
-            any_choice = any_choice || cursor[i] + 1 >= prompt_lens[i];
-        }
+        const bool any_choice = any_choice_row;
         if (!host_path) {
             if (any_choice) {
                 ATLAS_HIP(hipMemcpyAsync(choice.data(), m->choice_dev, (size_t)n * 4,
