@@ -42,9 +42,10 @@ namespace {
 // on the 7B bf16 decode: 2.86 vs 2.99 ms/token at ctx 400, 3.12 vs 3.04 at
 // 656, 3.66 vs 3.34 at 2192 and 4.23 vs 3.65 at 4240 (fused vs long).
 constexpr int kLongAttnFrom = 512;
-// Prompt tokens per prefill step: the multi-row step's rows (the multi-row
-// GEMV for 2-3 rows, MFMA tiles up to 8).
-constexpr int kPrefillChunk = 8;
+// Rows of the multi-row step, and prompt tokens per prefill step: the
+// multi-row GEMV for 2-3 rows, the skinny MFMA kernel for 4-16.
+constexpr int kPrefillChunk = 16;
+constexpr int kMaxRows = kPrefillChunk;
 
 struct DevMat {
     int fmt = WF_BF16;
@@ -121,7 +122,7 @@ struct atlas_model {
     int attn_splits = 1;           // fused kernel: maximum (grid) split count
     int attn_splits_unfused = 1;
     int attn_splits_long = 1;      // long-context step: split kernel grid (adaptive)
-    int attn_splits_batch[9] = {}; // long-context batch step of n sequences: split grid
+    int attn_splits_batch[kMaxRows + 1] = {};   // two-kernel batch step of n rows: split grid
     int long_from = kLongAttnFrom; // positions >= this replay the long-context step
     int pos = 0;
     hipStream_t st = nullptr;
@@ -129,14 +130,14 @@ struct atlas_model {
     // captured decode steps per mode: 0 forward, 1 + greedy choice, 2 + sampled choice
     hipGraphExec_t gexec[3] = {nullptr, nullptr, nullptr};
     hipGraphExec_t gexec_long[3] = {nullptr, nullptr, nullptr};
-    hipGraphExec_t bgexec[9] = {};   // ragged batch step per batch size 1..8
-    hipGraphExec_t bgexec_long[9] = {};   // ... its long-context variant
-    hipGraphExec_t pgexec[9] = {};        // prefill step (no lm_head) per row count
-    hipGraphExec_t pgexec_long[9] = {};
+    hipGraphExec_t bgexec[kMaxRows + 1] = {};       // multi-row step per row count
+    hipGraphExec_t bgexec_long[kMaxRows + 1] = {};  // ... its two-kernel attention variant
+    hipGraphExec_t pgexec[kMaxRows + 1] = {};       // prefill step (no lm_head) per row count
+    hipGraphExec_t pgexec_long[kMaxRows + 1] = {};
     // pinned staging ring for the batch step's tokens / positions / slots:
     // entry k is rewritten only after its event (the copies) completed
     static constexpr int kRing = 8;
-    int* ring = nullptr;             // [kRing][3][8]
+    int* ring = nullptr;             // [kRing][3][kMaxRows]
     hipEvent_t ring_ev[kRing] = {};
     bool ring_used[kRing] = {};
     // greedy choice settings baked into the captured graph
@@ -478,7 +479,7 @@ void drop_graphs(atlas_model* m) {
             g = nullptr;
         }
     for (auto* arr : {m->pgexec, m->pgexec_long})
-        for (int k = 0; k < 9; ++k)
+        for (int k = 0; k <= kMaxRows; ++k)
             if (arr[k]) {
                 (void)hipGraphExecDestroy(arr[k]);
                 arr[k] = nullptr;
@@ -980,7 +981,7 @@ int set_tensor_dev(atlas_model* m, int kind, int layer, const void* src, int src
 
 // ---- the ragged batch step ----------------------------------------------------
 // n rows of activations through w: the batch-1 GEMV for one row, the skinny
-// launcher for 2..8 (the multi-row GEMV for 2-3 rows, MFMA tiles above)
+// launcher for 2..16 (the multi-row GEMV for 2-3 rows, MFMA tiles above)
 int bmm(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int epi) {
     if (n == 1) return gemv(m, w, x, y, epi);
     return skinny(m, w, x, y, n, epi);
@@ -1280,7 +1281,7 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     // split-K partials of the ragged batch's skinny GEMMs, allocated now so
     // that no later launch (graph capture included) allocates
     {
-        const int nb = R < 8 ? R : 8;
+        const int nb = R < kMaxRows ? R : kMaxRows;
         const int shapes[5][2] = {{m->qkv_rows, d}, {d, c.n_heads * hd}, {2 * c.ffn_hidden, d},
                                   {d, c.ffn_hidden}, {c.vocab, d}};
         for (const auto& sh : shapes)
@@ -1296,7 +1297,7 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     // batch step's n x n_heads x attn_splits_batch[n]
     size_t part_slots = std::max((size_t)R * c.n_heads * m->attn_splits,
                                  (size_t)c.n_heads * m->attn_splits_long);
-    for (int n = 1; n <= R && n <= 8; ++n) {
+    for (int n = 1; n <= R && n <= kMaxRows; ++n) {
         m->attn_splits_batch[n] = attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
         part_slots = std::max(part_slots, (size_t)n * c.n_heads * m->attn_splits_batch[n]);
     }
@@ -1903,7 +1904,7 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
     std::vector<int> rows_of(n_seqs);
     std::vector<float> lg;
     if (!m->ring) {
-        ATLAS_HIP(hipHostMalloc((void**)&m->ring, sizeof(int) * 24 * atlas_model::kRing));
+        ATLAS_HIP(hipHostMalloc((void**)&m->ring, sizeof(int) * 3 * kMaxRows * atlas_model::kRing));
         for (auto& e : m->ring_ev) ATLAS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     int ring_next = 0;
@@ -1957,15 +1958,17 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
             // may still be queued when the next step's values are written
             const int k = ring_next++ % atlas_model::kRing;
             if (m->ring_used[k]) ATLAS_HIP(hipEventSynchronize(m->ring_ev[k]));
-            int* e = m->ring + (size_t)k * 24;
+            int* e = m->ring + (size_t)k * 3 * kMaxRows;
             for (int j = 0; j < n; ++j) {
                 e[j] = (int)toks[j];
-                e[8 + j] = poss[j];
-                e[16 + j] = slots[j];
+                e[kMaxRows + j] = poss[j];
+                e[2 * kMaxRows + j] = slots[j];
             }
             ATLAS_HIP(hipMemcpyAsync(m->tok_dev, e, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
-            ATLAS_HIP(hipMemcpyAsync(m->pos_dev, e + 8, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
-            ATLAS_HIP(hipMemcpyAsync(m->slot_dev, e + 16, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+            ATLAS_HIP(hipMemcpyAsync(m->pos_dev, e + kMaxRows, (size_t)n * 4, hipMemcpyHostToDevice,
+                                     m->st));
+            ATLAS_HIP(hipMemcpyAsync(m->slot_dev, e + 2 * kMaxRows, (size_t)n * 4,
+                                     hipMemcpyHostToDevice, m->st));
             ATLAS_HIP(hipEventRecord(m->ring_ev[k], m->st));
             m->ring_used[k] = true;
         }

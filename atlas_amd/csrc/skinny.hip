@@ -1,4 +1,4 @@
-// skinny.hip -- small ragged batch GEMM Y[n, m] = sum_k W[m, k] X[n, k], 1 <= N <= 8.
+// skinny.hip -- small ragged batch GEMM Y[n, m] = sum_k W[m, k] X[n, k], 1 <= N <= 16.
 //
 // The reference has no batched decode (each sequence runs its own GEMV,
 // crates/atlas-model/src/lib.rs:487-499).  With N decode rows packed
@@ -16,6 +16,10 @@
 //    at most 8 significant bits).  An int4 tile is one 32-element scale
 //    block of each row, so the block scale applies to the tile's product.
 //  * D: lane (g, n) holds D[4g + v][n]: sequences 2g, 2g+1 of row n.
+//  * N > 8: NA = 2 A tiles (sequences 0-7 and 8-15) share every B operand;
+//    a wave then keeps half as many k tiles (KTW = SK_KTW / NA), so the A
+//    operands fit the 128 VGPRs of a 1024-thread block, and K splits twice
+//    as often.
 //
 // Work split: a 1024-thread block (16 waves) owns a K-slice of at most 128
 // tiles (4096 k); wave w owns a fixed run of <= 8 of its tiles and keeps
@@ -120,9 +124,10 @@ __device__ __forceinline__ bf16x8 sk_operand(const SkFrag<FMT>& f) {
 
 // grid (tile blocks, K splits); block 1024 threads.  partial: [splits][N][M]
 // (used when gridDim.y > 1).  kt_split: 32-k tiles per K split (<= 128).
-template <int FMT>
+template <int FMT, int NA>
 __global__ __launch_bounds__(1024) void skinny_kernel(GemvArgs a, float* __restrict__ partial,
                                                       int kt_split, int cpb_shift) {
+    constexpr int KTW = SK_KTW / NA;                             // k tiles per wave
     const int lane = threadIdx.x & 63;
     // wave-uniform by construction; readfirstlane lets the compiler see it
     // (per-lane branches around the loads would serialise them)
@@ -132,110 +137,122 @@ __global__ __launch_bounds__(1024) void skinny_kernel(GemvArgs a, float* __restr
     const int kt_total = a.K / 32;
     const int kt0 = blockIdx.y * kt_split;
     const int kt1 = min(kt_total, kt0 + kt_split);
-    const int per = (kt1 - kt0 + SK_WAVES - 1) / SK_WAVES;      // <= SK_KTW
+    const int per = (kt1 - kt0 + SK_WAVES - 1) / SK_WAVES;      // <= KTW
     const int w0 = kt0 + wave * per;
     const int nkt = max(0, min(per, kt1 - w0));                  // wave-uniform
     const int n_tiles = (M + 15) / 16;
     const int step = gridDim.x;
     const int t0 = blockIdx.x;
 
-    // ---- x of this lane's A operands: every load issued before the
-    // weights', so the conversion waits for x alone
-    // (lanes of rows i >= 2N read sequence 0 and are zeroed at conversion,
-    // so no lane-divergent branch separates the loads from their use)
+    // ---- x of this lane's A operands (tile na: sequence 8 na + li / 2),
+    // every load issued before the weights', so the conversion waits for x
+    // alone (lanes of rows i >= 2N read sequence 0 and are zeroed at
+    // conversion, so no lane-divergent branch separates the loads from their use)
     const int s = li >> 1;
-    const bool lo = li & 1, real = s < N;
-    const float* xr = a.x + (real ? (long)s * a.x_stride_n : 0);
-    float xv[SK_KTW][8];
-    // Every one of the SK_KTW slots is loaded and multiplied (straight-line
+    const bool lo = li & 1;
+    // Every one of the KTW slots is loaded and multiplied (straight-line
     // code keeps the wait counts exact); slots j >= nkt re-read a valid tile
     // and get a zero A operand.
     auto ktile = [&](int j) { return min(w0 + j, kt1 - 1); };
-    if (a.x_vec) {
+    float xv[NA][KTW][8];
 #pragma unroll
-        for (int j = 0; j < SK_KTW; ++j) {
-            const long k = (long)ktile(j) * 32 + 8 * g;
-            const f32x4 p0 = *reinterpret_cast<const f32x4*>(xr + k);
-            const f32x4 p1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
-            xv[j][0] = p0.x; xv[j][1] = p0.y; xv[j][2] = p0.z; xv[j][3] = p0.w;
-            xv[j][4] = p1.x; xv[j][5] = p1.y; xv[j][6] = p1.z; xv[j][7] = p1.w;
-        }
-    } else {
+    for (int na = 0; na < NA; ++na) {
+        const bool real = 8 * na + s < N;
+        const float* xr = a.x + (real ? (long)(8 * na + s) * a.x_stride_n : 0);
+        if (a.x_vec) {
 #pragma unroll
-        for (int j = 0; j < SK_KTW; ++j) {
-            const long k = (long)ktile(j) * 32 + 8 * g;
+            for (int j = 0; j < KTW; ++j) {
+                const long k = (long)ktile(j) * 32 + 8 * g;
+                const f32x4 p0 = *reinterpret_cast<const f32x4*>(xr + k);
+                const f32x4 p1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
+                xv[na][j][0] = p0.x; xv[na][j][1] = p0.y; xv[na][j][2] = p0.z; xv[na][j][3] = p0.w;
+                xv[na][j][4] = p1.x; xv[na][j][5] = p1.y; xv[na][j][6] = p1.z; xv[na][j][7] = p1.w;
+            }
+        } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) xv[j][e] = xr[(k + e) * a.x_stride_k];
+            for (int j = 0; j < KTW; ++j) {
+                const long k = (long)ktile(j) * 32 + 8 * g;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[na][j][e] = xr[(k + e) * a.x_stride_k];
+            }
         }
     }
 
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- weights of the first tile (one buffer, refilled in place)
-    SkFrag<FMT> cur[SK_KTW];
+    SkFrag<FMT> cur[KTW];
     {
         const SkRow r = sk_row<FMT>(a, min(t0 * 16 + li, M - 1));
 #pragma unroll
-        for (int j = 0; j < SK_KTW; ++j) sk_load<FMT>(r, ktile(j), g, cpb_shift, cur[j]);
+        for (int j = 0; j < KTW; ++j) sk_load<FMT>(r, ktile(j), g, cpb_shift, cur[j]);
     }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- A operands, converted once (rows i >= 2N stay zero)
-    bf16x8 A[SK_KTW];
+    bf16x8 A[NA][KTW];
 #pragma unroll
-    for (int j = 0; j < SK_KTW; ++j) {
-        if (!real || j >= nkt) {
+    for (int na = 0; na < NA; ++na)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) xv[j][e] = 0.f;
+        for (int j = 0; j < KTW; ++j) {
+            if (8 * na + s >= N || j >= nkt) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[na][j][e] = 0.f;
+            }
+            u32x4 xa;
+            xa.x = pack2(split_part(xv[na][j][0], lo), split_part(xv[na][j][1], lo));
+            xa.y = pack2(split_part(xv[na][j][2], lo), split_part(xv[na][j][3], lo));
+            xa.z = pack2(split_part(xv[na][j][4], lo), split_part(xv[na][j][5], lo));
+            xa.w = pack2(split_part(xv[na][j][6], lo), split_part(xv[na][j][7], lo));
+            A[na][j] = __builtin_bit_cast(bf16x8, xa);
         }
-        u32x4 xa;
-        xa.x = pack2(split_part(xv[j][0], lo), split_part(xv[j][1], lo));
-        xa.y = pack2(split_part(xv[j][2], lo), split_part(xv[j][3], lo));
-        xa.z = pack2(split_part(xv[j][4], lo), split_part(xv[j][5], lo));
-        xa.w = pack2(split_part(xv[j][6], lo), split_part(xv[j][7], lo));
-        A[j] = __builtin_bit_cast(bf16x8, xa);
-    }
 
-    __shared__ f32x4 red[2][SK_WAVES][64];
+    __shared__ f32x4 red[2][NA][SK_WAVES][64];
     const bool split_out = gridDim.y > 1;
     int buf = 0;
     const int my_tiles = t0 < n_tiles ? (n_tiles - 1 - t0) / step + 1 : 0;
     int t = t0;
     for (int i = 0; i < my_tiles; ++i, t += step) {      // block-uniform trip count
         const SkRow rn = sk_row<FMT>(a, min((t + step) * 16 + li, M - 1));
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 acc[NA];
+#pragma unroll
+        for (int na = 0; na < NA; ++na) acc[na] = f32x4{0.f, 0.f, 0.f, 0.f};
         // MFMAs over the tile; with REFILL each fragment's buffer takes the
         // next tile's fragment as soon as it has become an operand (two
         // straight-line versions keep the wait counts exact)
         auto body = [&](auto refill) {
 #pragma unroll
-            for (int j = 0; j < SK_KTW; ++j) {
+            for (int j = 0; j < KTW; ++j) {
                 bf16x8 B = sk_operand<FMT>(cur[j]);
                 if constexpr (FMT == WF_BF16) asm volatile("" : "+v"(B));
                 float sc = 1.0f;
                 if constexpr (FMT == WF_I4) sc = cur[j].s;
                 if constexpr (decltype(refill)::value) sk_load<FMT>(rn, ktile(j), g, cpb_shift, cur[j]);
-                if constexpr (FMT == WF_I4) {
-                    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        A[j], B, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    acc += d * sc;
-                } else {
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j], B, acc, 0, 0, 0);
+#pragma unroll
+                for (int na = 0; na < NA; ++na) {
+                    if constexpr (FMT == WF_I4) {
+                        const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            A[na][j], B, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        acc[na] += d * sc;
+                    } else {
+                        acc[na] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[na][j], B, acc[na], 0, 0, 0);
+                    }
                 }
             }
         };
         if (i + 1 < my_tiles) body(std::true_type{});
         else body(std::false_type{});
-        red[buf][wave][lane] = acc;
+#pragma unroll
+        for (int na = 0; na < NA; ++na) red[buf][na][wave][lane] = acc[na];
         __syncthreads();
-        if (threadIdx.x < 128) {
-            // thread (l, sp): sequence 2*(l/16) + sp of row 16 t + l % 16
-            const int l = threadIdx.x & 63, sp = threadIdx.x >> 6;
-            const int sq = 2 * (l >> 4) + sp, row = t * 16 + (l & 15);
+        if (threadIdx.x < 128 * NA) {
+            // thread (na, sp, l): sequence 8 na + 2 (l / 16) + sp of row 16 t + l % 16
+            const int l = threadIdx.x & 63, sp = (threadIdx.x >> 6) & 1, na = threadIdx.x >> 7;
+            const int sq = 8 * na + 2 * (l >> 4) + sp, row = t * 16 + (l & 15);
             float v = 0.f;
 #pragma unroll
             for (int w = 0; w < SK_WAVES; ++w) {
-                const f32x4 pr = red[buf][w][l];
+                const f32x4 pr = red[buf][na][w][l];
                 v += sp ? pr.z + pr.w : pr.x + pr.y;
             }
             if constexpr (FMT == WF_I8) v *= a.scales[min(row, M - 1)];
@@ -264,10 +281,10 @@ __global__ __launch_bounds__(1024) void skinny_kernel(GemvArgs a, float* __restr
 // skinny_kernel.
 constexpr int SKI4_MAX_ROWB = 2048;     // packed bytes of a row's K slice (4096 k)
 
-template <int PFN, int WAVES>
+template <int PFN, int WAVES, int NA>
 __global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float* __restrict__ partial,
                                                                int kt_split, int cpb_shift) {
-    constexpr int KTW = SK_KT_BLOCK / WAVES;                     // 32-k tiles per wave
+    constexpr int KTW = SK_KT_BLOCK / WAVES / NA;                // 32-k tiles per wave
     constexpr int THREADS = 64 * WAVES;
     constexpr int NPC = 16 * (SKI4_MAX_ROWB / 16) / THREADS;     // pieces per thread
     const int lane = threadIdx.x & 63;
@@ -292,7 +309,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float
 
     __shared__ __align__(16) uint8_t wt[2][16 * ROWP];           // 2 x 33 KB
     __shared__ __align__(16) float sct[2][16][SKI4_MAX_ROWB / 16 + 4];
-    __shared__ f32x4 red[2][WAVES][64];
+    __shared__ f32x4 red[2][NA][WAVES][64];
 
     // ---- this thread's pieces of every tile (fixed): 16-byte data pieces
     // q = 0, 1 and scale words q = 0, 1 as (row in tile, byte/word column);
@@ -343,38 +360,42 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float
     for (int p = 0; p < PFN; ++p) fetch(min(t0 + p * step, n_tiles - 1), pf[p]);
     __builtin_amdgcn_sched_barrier(0);
     const int s = li >> 1;
-    const bool lo = li & 1, real = s < N;
-    const float* xr = a.x + (real ? (long)s * a.x_stride_n : 0);
+    const bool lo = li & 1;
     auto ktile = [&](int j) { return kt0 + min(w0 + j, nks - 1); };
-    bf16x8 A[KTW];
+    bf16x8 A[NA][KTW];
 #pragma unroll
-    for (int h = 0; h < KTW; h += KTW / 2) {
-        float xv[KTW / 2][8];
+    for (int na = 0; na < NA; ++na) {
+        const bool real = 8 * na + s < N;
+        const float* xr = a.x + (real ? (long)(8 * na + s) * a.x_stride_n : 0);
 #pragma unroll
-        for (int j = 0; j < KTW / 2; ++j) {
-            const long k = (long)ktile(h + j) * 32 + 8 * g;
-            if (a.x_vec) {
-                const f32x4 p0 = *reinterpret_cast<const f32x4*>(xr + k);
-                const f32x4 p1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
-                xv[j][0] = p0.x; xv[j][1] = p0.y; xv[j][2] = p0.z; xv[j][3] = p0.w;
-                xv[j][4] = p1.x; xv[j][5] = p1.y; xv[j][6] = p1.z; xv[j][7] = p1.w;
-            } else {
+        for (int h = 0; h < KTW; h += KTW / 2) {
+            float xv[KTW / 2][8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xv[j][e] = xr[(k + e) * a.x_stride_k];
+            for (int j = 0; j < KTW / 2; ++j) {
+                const long k = (long)ktile(h + j) * 32 + 8 * g;
+                if (a.x_vec) {
+                    const f32x4 p0 = *reinterpret_cast<const f32x4*>(xr + k);
+                    const f32x4 p1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
+                    xv[j][0] = p0.x; xv[j][1] = p0.y; xv[j][2] = p0.z; xv[j][3] = p0.w;
+                    xv[j][4] = p1.x; xv[j][5] = p1.y; xv[j][6] = p1.z; xv[j][7] = p1.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xv[j][e] = xr[(k + e) * a.x_stride_k];
+                }
             }
-        }
 #pragma unroll
-        for (int j = 0; j < KTW / 2; ++j) {
-            if (!real || h + j >= nkt) {
+            for (int j = 0; j < KTW / 2; ++j) {
+                if (!real || h + j >= nkt) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xv[j][e] = 0.f;
+                    for (int e = 0; e < 8; ++e) xv[j][e] = 0.f;
+                }
+                u32x4 xa;
+                xa.x = pack2(split_part(xv[j][0], lo), split_part(xv[j][1], lo));
+                xa.y = pack2(split_part(xv[j][2], lo), split_part(xv[j][3], lo));
+                xa.z = pack2(split_part(xv[j][4], lo), split_part(xv[j][5], lo));
+                xa.w = pack2(split_part(xv[j][6], lo), split_part(xv[j][7], lo));
+                A[na][h + j] = __builtin_bit_cast(bf16x8, xa);
             }
-            u32x4 xa;
-            xa.x = pack2(split_part(xv[j][0], lo), split_part(xv[j][1], lo));
-            xa.y = pack2(split_part(xv[j][2], lo), split_part(xv[j][3], lo));
-            xa.z = pack2(split_part(xv[j][4], lo), split_part(xv[j][5], lo));
-            xa.w = pack2(split_part(xv[j][6], lo), split_part(xv[j][7], lo));
-            A[h + j] = __builtin_bit_cast(bf16x8, xa);
         }
     }
 
@@ -387,7 +408,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float
         stash(f, b);
         if (i + PFN < my_tiles) fetch(t0 + (i + PFN) * step, f);
         __syncthreads();
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 acc[NA];
+#pragma unroll
+        for (int na = 0; na < NA; ++na) acc[na] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < KTW; ++j) {
             const int c = min(w0 + j, nks - 1);                 // slice chunk
@@ -400,19 +423,23 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float
             bb.y = pack_f32_pair(s8_at(hi, 1), s8_at(lw, 1));
             bb.z = pack_f32_pair(s8_at(hi, 2), s8_at(lw, 2));
             bb.w = pack_f32_pair(s8_at(hi, 3), s8_at(lw, 3));
-            const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                A[j], __builtin_bit_cast(bf16x8, bb), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            acc += d * sc;
+#pragma unroll
+            for (int na = 0; na < NA; ++na) {
+                const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    A[na][j], __builtin_bit_cast(bf16x8, bb), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                acc[na] += d * sc;
+            }
         }
-        red[b][wave][lane] = acc;
+#pragma unroll
+        for (int na = 0; na < NA; ++na) red[b][na][wave][lane] = acc[na];
         __syncthreads();
-        if (threadIdx.x < 128) {
-            const int l = threadIdx.x & 63, sp = threadIdx.x >> 6;
-            const int sq = 2 * (l >> 4) + sp, row = t * 16 + (l & 15);
+        if (threadIdx.x < 128 * NA) {
+            const int l = threadIdx.x & 63, sp = (threadIdx.x >> 6) & 1, na = threadIdx.x >> 7;
+            const int sq = 8 * na + 2 * (l >> 4) + sp, row = t * 16 + (l & 15);
             float v = 0.f;
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) {
-                const f32x4 pr = red[b][w][l];
+                const f32x4 pr = red[b][na][w][l];
                 v += sp ? pr.z + pr.w : pr.x + pr.y;
             }
             if (split_out) {
@@ -476,39 +503,52 @@ static int ensure_partial(size_t bytes) {
     return ATLAS_OK;
 }
 
-// K splits launch_skinny uses for this K
-static int skinny_splits(int K) {
-    const int kt_total = K / 32;
-    return (kt_total + SK_KT_BLOCK - 1) / SK_KT_BLOCK;
+// A tiles of an N-row launch, and the K splits it uses (a block covers
+// SK_KT_BLOCK / NA k tiles)
+static int skinny_na(int N) { return N > 8 ? 2 : 1; }
+static int skinny_splits(int K, int N) {
+    const int kt_total = K / 32, kt_block = SK_KT_BLOCK / skinny_na(N);
+    return (kt_total + kt_block - 1) / kt_block;
 }
 
 // Allocate the split-K partials an (M, N, K) launch needs, so that later
-// launches (e.g. under graph capture) allocate nothing.
+// launches (e.g. under graph capture) allocate nothing; an N-row reservation
+// covers every smaller N.
 int skinny_reserve(int M, int N, int K) {
-    const int splits = skinny_splits(K);
+    int splits = skinny_splits(K, N);
+    if (N > 8) splits = std::max(splits, skinny_splits(K, 8));
     if (splits <= 1) return ATLAS_OK;
     return ensure_partial((size_t)splits * N * M * sizeof(float));
 }
 
-template <int FMT>
-static int launch_skinny(const GemvArgs& a, hipStream_t st) {
-    const int kt_total = a.K / 32;
-    const int splits = skinny_splits(a.K);
-    const int kt_split = (kt_total + splits - 1) / splits;
-    const int n_tiles = (a.M + 15) / 16;
-    static int resident = 0;     // blocks of 1024 threads one CU holds
+// blocks of 1024 threads one CU holds for kernel `kern` (cached per kernel)
+template <const void* (*KERN)()>
+static int skinny_resident() {
+    static int resident = 0;
     if (resident == 0) {
         int n = 0;
-        const void* kern = FMT == WF_I4 ? (const void*)skinny_i4_kernel<1, 16>
-                                        : (const void*)skinny_kernel<FMT>;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 1024, 0) != hipSuccess ||
-            n < 1) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, KERN(), 1024, 0) != hipSuccess || n < 1) {
             (void)hipGetLastError();
             n = 1;
         }
         resident = n;
     }
-    int bx = resident * device_cu_count();
+    return resident;
+}
+
+template <int FMT, int NA>
+static const void* skinny_kernel_ptr() {
+    if constexpr (FMT == WF_I4) return (const void*)skinny_i4_kernel<1, 16, NA>;
+    else return (const void*)skinny_kernel<FMT, NA>;
+}
+
+template <int FMT, int NA>
+static int launch_skinny(const GemvArgs& a, hipStream_t st) {
+    const int kt_total = a.K / 32;
+    const int splits = skinny_splits(a.K, a.N);
+    const int kt_split = (kt_total + splits - 1) / splits;
+    const int n_tiles = (a.M + 15) / 16;
+    int bx = skinny_resident<skinny_kernel_ptr<FMT, NA>>() * device_cu_count();
     if (bx > n_tiles) bx = n_tiles;
     if (splits > 1) {
         int rc = ensure_partial((size_t)splits * a.N * a.M * sizeof(float));
@@ -517,10 +557,10 @@ static int launch_skinny(const GemvArgs& a, hipStream_t st) {
     int cpb_shift = 0;
     while ((1 << cpb_shift) < a.cpb) ++cpb_shift;
     if constexpr (FMT == WF_I4)
-        hipLaunchKernelGGL((skinny_i4_kernel<1, 16>), dim3(bx, splits), dim3(1024), 0, st, a,
+        hipLaunchKernelGGL((skinny_i4_kernel<1, 16, NA>), dim3(bx, splits), dim3(1024), 0, st, a,
                            g_partial, kt_split, cpb_shift);
     else
-        hipLaunchKernelGGL((skinny_kernel<FMT>), dim3(bx, splits), dim3(1024), 0, st, a,
+        hipLaunchKernelGGL((skinny_kernel<FMT, NA>), dim3(bx, splits), dim3(1024), 0, st, a,
                            g_partial, kt_split, cpb_shift);
     ATLAS_LAUNCH_CHECK("skinny");
     if (splits > 1) {
@@ -534,11 +574,16 @@ static int launch_skinny(const GemvArgs& a, hipStream_t st) {
     return ATLAS_OK;
 }
 
+template <int FMT>
+static int launch_skinny_n(const GemvArgs& a, hipStream_t st) {
+    return a.N > 8 ? launch_skinny<FMT, 2>(a, st) : launch_skinny<FMT, 1>(a, st);
+}
+
 int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     GemvArgs a = a_in;
     gemv_fill_int4_index(a);
     a.x_vec = a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0;
-    ATLAS_REQUIRE(a.N >= 1 && a.N <= 8, "skinny: N=%d outside 1..8", a.N);
+    ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16", a.N);
     ATLAS_REQUIRE(a.w && a.x && a.y, "skinny: null pointer");
     ATLAS_REQUIRE(a.fmt == WF_BF16 || a.scales, "skinny: null scales");
     if (a.epi == EPI_SILU_MUL) ATLAS_REQUIRE(a.M % 2 == 0, "skinny: silu-mul needs even rows");
@@ -555,15 +600,15 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     switch (a.fmt) {
     case WF_BF16:
         ATLAS_REQUIRE((al & 15) == 0, "skinny bf16: weights not 16-byte aligned");
-        return launch_skinny<WF_BF16>(a, st);
+        return launch_skinny_n<WF_BF16>(a, st);
     case WF_I8:
         ATLAS_REQUIRE((al & 7) == 0, "skinny int8: weights not 8-byte aligned");
-        return launch_skinny<WF_I8>(a, st);
+        return launch_skinny_n<WF_I8>(a, st);
     case WF_I4:
         ATLAS_REQUIRE((al & 3) == 0, "skinny int4: weights not 4-byte aligned");
         ATLAS_REQUIRE(a.block % 32 == 0 && (a.cpb & (a.cpb - 1)) == 0 && a.bpr > 0,
                       "skinny int4: block %d must be 32 * 2^j and divide K", a.block);
-        return launch_skinny<WF_I4>(a, st);
+        return launch_skinny_n<WF_I4>(a, st);
     }
     set_error(ATLAS_EUNSUPPORTED, "skinny: weight format %d", a.fmt);
     return ATLAS_EUNSUPPORTED;

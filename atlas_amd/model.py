@@ -205,7 +205,7 @@ class OlmoModel:
         check(load().atlas_model_prefill(self._h, _p(t), len(tokens)))
 
     def set_prefill_chunk(self, chunk: int) -> None:
-        """Tokens per prefill step, 1..8 (1 = token by token)."""
+        """Tokens per prefill step, 1..16 (1 = token by token)."""
         check(load().atlas_model_set_prefill_chunk(self._h, chunk))
 
     def use_graph(self, enable: bool) -> None:

@@ -151,6 +151,17 @@ def test_skinny(orc, fmt, n):
     _skinny_check(orc, fmt, n, M, K)
 
 
+# 9-16 rows: two MFMA A tiles share each weight tile (half the k tiles per
+# wave, so K = 4096 already splits across blocks)
+@pytest.mark.parametrize("fmt,n,M,K", [
+    ("bf16", 9, 1000, 512), ("bf16", 16, 4096, 4096), ("bf16", 13, 777, 11008),
+    ("int8", 16, 1000, 4096), ("int8", 9, 4096, 11008),
+    ("int4", 16, 2048, 4096), ("int4", 12, 1000, 11008)])
+def test_skinny_two_a_tiles(orc, fmt, n, M, K):
+    print(f"skinny two tiles {fmt} n={n} M={M} K={K}", flush=True)
+    _skinny_check(orc, fmt, n, M, K, 32, seed=3)
+
+
 # Two and three rows take the multi-row GEMV: the 7B shapes (three rows of
 # K = 11008 fill 132 KB of LDS), odd row counts, K not a multiple of one
 # wave step, int4 blocks of 128, and a 3 x 32 matrix.
