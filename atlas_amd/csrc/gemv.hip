@@ -11,8 +11,8 @@
 //    walks the whole K with 128-bit nontemporal loads (lane i reads the i-th
 //    16-byte chunk of every row, so one instruction reads 1 KiB contiguous
 //    per row);
-//  * x is staged once per block in LDS as f32 with an XOR swizzle on 16-byte
-//    pieces (piece p lives at p ^ ((p >> 3) & 7)), which makes the per-lane
+//  * x is staged once per block in LDS as f32 in 16-byte pieces with one
+//    empty piece after every 16 (xpad below), which keeps the per-lane
 //    ds_read_b128 of consecutive chunks bank-conflict free;
 //  * one x read feeds ROWS rows, so LDS traffic stays below HBM traffic even
 //    for int4 (32 f32 of x per 16 bytes of weights);
@@ -107,27 +107,68 @@ __device__ __forceinline__ float block_sum256(float v, float* red4) {
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
-// Every global read of the staging is issued before the first use, so a
-// norm prologue costs one round trip, not two (sum of squares, then x, w):
-// a thread owns the 16-byte pieces p = tid + 256 j, j < PPT, in registers.
-template <bool SWZ, int PPT>
-__device__ __forceinline__ void stage_x_regs(const GemvArgs& a, f32x4* xs, int K) {
-    __shared__ float red4[4];
+// Staging comes in two halves: `*_issue` sends every global read of x (and
+// of the prologue's vectors) and `*_finish` consumes them.  Where the first
+// weight loads go relative to them is a per-format choice (the kernel body
+// explains it).
+//
+// Register staging: a thread owns the 16-byte pieces p = tid + 256 j,
+// j < PPT; a norm prologue costs one round trip, not two (sum of squares,
+// then x, w).
+template <int PPT>
+struct XRegs { f32x4 x[PPT], y[PPT], w[PPT]; };
+
+// guarded loads: only the vectors the prologue uses, only pieces below K
+template <int PPT>
+__device__ __forceinline__ void stage_regs_issue(const GemvArgs& a, XRegs<PPT>& r, int K) {
     const int np = K >> 2;
     const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
     const f32x4* yin = reinterpret_cast<const f32x4*>(a.pro_y);
     const f32x4* win = reinterpret_cast<const f32x4*>(a.pro_w);
     const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
-    f32x4 xv[PPT], yv[PPT], wv[PPT];
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
         const int p = threadIdx.x + 256 * j;
         if (p < np) {
-            xv[j] = xin[p];
-            if (res) yv[j] = yin[p];
-            if (norm) wv[j] = win[p];
+            r.x[j] = xin[p];
+            if (res) r.y[j] = yin[p];
+            if (norm) r.w[j] = win[p];
         }
     }
+}
+
+// unconditional buffer loads: a vector the prologue does not use gets an
+// empty range and reads as zeros without touching memory, as do pieces past
+// K.  Guarded loads split the issue into branches, after which the compiler
+// waits for every load in flight, including weight loads issued between
+// the two halves.
+template <int PPT>
+__device__ __forceinline__ void stage_regs_issue_buf(const GemvArgs& a, XRegs<PPT>& r, int K) {
+    const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
+    const __amdgpu_buffer_rsrc_t xb =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.x), (short)0, K * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t yb = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(res ? a.pro_y : a.x), (short)0, res ? K * 4 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wb = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(norm ? a.pro_w : a.x), (short)0, norm ? K * 4 : 0, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+        const int off = (int)threadIdx.x * 16;
+        r.x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xb, off, 4096 * j, 0));
+        r.y[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(yb, off, 4096 * j, 0));
+        r.w[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wb, off, 4096 * j, 0));
+    }
+}
+
+template <bool SWZ, int PPT>
+__device__ __forceinline__ void stage_regs_finish(const GemvArgs& a, XRegs<PPT>& r, f32x4* xs,
+                                                  int K) {
+    __shared__ float red4[4];
+    const int np = K >> 2;
+    const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
+    const f32x4 (&xv)[PPT] = r.x;
+    const f32x4 (&yv)[PPT] = r.y;
+    const f32x4 (&wv)[PPT] = r.w;
     float inv = 1.0f;
     if (norm) {
         float ss = 0.f;
@@ -149,31 +190,33 @@ __device__ __forceinline__ void stage_x_regs(const GemvArgs& a, f32x4* xs, int K
     for (int j = 0; j < PPT; ++j) {
         const int p = threadIdx.x + 256 * j;
         if (p < np) {
-            f32x4 r;
-            if (res) r = xv[j] + (yv[j] * inv) * wv[j];
-            else if (norm) r = (xv[j] * inv) * wv[j];
-            else r = xv[j];
-            xs[SWZ ? xpad(p) : p] = r;
-            if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = r;
+            f32x4 v;
+            if (res) v = xv[j] + (yv[j] * inv) * wv[j];
+            else if (norm) v = (xv[j] * inv) * wv[j];
+            else v = xv[j];
+            xs[SWZ ? xpad(p) : p] = v;
+            if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = v;
         }
     }
 }
 
-// Plain x (no prologue) of up to 256 * PPT pieces: every load is issued
-// before the first LDS write, so staging costs one round trip for any K the
-// registers hold (PPT = 12: K <= 12288).  Buffer loads address all pieces
-// from one VGPR offset (the piece stride goes in the SGPR offset), and reads
-// past the end of x return zeros that are never stored.
-template <bool SWZ, int PPT>
-__device__ __forceinline__ void stage_x_plain(const GemvArgs& a, f32x4* xs, int K) {
-    const int np = K >> 2;
+// Plain x (no prologue) of up to 256 * PPT pieces, one round trip for any K
+// the registers hold (PPT = 12: K <= 12288).  Buffer loads address all
+// pieces from one VGPR offset (the piece stride goes in the SGPR offset),
+// and reads past the end of x return zeros that are never stored.
+template <int PPT>
+__device__ __forceinline__ void stage_plain_issue(const GemvArgs& a, f32x4 (&xv)[PPT], int K) {
     const __amdgpu_buffer_rsrc_t xb =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.x), (short)0, K * 4, 0x00020000);
-    f32x4 xv[PPT];
 #pragma unroll
     for (int j = 0; j < PPT; ++j)
         xv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                               xb, (int)threadIdx.x * 16, 4096 * j, 0));
+}
+
+template <bool SWZ, int PPT>
+__device__ __forceinline__ void stage_plain_finish(const f32x4 (&xv)[PPT], f32x4* xs, int K) {
+    const int np = K >> 2;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
         const int p = threadIdx.x + 256 * j;
@@ -181,17 +224,19 @@ __device__ __forceinline__ void stage_x_plain(const GemvArgs& a, f32x4* xs, int 
     }
 }
 
-// General staging: any K the LDS holds, and the SwiGLU prologue.
+// Which staging a batch-1 launch takes.  The register staging also takes
+// plain x at K <= 4096 (four loads per thread, where the plain path's
+// twelve would mostly read past K).
+enum { STAGE_REGS = 0, STAGE_PLAIN = 1, STAGE_LOOP = 2 };
+__device__ __forceinline__ int stage_kind(const GemvArgs& a, int K) {
+    if (a.pro != PRO_SILU && K <= 256 * 4 * 4) return STAGE_REGS;    // d_model <= 4096: 48 VGPRs
+    if (a.pro == PRO_X && K <= 256 * 4 * 12) return STAGE_PLAIN;     // e.g. the W_down input
+    return STAGE_LOOP;
+}
+
+// Looped staging: any K the LDS holds, and the SwiGLU prologue.
 template <bool SWZ>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, f32x4* xs, int K) {
-    if (a.pro != PRO_SILU && K <= 256 * 4 * 4) {    // d_model <= 4096: 48 VGPRs
-        stage_x_regs<SWZ, 4>(a, xs, K);
-        return;
-    }
-    if (a.pro == PRO_X && K <= 256 * 4 * 12) {      // e.g. the W_down input
-        stage_x_plain<SWZ, 12>(a, xs, K);
-        return;
-    }
+__device__ __forceinline__ void stage_x_loop(const GemvArgs& a, f32x4* xs, int K) {
     __shared__ float red4[4];
     const int np = K >> 2;
     const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
@@ -369,11 +414,55 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
 
     u32x4 cur[UNROLL][ROWS];
     float scur[UNROLL][ROWS];
-    // the first weight loads go out before x is staged, hiding the staging
+    // Where the first weight step goes relative to x's reads.  Vector loads
+    // return in order, so x read after a grid-wide burst of weight loads
+    // arrives only when that burst has, and the next weight step goes out
+    // only then.  bf16 and int8 still do best with the weights first
+    // (measured at the 7B shapes): their 16-byte loads per lane and step
+    // keep HBM busy across the staging.  int4 waves read 4 bytes of weights
+    // per 32 x values and gain from x first (4096 x 4096: 5.8 -> 5.3 us;
+    // 11008 x 4096: 10.3 -> 9.4 us).  In that order the first weight step is
+    // loaded even by a wave without rows (row and chunk are clamped into the
+    // matrix): a load under a branch would make the compiler wait for it
+    // before x's last piece is stored.
     const int npad = (K >> 2) + ((K >> 2) + 15) / 16;     // padded pieces per x row
-    if (total > 0) load(0, cur, scur);
-    if constexpr (NX == 1) stage_x<true>(a, xs, K);
-    else stage_xn<NX>(a, xs, K, npad);
+    if constexpr (NX == 1) {
+        const int kind = stage_kind(a, K);
+        if constexpr (FMT == WF_I4) {
+            if (kind == STAGE_REGS) {
+                XRegs<4> r;
+                stage_regs_issue_buf<4>(a, r, K);
+                __builtin_amdgcn_sched_barrier(0);
+                load(0, cur, scur);
+                stage_regs_finish<true, 4>(a, r, xs, K);
+            } else if (kind == STAGE_PLAIN) {
+                f32x4 xv[12];
+                stage_plain_issue<12>(a, xv, K);
+                __builtin_amdgcn_sched_barrier(0);
+                load(0, cur, scur);
+                stage_plain_finish<true, 12>(xv, xs, K);
+            } else {
+                load(0, cur, scur);
+                stage_x_loop<true>(a, xs, K);
+            }
+        } else {
+            if (total > 0) load(0, cur, scur);
+            if (kind == STAGE_REGS) {
+                XRegs<4> r;
+                stage_regs_issue<4>(a, r, K);
+                stage_regs_finish<true, 4>(a, r, xs, K);
+            } else if (kind == STAGE_PLAIN) {
+                f32x4 xv[12];
+                stage_plain_issue<12>(a, xv, K);
+                stage_plain_finish<true, 12>(xv, xs, K);
+            } else {
+                stage_x_loop<true>(a, xs, K);
+            }
+        }
+    } else {
+        if (total > 0) load(0, cur, scur);
+        stage_xn<NX>(a, xs, K, npad);
+    }
     __syncthreads();
 
     float acc[ROWS][NX];
