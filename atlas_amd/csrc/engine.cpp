@@ -46,6 +46,10 @@ constexpr int kLongAttnFrom = 512;
 // multi-row GEMV for 2-3 rows, the skinny MFMA kernel for 4-16.
 constexpr int kPrefillChunk = 16;
 constexpr int kMaxRows = kPrefillChunk;
+// Prompt chunks of bf16 models whose GEMM inner dims are multiples of 128
+// go through the tiled MFMA GEMM (gemm_rows_launch), up to this many rows
+// per step, replayed eagerly (the captured steps stop at kMaxRows rows).
+constexpr int kPrefillBig = 128;
 
 struct DevMat {
     int fmt = WF_BF16;
@@ -97,7 +101,8 @@ struct atlas_model {
     std::vector<uint8_t> sliding;
     int hd = 0, kvd = 0, qkv_rows = 0, B = 1;
     int R = 1;                       // rows of the multi-row step buffers: max(B, prefill chunk)
-    int prefill_chunk = kPrefillChunk;   // prompt tokens per prefill step (1: token by token)
+    int prefill_chunk = kPrefillBig;     // prompt tokens per prefill step (1: token by token)
+    bool big_prefill = false;            // chunks of up to kPrefillBig rows (see kPrefillBig)
     float scale = 1.f;
     std::vector<LayerW> L;
     uint16_t* embed = nullptr;
@@ -1022,7 +1027,8 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
             a.scale = m->scale; a.window = L.window; a.max_rows = c.max_seq;
             a.adaptive = 1;
-            const int sp = m->attn_splits_batch[n];
+            const int sp = n <= kMaxRows ? m->attn_splits_batch[n]
+                                         : attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
             const size_t np = (size_t)n * c.n_heads * sp;
             a.part_m = m->attn_part; a.part_l = m->attn_part + np; a.part_o = m->attn_part + 2 * np;
             TRY(attn_batch_launch(a, sp, n, m->st));
@@ -1128,7 +1134,8 @@ int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool lo
 // other rows read; the rows of a ragged batch live in different slots, the
 // rows of a prefill chunk in one.)
 int prefill(atlas_model* m, const uint32_t* toks, int n) {
-    const int chunk = m->fused ? std::min(m->prefill_chunk, std::min(m->R, kPrefillChunk)) : 1;
+    const int cap = !m->fused ? 1 : m->big_prefill ? kPrefillBig : std::min(m->R, kPrefillChunk);
+    const int chunk = std::min(m->prefill_chunk, cap);
     int done = 0;
     while (done < n) {
         const int k = std::min(chunk, n - done);
@@ -1141,7 +1148,7 @@ int prefill(atlas_model* m, const uint32_t* toks, int n) {
             ++done;
             continue;
         }
-        int host[3][kPrefillChunk];
+        int host[3][kPrefillBig];
         for (int j = 0; j < k; ++j) {
             host[0][j] = (int)toks[done + j];
             host[1][j] = m->pos + j;
@@ -1150,7 +1157,10 @@ int prefill(atlas_model* m, const uint32_t* toks, int n) {
         ATLAS_HIP(hipMemcpyAsync(m->tok_dev, host[0], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
         ATLAS_HIP(hipMemcpyAsync(m->pos_dev, host[1], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
         ATLAS_HIP(hipMemcpyAsync(m->slot_dev, host[2], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
-        TRY(run_batch_step(m, k, std::vector<int>(k, 0), true, false));
+        // chunks beyond the captured row counts run eagerly: ~260 launches
+        // queue while the first GEMMs run
+        if (k > kMaxRows) TRY(batch_step(m, k, std::vector<int>(k, 0), true, false));
+        else TRY(run_batch_step(m, k, std::vector<int>(k, 0), true, false));
         ATLAS_HIP(hipStreamSynchronize(m->st));      // host[] lives on this frame
         m->pos += k;
         done += k;
@@ -1200,7 +1210,14 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->kvd = c.n_kv_heads * hd;
     m->qkv_rows = c.d_model + 2 * m->kvd;
     m->B = c.max_batch < 1 ? 1 : c.max_batch;
-    m->R = std::max(m->B, kPrefillChunk);
+    // big prompt chunks: bf16 weights, the fused (post-norm) step, and every
+    // GEMM inner dimension (d_model, n_heads * head_dim, ffn_hidden) a
+    // multiple of the tiled GEMM's 128
+    m->big_prefill = fmt == WF_BF16 && c.post_norm &&
+                     attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
+                     attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && c.d_model % 128 == 0 &&
+                     (c.n_heads * hd) % 128 == 0 && c.ffn_hidden % 128 == 0;
+    m->R = std::max(m->B, m->big_prefill ? kPrefillBig : kPrefillChunk);
     // scale = attn_factor / sqrt(head_dim) (lib.rs:632, 1331-1335)
     m->scale = 1.0f / sqrtf((float)hd);
     const float af = c.yarn ? c.yarn_attn_factor : 1.0f;
@@ -1284,8 +1301,10 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         const int nb = R < kMaxRows ? R : kMaxRows;
         const int shapes[5][2] = {{m->qkv_rows, d}, {d, c.n_heads * hd}, {2 * c.ffn_hidden, d},
                                   {d, c.ffn_hidden}, {c.vocab, d}};
-        for (const auto& sh : shapes)
+        for (const auto& sh : shapes) {
             if (sh[1] % 32 == 0 && skinny_reserve(sh[0], nb, sh[1])) return fail(m);
+            if (m->big_prefill && gemm_rows_reserve(sh[0], kPrefillBig, sh[1])) return fail(m);
+        }
     }
     // fused step: post-norm model whose attention shape the fused kernel
     // covers and whose GEMVs take the aligned fast path (d % 32 == 0)
@@ -1297,9 +1316,10 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     // batch step's n x n_heads x attn_splits_batch[n]
     size_t part_slots = std::max((size_t)R * c.n_heads * m->attn_splits,
                                  (size_t)c.n_heads * m->attn_splits_long);
-    for (int n = 1; n <= R && n <= kMaxRows; ++n) {
-        m->attn_splits_batch[n] = attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
-        part_slots = std::max(part_slots, (size_t)n * c.n_heads * m->attn_splits_batch[n]);
+    for (int n = 1; n <= R; ++n) {
+        const int sp = attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
+        if (n <= kMaxRows) m->attn_splits_batch[n] = sp;
+        part_slots = std::max(part_slots, (size_t)n * c.n_heads * sp);
     }
     if (dalloc(m, (void**)&m->attn_part, part_slots * (hd + 2) * 4) ||
         dalloc(m, (void**)&m->attn_counters, (size_t)R * c.n_kv_heads * 4))
@@ -1471,8 +1491,8 @@ ATLAS_API int atlas_model_set_long_context(atlas_model* m, int from_pos) {
 
 ATLAS_API int atlas_model_set_prefill_chunk(atlas_model* m, int chunk) {
     ATLAS_REQUIRE(m, "set_prefill_chunk: null model");
-    ATLAS_REQUIRE(chunk >= 1 && chunk <= kPrefillChunk, "set_prefill_chunk: %d outside 1..%d", chunk,
-                  kPrefillChunk);
+    ATLAS_REQUIRE(chunk >= 1 && chunk <= kPrefillBig, "set_prefill_chunk: %d outside 1..%d", chunk,
+                  kPrefillBig);
     m->prefill_chunk = chunk;
     return ATLAS_OK;
 }

@@ -50,6 +50,10 @@ constexpr int kGemvMaxNx = 4;
 bool gemv_multi_ok(const GemvArgs& a);
 int gemv_multi_launch(const GemvArgs& a, hipStream_t st);
 int skinny_reserve(int M, int N, int K);
+// 17..128 rows of bf16 weights: the tiled MFMA GEMM (skinny_launch routes there)
+bool gemm_rows_ok(const GemvArgs& a);
+int gemm_rows_launch(const GemvArgs& a, hipStream_t st);
+int gemm_rows_reserve(int M, int N, int K);
 int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,
                         hipStream_t st);
 

@@ -490,15 +490,13 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemvArgs a, const fl
 static float* g_partial = nullptr;
 static size_t g_partial_bytes = 0;
 
+// A buffer that grows is replaced, never freed: graphs captured earlier
+// keep pointing at the old one, which still covers their launches.
 static int ensure_partial(size_t bytes) {
     if (bytes <= g_partial_bytes) return ATLAS_OK;
-    if (g_partial) {
-        ATLAS_HIP(hipDeviceSynchronize());
-        ATLAS_HIP(hipFree(g_partial));
-        g_partial = nullptr;
-        g_partial_bytes = 0;
-    }
-    ATLAS_HIP(hipMalloc((void**)&g_partial, bytes));
+    float* p = nullptr;
+    ATLAS_HIP(hipMalloc((void**)&p, bytes));
+    g_partial = p;
     g_partial_bytes = bytes;
     return ATLAS_OK;
 }
@@ -574,6 +572,216 @@ static int launch_skinny(const GemvArgs& a, hipStream_t st) {
     return ATLAS_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Prompt chunks: Y[n, m] = sum_k W[m, k] X[n, k] for 17 <= N <= 128 rows of
+// bf16 weights.  Same operand roles and hi/lo split as skinny_kernel, but
+// every A fragment now feeds many weight tiles, so the matrix cores do the
+// work and the weights stream once per chunk:
+//  * a 256-thread block owns 128 weight rows (wave w: rows 32 w .. +31, two
+//    B fragments per 32-k step) and all NT 16-row tiles of X;
+//  * A fragments (X hi and lo, bf16) go through LDS, 2 k steps per chunk,
+//    double-buffered: each chunk's global reads are issued one chunk ahead
+//    and converted after the MFMAs of the current one;
+//  * B fragments (16 B per lane, straight from HBM) are refilled in place
+//    four k steps ahead, as soon as each has become an operand;
+//  * K splits over blockIdx.y when the row blocks alone leave CUs idle;
+//    partials are summed by skinny_reduce_kernel in a fixed order.
+// Per 32-k step a wave issues NT x 2 x 2 MFMAs (tiles x B fragments x hi/lo).
+constexpr int GR_ROWS = 128;        // weight rows per block
+constexpr int GR_MAX_N = 128;       // activation rows per launch
+
+// hi / lo bf16 parts of 8 floats, packed as MFMA operands
+__device__ __forceinline__ void split8(const f32x4 p0, const f32x4 p1, u32x4& hi, u32x4& lo) {
+    const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    uint32_t h[8], l[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t u = __float_as_uint(v[e]);
+        h[e] = u >> 16;
+        l[e] = bf16_rne_bits(v[e] - __uint_as_float(u & 0xFFFF0000u));
+    }
+    hi = u32x4{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
+    lo = u32x4{pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])};
+}
+
+template <int NT>
+__global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __restrict__ partial,
+                                                           int steps_per_split) {
+    constexpr int ITEMS = 2 * NT * 64 / 256;      // A items (8 floats) per thread per chunk
+    __shared__ u32x4 As[2][2][NT][2][64];         // [buf][k step][tile][hi/lo][lane]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, li = lane & 15;
+    const int M = a.M, N = a.N;
+    const int s0 = blockIdx.y * steps_per_split;
+    const int s1 = min(a.K / 32, s0 + steps_per_split);   // s1 - s0: a multiple of 4
+    const int m0 = blockIdx.x * GR_ROWS + wave * 32;
+    const long ldw = a.ldw > 0 ? a.ldw : (long)a.K * 2;
+    const uint8_t* wrow[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        wrow[j] = reinterpret_cast<const uint8_t*>(a.w) + (long)min(m0 + 16 * j + li, M - 1) * ldw +
+                  16 * g;
+    auto bload = [&](int s, int j) {
+        return ldg_stream(reinterpret_cast<const u32x4*>(wrow[j] + (long)s * 64));
+    };
+    // A item q of this thread: (k step st, tile t, row i, k group gg) of a chunk
+    auto xload = [&](int chunk, int q, f32x4& p0, f32x4& p1) {
+        const int it = (int)threadIdx.x + 256 * q;
+        const int gg = it & 3, ii = (it >> 2) & 15, t = (it >> 6) % NT, st = it / (64 * NT);
+        const int n = t * 16 + ii;
+        const long k = (long)(s0 + 2 * chunk + st) * 32 + 8 * gg;
+        const float* xr = a.x + (long)min(n, N - 1) * a.x_stride_n + k;
+        p0 = *reinterpret_cast<const f32x4*>(xr);
+        p1 = *reinterpret_cast<const f32x4*>(xr + 4);
+        if (n >= N) p0 = p1 = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto xstore = [&](int buf, int q, const f32x4& p0, const f32x4& p1) {
+        const int it = (int)threadIdx.x + 256 * q;
+        const int gg = it & 3, ii = (it >> 2) & 15, t = (it >> 6) % NT, st = it / (64 * NT);
+        u32x4 hi, lo;
+        split8(p0, p1, hi, lo);
+        As[buf][st][t][0][16 * gg + ii] = hi;
+        As[buf][st][t][1][16 * gg + ii] = lo;
+    };
+
+    const int nsteps = s1 - s0;                   // k steps of this split
+    const int nchunks = nsteps / 2;
+    f32x4 xr0[ITEMS], xr1[ITEMS];                 // the next chunk's A items
+#pragma unroll
+    for (int q = 0; q < ITEMS; ++q) xload(0, q, xr0[q], xr1[q]);
+#pragma unroll
+    for (int q = 0; q < ITEMS; ++q) xstore(0, q, xr0[q], xr1[q]);
+#pragma unroll
+    for (int q = 0; q < ITEMS; ++q) xload(min(1, nchunks - 1), q, xr0[q], xr1[q]);
+    u32x4 B[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) B[u][j] = bload(s0 + u, j);
+    __syncthreads();
+
+    f32x4 acc[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // one chunk: stash the next chunk's items, read the one after, then the
+    // MFMAs of k steps 2c, 2c+1 (B slots u0, u0+1)
+    auto chunk_body = [&](int c, int buf, int u0) {
+        if (c + 1 < nchunks) {
+#pragma unroll
+            for (int q = 0; q < ITEMS; ++q) xstore(buf ^ 1, q, xr0[q], xr1[q]);
+        }
+        const int cn = min(c + 2, nchunks - 1);
+#pragma unroll
+        for (int q = 0; q < ITEMS; ++q) xload(cn, q, xr0[q], xr1[q]);
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int u = u0 + st, s = s0 + 2 * c + st;
+            bf16x8 b[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                b[j] = __builtin_bit_cast(bf16x8, B[u][j]);
+                asm volatile("" : "+v"(b[j]));
+                B[u][j] = bload(min(s + 4, s1 - 1), j);       // refill: step s + 4
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const bf16x8 ah = __builtin_bit_cast(bf16x8, As[buf][st][t][0][lane]);
+                const bf16x8 al = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[j], acc[t][j], 0, 0, 0);
+                    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], acc[t][j], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    };
+    // block-uniform trip count: four k steps (two chunks, buffers 0 and 1)
+    for (int c = 0; c < nchunks; c += 2) {
+        chunk_body(c, 0, 0);
+        chunk_body(c + 1, 1, 2);
+    }
+
+    // ---- epilogue: lane (g, li) holds D[4 g + v][li] of tile (t, j)
+    const bool split_out = gridDim.y > 1;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int m = m0 + 16 * j + li;
+            const float vals[4] = {acc[t][j].x, acc[t][j].y, acc[t][j].z, acc[t][j].w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = t * 16 + 4 * g + v;
+                const float val = vals[v];
+                if (split_out) {
+                    if (n < N && m < M) partial[((long)blockIdx.y * N + n) * M + m] = val;
+                } else if (a.epi == EPI_SILU_MUL) {
+                    const float up = __shfl_xor(val, 1, 64);   // rows (2i, 2i+1) = (gate, up)
+                    if ((m & 1) == 0 && n < N && m + 1 < M)
+                        a.y[n * a.y_stride_n + (long)(m >> 1) * a.y_stride_m] =
+                            val / (1.0f + expf(-val)) * up;
+                } else if (n < N && m < M) {
+                    a.y[n * a.y_stride_n + (long)m * a.y_stride_m] = val;
+                }
+            }
+        }
+}
+
+// K splits of a rows launch: enough (row block, split) blocks for two per CU,
+// each split a multiple of four k steps
+static void gemm_rows_split(int M, int K, int& splits, int& steps) {
+    const int bx = (M + GR_ROWS - 1) / GR_ROWS, ksteps = K / 32;
+    int want = (2 * device_cu_count() + bx - 1) / bx;
+    want = std::max(1, std::min(want, ksteps / 4));
+    steps = ((ksteps + want - 1) / want + 3) / 4 * 4;
+    splits = (ksteps + steps - 1) / steps;
+}
+
+bool gemm_rows_ok(const GemvArgs& a) {
+    return a.fmt == WF_BF16 && a.N > 16 && a.N <= GR_MAX_N && a.K % 128 == 0 && a.M > 0 &&
+           a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0 &&
+           ((uintptr_t)a.w & 15) == 0 && (a.ldw == 0 || a.ldw % 16 == 0) &&
+           (a.epi == EPI_STORE || (a.epi == EPI_SILU_MUL && a.M % 2 == 0));
+}
+
+int gemm_rows_reserve(int M, int N, int K) {
+    int splits, steps;
+    gemm_rows_split(M, K, splits, steps);
+    if (splits <= 1) return ATLAS_OK;
+    return ensure_partial((size_t)splits * N * M * sizeof(float));
+}
+
+int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
+    ATLAS_REQUIRE(gemm_rows_ok(a), "gemm rows: unsupported shape (fmt %d, n %d, k %d)", a.fmt, a.N,
+                  a.K);
+    int splits, steps;
+    gemm_rows_split(a.M, a.K, splits, steps);
+    if (splits > 1) {
+        int rc = ensure_partial((size_t)splits * a.N * a.M * sizeof(float));
+        if (rc) return rc;
+    }
+    const dim3 grid((a.M + GR_ROWS - 1) / GR_ROWS, splits);
+    const int nt = (a.N + 15) / 16;
+    if (nt <= 2) hipLaunchKernelGGL(gemm_rows_kernel<2>, grid, dim3(256), 0, st, a, g_partial, steps);
+    else if (nt <= 4) hipLaunchKernelGGL(gemm_rows_kernel<4>, grid, dim3(256), 0, st, a, g_partial, steps);
+    else hipLaunchKernelGGL(gemm_rows_kernel<8>, grid, dim3(256), 0, st, a, g_partial, steps);
+    ATLAS_LAUNCH_CHECK("gemm_rows");
+    if (splits > 1) {
+        const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
+        long rb = ((long)a.N * m_out + 255) / 256;
+        if (rb > 4096) rb = 4096;
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, g_partial,
+                           splits);
+        ATLAS_LAUNCH_CHECK("gemm_rows_reduce");
+    }
+    return ATLAS_OK;
+}
+
 template <int FMT>
 static int launch_skinny_n(const GemvArgs& a, hipStream_t st) {
     return a.N > 8 ? launch_skinny<FMT, 2>(a, st) : launch_skinny<FMT, 1>(a, st);
@@ -583,7 +791,9 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     GemvArgs a = a_in;
     gemv_fill_int4_index(a);
     a.x_vec = a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0;
-    ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16", a.N);
+    if (a.N > 16 && gemm_rows_ok(a)) return gemm_rows_launch(a, st);
+    ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17..128 rows: bf16 weights, "
+                  "K %% 128 == 0)", a.N);
     ATLAS_REQUIRE(a.w && a.x && a.y, "skinny: null pointer");
     ATLAS_REQUIRE(a.fmt == WF_BF16 || a.scales, "skinny: null scales");
     if (a.epi == EPI_SILU_MUL) ATLAS_REQUIRE(a.M % 2 == 0, "skinny: silu-mul needs even rows");

@@ -196,19 +196,23 @@ def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int
     # the prompt: token by token (the reference's loop), then through the
     # multi-row prefill step; the second leaves the state the decode continues
     pre = {}
-    for chunk in (1, 16):
+    # 128-row chunks take the tiled MFMA GEMM (bf16 weights only)
+    for chunk in ((1, 16, 128) if fmt == 1 else (1, 16)):
         m.reset()
         m.set_prefill_chunk(chunk)
-        m.prefill([int(t) for t in prompt[:4]])          # capture the step graphs
+        # capture the step graphs (and, for 128, run the eager chunk once)
+        m.prefill([int(t) for t in prompt[:4 if chunk <= 16 else -1]])
         m.reset()
         t0 = time.perf_counter()
         m.prefill([int(t) for t in prompt[:-1]])
         dt_p = time.perf_counter() - t0
-        pre["token_by_token_s" if chunk == 1 else "chunk16_s"] = round(dt_p, 4)
+        pre["token_by_token_s" if chunk == 1 else f"chunk{chunk}_s"] = round(dt_p, 4)
         log(f"fmt {fmt}: prompt of {len(prompt) - 1} tokens prefilled {chunk} per step in "
             f"{dt_p * 1e3:.1f} ms ({(len(prompt) - 1) / dt_p:.0f} tok/s)")
     pre["tokens"] = len(prompt) - 1
-    pre["chunk16_tok_s"] = round((len(prompt) - 1) / pre["chunk16_s"], 1)
+    for chunk in (16, 128):
+        if f"chunk{chunk}_s" in pre:
+            pre[f"chunk{chunk}_tok_s"] = round((len(prompt) - 1) / pre[f"chunk{chunk}_s"], 1)
     PREFILL[fmt] = pre
     toks = m.decode_greedy(int(prompt[-1]), warmup)
     t0 = time.perf_counter()

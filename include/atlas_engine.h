@@ -130,7 +130,9 @@ int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits
  * token-by-token loop (lib.rs:1612-1618) would.  Extension: the reference
  * feeds one token per forward.                                              */
 int atlas_model_prefill(atlas_model* m, const uint32_t* tokens, int n);
-/* Tokens per prefill step, 1..16 (default 16; 1 = token by token). */
+/* Tokens per prefill step, 1..128 (default 128; 1 = token by token).  Chunks
+ * above 16 need bf16 weights and GEMM inner dims that are multiples of 128
+ * (the tiled MFMA GEMM); other models cap them at 16. */
 int atlas_model_set_prefill_chunk(atlas_model* m, int chunk);
 
 /* generate_with_sampling: resets, feeds the prompt (atlas_model_prefill), then

@@ -250,9 +250,10 @@ def test_ragged_batch_long_context(orc):
 
 
 def test_prefill_chunks_match_token_by_token(orc):
-    # the prompt through the multi-row step (8 tokens per step: multi-row GEMV
-    # for the 2-3 token remainders, MFMA tiles above, per-row causal
-    # attention) leaves the same state as the reference's token-by-token loop:
+    # the prompt through the multi-row step (default chunks of 128 tokens: the
+    # tiled MFMA GEMM above 16 rows, the skinny MFMA kernel for 4-16, the
+    # multi-row GEMV for 2-3, per-row causal attention) leaves the same state
+    # as the reference's token-by-token loop:
     # the next token's logits agree with the oracle and with chunk size 1, for
     # remainders of every size and a prompt that crosses the long-context
     # threshold (512) inside a chunk
