@@ -1133,6 +1133,29 @@ int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool lo
 // (The fused attention kernel writes a row's K/V in the same launch that
 // other rows read; the rows of a ragged batch live in different slots, the
 // rows of a prefill chunk in one.)
+// k >= 2 prompt tokens of the sequence in KV slot `slot` at positions
+// pos0 .. pos0 + k - 1, as one multi-row step without the lm_head
+int prefill_rows(atlas_model* m, int slot, int pos0, const uint32_t* toks, int k) {
+    ATLAS_REQUIRE(k >= 2 && k <= m->R && k <= kPrefillBig, "prefill: %d rows", k);
+    ATLAS_REQUIRE(pos0 + k <= m->cfg.max_seq, "prefill: position %d + %d exceeds max_seq %d", pos0,
+                  k, m->cfg.max_seq);
+    int host[3][kPrefillBig];
+    for (int j = 0; j < k; ++j) {
+        host[0][j] = (int)toks[j];
+        host[1][j] = pos0 + j;
+        host[2][j] = slot;
+    }
+    ATLAS_HIP(hipMemcpyAsync(m->tok_dev, host[0], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipMemcpyAsync(m->pos_dev, host[1], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipMemcpyAsync(m->slot_dev, host[2], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
+    // chunks beyond the captured row counts run eagerly: ~260 launches
+    // queue while the first GEMMs run
+    if (k > kMaxRows) TRY(batch_step(m, k, std::vector<int>(k, slot), true, false));
+    else TRY(run_batch_step(m, k, std::vector<int>(k, slot), true, false));
+    ATLAS_HIP(hipStreamSynchronize(m->st));      // host[] lives on this frame
+    return ATLAS_OK;
+}
+
 int prefill(atlas_model* m, const uint32_t* toks, int n) {
     const int cap = !m->fused ? 1 : m->big_prefill ? kPrefillBig : std::min(m->R, kPrefillChunk);
     const int chunk = std::min(m->prefill_chunk, cap);
@@ -1148,20 +1171,7 @@ int prefill(atlas_model* m, const uint32_t* toks, int n) {
             ++done;
             continue;
         }
-        int host[3][kPrefillBig];
-        for (int j = 0; j < k; ++j) {
-            host[0][j] = (int)toks[done + j];
-            host[1][j] = m->pos + j;
-            host[2][j] = 0;
-        }
-        ATLAS_HIP(hipMemcpyAsync(m->tok_dev, host[0], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
-        ATLAS_HIP(hipMemcpyAsync(m->pos_dev, host[1], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
-        ATLAS_HIP(hipMemcpyAsync(m->slot_dev, host[2], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
-        // chunks beyond the captured row counts run eagerly: ~260 launches
-        // queue while the first GEMMs run
-        if (k > kMaxRows) TRY(batch_step(m, k, std::vector<int>(k, 0), true, false));
-        else TRY(run_batch_step(m, k, std::vector<int>(k, 0), true, false));
-        ATLAS_HIP(hipStreamSynchronize(m->st));      // host[] lives on this frame
+        TRY(prefill_rows(m, 0, m->pos, toks + done, k));
         m->pos += k;
         done += k;
     }
@@ -1934,6 +1944,21 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
     // prefill_chunk rows per sequence).  Such a step takes the two-kernel
     // attention variant, which writes every row's K/V before any row attends.
     const int cap = std::min(kPrefillChunk, m->R);
+    // Long prompts first take the tiled GEMM's big chunks, one sequence at a
+    // time in its own slot, while more than kMaxRows of their tokens before
+    // the last remain; the rest joins the shared steps below.
+    if (m->fused && m->big_prefill && m->prefill_chunk > kMaxRows) {
+        for (int i = 0; i < n_seqs; ++i) {
+            if (done[i]) continue;
+            while (prompt_lens[i] - 1 - cursor[i] > kMaxRows) {
+                const int k = std::min(std::min(m->prefill_chunk, kPrefillBig),
+                                       prompt_lens[i] - 1 - cursor[i]);
+                TRY(prefill_rows(m, i, pos[i], prompts + off[i] + cursor[i], k));
+                cursor[i] += k;
+                pos[i] += k;
+            }
+        }
+    }
     bool any_choice_row = false;
     while (true) {
         int n = 0;
