@@ -150,34 +150,62 @@ __device__ __forceinline__ void scan_update(const float (&q)[G][HD / 16], float 
 
 // Scan cache rows [b0, e1) into the (wave, row) group's state (NG groups per
 // block).  kb/vb: dim 0 of the KV head in row 0, lane_dims: the lane's
-// first dim (lane_dim(dl, 0)).
+// first dim (lane_dim(dl, 0)).  scan_start issues the first step's loads;
+// scan_run scores everything.  A caller can put independent work (the fused
+// kernel's QK-norm/RoPE prep) between them, so that work and the first
+// load's latency overlap.
+template <int HD>
+struct ScanState {
+    static constexpr int P = ScanShape<HD>::P, DPL = HD / 16;
+    ScanBufs b;
+    int t, steps;
+    float ka[P][DPL], va[P][DPL];
+};
+
+template <int HD, int NG>
+__device__ __forceinline__ void scan_start(ScanState<HD>& s, const float* kb, const float* vb,
+                                           long kv_stride, int lane_dims, int b0, int e1,
+                                           int group) {
+    constexpr int S = NG * ScanShape<HD>::P;
+    // Block-uniform trip count and one exit, at the bottom of the loop: with a
+    // divergent or mid-body exit the compiler must assume the other buffer's
+    // loads may still be in flight at the loop head and waits for them there,
+    // serialising the two buffers again.
+    s.steps = __builtin_amdgcn_readfirstlane(e1 > b0 ? (e1 - b0 + S - 1) / S : 0);
+    s.t = b0 + group * ScanShape<HD>::P;
+    if (s.steps == 0) return;
+    s.b = scan_bufs(kb, vb, kv_stride, e1, lane_dims);
+    scan_load<HD>(s.b, s.t, s.ka, s.va);
+}
+
+template <int HD, int G, int NG>
+__device__ __forceinline__ void scan_run(ScanState<HD>& s, int e1, const float (&q)[G][HD / 16],
+                                         float (&m)[G], float (&l)[G], float (&o)[G][HD / 16]) {
+    constexpr int P = ScanShape<HD>::P, DPL = HD / 16, S = NG * P;
+    if (s.steps == 0) return;
+    int t = s.t;
+    float kn[P][DPL], vn[P][DPL];
+    for (int pair = 0; pair < s.steps / 2; ++pair) {
+        scan_load<HD>(s.b, t + S, kn, vn);
+        __builtin_amdgcn_sched_barrier(0);
+        scan_update<HD, G>(q, m, l, o, s.ka, s.va, t, e1);
+        t += S;
+        scan_load<HD>(s.b, t + S, s.ka, s.va);       // past the end: zeros, no traffic
+        __builtin_amdgcn_sched_barrier(0);
+        scan_update<HD, G>(q, m, l, o, kn, vn, t, e1);
+        t += S;
+    }
+    if (s.steps & 1) scan_update<HD, G>(q, m, l, o, s.ka, s.va, t, e1);
+}
+
 template <int HD, int G, int NG>
 __device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long kv_stride,
                                           int lane_dims, int b0, int e1, int group,
                                           const float (&q)[G][HD / 16], float (&m)[G],
                                           float (&l)[G], float (&o)[G][HD / 16]) {
-    constexpr int P = ScanShape<HD>::P, DPL = HD / 16, S = NG * P;
-    // Block-uniform trip count and one exit, at the bottom of the loop: with a
-    // divergent or mid-body exit the compiler must assume the other buffer's
-    // loads may still be in flight at the loop head and waits for them there,
-    // serialising the two buffers again.
-    const int steps = __builtin_amdgcn_readfirstlane(e1 > b0 ? (e1 - b0 + S - 1) / S : 0);
-    if (steps == 0) return;
-    const ScanBufs b = scan_bufs(kb, vb, kv_stride, e1, lane_dims);
-    int t = b0 + group * P;
-    float ka[P][DPL], va[P][DPL], kn[P][DPL], vn[P][DPL];
-    scan_load<HD>(b, t, ka, va);
-    for (int pair = 0; pair < steps / 2; ++pair) {
-        scan_load<HD>(b, t + S, kn, vn);
-        __builtin_amdgcn_sched_barrier(0);
-        scan_update<HD, G>(q, m, l, o, ka, va, t, e1);
-        t += S;
-        scan_load<HD>(b, t + S, ka, va);       // past the end: zeros, no traffic
-        __builtin_amdgcn_sched_barrier(0);
-        scan_update<HD, G>(q, m, l, o, kn, vn, t, e1);
-        t += S;
-    }
-    if (steps & 1) scan_update<HD, G>(q, m, l, o, ka, va, t, e1);
+    ScanState<HD> s;
+    scan_start<HD, NG>(s, kb, vb, kv_stride, lane_dims, b0, e1, group);
+    scan_run<HD, G, NG>(s, e1, q, m, l, o);
 }
 
 template <int HD, int G, int W>
@@ -202,6 +230,11 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     const int b1 = min(pos + 1, b0 + chunk);
     const long kv_stride = (long)a.n_kv * HD;
     const float sc = a.scale * LOG2E;
+    // the scan's first K/V step goes out before q's loads
+    ScanState<HD> scan;
+    scan_start<HD, 4 * W>(scan, a.k_cache + cache0 + (long)kvh * HD, a.v_cache + cache0 + (long)kvh * HD,
+                          kv_stride, lane_dim(dl, 0), b0, b1, wave * 4 + row);
+    __builtin_amdgcn_sched_barrier(0);
 
     // q for the G heads of this group, this lane's dims
     float q[G][DPL];
@@ -222,8 +255,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    attn_scan<HD, G, 4 * W>(a.k_cache + cache0 + (long)kvh * HD, a.v_cache + cache0 + (long)kvh * HD,
-                            kv_stride, lane_dim(dl, 0), b0, b1, wave * 4 + row, q, m, l, o);
+    scan_run<HD, G, 4 * W>(scan, b1, q, m, l, o);
 
     // ---- merge the 16 (wave,row) states of this block through LDS ---------
     __shared__ float s_m[4 * W][G], s_l[4 * W][G];
@@ -398,6 +430,13 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     float* kc = a.k_cache + (long)slot * a.slot_stride;
     float* vc = a.v_cache + (long)slot * a.slot_stride;
 
+    // the first step of the history scan (rows < pos, untouched by this
+    // launch) goes out before the prep, whose latency it then overlaps
+    ScanState<HD> scan;
+    scan_start<HD, 4 * W>(scan, kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, lane_dim(dl, 0),
+                          b0, e1, wave * 4 + row);
+    __builtin_amdgcn_sched_barrier(0);
+
     __shared__ float sq[G][HD], sk[HD], sv[HD];
     // ---- prep: QK-norm + RoPE of the G q heads and k, wave per vector -----
     const float* cr = a.cos_tab + (long)pos * (HD / 2);
@@ -463,8 +502,7 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    attn_scan<HD, G, 4 * W>(kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, lane_dim(dl, 0), b0,
-                            e1, wave * 4 + row, q, m, l, o);
+    scan_run<HD, G, 4 * W>(scan, e1, q, m, l, o);
     if (owner && wave == 0 && row == 0) {
         // position pos from LDS (the 16 lanes of row 0 of wave 0)
         constexpr int P = ScanShape<HD>::P;
