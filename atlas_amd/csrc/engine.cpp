@@ -46,8 +46,8 @@ constexpr int kLongAttnFrom = 512;
 // multi-row GEMV for 2-3 rows, the skinny MFMA kernel for 4-16.
 constexpr int kPrefillChunk = 16;
 constexpr int kMaxRows = kPrefillChunk;
-// Prompt chunks of bf16 models whose GEMM inner dims are multiples of 128
-// go through the tiled MFMA GEMM (gemm_rows_launch), up to this many rows
+// Prompt chunks of models whose GEMM inner dims are multiples of 128 go
+// through the tiled MFMA GEMM (gemm_rows_launch), up to this many rows
 // per step, replayed eagerly (the captured steps stop at kMaxRows rows).
 constexpr int kPrefillBig = 128;
 
@@ -1220,10 +1220,11 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->kvd = c.n_kv_heads * hd;
     m->qkv_rows = c.d_model + 2 * m->kvd;
     m->B = c.max_batch < 1 ? 1 : c.max_batch;
-    // big prompt chunks: bf16 weights, the fused (post-norm) step, and every
-    // GEMM inner dimension (d_model, n_heads * head_dim, ffn_hidden) a
-    // multiple of the tiled GEMM's 128
-    m->big_prefill = fmt == WF_BF16 && c.post_norm &&
+    // big prompt chunks: the fused (post-norm) step, every GEMM inner
+    // dimension (d_model, n_heads * head_dim, ffn_hidden) a multiple of the
+    // tiled GEMM's 128, and int4 blocks of 32 * 2^j
+    const int i4_cpb = fmt == WF_I4 && c.int4_block > 0 ? c.int4_block / 32 : 1;
+    m->big_prefill = (i4_cpb & (i4_cpb - 1)) == 0 && c.post_norm &&
                      attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
                      attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && c.d_model % 128 == 0 &&
                      (c.n_heads * hd) % 128 == 0 && c.ffn_hidden % 128 == 0;

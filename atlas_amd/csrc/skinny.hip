@@ -574,7 +574,9 @@ static int launch_skinny(const GemvArgs& a, hipStream_t st) {
 
 // ---------------------------------------------------------------------------
 // Prompt chunks: Y[n, m] = sum_k W[m, k] X[n, k] for 17 <= N <= 128 rows of
-// bf16 weights.  Same operand roles and hi/lo split as skinny_kernel, but
+// bf16, int8 or int4 weights (dequantised to exact bf16 operands as in
+// skinny_kernel: int8 row scales in the epilogue, int4 block scales on each
+// 32-k step's product).  Same operand roles and hi/lo split as skinny_kernel, but
 // every A fragment now feeds many weight tiles, so the matrix cores do the
 // work and the weights stream once per chunk:
 //  * a 256-thread block owns 128 weight rows (wave w: rows 32 w .. +31, two
@@ -604,9 +606,9 @@ __device__ __forceinline__ void split8(const f32x4 p0, const f32x4 p1, u32x4& hi
     lo = u32x4{pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])};
 }
 
-template <int NT>
+template <int FMT, int NT>
 __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __restrict__ partial,
-                                                           int steps_per_split) {
+                                                           int steps_per_split, int cpb_shift) {
     constexpr int ITEMS = 2 * NT * 64 / 256;      // A items (8 floats) per thread per chunk
     __shared__ u32x4 As[2][2][NT][2][64];         // [buf][k step][tile][hi/lo][lane]
     const int lane = threadIdx.x & 63;
@@ -616,15 +618,9 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
     const int s0 = blockIdx.y * steps_per_split;
     const int s1 = min(a.K / 32, s0 + steps_per_split);   // s1 - s0: a multiple of 4
     const int m0 = blockIdx.x * GR_ROWS + wave * 32;
-    const long ldw = a.ldw > 0 ? a.ldw : (long)a.K * 2;
-    const uint8_t* wrow[2];
+    SkRow wrow[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-        wrow[j] = reinterpret_cast<const uint8_t*>(a.w) + (long)min(m0 + 16 * j + li, M - 1) * ldw +
-                  16 * g;
-    auto bload = [&](int s, int j) {
-        return ldg_stream(reinterpret_cast<const u32x4*>(wrow[j] + (long)s * 64));
-    };
+    for (int j = 0; j < 2; ++j) wrow[j] = sk_row<FMT>(a, min(m0 + 16 * j + li, M - 1));
     // A item q of this thread: (k step st, tile t, row i, k group gg) of a chunk
     auto xload = [&](int chunk, int q, f32x4& p0, f32x4& p1) {
         const int it = (int)threadIdx.x + 256 * q;
@@ -654,11 +650,11 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
     for (int q = 0; q < ITEMS; ++q) xstore(0, q, xr0[q], xr1[q]);
 #pragma unroll
     for (int q = 0; q < ITEMS; ++q) xload(min(1, nchunks - 1), q, xr0[q], xr1[q]);
-    u32x4 B[4][2];
+    SkFrag<FMT> B[4][2];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) B[u][j] = bload(s0 + u, j);
+        for (int j = 0; j < 2; ++j) sk_load<FMT>(wrow[j], s0 + u, g, cpb_shift, B[u][j]);
     __syncthreads();
 
     f32x4 acc[NT][2];
@@ -681,11 +677,14 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
         for (int st = 0; st < 2; ++st) {
             const int u = u0 + st, s = s0 + 2 * c + st;
             bf16x8 b[2];
+            float sc[2] = {1.0f, 1.0f};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                b[j] = __builtin_bit_cast(bf16x8, B[u][j]);
-                asm volatile("" : "+v"(b[j]));
-                B[u][j] = bload(min(s + 4, s1 - 1), j);       // refill: step s + 4
+                b[j] = sk_operand<FMT>(B[u][j]);
+                if constexpr (FMT == WF_BF16) asm volatile("" : "+v"(b[j]));
+                if constexpr (FMT == WF_I4) sc[j] = B[u][j].s;
+                // refill: step s + 4
+                sk_load<FMT>(wrow[j], min(s + 4, s1 - 1), g, cpb_shift, B[u][j]);
             }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -693,8 +692,16 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
                 const bf16x8 al = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane]);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[j], acc[t][j], 0, 0, 0);
-                    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], acc[t][j], 0, 0, 0);
+                    if constexpr (FMT == WF_I4) {
+                        // the step is one scale block of the lane's row
+                        f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            ah, b[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], d, 0, 0, 0);
+                        acc[t][j] += d * sc[j];
+                    } else {
+                        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[j], acc[t][j], 0, 0, 0);
+                        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], acc[t][j], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -713,7 +720,10 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int m = m0 + 16 * j + li;
-            const float vals[4] = {acc[t][j].x, acc[t][j].y, acc[t][j].z, acc[t][j].w};
+            float rs = 1.0f;                                   // int8 row scale
+            if constexpr (FMT == WF_I8) rs = a.scales[min(m, M - 1)];
+            const float vals[4] = {acc[t][j].x * rs, acc[t][j].y * rs, acc[t][j].z * rs,
+                                   acc[t][j].w * rs};
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int n = t * 16 + 4 * g + v;
@@ -742,11 +752,29 @@ static void gemm_rows_split(int M, int K, int& splits, int& steps) {
     splits = (ksteps + steps - 1) / steps;
 }
 
+// a: after gemv_fill_int4_index (int4 bpr / cpb)
 bool gemm_rows_ok(const GemvArgs& a) {
-    return a.fmt == WF_BF16 && a.N > 16 && a.N <= GR_MAX_N && a.K % 128 == 0 && a.M > 0 &&
+    const uintptr_t wa = (uintptr_t)a.w;
+    const bool fmt_ok =
+        a.fmt == WF_BF16 ? (wa & 15) == 0 && (a.ldw == 0 || a.ldw % 16 == 0)
+        : a.fmt == WF_I8 ? a.scales && (wa & 7) == 0 && (a.ldw == 0 || a.ldw % 8 == 0)
+        : a.fmt == WF_I4 ? a.scales && (wa & 3) == 0 && a.ldw == 0 && a.block % 32 == 0 &&
+                               a.bpr > 0 && (a.cpb & (a.cpb - 1)) == 0
+                         : false;
+    return fmt_ok && a.N > 16 && a.N <= GR_MAX_N && a.K % 128 == 0 && a.M > 0 &&
            a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0 &&
-           ((uintptr_t)a.w & 15) == 0 && (a.ldw == 0 || a.ldw % 16 == 0) &&
            (a.epi == EPI_STORE || (a.epi == EPI_SILU_MUL && a.M % 2 == 0));
+}
+
+template <int FMT>
+static void gemm_rows_go(const GemvArgs& a, dim3 grid, int steps, int cpb_shift, hipStream_t st) {
+    const int nt = (a.N + 15) / 16;
+    if (nt <= 2)
+        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 2>), grid, dim3(256), 0, st, a, g_partial, steps, cpb_shift);
+    else if (nt <= 4)
+        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 4>), grid, dim3(256), 0, st, a, g_partial, steps, cpb_shift);
+    else if constexpr (FMT != WF_I4)
+        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 8>), grid, dim3(256), 0, st, a, g_partial, steps, cpb_shift);
 }
 
 int gemm_rows_reserve(int M, int N, int K) {
@@ -756,9 +784,8 @@ int gemm_rows_reserve(int M, int N, int K) {
     return ensure_partial((size_t)splits * N * M * sizeof(float));
 }
 
-int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
-    ATLAS_REQUIRE(gemm_rows_ok(a), "gemm rows: unsupported shape (fmt %d, n %d, k %d)", a.fmt, a.N,
-                  a.K);
+// one launch (+ split-K reduce) over all a.N <= 128 rows
+static int gemm_rows_part(const GemvArgs& a, hipStream_t st) {
     int splits, steps;
     gemm_rows_split(a.M, a.K, splits, steps);
     if (splits > 1) {
@@ -766,10 +793,11 @@ int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
         if (rc) return rc;
     }
     const dim3 grid((a.M + GR_ROWS - 1) / GR_ROWS, splits);
-    const int nt = (a.N + 15) / 16;
-    if (nt <= 2) hipLaunchKernelGGL(gemm_rows_kernel<2>, grid, dim3(256), 0, st, a, g_partial, steps);
-    else if (nt <= 4) hipLaunchKernelGGL(gemm_rows_kernel<4>, grid, dim3(256), 0, st, a, g_partial, steps);
-    else hipLaunchKernelGGL(gemm_rows_kernel<8>, grid, dim3(256), 0, st, a, g_partial, steps);
+    int cpb_shift = 0;
+    while ((1 << cpb_shift) < a.cpb) ++cpb_shift;
+    if (a.fmt == WF_BF16) gemm_rows_go<WF_BF16>(a, grid, steps, cpb_shift, st);
+    else if (a.fmt == WF_I8) gemm_rows_go<WF_I8>(a, grid, steps, cpb_shift, st);
+    else gemm_rows_go<WF_I4>(a, grid, steps, cpb_shift, st);
     ATLAS_LAUNCH_CHECK("gemm_rows");
     if (splits > 1) {
         const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
@@ -778,6 +806,24 @@ int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
         hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, g_partial,
                            splits);
         ATLAS_LAUNCH_CHECK("gemm_rows_reduce");
+    }
+    return ATLAS_OK;
+}
+
+int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
+    ATLAS_REQUIRE(gemm_rows_ok(a), "gemm rows: unsupported shape (fmt %d, n %d, k %d)", a.fmt, a.N,
+                  a.K);
+    // int4 keeps at most four 16-row tiles per launch: its per-step scaled
+    // products need more registers than eight tiles leave (the weights then
+    // stream twice per 128-row chunk, at a quarter of bf16's bytes)
+    const int cap = a.fmt == WF_I4 ? 64 : GR_MAX_N;
+    for (int n0 = 0; n0 < a.N; n0 += cap) {
+        GemvArgs p = a;
+        p.N = std::min(cap, a.N - n0);
+        p.x = a.x + (long)n0 * a.x_stride_n;
+        p.y = a.y + (long)n0 * a.y_stride_n;
+        int rc = gemm_rows_part(p, st);
+        if (rc) return rc;
     }
     return ATLAS_OK;
 }
@@ -792,8 +838,8 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     gemv_fill_int4_index(a);
     a.x_vec = a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0;
     if (a.N > 16 && gemm_rows_ok(a)) return gemm_rows_launch(a, st);
-    ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17..128 rows: bf16 weights, "
-                  "K %% 128 == 0)", a.N);
+    ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17..128 rows need K %% 128 == 0 "
+                  "and, for int4, blocks of 32 * 2^j)", a.N);
     ATLAS_REQUIRE(a.w && a.x && a.y, "skinny: null pointer");
     ATLAS_REQUIRE(a.fmt == WF_BF16 || a.scales, "skinny: null scales");
     if (a.epi == EPI_SILU_MUL) ATLAS_REQUIRE(a.M % 2 == 0, "skinny: silu-mul needs even rows");

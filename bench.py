@@ -196,8 +196,8 @@ def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int
     # the prompt: token by token (the reference's loop), then through the
     # multi-row prefill step; the second leaves the state the decode continues
     pre = {}
-    # 128-row chunks take the tiled MFMA GEMM (bf16 weights only)
-    for chunk in ((1, 16, 128) if fmt == 1 else (1, 16)):
+    # 128-row chunks take the tiled MFMA GEMM
+    for chunk in (1, 16, 128):
         m.reset()
         m.set_prefill_chunk(chunk)
         # capture the step graphs (and, for 128, run the eager chunk once)

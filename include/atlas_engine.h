@@ -131,8 +131,8 @@ int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits
  * feeds one token per forward.                                              */
 int atlas_model_prefill(atlas_model* m, const uint32_t* tokens, int n);
 /* Tokens per prefill step, 1..128 (default 128; 1 = token by token).  Chunks
- * above 16 need bf16 weights and GEMM inner dims that are multiples of 128
- * (the tiled MFMA GEMM); other models cap them at 16. */
+ * above 16 need GEMM inner dims that are multiples of 128 and, for int4,
+ * blocks of 32 * 2^j (the tiled MFMA GEMM); other models cap them at 16. */
 int atlas_model_set_prefill_chunk(atlas_model* m, int chunk);
 
 /* generate_with_sampling: resets, feeds the prompt (atlas_model_prefill), then

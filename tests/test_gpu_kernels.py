@@ -162,16 +162,20 @@ def test_skinny_two_a_tiles(orc, fmt, n, M, K):
     _skinny_check(orc, fmt, n, M, K, 32, seed=3)
 
 
-# 17-128 rows of bf16 weights: the tiled MFMA GEMM of prompt chunks.  Cases:
-# one and eight 16-row tiles with a ragged last tile, K split across blocks
-# (K = 11008: 344 k steps) and unsplit (70 000 rows fill the grid), rows not
-# a multiple of the 128-row block.
-@pytest.mark.parametrize("n,M,K", [
-    (17, 1000, 512), (32, 4096, 4096), (61, 777, 11008), (100, 2048, 1024), (128, 4096, 4096),
-    (40, 70000, 128), (128, 130, 256)])
-def test_gemm_rows(orc, n, M, K):
-    print(f"gemm rows bf16 n={n} M={M} K={K}", flush=True)
-    _skinny_check(orc, "bf16", n, M, K, 32, seed=5)
+# 17-128 rows: the tiled MFMA GEMM of prompt chunks.  Cases: one and eight
+# 16-row tiles with a ragged last tile, K split across blocks (K = 11008: 344
+# k steps) and unsplit (70 000 rows fill the grid), rows not a multiple of
+# the 128-row block; int8 row scales, int4 blocks of 32 and 128.
+@pytest.mark.parametrize("fmt,n,M,K,block", [
+    ("bf16", 17, 1000, 512, 32), ("bf16", 32, 4096, 4096, 32), ("bf16", 61, 777, 11008, 32),
+    ("bf16", 100, 2048, 1024, 32), ("bf16", 128, 4096, 4096, 32), ("bf16", 40, 70000, 128, 32),
+    ("bf16", 128, 130, 256, 32),
+    ("int8", 17, 1000, 512, 32), ("int8", 128, 4096, 4096, 32), ("int8", 70, 777, 11008, 32),
+    ("int4", 20, 1000, 512, 32), ("int4", 128, 4096, 4096, 32), ("int4", 90, 777, 11008, 32),
+    ("int4", 48, 2048, 1024, 128)])
+def test_gemm_rows(orc, fmt, n, M, K, block):
+    print(f"gemm rows {fmt} n={n} M={M} K={K} block={block}", flush=True)
+    _skinny_check(orc, fmt, n, M, K, block, seed=5)
 
 
 # Two and three rows take the multi-row GEMV: the 7B shapes (three rows of
