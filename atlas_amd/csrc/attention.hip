@@ -739,6 +739,153 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
     return ATLAS_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Prompt chunk attention: n query rows of ONE sequence at consecutive
+// positions pos_dev[0] .. + n - 1, all in cache slot slot_dev[0], whose K/V
+// rows are already in the cache (the QK-norm / RoPE / KV-write kernel ran).
+// Row j attends to positions [t_lo(p_j), p_j] with the reference's causal and
+// sliding-window rule (crates/atlas-model/src/lib.rs:689-721): the same
+// online softmax as attn_scan, but a block of 16 rows shares every K/V tile
+// (32 positions staged once in LDS), so the history is read once per 16 rows
+// instead of once per row.  Grid (n_heads, ceil(n / 16)), 16 waves: wave w
+// serves rows 16-lane group by group (w % 4: four rows) over the tile
+// positions 8 (w / 4) .. + 7; the four partial states of a row meet in LDS at
+// the end.  (With one 4-wave block per CU the dependent DPP / exp chains had
+// nothing to hide behind: 166 us per launch at 2047-token prompts.)
+constexpr int APF_ROWS = 16, APF_TK = 32, APF_KS = 4;
+
+__global__ __launch_bounds__(1024) void attn_prefill_kernel(AttnArgs a, int n) {
+    constexpr int HD = 128, DPL = HD / 16, PPS = APF_TK / APF_KS;   // positions per split
+    constexpr float LOG2E = 1.4426950408889634f;
+    __shared__ f32x4 tk[APF_TK][HD / 4], tv[APF_TK][HD / 4];
+    __shared__ float s_m[APF_KS][APF_ROWS], s_l[APF_KS][APF_ROWS];
+    __shared__ float s_o[APF_KS][APF_ROWS][HD];
+    const int qh = blockIdx.x, G = a.n_heads / a.n_kv, kvh = qh / G;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int dl = lane & 15, gi = (wave & 3) * 4 + (lane >> 4), ks = wave >> 2;
+    const int p0 = a.pos_dev[0];
+    const long kv_stride = (long)a.n_kv * HD;
+    const float* kb = a.k_cache + (long)a.slot_dev[0] * a.slot_stride + (long)kvh * HD;
+    const float* vb = a.v_cache + (long)a.slot_dev[0] * a.slot_stride + (long)kvh * HD;
+    const int r0 = blockIdx.y * APF_ROWS;
+    const int j = r0 + gi;                                      // this group's row
+    const int pj = p0 + min(j, n - 1);
+    const int loj = (a.window > 0 && pj >= a.window) ? pj - a.window + 1 : 0;
+    // the block's position range: the first row's window start .. its last row
+    const int pf = p0 + r0, pl = p0 + min(r0 + APF_ROWS, n) - 1;
+    const int lo_b = (a.window > 0 && pf >= a.window) ? pf - a.window + 1 : 0;
+    const int ntiles = (pl - lo_b) / APF_TK + 1;
+
+    // q of this row, scaled into exp2 space
+    float q[DPL];
+    {
+        const float* qr = a.q + (long)min(j, n - 1) * a.q_stride + (long)qh * HD;
+        const float sc = a.scale * LOG2E;
+#pragma unroll
+        for (int d = 0; d < DPL; d += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(qr + lane_dim(dl, d));
+            q[d] = v.x * sc; q[d + 1] = v.y * sc; q[d + 2] = v.z * sc; q[d + 3] = v.w * sc;
+        }
+    }
+    // tile loads: 2 x 32 rows x 32 pieces = 2048 pieces, 2 per thread
+    f32x4 pre[2];
+    auto fetch = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = (int)threadIdx.x + 1024 * i;
+            const int r = (idx >> 5) & (APF_TK - 1), c = idx & 31;
+            const long row = min(t0 + r, pl);                   // rows past pl: masked
+            pre[i] = *reinterpret_cast<const f32x4*>((i == 0 ? kb : vb) + row * kv_stride + 4 * c);
+        }
+    };
+    auto stash = [&]() {
+        const int r = ((int)threadIdx.x >> 5) & (APF_TK - 1), c = threadIdx.x & 31;
+        tk[r][c] = pre[0];
+        tv[r][c] = pre[1];
+    };
+    float m = -INFINITY, l = 0.f, o[DPL];
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[d] = 0.f;
+    fetch(lo_b);
+    stash();
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {            // block-uniform trip count
+        const int t0 = lo_b + it * APF_TK;
+        if (it + 1 < ntiles) fetch(t0 + APF_TK);
+#pragma unroll
+        for (int s2 = ks * PPS; s2 < ks * PPS + PPS; s2 += 2) {
+            float sv[2], vf[2][DPL];
+            float smax = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int t = t0 + s2 + i;
+                const f32x4 k0 = tk[s2 + i][dl], k1 = tk[s2 + i][16 + dl];
+                const f32x4 v0 = tv[s2 + i][dl], v1 = tv[s2 + i][16 + dl];
+                float acc = q[0] * k0.x;
+                acc += q[1] * k0.y; acc += q[2] * k0.z; acc += q[3] * k0.w;
+                acc += q[4] * k1.x; acc += q[5] * k1.y; acc += q[6] * k1.z; acc += q[7] * k1.w;
+                acc = row16_sum(acc);
+                sv[i] = (t >= loj && t <= pj) ? acc : -INFINITY;
+                smax = fmaxf(smax, sv[i]);
+                vf[i][0] = v0.x; vf[i][1] = v0.y; vf[i][2] = v0.z; vf[i][3] = v0.w;
+                vf[i][4] = v1.x; vf[i][5] = v1.y; vf[i][6] = v1.z; vf[i][7] = v1.w;
+            }
+            if (smax != -INFINITY) {
+                const float mn = fmaxf(m, smax);
+                const float corr = m == -INFINITY ? 0.f : exp2f(m - mn);
+                const float e0 = sv[0] == -INFINITY ? 0.f : exp2f(sv[0] - mn);
+                const float e1 = sv[1] == -INFINITY ? 0.f : exp2f(sv[1] - mn);
+                l = l * corr + e0 + e1;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) o[d] = o[d] * corr + e0 * vf[0][d] + e1 * vf[1][d];
+                m = mn;
+            }
+        }
+        __syncthreads();
+        if (it + 1 < ntiles) {
+            stash();
+            __syncthreads();
+        }
+    }
+    // ---- merge the four key splits of each row
+    if (dl == 0) { s_m[ks][gi] = m; s_l[ks][gi] = l; }
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) s_o[ks][gi][lane_dim(dl, d)] = o[d];
+    __syncthreads();
+    for (int e = threadIdx.x; e < APF_ROWS * HD; e += 1024) {
+        const int r = e / HD, d = e % HD, jr = r0 + r;
+        if (jr >= n) continue;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k2 = 0; k2 < APF_KS; ++k2) mx = fmaxf(mx, s_m[k2][r]);
+        float lsum = 0.f, osum = 0.f;
+#pragma unroll
+        for (int k2 = 0; k2 < APF_KS; ++k2) {
+            const float w = s_m[k2][r] == -INFINITY ? 0.f : exp2f(s_m[k2][r] - mx);
+            lsum += s_l[k2][r] * w;
+            osum += s_o[k2][r][d] * w;
+        }
+        a.out[(long)jr * a.out_stride + (long)qh * HD + d] = osum / lsum;
+    }
+}
+
+bool attn_prefill_ok(const AttnArgs& a) {
+    const uintptr_t al = (uintptr_t)a.q | (uintptr_t)a.k_cache | (uintptr_t)a.v_cache |
+                         (uintptr_t)a.out;
+    return a.head_dim == 128 && a.n_kv > 0 && a.n_heads % a.n_kv == 0 && (al & 15) == 0 &&
+           a.q_stride % 4 == 0 && a.out_stride % 4 == 0 && a.slot_stride % 4 == 0 &&
+           a.pos_dev && a.slot_dev && attn_rows_fit(a.max_rows, a.n_kv, a.head_dim);
+}
+
+int attn_prefill_launch(const AttnArgs& a, int n, hipStream_t st) {
+    ATLAS_REQUIRE(attn_prefill_ok(a) && n >= 1, "attention: prompt-chunk kernel needs head_dim 128, "
+                  "16-byte alignment and device positions/slot (n %d)", n);
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.n_heads, (n + APF_ROWS - 1) / APF_ROWS), dim3(1024),
+                       0, st, a, n);
+    ATLAS_LAUNCH_CHECK("attn_prefill");
+    return ATLAS_OK;
+}
+
 int attn_batch_launch(const AttnArgs& a, int n_splits, int n_seq, hipStream_t st) {
     ATLAS_REQUIRE(attn_fused_supported(a.n_heads, a.n_kv, a.head_dim),
                   "attention: batch path needs head_dim 64/128/256 and group 1/2/4/8");

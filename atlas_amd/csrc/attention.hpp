@@ -107,5 +107,10 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st);
 // n_seq) and split merge, no generic fallback; partials are the caller's,
 // [n_seq][n_heads][n_splits] (+ head_dim for part_o)
 int attn_batch_launch(const AttnArgs& a, int n_splits, int n_seq, hipStream_t st);
+// n prompt rows of one sequence at consecutive positions pos_dev[0].. in slot
+// slot_dev[0] (q rows q_stride apart, out rows out_stride apart), K/V already
+// written: query-tiled causal attention, head_dim 128
+bool attn_prefill_ok(const AttnArgs& a);
+int attn_prefill_launch(const AttnArgs& a, int n, hipStream_t st);
 
 }  // namespace atlas

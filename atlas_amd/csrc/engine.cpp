@@ -1031,7 +1031,10 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
                                          : attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
             const size_t np = (size_t)n * c.n_heads * sp;
             a.part_m = m->attn_part; a.part_l = m->attn_part + np; a.part_o = m->attn_part + 2 * np;
-            TRY(attn_batch_launch(a, sp, n, m->st));
+            // a prompt chunk (one sequence, consecutive positions, one slot):
+            // 16 rows share each K/V tile
+            if (!with_head && attn_prefill_ok(a)) TRY(attn_prefill_launch(a, n, m->st));
+            else TRY(attn_batch_launch(a, sp, n, m->st));
         } else if (m->fused) {
             // one launch: every sequence's QK-norm/RoPE/KV write and attention
             AttnFusedArgs a{};

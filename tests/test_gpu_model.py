@@ -289,6 +289,29 @@ def test_prefill_chunks_match_token_by_token(orc):
         assert _top2_margin(lg) <= 2 * LOGIT_TOL * np.max(np.abs(lg)), k
 
 
+def test_prefill_chunks_head_dim_128(orc):
+    # head_dim 128 takes the query-tiled prompt attention (16 rows per K/V
+    # tile): chunks of 128 with sliding-window layers (window 16 < chunk),
+    # ragged last row blocks and a later chunk that starts mid-window; the
+    # next token's logits agree with the oracle
+    cfg = modelgen.olmo3_small_config(n_heads=2, n_kv_heads=2, max_seq=320)
+    W = modelgen.make_weights(cfg, seed=73)
+    toks = [int(t) for t in np.random.default_rng(14).integers(0, cfg["vocab"], 300)]
+    m = modelgen.engine_model(W)
+    o = modelgen.oracle_model(W, threads=8)
+    ref = {}
+    o.reset()
+    for i, t in enumerate(toks):
+        lg = o.forward_one(t)
+        if i + 1 in (20, 129, 150, 300):
+            ref[i + 1] = lg
+    for n, r in ref.items():
+        print(f"prefill hd128: {n - 1} prompt tokens", flush=True)
+        m.reset()
+        m.prefill(toks[:n - 1])
+        assert _rel(m.forward_one(toks[n - 1]), r) <= LOGIT_TOL, n
+
+
 def test_long_context_attention_path(orc):
     # positions >= from_pos replay the long-context step (QK-norm/RoPE/KV-write
     # kernel, adaptive split kernel, split merge); forcing it from position 8
