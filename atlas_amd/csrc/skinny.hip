@@ -742,11 +742,13 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
         }
 }
 
-// K splits of a rows launch: enough (row block, split) blocks for two per CU,
-// each split a multiple of four k steps
+// K splits of a rows launch: enough (row block, split) blocks for one per
+// CU, each split a multiple of four k steps.  (Two per CU, the occupancy
+// limit, measured 3% slower over the 7B GEMMs at 128 rows and 8% at 64:
+// the extra partials and reduce cost more than the second block gains.)
 static void gemm_rows_split(int M, int K, int& splits, int& steps) {
     const int bx = (M + GR_ROWS - 1) / GR_ROWS, ksteps = K / 32;
-    int want = (2 * device_cu_count() + bx - 1) / bx;
+    int want = (device_cu_count() + bx - 1) / bx;
     want = std::max(1, std::min(want, ksteps / 4));
     steps = ((ksteps + want - 1) / want + 3) / 4 * 4;
     splits = (ksteps + steps - 1) / steps;
