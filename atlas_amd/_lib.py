@@ -97,6 +97,7 @@ SIGNATURES = {
     "atlas_gemv_swiglu_f32": (I, [I, P, P, I, P, P, I, I]),
     "atlas_gemv_fused_f32": (I, [I, P, P, I, P, P, I, I, I, P, P, F, P]),
     "atlas_gemm_skinny_f32": (I, [I, P, P, I, P, P, I, I, I]),
+    "atlas_gemm_skinny_swiglu_f32": (I, [I, P, P, I, P, P, I, I, I]),
     "atlas_rmsnorm_rows_f32": (I, [P, P, P, I, I, F]),
     "atlas_residual_rmsnorm_f32": (I, [P, P, P, I, I, F]),
     "atlas_qkv_post_f32": (I, [P, P, P, F, P, P, P, P, I, I, I, I]),

@@ -651,23 +651,6 @@ int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream
 
 // ---------------------------------------------------------------------------
 
-static float* g_part = nullptr;
-static size_t g_part_bytes = 0;
-
-int attn_reserve(int n_heads, int head_dim, int n_splits) {
-    const size_t need = (size_t)n_heads * n_splits * (head_dim + 2) * sizeof(float);
-    if (need <= g_part_bytes) return ATLAS_OK;
-    if (g_part) {
-        ATLAS_HIP(hipDeviceSynchronize());
-        ATLAS_HIP(hipFree(g_part));
-        g_part = nullptr;
-        g_part_bytes = 0;
-    }
-    ATLAS_HIP(hipMalloc((void**)&g_part, need));
-    g_part_bytes = need;
-    return ATLAS_OK;
-}
-
 int attn_max_splits(int n_kv) {
     // Measured on MI355X (7B shapes, ctx 64..8192): the merge's device-scope
     // release (an L2 write-back per block) makes grids beyond ~128 blocks
@@ -721,11 +704,15 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
     if (n_splits < 1) n_splits = 1;
     if (n_splits > kAttnMaxSplits) n_splits = kAttnMaxSplits;
     if (n_splits > 1 && !a.part_m) {
-        int rc = attn_reserve(a.n_heads, a.head_dim, n_splits);
+        // the calling thread's scratch (no model owns this call)
+        void* p = nullptr;
+        const size_t need = (size_t)a.n_heads * n_splits * (a.head_dim + 2) * sizeof(float);
+        int rc = thread_scratch(SCR_ATTN, need, &p);
         if (rc) return rc;
-        a.part_m = g_part;
-        a.part_l = g_part + (size_t)a.n_heads * n_splits;
-        a.part_o = g_part + (size_t)2 * a.n_heads * n_splits;
+        float* part = static_cast<float*>(p);
+        a.part_m = part;
+        a.part_l = part + (size_t)a.n_heads * n_splits;
+        a.part_o = part + (size_t)2 * a.n_heads * n_splits;
     }
     ATLAS_REQUIRE(n_splits == 1 || (a.part_l && a.part_o), "attention: partial buffers missing");
 #define ATLAS_ATTN_CASE(HDV, GV) \

@@ -14,7 +14,7 @@ struct AttnArgs {
     const int* pos_dev;      // device-resident position (graph replay)
     float scale;
     int window;              // 0 = full attention
-    float* part_m;           // split partials: the caller's, or null for library scratch
+    float* part_m;           // split partials: the caller's, or null for the calling thread's scratch
     float* part_l;
     float* part_o;
     int max_rows;            // cache rows that may be read (max_seq), > 0
@@ -101,7 +101,6 @@ int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream
 int attn_pick_splits(int n_kv, int max_ctx);
 // split count of the two-kernel path (attn_launch) for a live context
 int attn_pick_splits_unfused(int n_kv, int ctx);
-int attn_reserve(int n_heads, int head_dim, int n_splits);
 int attn_launch(AttnArgs a, int n_splits, hipStream_t st);
 // n_seq sequences of one batch step: split kernel (grid n_kv x n_splits x
 // n_seq) and split merge, no generic fallback; partials are the caller's,

@@ -104,16 +104,11 @@ ATLAS_API void atlas_decode_attention(const float* q, const float* k_cache, cons
     attn_launch(a, attn_pick_splits_unfused(n_kv, ctx), stream());
 }
 
+// per-block argmax keys in the calling thread's scratch
 static unsigned long long* argmax_scratch() {
-    static unsigned long long* p = nullptr;
-    if (!p) {
-        if (hipMalloc((void**)&p, ARGMAX_MAX_PARTS * sizeof(unsigned long long)) != hipSuccess) {
-            (void)hipGetLastError();
-            p = nullptr;
-            set_error(ATLAS_ENOMEM, "argmax scratch allocation failed");
-        }
-    }
-    return p;
+    void* p = nullptr;
+    if (thread_scratch(SCR_ARGMAX, ARGMAX_MAX_PARTS * sizeof(unsigned long long), &p)) return nullptr;
+    return static_cast<unsigned long long*>(p);
 }
 
 ATLAS_API void atlas_gpu_argmax(const float* x, float* out_f32, int n) {
@@ -176,6 +171,17 @@ ATLAS_API int atlas_gemm_skinny_f32(int fmt, const void* w, const float* scales,
     return skinny_launch(a, stream());
 }
 
+ATLAS_API int atlas_gemm_skinny_swiglu_f32(int fmt, const void* w, const float* scales,
+                                           int block, const float* x, float* h_out, int h, int n,
+                                           int k) {
+    ATLAS_REQUIRE(h >= 0, "gemm_skinny_swiglu: h < 0");
+    GemvArgs a{};
+    a.fmt = fmt; a.w = w; a.scales = scales; a.block = block; a.x = x; a.y = h_out;
+    a.M = 2 * h; a.K = k; a.N = n; a.epi = EPI_SILU_MUL;
+    a.x_stride_n = k; a.x_stride_k = 1; a.y_stride_n = h; a.y_stride_m = 1;
+    return skinny_launch(a, stream());
+}
+
 ATLAS_API int atlas_rmsnorm_rows_f32(const float* x, const float* w, float* out, int n, int rows,
                                      float eps) {
     return rmsnorm_launch(x, w, out, n, rows, n, eps, stream());
@@ -210,38 +216,26 @@ ATLAS_API int atlas_attention_fused_f32(const float* qkv, const float* q_norm,
     const int ctx = (window > 0 && pos + 1 > window) ? window : pos + 1;
     if (n_splits <= 0) n_splits = attn_pick_splits(n_kv, ctx);
     ATLAS_REQUIRE(n_splits <= 1024, "attention_fused: n_splits %d", n_splits);
-    // scratch: position, merge counters (zeroed once; the kernel leaves them
-    // at zero), split partials
-    static int* d_pos = nullptr;
-    static int* d_cnt = nullptr;
-    static int cnt_cap = 0;
-    static float* d_part = nullptr;
-    static size_t part_cap = 0;
-    if (!d_pos) ATLAS_HIP(hipMalloc((void**)&d_pos, sizeof(int)));
-    if (n_kv > cnt_cap) {
-        ATLAS_HIP(hipDeviceSynchronize());
-        if (d_cnt) ATLAS_HIP(hipFree(d_cnt));
-        ATLAS_HIP(hipMalloc((void**)&d_cnt, (size_t)n_kv * sizeof(int)));
-        ATLAS_HIP(hipMemset(d_cnt, 0, (size_t)n_kv * sizeof(int)));
-        cnt_cap = n_kv;
-    }
-    const size_t need = (size_t)n_heads * n_splits * (head_dim + 2);
-    if (need > part_cap) {
-        ATLAS_HIP(hipDeviceSynchronize());
-        if (d_part) ATLAS_HIP(hipFree(d_part));
-        ATLAS_HIP(hipMalloc((void**)&d_part, need * sizeof(float)));
-        part_cap = need;
-    }
+    // the calling thread's scratch: position, merge counters (cleared when
+    // grown; the kernel leaves them at zero), split partials
+    void *d_pos = nullptr, *d_cnt = nullptr, *d_part_v = nullptr;
+    const size_t need = (size_t)n_heads * n_splits * (head_dim + 2) * sizeof(float);
+    int rc = thread_scratch(SCR_FUSED_POS, sizeof(int), &d_pos);
+    if (!rc) rc = thread_scratch(SCR_FUSED_CNT, (size_t)n_kv * sizeof(int), &d_cnt, true);
+    if (!rc) rc = thread_scratch(SCR_FUSED_PART, need, &d_part_v);
+    if (rc) return rc;
+    float* d_part = static_cast<float*>(d_part_v);
     ATLAS_HIP(hipMemcpyAsync(d_pos, &pos, sizeof(int), hipMemcpyHostToDevice, stream()));
     AttnFusedArgs a{};
     a.qkv = qkv; a.qkv_stride = 0; a.q_norm = q_norm; a.k_norm = k_norm; a.qk_eps = qk_eps;
     a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.k_cache = k_cache; a.v_cache = v_cache;
-    a.slot_stride = 0; a.slot_dev = nullptr; a.pos_dev = d_pos; a.out = out; a.out_stride = 0;
+    a.slot_stride = 0; a.slot_dev = nullptr; a.pos_dev = static_cast<const int*>(d_pos);
+    a.out = out; a.out_stride = 0;
     a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = head_dim; a.scale = scale; a.window = window;
     a.part_m = d_part;
     a.part_l = d_part + (size_t)n_heads * n_splits;
     a.part_o = d_part + (size_t)2 * n_heads * n_splits;
-    a.counters = d_cnt;
+    a.counters = static_cast<int*>(d_cnt);
     a.min_chunk = min_chunk > 0 ? min_chunk : 0;
     a.max_rows = pos + 1;
     return attn_fused_launch(a, n_splits, 1, stream());

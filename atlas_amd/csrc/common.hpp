@@ -21,8 +21,27 @@ namespace atlas {
 
 void set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
-hipStream_t stream();          // current launch stream
+hipStream_t stream();          // the calling thread's launch stream
 int device_cu_count();         // CUs of the current device (cached)
+
+// Device scratch owned by the calling thread on the current device, for entry
+// points that are not handed a workspace (split partials of the reference-ABI
+// attention, split-K partials of the skinny GEMMs, argmax partials).  Each
+// slot grows stream-ordered on the thread's current stream (the old buffer is
+// freed after the work already queued there; a thread that switched streams
+// waits for the previous one first) and is kept until the process ends.  Two
+// threads never share a slot; calls of one thread on two streams at once do.
+// zero_new: a grown slot is cleared (fill kernel) before it is returned.
+enum ScratchSlot {
+    SCR_ATTN = 0,       // atlas_decode_attention split partials
+    SCR_GEMM,           // skinny / prompt-GEMM split-K partials
+    SCR_ARGMAX,         // argmax per-block keys
+    SCR_FUSED_PART,     // atlas_attention_fused_f32 split partials
+    SCR_FUSED_CNT,      // ... its merge counters (kept at zero by the kernel)
+    SCR_FUSED_POS,      // ... its position word
+    SCR_N
+};
+int thread_scratch(int slot, size_t bytes, void** out, bool zero_new = false);
 
 // Check a HIP call; on failure record the error and return ATLAS_EHIP.
 #define ATLAS_HIP(call)                                                        \

@@ -116,6 +116,10 @@ struct atlas_model {
     float *xb = nullptr, *y2 = nullptr;
     float* attn_part = nullptr;
     int* attn_counters = nullptr;
+    // split-K partials of the multi-row GEMMs (ragged batch, prompt chunks):
+    // the model's own, so captured steps never point at shared scratch
+    float* gemm_part = nullptr;
+    size_t gemm_part_bytes = 0;
     bool fused = false;
     int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
     uint32_t *tok_dev = nullptr, *hist = nullptr, *suppress_dev = nullptr, *choice_dev = nullptr;
@@ -221,6 +225,8 @@ int skinny(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int
     a.x_stride_k = 1;
     a.y_stride_n = epi == EPI_SILU_MUL ? w.rows / 2 : w.rows;
     a.y_stride_m = 1;
+    a.partial = m->gemm_part;
+    a.partial_bytes = m->gemm_part_bytes;
     return skinny_launch(a, m->st);
 }
 
@@ -992,10 +998,15 @@ int bmm(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int ep
     return skinny(m, w, x, y, n, epi);
 }
 
-// with_head = false: a prefill chunk, no final norm / lm_head / choice
+// prompt_chunk = true: the n rows are ONE sequence's prompt tokens at
+// consecutive positions pos_dev[0] .. + n - 1, all in slot slots[0] (only
+// prefill_rows sets it); the step then skips the final norm, lm_head and
+// choice, and its attention may take the query-tiled prompt kernel, which
+// relies on exactly that layout.  Ragged rows (any other caller) pass false.
 int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx,
-               bool with_head = true) {
+               bool prompt_chunk = false) {
     const atlas_model_config& c = m->cfg;
+    const bool with_head = !prompt_chunk;
     const int d = c.d_model;
     TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, n, m->st));
     for (int li = 0; li < c.n_layers; ++li) {
@@ -1033,7 +1044,7 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             a.part_m = m->attn_part; a.part_l = m->attn_part + np; a.part_o = m->attn_part + 2 * np;
             // a prompt chunk (one sequence, consecutive positions, one slot):
             // 16 rows share each K/V tile
-            if (!with_head && attn_prefill_ok(a)) TRY(attn_prefill_launch(a, n, m->st));
+            if (prompt_chunk && attn_prefill_ok(a)) TRY(attn_prefill_launch(a, n, m->st));
             else TRY(attn_batch_launch(a, sp, n, m->st));
         } else if (m->fused) {
             // one launch: every sequence's QK-norm/RoPE/KV write and attention
@@ -1098,15 +1109,16 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
 // variant (fused models: tokens, positions and slots are read from device
 // memory); long_ctx picks the long-context variant
 int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_ctx,
-                   bool with_head = true) {
+                   bool prompt_chunk = false) {
     long_ctx = long_ctx && m->fused;
-    if (!m->use_graph || !m->fused) return batch_step(m, n, slots, long_ctx, with_head);
+    const bool with_head = !prompt_chunk;
+    if (!m->use_graph || !m->fused) return batch_step(m, n, slots, long_ctx, prompt_chunk);
     hipGraphExec_t& ge = with_head ? (long_ctx ? m->bgexec_long[n] : m->bgexec[n])
                                    : (long_ctx ? m->pgexec_long[n] : m->pgexec[n]);
     if (!ge) {
         hipGraph_t g = nullptr;
         ATLAS_HIP(hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
-        int rc = batch_step(m, n, slots, long_ctx, with_head);
+        int rc = batch_step(m, n, slots, long_ctx, prompt_chunk);
         hipError_t e = hipStreamEndCapture(m->st, &g);
         if (rc) {
             if (g) (void)hipGraphDestroy(g);
@@ -1153,8 +1165,8 @@ int prefill_rows(atlas_model* m, int slot, int pos0, const uint32_t* toks, int k
     ATLAS_HIP(hipMemcpyAsync(m->slot_dev, host[2], (size_t)k * 4, hipMemcpyHostToDevice, m->st));
     // chunks beyond the captured row counts run eagerly: ~260 launches
     // queue while the first GEMMs run
-    if (k > kMaxRows) TRY(batch_step(m, k, std::vector<int>(k, slot), true, false));
-    else TRY(run_batch_step(m, k, std::vector<int>(k, slot), true, false));
+    if (k > kMaxRows) TRY(batch_step(m, k, std::vector<int>(k, slot), true, /*prompt_chunk=*/true));
+    else TRY(run_batch_step(m, k, std::vector<int>(k, slot), true, /*prompt_chunk=*/true));
     ATLAS_HIP(hipStreamSynchronize(m->st));      // host[] lives on this frame
     return ATLAS_OK;
 }
@@ -1308,17 +1320,21 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     m->attn_splits = attn_pick_splits(c.n_kv_heads, c.max_seq);
     m->attn_splits_unfused = m->attn_splits;
     m->attn_splits_long = attn_splits_for(c.n_kv_heads, c.max_seq);
-    if (attn_reserve(c.n_heads, hd, m->attn_splits_unfused)) return fail(m);
-    // split-K partials of the ragged batch's skinny GEMMs, allocated now so
-    // that no later launch (graph capture included) allocates
+    // split-K partials of the ragged batch's skinny GEMMs and the prompt
+    // chunks' tiled GEMMs, allocated now so that no later launch (graph
+    // capture included) allocates
     {
         const int nb = R < kMaxRows ? R : kMaxRows;
         const int shapes[5][2] = {{m->qkv_rows, d}, {d, c.n_heads * hd}, {2 * c.ffn_hidden, d},
                                   {d, c.ffn_hidden}, {c.vocab, d}};
+        size_t need = 0;
         for (const auto& sh : shapes) {
-            if (sh[1] % 32 == 0 && skinny_reserve(sh[0], nb, sh[1])) return fail(m);
-            if (m->big_prefill && gemm_rows_reserve(sh[0], kPrefillBig, sh[1])) return fail(m);
+            if (sh[1] % 32 == 0) need = std::max(need, skinny_partial_bytes(sh[0], nb, sh[1]));
+            if (m->big_prefill)
+                need = std::max(need, gemm_rows_partial_bytes(sh[0], kPrefillBig, sh[1]));
         }
+        if (need && dalloc(m, (void**)&m->gemm_part, need)) return fail(m);
+        m->gemm_part_bytes = need;
     }
     // fused step: post-norm model whose attention shape the fused kernel
     // covers and whose GEMVs take the aligned fast path (d % 32 == 0)

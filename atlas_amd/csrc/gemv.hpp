@@ -36,6 +36,8 @@ struct GemvArgs {
     float* pro_out;          // RESNORM / RMSNORM: x written out by block 0 (nullable)
     unsigned long long* arg_part;   // EPI_ARGMAX: per-wave (value, index) keys
     long ldw;                // bytes between weight rows (multiple of 16); 0 = packed rows
+    float* partial;          // skinny / prompt GEMM split-K partials (null: the thread's scratch)
+    size_t partial_bytes;    // ... their size
 };
 
 enum { GEMV_MAX_WAVES = 16384 };    // bound on persistent waves (argmax partials)
@@ -49,11 +51,11 @@ int skinny_launch(const GemvArgs& a, hipStream_t st);   // 1 <= N <= 8
 constexpr int kGemvMaxNx = 4;
 bool gemv_multi_ok(const GemvArgs& a);
 int gemv_multi_launch(const GemvArgs& a, hipStream_t st);
-int skinny_reserve(int M, int N, int K);
+size_t skinny_partial_bytes(int M, int N, int K);    // split-K partials of (M, N, K)
 // 17..128 rows of bf16 weights: the tiled MFMA GEMM (skinny_launch routes there)
 bool gemm_rows_ok(const GemvArgs& a);
 int gemm_rows_launch(const GemvArgs& a, hipStream_t st);
-int gemm_rows_reserve(int M, int N, int K);
+size_t gemm_rows_partial_bytes(int M, int N, int K);
 int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,
                         hipStream_t st);
 

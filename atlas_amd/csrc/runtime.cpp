@@ -28,9 +28,64 @@ void clear_error() {
     t_err_msg[0] = 0;
 }
 
-static hipStream_t g_stream = nullptr;      // null stream by default
+// Each host thread launches on its own current stream (the null stream until
+// atlas_set_stream), so two threads driving the library never share one.
+static thread_local hipStream_t g_stream = nullptr;
 
 hipStream_t stream() { return g_stream; }
+
+namespace {
+constexpr int kScratchDevices = 16;
+struct ScratchBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    hipStream_t last = nullptr;   // stream of the most recent use
+};
+struct ThreadScratch {
+    ScratchBuf b[kScratchDevices][SCR_N];
+};
+thread_local ThreadScratch t_scratch;
+}  // namespace
+
+int thread_scratch(int slot, size_t bytes, void** out, bool zero_new) {
+    ATLAS_REQUIRE(out && slot >= 0 && slot < SCR_N, "scratch: bad slot %d", slot);
+    *out = nullptr;
+    int dev = 0;
+    ATLAS_HIP(hipGetDevice(&dev));
+    ATLAS_REQUIRE(dev >= 0 && dev < kScratchDevices, "scratch: device %d", dev);
+    ScratchBuf& s = t_scratch.b[dev][slot];
+    hipStream_t st = g_stream;
+    if (bytes > s.cap) {
+        if (s.p) {
+            // the old buffer may still be read by work queued on the stream
+            // of its last use: free it after that work
+            if (s.last != st) ATLAS_HIP(hipStreamSynchronize(s.last));
+            ATLAS_HIP(hipFreeAsync(s.p, st));
+            s.p = nullptr;
+            s.cap = 0;
+        }
+        const size_t cap = (bytes + 65535) / 65536 * 65536;
+        void* p = nullptr;
+        if (hipMallocAsync(&p, cap, st) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            set_error(ATLAS_ENOMEM, "scratch: device allocation of %zu bytes failed", cap);
+            return ATLAS_ENOMEM;
+        }
+        if (zero_new) {
+            const int rc = ew_launch(EW_FILL, nullptr, nullptr, reinterpret_cast<float*>(p), 0.0f,
+                                     (long)(cap / 4), st);
+            if (rc) {
+                (void)hipFreeAsync(p, st);
+                return rc;
+            }
+        }
+        s.p = p;
+        s.cap = cap;
+    }
+    s.last = st;
+    *out = s.p;
+    return ATLAS_OK;
+}
 
 int device_cu_count() {
     static int cached[64] = {0};

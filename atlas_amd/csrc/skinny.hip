@@ -486,19 +486,19 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemvArgs a, const fl
     }
 }
 
-// scratch for split-K partials (grown on demand, never shrunk)
-static float* g_partial = nullptr;
-static size_t g_partial_bytes = 0;
-
-// A buffer that grows is replaced, never freed: graphs captured earlier
-// keep pointing at the old one, which still covers their launches.
-static int ensure_partial(size_t bytes) {
-    if (bytes <= g_partial_bytes) return ATLAS_OK;
-    float* p = nullptr;
-    ATLAS_HIP(hipMalloc((void**)&p, bytes));
-    g_partial = p;
-    g_partial_bytes = bytes;
-    return ATLAS_OK;
+// Split-K partials: the caller's buffer (GemvArgs.partial, e.g. a model's,
+// which a captured step may point at) or the calling thread's scratch.
+static int partial_for(const GemvArgs& a, size_t bytes, float** out) {
+    if (a.partial) {
+        ATLAS_REQUIRE(bytes <= a.partial_bytes, "split-K partials: %zu bytes needed, %zu given",
+                      bytes, a.partial_bytes);
+        *out = a.partial;
+        return ATLAS_OK;
+    }
+    void* p = nullptr;
+    const int rc = thread_scratch(SCR_GEMM, bytes, &p);
+    *out = static_cast<float*>(p);
+    return rc;
 }
 
 // A tiles of an N-row launch, and the K splits it uses (a block covers
@@ -509,14 +509,13 @@ static int skinny_splits(int K, int N) {
     return (kt_total + kt_block - 1) / kt_block;
 }
 
-// Allocate the split-K partials an (M, N, K) launch needs, so that later
-// launches (e.g. under graph capture) allocate nothing; an N-row reservation
+// Bytes of split-K partials an (M, N, K) launch needs; an N-row size
 // covers every smaller N.
-int skinny_reserve(int M, int N, int K) {
+size_t skinny_partial_bytes(int M, int N, int K) {
     int splits = skinny_splits(K, N);
     if (N > 8) splits = std::max(splits, skinny_splits(K, 8));
-    if (splits <= 1) return ATLAS_OK;
-    return ensure_partial((size_t)splits * N * M * sizeof(float));
+    if (splits <= 1) return 0;
+    return (size_t)splits * N * M * sizeof(float);
 }
 
 // blocks of 1024 threads one CU holds for kernel `kern` (cached per kernel)
@@ -548,25 +547,26 @@ static int launch_skinny(const GemvArgs& a, hipStream_t st) {
     const int n_tiles = (a.M + 15) / 16;
     int bx = skinny_resident<skinny_kernel_ptr<FMT, NA>>() * device_cu_count();
     if (bx > n_tiles) bx = n_tiles;
+    float* partial = nullptr;
     if (splits > 1) {
-        int rc = ensure_partial((size_t)splits * a.N * a.M * sizeof(float));
+        int rc = partial_for(a, (size_t)splits * a.N * a.M * sizeof(float), &partial);
         if (rc) return rc;
     }
     int cpb_shift = 0;
     while ((1 << cpb_shift) < a.cpb) ++cpb_shift;
     if constexpr (FMT == WF_I4)
         hipLaunchKernelGGL((skinny_i4_kernel<1, 16, NA>), dim3(bx, splits), dim3(1024), 0, st, a,
-                           g_partial, kt_split, cpb_shift);
+                           partial, kt_split, cpb_shift);
     else
         hipLaunchKernelGGL((skinny_kernel<FMT, NA>), dim3(bx, splits), dim3(1024), 0, st, a,
-                           g_partial, kt_split, cpb_shift);
+                           partial, kt_split, cpb_shift);
     ATLAS_LAUNCH_CHECK("skinny");
     if (splits > 1) {
         const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
         long rb = ((long)a.N * m_out + 255) / 256;
         if (rb > 4096) rb = 4096;
         hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a,
-                           g_partial, splits);
+                           partial, splits);
         ATLAS_LAUNCH_CHECK("skinny_reduce");
     }
     return ATLAS_OK;
@@ -768,44 +768,55 @@ bool gemm_rows_ok(const GemvArgs& a) {
            (a.epi == EPI_STORE || (a.epi == EPI_SILU_MUL && a.M % 2 == 0));
 }
 
+// int4 launches hold at most four 16-row tiles (gemm_rows_launch splits
+// larger chunks); anything else is refused rather than left unwritten
 template <int FMT>
-static void gemm_rows_go(const GemvArgs& a, dim3 grid, int steps, int cpb_shift, hipStream_t st) {
+static int gemm_rows_go(const GemvArgs& a, float* partial, dim3 grid, int steps, int cpb_shift,
+                        hipStream_t st) {
     const int nt = (a.N + 15) / 16;
     if (nt <= 2)
-        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 2>), grid, dim3(256), 0, st, a, g_partial, steps, cpb_shift);
+        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 2>), grid, dim3(256), 0, st, a, partial, steps, cpb_shift);
     else if (nt <= 4)
-        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 4>), grid, dim3(256), 0, st, a, g_partial, steps, cpb_shift);
+        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 4>), grid, dim3(256), 0, st, a, partial, steps, cpb_shift);
     else if constexpr (FMT != WF_I4)
-        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 8>), grid, dim3(256), 0, st, a, g_partial, steps, cpb_shift);
+        hipLaunchKernelGGL((gemm_rows_kernel<FMT, 8>), grid, dim3(256), 0, st, a, partial, steps, cpb_shift);
+    else {
+        set_error(ATLAS_EUNSUPPORTED, "gemm rows: int4 launches take at most 64 rows (got %d)", a.N);
+        return ATLAS_EUNSUPPORTED;
+    }
+    return ATLAS_OK;
 }
 
-int gemm_rows_reserve(int M, int N, int K) {
+size_t gemm_rows_partial_bytes(int M, int N, int K) {
     int splits, steps;
     gemm_rows_split(M, K, splits, steps);
-    if (splits <= 1) return ATLAS_OK;
-    return ensure_partial((size_t)splits * N * M * sizeof(float));
+    if (splits <= 1) return 0;
+    return (size_t)splits * N * M * sizeof(float);
 }
 
 // one launch (+ split-K reduce) over all a.N <= 128 rows
 static int gemm_rows_part(const GemvArgs& a, hipStream_t st) {
     int splits, steps;
     gemm_rows_split(a.M, a.K, splits, steps);
+    float* partial = nullptr;
     if (splits > 1) {
-        int rc = ensure_partial((size_t)splits * a.N * a.M * sizeof(float));
+        int rc = partial_for(a, (size_t)splits * a.N * a.M * sizeof(float), &partial);
         if (rc) return rc;
     }
     const dim3 grid((a.M + GR_ROWS - 1) / GR_ROWS, splits);
     int cpb_shift = 0;
     while ((1 << cpb_shift) < a.cpb) ++cpb_shift;
-    if (a.fmt == WF_BF16) gemm_rows_go<WF_BF16>(a, grid, steps, cpb_shift, st);
-    else if (a.fmt == WF_I8) gemm_rows_go<WF_I8>(a, grid, steps, cpb_shift, st);
-    else gemm_rows_go<WF_I4>(a, grid, steps, cpb_shift, st);
+    int rc;
+    if (a.fmt == WF_BF16) rc = gemm_rows_go<WF_BF16>(a, partial, grid, steps, cpb_shift, st);
+    else if (a.fmt == WF_I8) rc = gemm_rows_go<WF_I8>(a, partial, grid, steps, cpb_shift, st);
+    else rc = gemm_rows_go<WF_I4>(a, partial, grid, steps, cpb_shift, st);
+    if (rc) return rc;
     ATLAS_LAUNCH_CHECK("gemm_rows");
     if (splits > 1) {
         const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
         long rb = ((long)a.N * m_out + 255) / 256;
         if (rb > 4096) rb = 4096;
-        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, g_partial,
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, partial,
                            splits);
         ATLAS_LAUNCH_CHECK("gemm_rows_reduce");
     }
@@ -854,6 +865,18 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     // is within 3%); from four rows on, the LDS reads of the x rows per
     // weight chunk make it no faster than the MFMA kernel.
     if (a.N <= 3 && gemv_multi_ok(a)) return gemv_multi_launch(a, st);
+    // One row is the batch-1 GEMV (int4 11008 x 4096: 10 us against 15.6 us
+    // for the MFMA tiles, whose 16 rows would be 15 / 16 padding).
+    if (a.N == 1 && a.x_stride_k == 1 && a.y_stride_m == 1 && (a.epi == EPI_STORE ||
+                                                               a.epi == EPI_SILU_MUL)) {
+        const uintptr_t al = (uintptr_t)a.w | (uintptr_t)a.x;
+        if ((al & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
+            gemv_x_lds_bytes(a.K) <= 160 * 1024) {
+            GemvArgs g = a;
+            g.N = 1;
+            return gemv_launch(g, st);
+        }
+    }
     const uintptr_t al = (uintptr_t)a.w;
     switch (a.fmt) {
     case WF_BF16:

@@ -170,6 +170,12 @@ int atlas_gemv_fused_f32(int fmt, const void* w, const float* scales, int block,
  * chunks; other shapes outside 1..16 return ATLAS_EINVAL.                   */
 int atlas_gemm_skinny_f32(int fmt, const void* w, const float* scales, int block,
                           const float* x, float* y, int m, int n, int k);
+/* The same row counts with the SwiGLU epilogue: W has 2*h rows interleaved
+ * (gate_0, up_0, gate_1, ...) and H[n, i] = silu(gate_i . X[n]) * (up_i . X[n])
+ * (FeedForward::forward, crates/atlas-model/src/lib.rs:911-924), H [n x h]
+ * row-major.  Extension: the ragged batch's and the prompt chunks' gate/up.  */
+int atlas_gemm_skinny_swiglu_f32(int fmt, const void* w, const float* scales, int block,
+                                 const float* x, float* h_out, int h, int n, int k);
 
 /* out = rmsnorm(x) * w row-wise over `rows` rows of length n (ld = n).      */
 int atlas_rmsnorm_rows_f32(const float* x, const float* w, float* out, int n, int rows,

@@ -191,6 +191,40 @@ def test_skinny_multi_row(orc, fmt, n, M, K, block):
     _skinny_check(orc, fmt, n, M, K, block, seed=7)
 
 
+# The ragged batch's three- and five-row GEMMs at the 7B decode shapes
+# (BASELINE.json configs[2] asks for 1/3/5/8 rows of 11008 x 4096).
+@pytest.mark.parametrize("M,K", [(4096, 4096), (11008, 4096)])
+@pytest.mark.parametrize("n", [3, 5])
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
+def test_skinny_7b_rows(orc, fmt, n, M, K):
+    print(f"skinny 7B {fmt} n={n} M={M} K={K}", flush=True)
+    _skinny_check(orc, fmt, n, M, K, 32, seed=11)
+
+
+# SwiGLU epilogue over n rows: one row (batch-1 GEMV), two (multi-row GEMV),
+# five (MFMA skinny tiles, split-K reduce applies SwiGLU), twenty rows at
+# K = 128 (the prompt GEMM's unsplit epilogue: gate/up pairs meet across
+# lanes) and at K = 4096 (split, SwiGLU in the reduce).
+@pytest.mark.parametrize("fmt,n,h,K", [
+    ("bf16", 1, 1000, 512), ("int8", 2, 700, 1024), ("int4", 5, 512, 2048),
+    ("bf16", 20, 640, 128), ("int8", 20, 640, 128), ("int4", 20, 640, 128),
+    ("bf16", 20, 2048, 4096), ("int4", 33, 1024, 4096)])
+def test_gemm_skinny_swiglu(orc, fmt, n, h, K):
+    print(f"skinny swiglu {fmt} n={n} h={h} K={K}", flush=True)
+    w = _w((2 * h, K), 97 + n)
+    x = np.random.default_rng(n).standard_normal((n, K)).astype(np.float32)
+    view, dw, ds, fid, bs = _stored(orc, fmt, w, 32)
+    y = orc.linear_batch(view, x)                     # [n, 2h]: gate_i, up_i interleaved
+    ref = np.array([[orc.silu(float(g)) for g in row] for row in y[:, 0::2]], np.float32)
+    ref *= y[:, 1::2]
+    dx, dh = Dev(x), Dev.empty((n, h))
+    assert lib().atlas_gemm_skinny_swiglu_f32(fid, dw.ptr, ds.ptr if ds else None, bs, dx.ptr,
+                                              dh.ptr, h, n, K) == 0
+    got = dh.get()
+    for i in range(n):
+        assert rel_err(got[i], ref[i]) <= GEMV_TOL, i
+
+
 def test_sgemm_bf16_reference_layout(orc):
     # crates/atlas-tensor/src/lib.rs:44-47: B is [k x n] row-major, C [m x n]
     M, K = 256, 512
@@ -203,6 +237,46 @@ def test_sgemm_bf16_reference_layout(orc):
         lib().atlas_sgemm_bf16_f32(dw.ptr, dx.ptr, dc.ptr, M, n, K)
         sync()
         assert rel_err(dc.get(), ref) <= GEMV_TOL, n
+
+
+def test_tensor_mirrors_host_slices_rope_and_cache(orc):
+    # GpuMatrix::sgemm with host slices (H2D rhs, D2H out; crates/atlas-tensor/
+    # src/lib.rs:371-400) over f32 and bf16 weights, one and several columns;
+    # GpuRopeTables::apply_to (lib.rs:681-692) and GpuKvCache::{write,
+    # decode_attention} (lib.rs:722-770) against the oracle
+    from atlas_amd.tensor import GpuKvCache, GpuMatrix, GpuRopeTables, GpuVec
+    M, K = 768, 1024
+    w = _w((M, K), 61)
+    bits = orc.bf16_from_f32(w)
+    for mat, view in ((GpuMatrix.upload(w, M, K), orc.MatView.f32(w)),
+                      (GpuMatrix.upload_bf16(bits, M, K), orc.MatView.bf16(bits, M, K))):
+        for n in (1, 3):
+            rhs = np.random.default_rng(n).standard_normal((K, n)).astype(np.float32)
+            out = np.empty((M, n), np.float32)
+            assert mat.sgemm(rhs, K, n, out)
+            ref = np.stack([orc.linear(view, rhs[:, j].copy()) for j in range(n)], axis=1)
+            assert rel_err(out, ref) <= GEMV_TOL, (mat, n)
+    H, KVH, hd, S = 8, 2, 128, 300
+    cos, sin, _ = orc.rope_tables(hd, S, 500000.0, dict(factor=8.0, orig_max_pos=8192,
+                                                        attn_factor=1.2079441541679836,
+                                                        beta_fast=32.0, beta_slow=1.0))
+    tabs = GpuRopeTables.upload(cos.reshape(-1), sin.reshape(-1), S, hd // 2)
+    q = np.random.default_rng(3).standard_normal(H * hd).astype(np.float32)
+    qd = GpuVec.from_slice(q)
+    tabs.apply_to(qd, H, hd, 257)
+    want = np.concatenate([orc.rope_apply(q[h * hd:(h + 1) * hd], cos[257], sin[257])
+                           for h in range(H)])
+    assert rel_err(qd.download(), want) <= 1e-6
+    cache = GpuKvCache.new(S, KVH, hd)
+    kc = np.random.default_rng(4).standard_normal((S, KVH * hd)).astype(np.float32)
+    vc = np.random.default_rng(5).standard_normal((S, KVH * hd)).astype(np.float32)
+    for p in range(S):
+        cache.write(p, GpuVec.from_slice(kc[p]), GpuVec.from_slice(vc[p]))
+    scale = 1.2079441541679836 / math.sqrt(hd)
+    for pos, window in ((0, 0), (299, 0), (299, 64)):
+        got = cache.decode_attention(qd, H, pos, scale, window).download()
+        ref = orc.attention(qd.download(), kc, vc, H, KVH, hd, pos, scale, window)
+        assert rel_err(got, ref) <= ATTN_TOL, (pos, window)
 
 
 def test_sgemm_vec_ones_literal():

@@ -312,6 +312,31 @@ def test_prefill_chunks_head_dim_128(orc):
         assert _rel(m.forward_one(toks[n - 1]), r) <= LOGIT_TOL, n
 
 
+@pytest.mark.parametrize("H,KVH,d", [(4, 2, 512), (8, 2, 1024)])
+def test_prefill_chunks_gqa_head_dim_128(orc, H, KVH, d):
+    # the query-tiled prompt attention with GQA groups 2 and 4 (kv head =
+    # q head / group) and prompts up to 699 positions, with a window of 256
+    # that later chunks start inside
+    cfg = modelgen.olmo3_small_config(n_layers=2, n_heads=H, n_kv_heads=KVH, d_model=d,
+                                      ffn_hidden=1024, max_seq=720, sliding_window=256,
+                                      layer_sliding=[1, 0])
+    W = modelgen.make_weights(cfg, seed=79)
+    toks = [int(t) for t in np.random.default_rng(15).integers(0, cfg["vocab"], 700)]
+    m = modelgen.engine_model(W)
+    o = modelgen.oracle_model(W, threads=8)
+    ref = {}
+    o.reset()
+    for i, t in enumerate(toks):
+        lg = o.forward_one(t)
+        if i + 1 in (20, 129, 300, 700):
+            ref[i + 1] = lg
+    for n, r in ref.items():
+        print(f"prefill GQA {H}/{KVH} hd128: {n - 1} prompt tokens", flush=True)
+        m.reset()
+        m.prefill(toks[:n - 1])
+        assert _rel(m.forward_one(toks[n - 1]), r) <= LOGIT_TOL, n
+
+
 def test_long_context_attention_path(orc):
     # positions >= from_pos replay the long-context step (QK-norm/RoPE/KV-write
     # kernel, adaptive split kernel, split merge); forcing it from position 8
