@@ -102,6 +102,8 @@ SIGNATURES = {
     "atlas_residual_rmsnorm_f32": (I, [P, P, P, I, I, F]),
     "atlas_qkv_post_f32": (I, [P, P, P, F, P, P, P, P, I, I, I, I]),
     "atlas_attention_fused_f32": (I, [P, P, P, F, P, P, P, P, P, I, I, I, I, F, I, I, I]),
+    "atlas_decode_attention_noalloc": (I, [P, P, P, P, I, I, I, I, F, I]),
+    "atlas_decode_attention_noalloc_max_bytes": (I64, []),
     "atlas_argmax_u32": (I, [P, I, P]),
     "atlas_quantize_int8_dev": (I, [P, I, I, I, P, P]),
     "atlas_quantize_int4_dev": (I, [P, I, I64, I, P, P]),

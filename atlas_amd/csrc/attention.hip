@@ -23,6 +23,7 @@
 //  * the split count is fixed at launch and `pos` may come from device
 //    memory, so the same launch can be captured once and replayed per token.
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 #include "attention.hpp"
@@ -896,6 +897,65 @@ int attn_batch_launch(const AttnArgs& a, int n_splits, int n_seq, hipStream_t st
 #undef ATLAS_BATCH_CASE
     set_error(ATLAS_EUNSUPPORTED, "attention: batch shape");
     return ATLAS_EUNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// The no-allocation variant of atlas_decode_attention: its split partials live
+// in `scratch`, a fixed device array of this file that every GPU holds until
+// the process ends.  Host code never passes the array's name to a kernel (in
+// host code it is only a stand-in for the symbol): the device address of each
+// GPU's copy comes from hipGetSymbolAddress on the first call made on that
+// device and is kept per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;     // 8 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kNoAllocDevices = 64;
+static std::mutex g_noalloc_mu;
+static float* g_noalloc_ptr[kNoAllocDevices] = {};
+
+// device address of the current device's copy of `scratch` (resolved once)
+static int noalloc_scratch(float** out) {
+    int dev = 0;
+    ATLAS_HIP(hipGetDevice(&dev));
+    ATLAS_REQUIRE(dev >= 0 && dev < kNoAllocDevices, "decode_attention_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            set_error(ATLAS_EHIP, "decode_attention_noalloc: scratch symbol address: %s",
+                      hipGetErrorString(e));
+            return ATLAS_EHIP;
+        }
+        g_noalloc_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_noalloc_ptr[dev];
+    return ATLAS_OK;
+}
+
+size_t attn_noalloc_max_bytes() { return kNoAllocScratchBytes; }
+
+int attn_launch_noalloc(AttnArgs a, int n_splits, hipStream_t st) {
+    if (n_splits < 1) n_splits = 1;
+    if (n_splits > kAttnMaxSplits) n_splits = kAttnMaxSplits;
+    if (n_splits > 1) {
+        const size_t need = (size_t)a.n_heads * n_splits * (a.head_dim + 2) * sizeof(float);
+        if (need > kNoAllocScratchBytes) {
+            set_error(ATLAS_EINVAL,
+                      "decode_attention_noalloc: %d heads x %d splits x (head_dim %d + 2) floats "
+                      "need %zu bytes of partials, above the fixed %zu-byte workspace",
+                      a.n_heads, n_splits, a.head_dim, need, kNoAllocScratchBytes);
+            return ATLAS_EINVAL;
+        }
+        float* part = nullptr;
+        const int rc = noalloc_scratch(&part);
+        if (rc) return rc;
+        a.part_m = part;
+        a.part_l = part + (size_t)a.n_heads * n_splits;
+        a.part_o = part + (size_t)2 * a.n_heads * n_splits;
+    }
+    return attn_launch(a, n_splits, st);
 }
 
 }  // namespace atlas

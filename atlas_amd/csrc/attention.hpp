@@ -102,6 +102,10 @@ int attn_pick_splits(int n_kv, int max_ctx);
 // split count of the two-kernel path (attn_launch) for a live context
 int attn_pick_splits_unfused(int n_kv, int ctx);
 int attn_launch(AttnArgs a, int n_splits, hipStream_t st);
+// attn_launch with its split partials in the library's fixed device
+// workspace (no allocation; concurrent calls on one GPU share it)
+int attn_launch_noalloc(AttnArgs a, int n_splits, hipStream_t st);
+size_t attn_noalloc_max_bytes();
 // n_seq sequences of one batch step: split kernel (grid n_kv x n_splits x
 // n_seq) and split merge, no generic fallback; partials are the caller's,
 // [n_seq][n_heads][n_splits] (+ head_dim for part_o)

@@ -104,6 +104,25 @@ ATLAS_API void atlas_decode_attention(const float* q, const float* k_cache, cons
     attn_launch(a, attn_pick_splits_unfused(n_kv, ctx), stream());
 }
 
+ATLAS_API int atlas_decode_attention_noalloc(const float* q, const float* k_cache,
+                                             const float* v_cache, float* out, int n_heads,
+                                             int n_kv, int head_dim, int pos, float scale,
+                                             int window) {
+    ATLAS_REQUIRE(pos >= 0, "decode_attention_noalloc: pos < 0");
+    AttnArgs a{};
+    a.q = q; a.k_cache = k_cache; a.v_cache = v_cache; a.out = out;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.head_dim = head_dim;
+    a.pos = pos; a.pos_dev = nullptr; a.scale = scale; a.window = window;
+    a.max_rows = pos + 1;
+    const int ctx = (window > 0 && pos + 1 > window) ? window : pos + 1;
+    // the same split count as atlas_decode_attention, so the two agree
+    return attn_launch_noalloc(a, attn_pick_splits_unfused(n_kv, ctx), stream());
+}
+
+ATLAS_API int64_t atlas_decode_attention_noalloc_max_bytes(void) {
+    return (int64_t)attn_noalloc_max_bytes();
+}
+
 // per-block argmax keys in the calling thread's scratch
 static unsigned long long* argmax_scratch() {
     void* p = nullptr;

@@ -204,6 +204,21 @@ int atlas_attention_fused_f32(const float* qkv, const float* q_norm, const float
                               int head_dim, int pos, float scale, int window, int n_splits,
                               int min_chunk);
 
+/* No counterpart in the reference.  atlas_decode_attention for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): same arguments, same split count
+ * and results, but the split partials live in a fixed 8 MiB device workspace
+ * of the library (one per GPU, held until the process ends); no hipMalloc or
+ * hipFree is made.  Shapes whose partials (n_heads x splits x (head_dim + 2)
+ * floats) exceed the workspace return ATLAS_EINVAL.  Calls that overlap on
+ * one GPU (two streams or threads) share the workspace and race: serialise
+ * them.  Returns 0 or a negative ATLAS_E* code.                             */
+int atlas_decode_attention_noalloc(const float* q, const float* k_cache, const float* v_cache,
+                                   float* out, int n_heads, int n_kv_heads, int head_dim,
+                                   int pos, float scale, int window_size);
+/* Bytes of that workspace.                                                   */
+int64_t atlas_decode_attention_noalloc_max_bytes(void);
+
 /* Greedy choice: index of the last maximum of x[0..n) as u32 (device).      */
 int atlas_argmax_u32(const float* x, int n, uint32_t* out_idx);
 
