@@ -599,6 +599,316 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
     if (a.epi == EPI_ARGMAX && lane == 0) a.arg_part[blockIdx.x * 4 + wave] = best;
 }
 
+// ---------------------------------------------------------------------------
+// The batch-1 decode GEMV.  Same work split, staging, prologues and
+// epilogues as gemv_n1_kernel at NX = 1, with the inner loop rebuilt for
+// instruction count (the VALU issue rate limits int4 and weighs on int8):
+//  * a wave walks its (row group, k step) sequence with a cursor advanced
+//    by adds (no divisions per step); row addresses are wave-uniform and
+//    every row is its own buffer resource, so the loads take one VGPR of
+//    lane offset, the step offset in an SGPR and the unroll offset as an
+//    immediate, and chunks past a row's end read as zeros (no clamps: x's
+//    LDS copy is zero-padded to whole steps, so those chunks add nothing);
+//  * the x pieces of a chunk are read once from LDS for all ROWS rows;
+//  * int4 nibbles become f16 by the magic-number trick and multiply f32 x
+//    in v_fma_mix_f32 (one instruction per weight, conversion ~0.75 per
+//    weight), with exact per-chunk offset corrections (below).
+// ---------------------------------------------------------------------------
+
+// int4 chunk (32 weights, 4 words; word j holds elements 8j..8j+7, the even
+// element of a byte in its high nibble).  With n = s ^ 8 = q + 8 for the
+// stored nibble s of the signed value q, (w & 0x000F000F) ^ 0x64086408 is
+// the f16 pair (1024 + n1, 1024 + n5) of the word's odd elements in bytes 0
+// and 2 (0x6400 = 1024 leaves the low mantissa bits free, so the XOR sets
+// the exponent and flips the nibble's sign bit at once: one v_bitop3); with
+// mask 0x00F000F0 and 0x64806480 the even elements give (1024 + 16 n0,
+// 1024 + 16 n4); w >> 8 gives bytes 1 and 3.  Hence with sums acc_o over odd
+// and acc_e over even elements,
+//   sum_k q_k x_k = acc_e / 16 + acc_o - (72 S_even + 1032 S_odd),
+// S_* the chunk's x sums, whose weighted sum `corr` is staged per chunk.
+// Every f16 here is an exact integer; fma_mix rounds like an f32 FMA.
+__device__ __forceinline__ void fma_mix_lo(float& acc, uint32_t pair, float x) {
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(pair), "v"(x));
+}
+__device__ __forceinline__ void fma_mix_hi(float& acc, uint32_t pair, float x) {
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "+v"(acc) : "v"(pair), "v"(x));
+}
+
+// one word (8 weights) of an int4 chunk into the odd / even sums
+__device__ __forceinline__ void i4_word_mix(uint32_t w, const f32x4 xa, const f32x4 xb, float& ao,
+                                            float& ae) {
+    const uint32_t t8 = w >> 8;
+    const uint32_t o15 = (w & 0x000F000Fu) ^ 0x64086408u;   // elements 1, 5
+    const uint32_t e04 = (w & 0x00F000F0u) ^ 0x64806480u;   // elements 0, 4 (x16)
+    const uint32_t o37 = (t8 & 0x000F000Fu) ^ 0x64086408u;  // elements 3, 7
+    const uint32_t e26 = (t8 & 0x00F000F0u) ^ 0x64806480u;  // elements 2, 6 (x16)
+    fma_mix_lo(ao, o15, xa.y);
+    fma_mix_hi(ao, o15, xb.y);
+    fma_mix_lo(ao, o37, xa.w);
+    fma_mix_hi(ao, o37, xb.w);
+    fma_mix_lo(ae, e04, xa.x);
+    fma_mix_hi(ae, e04, xb.x);
+    fma_mix_lo(ae, e26, xa.z);
+    fma_mix_hi(ae, e26, xb.z);
+}
+
+// dot of a 16-byte chunk with its x pieces (bf16 / int8 / f32)
+template <int FMT>
+__device__ __forceinline__ float chunk_dot_x(const u32x4 w, const f32x4 (&x)[WT<FMT>::EPC / 4],
+                                             float acc) {
+    if constexpr (FMT == WF_F32) {
+        acc += __uint_as_float(w.x) * x[0].x;
+        acc += __uint_as_float(w.y) * x[0].y;
+        acc += __uint_as_float(w.z) * x[0].z;
+        acc += __uint_as_float(w.w) * x[0].w;
+    } else if constexpr (FMT == WF_BF16) {
+        acc += bf16_lo(w.x) * x[0].x;  acc += bf16_hi(w.x) * x[0].y;
+        acc += bf16_lo(w.y) * x[0].z;  acc += bf16_hi(w.y) * x[0].w;
+        acc += bf16_lo(w.z) * x[1].x;  acc += bf16_hi(w.z) * x[1].y;
+        acc += bf16_lo(w.w) * x[1].z;  acc += bf16_hi(w.w) * x[1].w;
+    } else {   // WF_I8
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc += s8_at(ww[j], 0) * x[j].x;
+            acc += s8_at(ww[j], 1) * x[j].y;
+            acc += s8_at(ww[j], 2) * x[j].z;
+            acc += s8_at(ww[j], 3) * x[j].w;
+        }
+    }
+    return acc;
+}
+
+// Pieces of x a row's steps read: whole steps, past K zero-filled.
+__host__ __device__ inline int v4_pieces(int fmt, int K, int U) {
+    const int epc = fmt == WF_F32 ? 4 : fmt == WF_BF16 ? 8 : fmt == WF_I8 ? 16 : 32;
+    const int chunks = K / epc, step = 64 * U;
+    return (chunks + step - 1) / step * step * (epc / 4);
+}
+
+// LDS bytes of the v4 kernel: padded x pieces, plus int4 per-chunk corrections
+inline size_t v4_lds_bytes(int fmt, int K, int U) {
+    const size_t np = (size_t)v4_pieces(fmt, K, U);
+    size_t b = (np + (np + 15) / 16) * 16;
+    if (fmt == WF_I4) b += np / 8 * 4;           // one float per 32-element chunk
+    return b;
+}
+
+template <int FMT, int ROWS, int U>
+__global__ __launch_bounds__(256) void gemv_v4_kernel(GemvArgs a) {
+    extern __shared__ f32x4 xs[];
+    constexpr int EPC = WT<FMT>::EPC;
+    constexpr int PPC = EPC / 4;
+    constexpr int STEP = 64 * U;
+    const int K = a.K, M = a.M;
+    const int lane = threadIdx.x & 63;
+    // wave-uniform: the cursor, row addresses and buffer resources live in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int chunks = K / EPC;
+    const int iters = (chunks + STEP - 1) / STEP;
+    const uint32_t row_bytes = (uint32_t)(K / EPC) * 16u;
+    const long pitch = a.ldw > 0 ? a.ldw : (long)row_bytes;
+    const char* Wb = static_cast<const char*>(a.w);
+    const int SEQ = (ROWS == 1 && a.epi == EPI_SILU_MUL) ? 2 : 1;
+    const int n_groups = ((M + ROWS - 1) / ROWS + SEQ - 1) / SEQ;
+    const int S = gridDim.x * 4;
+    const int g0 = blockIdx.x * 4 + wave;
+    const int my_groups = g0 < n_groups ? (n_groups - 1 - g0) / S + 1 : 0;
+    const int total = my_groups * SEQ * iters;
+    // int4 block-scale indexing inside a row (K % block == 0, block = 32 * 2^sh):
+    // chunk ch = ks * STEP + lane + 64 u uses scale (ch >> sh), split into a
+    // uniform, a lane and an immediate part (STEP and 64 u are multiples of 2^sh)
+    int sh = 0;
+    if constexpr (FMT == WF_I4) while ((1 << sh) < a.cpb) ++sh;
+    const int lane_soff = (lane >> sh) * 4;
+    // x piece of chunk ch: xpad((ks * STEP + lane + 64 u) * PPC) splits the
+    // same way (the step and unroll parts are multiples of 16 pieces)
+    const int lane_x = xpad(lane * PPC);
+
+    // ---- cursor over the wave's steps --------------------------------------
+    struct Cur { int ks, sq, grp; };
+    auto first_row = [&](const Cur& c) { return (c.grp * SEQ + c.sq) * ROWS; };
+    auto advance = [&](Cur& c) {
+        if (++c.ks == iters) {
+            c.ks = 0;
+            if (++c.sq == SEQ) { c.sq = 0; c.grp += S; }
+        }
+    };
+    // one step's weights (and int4 raw block scales) for rows r0 .. r0+ROWS-1
+    auto load = [&](const Cur& c, u32x4 (&wb)[U][ROWS], float (&sb)[U][ROWS]) {
+        const int r0 = first_row(c);
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const int row = r0 + r;
+            const bool ok = row < M;
+            const char* rp = Wb + (long)(ok ? row : 0) * pitch;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                uniform_ptr(rp), (short)0,
+                __builtin_amdgcn_readfirstlane(ok ? (int)row_bytes : 0), 0x00020000);
+            const int soff = __builtin_amdgcn_readfirstlane(c.ks * STEP * 16);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                wb[u][r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         rs, lane * 16 + u * 1024, soff, 2));
+            if constexpr (FMT == WF_I4) {
+                const float* sp = a.scales + (long)(ok ? row : 0) * a.bpr;
+                const __amdgpu_buffer_rsrc_t ss = __builtin_amdgcn_make_buffer_rsrc(
+                    uniform_ptr(sp), (short)0, __builtin_amdgcn_readfirstlane(ok ? a.bpr * 4 : 0),
+                    0x00020000);
+                const int s_soff = __builtin_amdgcn_readfirstlane(((c.ks * STEP) >> sh) * 4);
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    sb[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                             ss, lane_soff + ((64 * u) >> sh) * 4, s_soff, 0));
+            }
+        }
+    };
+
+    // ---- x staging (as gemv_n1_kernel), zero tail, int4 corrections --------
+    u32x4 bufA[U][ROWS], bufB[U][ROWS];
+    float sA[U][ROWS], sB[U][ROWS];
+    Cur cl{0, 0, g0};        // next step to load
+    const int kind = stage_kind(a, K);
+    if constexpr (FMT == WF_I4) {
+        if (kind == STAGE_REGS) {
+            XRegs<4> r;
+            stage_regs_issue_buf<4>(a, r, K);
+            __builtin_amdgcn_sched_barrier(0);
+            load(cl, bufA, sA);
+            stage_regs_finish<true, 4>(a, r, xs, K);
+        } else if (kind == STAGE_PLAIN) {
+            f32x4 xv[12];
+            stage_plain_issue<12>(a, xv, K);
+            __builtin_amdgcn_sched_barrier(0);
+            load(cl, bufA, sA);
+            stage_plain_finish<true, 12>(xv, xs, K);
+        } else {
+            load(cl, bufA, sA);
+            stage_x_loop<true>(a, xs, K);
+        }
+    } else {
+        load(cl, bufA, sA);
+        if (kind == STAGE_REGS) {
+            XRegs<4> r;
+            stage_regs_issue<4>(a, r, K);
+            stage_regs_finish<true, 4>(a, r, xs, K);
+        } else if (kind == STAGE_PLAIN) {
+            f32x4 xv[12];
+            stage_plain_issue<12>(a, xv, K);
+            stage_plain_finish<true, 12>(xv, xs, K);
+        } else {
+            stage_x_loop<true>(a, xs, K);
+        }
+    }
+    advance(cl);
+    const int np = K >> 2;
+    const int np_all = iters * STEP * PPC;
+    for (int p = np + (int)threadIdx.x; p < np_all; p += 256) xs[xpad(p)] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float* corr = nullptr;
+    if constexpr (FMT == WF_I4) {
+        __syncthreads();
+        corr = reinterpret_cast<float*>(xs + (np_all + (np_all + 15) / 16));
+        for (int c = threadIdx.x; c < iters * STEP; c += 256) {
+            const int b = xpad(c * PPC);
+            float se = 0.f, so = 0.f;
+#pragma unroll
+            for (int j = 0; j < PPC; ++j) {
+                const f32x4 v = xs[b + j];
+                se += v.x; so += v.y; se += v.z; so += v.w;
+            }
+            corr[c] = 72.0f * se + 1032.0f * so;
+        }
+    }
+    __syncthreads();
+
+    float acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+    unsigned long long best = 0;
+    float gate = 0.0f;
+    Cur cc{0, 0, g0};        // step being computed
+
+    auto compute = [&](const Cur& c, const u32x4 (&wb)[U][ROWS], const float (&sb)[U][ROWS]) {
+        const int xs_step = xpad(c.ks * STEP * PPC);             // uniform
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const f32x4* xb = xs + xs_step + xpad(64 * u * PPC) + lane_x;
+            if constexpr (FMT == WF_I4) {
+                // two x pieces (one word of every row) at a time
+                float ao[ROWS], ae[ROWS];
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) { ao[r] = 0.f; ae[r] = 0.f; }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 xa = xb[2 * j], xc = xb[2 * j + 1];
+#pragma unroll
+                    for (int r = 0; r < ROWS; ++r) {
+                        const u32x4 w = wb[u][r];
+                        const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+                        i4_word_mix(wj, xa, xc, ao[r], ae[r]);
+                    }
+                }
+                const float cr = corr[c.ks * STEP + 64 * u + lane];
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r)
+                    acc[r] = fmaf(sb[u][r], fmaf(ae[r], 0.0625f, ao[r]) - cr, acc[r]);
+            } else {
+                f32x4 x[PPC];
+#pragma unroll
+                for (int j = 0; j < PPC; ++j) x[j] = xb[j];
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) acc[r] = chunk_dot_x<FMT>(wb[u][r], x, acc[r]);
+            }
+        }
+        if (c.ks == iters - 1) {
+            const int r0 = first_row(c);
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
+            if constexpr (FMT == WF_I8) {
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) acc[r] *= a.scales[r0 + r < M ? r0 + r : M - 1];
+            }
+            if (a.epi == EPI_SILU_MUL) {
+                if constexpr (ROWS % 2 == 0) {
+#pragma unroll
+                    for (int r = 0; r < ROWS; r += 2)
+                        if (lane == r && r0 + r + 1 < M) a.y[(r0 + r) >> 1] = silu_f(acc[r]) * acc[r + 1];
+                } else if (ROWS == 1) {
+                    if ((r0 & 1) == 0) gate = acc[0];
+                    else if (lane == 0 && r0 < M) a.y[r0 >> 1] = silu_f(gate) * acc[0];
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r)
+                    if (lane == r && r0 + r < M) a.y[r0 + r] = acc[r];
+                if (a.epi == EPI_ARGMAX) {
+#pragma unroll
+                    for (int r = 0; r < ROWS; ++r)
+                        if (r0 + r < M) {
+                            const unsigned long long k = argkey_f(acc[r], r0 + r);
+                            best = k > best ? k : best;
+                        }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+        }
+    };
+
+    // two register buffers, renamed by unrolling the step loop by two
+    for (int t = 0; t < total; t += 2) {
+        if (t + 1 < total) { load(cl, bufB, sB); advance(cl); }
+        compute(cc, bufA, sA);
+        advance(cc);
+        if (t + 1 >= total) break;
+        if (t + 2 < total) { load(cl, bufA, sA); advance(cl); }
+        compute(cc, bufB, sB);
+        advance(cc);
+    }
+    if (a.epi == EPI_ARGMAX && lane == 0) a.arg_part[blockIdx.x * 4 + wave] = best;
+}
+
 // Any-shape fallback (K not a multiple of the chunk width, tiny matrices):
 // one wave per row, scalar loads.  Used for reference-API compatibility.
 template <int FMT>
@@ -786,12 +1096,81 @@ static const void* n1_kernel(int fmt, int rows, int unroll) {
     return nullptr;
 }
 
+// The decode kernel (gemv_v4_kernel) covers every fast-path shape except
+// int4 blocks that straddle rows or are not 32 * 2^j elements.
+static bool v4_ok(const GemvArgs& a, int unroll) {
+    if (a.fmt == WF_I4 && (a.bpr <= 0 || (a.cpb & (a.cpb - 1)) != 0)) return false;
+    return v4_lds_bytes(a.fmt, a.K, unroll) <= 160 * 1024;
+}
+
+// Launch shape of the decode kernel per (format, role): rows per wave,
+// chunk unroll, blocks per CU.  From a sweep of rows 1/2/4, unroll 1-8 and
+// 2-8 blocks per CU at the 7B shapes on MI355X over >= 1.2 GB of rotating
+// weights (the best shapes of a role lie within 1-3% of each other).
+static N1Shape v4_shape(int fmt, int M, int K, int epi) {
+    const bool gu = epi == EPI_SILU_MUL, wide = K > 4096, huge = M >= 65536, tall = M >= 8192;
+    switch (fmt) {
+    case WF_BF16:
+        if (gu || wide) return {2, 4, 4};
+        if (huge) return {2, 4, 6};
+        return tall ? N1Shape{2, 4, 3} : N1Shape{2, 4, 8};
+    case WF_I8:
+        if (gu) return {2, 2, 4};
+        if (wide) return {1, 4, 8};
+        if (huge) return {2, 4, 8};
+        return tall ? N1Shape{2, 2, 4} : N1Shape{1, 2, 4};
+    case WF_I4:
+        if (gu) return {2, 1, 3};
+        if (wide) return {2, 2, 4};
+        if (huge) return {2, 1, 8};
+        return tall ? N1Shape{2, 2, 2} : N1Shape{2, 2, 8};
+    default:
+        return {1, 4, 8};
+    }
+}
+
+#define ATLAS_V4_LIST(X)                                                           \
+    X(WF_BF16, 2, 4)                                                               \
+    X(WF_I8, 1, 2) X(WF_I8, 1, 4) X(WF_I8, 2, 2) X(WF_I8, 2, 4)                    \
+    X(WF_I4, 2, 1) X(WF_I4, 2, 2)                                                  \
+    X(WF_F32, 1, 4)
+
+static const void* v4_kernel(int fmt, int rows, int unroll) {
+#define ATLAS_V4_PTR(F, R, U) \
+    if (fmt == F && rows == R && unroll == U) return (const void*)gemv_v4_kernel<F, R, U>;
+    ATLAS_V4_LIST(ATLAS_V4_PTR)
+#undef ATLAS_V4_PTR
+    return nullptr;
+}
+
 // number of persistent waves gemv_launch uses (argmax partial count)
-int gemv_waves(const GemvArgs& a) {
+int gemv_waves(const GemvArgs& a_in) {
+    GemvArgs a = a_in;
+    gemv_fill_int4_index(a);
+    const N1Shape v4 = v4_shape(a.fmt, a.M, a.K, a.epi);
+    if (v4_ok(a, v4.unroll)) {
+        const void* kern = v4_kernel(a.fmt, v4.rows, v4.unroll);
+        return kern ? 4 * n1_blocks(kern, a.M, v4_lds_bytes(a.fmt, a.K, v4.unroll),
+                                    n1_group_rows(a, v4.rows), v4.bpc)
+                    : 0;
+    }
     const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
     const void* kern = n1_kernel(a.fmt, sh.rows, sh.unroll);
     return kern ? 4 * n1_blocks(kern, a.M, gemv_x_lds_bytes(a.K), n1_group_rows(a, sh.rows), sh.bpc)
                 : 0;
+}
+
+template <int FMT, int ROWS, int UNROLL>
+int launch_v4(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
+    const size_t lds = v4_lds_bytes(FMT, a.K, UNROLL);
+    auto kern = gemv_v4_kernel<FMT, ROWS, UNROLL>;
+    const int blocks = n1_blocks((const void*)kern, a.M, lds, n1_group_rows(a, ROWS), blocks_per_cu);
+    ATLAS_REQUIRE(blocks > 0, "gemv: the kernel does not fit a CU at K=%d", a.K);
+    if (a.epi == EPI_ARGMAX)
+        ATLAS_REQUIRE(blocks * 4 <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a);
+    ATLAS_LAUNCH_CHECK("gemv_v4");
+    return ATLAS_OK;
 }
 
 int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
@@ -820,6 +1199,13 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     const bool fast = (align & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
                       gemv_x_lds_bytes(a.K) <= 160 * 1024;
     if (fast) {
+        const N1Shape v4 = v4_shape(a.fmt, a.M, a.K, a.epi);
+        if (v4_ok(a, v4.unroll)) {
+#define ATLAS_V4(F, R, U) \
+            if (a.fmt == F && v4.rows == R && v4.unroll == U) return launch_v4<F, R, U>(a, st, v4.bpc);
+            ATLAS_V4_LIST(ATLAS_V4)
+#undef ATLAS_V4
+        }
         const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
 #define ATLAS_N1(F, R, U) \
         if (a.fmt == F && sh.rows == R && sh.unroll == U) return launch_n1<F, R, U>(a, st, sh.bpc);

@@ -237,7 +237,8 @@ def main() -> int:
     ap.add_argument("--loader-only", action="store_true", help="only the loader measurement")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="short program for rocprofv3 --pmc passes: a 1 GiB device copy "
-                         "(calibration), then one launch set of each bf16 decode GEMV kernel")
+                         "(calibration), then one launch set of each decode GEMV kernel of the "
+                         "bf16, int8 and int4 7B models and two decode steps each")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -509,10 +510,12 @@ def loader_bench(torch, am, n_layers: int = 4) -> dict:
 
 
 def pmc_probe(torch, lib, am) -> int:
-    """Dispatches whose HBM counters calibrate and measure `traffic`: three
-    copies of 1 GiB (2 GiB moved each: FETCH_SIZE and WRITE_SIZE of a plain
-    copy of known size), then the bf16 7B model's GEMV sets (bench_gemv which
-    = 3, 1, 2), one launch each."""
+    """Dispatches whose counters calibrate and measure the decode kernels:
+    three copies of 1 GiB (2 GiB moved each: FETCH_SIZE and WRITE_SIZE of a
+    plain copy of known size), then for the bf16, int8 and int4 7B models one
+    launch of each GEMV set (bench_gemv which = 3 gate/up, 1 QKV + W_o +
+    lm_head, 2 W_down) and two decode steps at positions 1 and 2 (attention,
+    argmax).  Kernels are told apart by name and grid size."""
     n = 1 << 28
     src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
@@ -521,17 +524,23 @@ def pmc_probe(torch, lib, am) -> int:
     torch.cuda.synchronize()
     log(f"pmc probe: copy of {n * 4} bytes x3 done")
     del src, dst
-    m = am.OlmoModel(am.ModelConfig.olmo3_actual_7b(), weight_format=am.W_BF16, int4_block=32)
-    m.init_random(7)
-    m.reset()
-    m.forward_one(1)
-    ms, launches, nbytes = C.c_float(), C.c_int(), C.c_int64()
-    for which in (3, 1, 2):
-        assert lib.atlas_model_bench_gemv(m._h, 1, which, C.byref(ms), C.byref(launches),
-                                          C.byref(nbytes)) == 0
-        log(f"pmc probe: GEMV set {which}: {launches.value} launches, {nbytes.value} "
-            f"algorithmic bytes, {ms.value:.3f} ms")
-    m.close()
+    for fmt, name in ((am.W_BF16, "bf16"), (am.W_INT8, "int8"), (am.W_INT4, "int4")):
+        import dataclasses
+        cfg = dataclasses.replace(am.ModelConfig.olmo3_actual_7b(), max_seq_len=256)
+        m = am.OlmoModel(cfg, weight_format=fmt, int4_block=32)
+        m.init_random(7)
+        m.reset()
+        m.forward_one(1)
+        ms, launches, nbytes = C.c_float(), C.c_int(), C.c_int64()
+        for which in (3, 1, 2):
+            assert lib.atlas_model_bench_gemv(m._h, 1, which, C.byref(ms), C.byref(launches),
+                                              C.byref(nbytes)) == 0
+            log(f"pmc probe {name}: GEMV set {which}: {launches.value} launches, {nbytes.value} "
+                f"algorithmic bytes, {ms.value:.3f} ms")
+        m.forward_one(2)
+        m.forward_one(3)
+        torch.cuda.synchronize()
+        m.close()
     return 0
 
 
