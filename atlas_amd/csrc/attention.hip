@@ -387,6 +387,62 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
     }
 }
 
+// Split merge of the fused kernel, run by the block that arrives last.  The
+// partials of query head qh, split s sit at index qh * n_splits + s (o: times
+// HD) of part_m / part_l / part_o; other XCDs wrote them, so they are read
+// with sc1 loads (past this XCD's L2, which can still hold an earlier
+// launch's lines).  A thread owns (head, dim) elements and reads the splits in
+// groups of 8, every load of a group issued before the first is used, with a
+// running maximum across groups: one memory round trip per 8 splits instead
+// of one per split.  Empty splits carry (m, l, o) = (-inf, 0, 0) and weigh 0;
+// the split holding pos is never empty, so the final maximum is finite.
+template <int HD, int G, int NT>
+__device__ __forceinline__ void merge_splits(const float* part_m, const float* part_l, const float* part_o,
+                                             int n_splits, int kvh, float* out) {
+    constexpr int SC1 = 16;                   // buffer cache policy: sc1
+    const int nh = n_splits * G;              // this kv head's (head, split) pairs
+    const long h0 = (long)kvh * G * n_splits;
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_m + h0), (short)0, nh * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rl =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_l + h0), (short)0, nh * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ro =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_o + h0 * HD), (short)0, nh * HD * 4, 0x00020000);
+    for (int e = threadIdx.x; e < G * HD; e += NT) {
+        const int h = e / HD, d = e % HD;
+        float M = -INFINITY, L = 0.f, O = 0.f;
+        for (int s0 = 0; s0 < n_splits; s0 += 8) {
+            float mv[8], lv[8], ov[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = h * n_splits + min(s0 + j, n_splits - 1);   // past the end: a copy
+                mv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, i * 4, 0, SC1));
+                lv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, i * 4, 0, SC1));
+                ov[j] = __builtin_bit_cast(float,
+                                           __builtin_amdgcn_raw_buffer_load_b32(ro, (i * HD + d) * 4, 0, SC1));
+            }
+            float cm = M;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (s0 + j >= n_splits) mv[j] = -INFINITY;                // ... which weighs 0
+                cm = fmaxf(cm, mv[j]);
+            }
+            if (cm == -INFINITY) continue;   // every split so far is empty
+            const float c = exp2f(M - cm);    // 0 while M = -inf
+            L *= c;
+            O *= c;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float w = exp2f(mv[j] - cm);
+                L += lv[j] * w;
+                O += ov[j] * w;
+            }
+            M = cm;
+        }
+        out[(long)(kvh * G + h) * HD + d] = O / L;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Fused decode attention for one layer: per-head QK-norm (eps 1e-6,
 // crates/atlas-model/src/lib.rs:660-672) and rotate-half RoPE from the tables
@@ -415,11 +471,13 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     const int slot = a.slot_dev ? a.slot_dev[seq] : 0;
     const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
     const int ctx = pos - t_lo + 1;
-    // active splits: all gridDim.y, or one per min_chunk positions of the live
-    // context (the grid is fixed when a decode step is captured once and
-    // replayed at every position; surplus blocks leave here)
+    // active splits: all gridDim.y, the measured rule for the live context,
+    // or one per min_chunk positions of it (the grid is fixed when a decode
+    // step is captured once and replayed at every position; surplus blocks
+    // leave here)
     int n_splits = gridDim.y;
-    if (a.min_chunk > 0) n_splits = min(n_splits, max(1, (ctx + a.min_chunk - 1) / a.min_chunk));
+    if (a.adaptive) n_splits = min(n_splits, attn_fused_splits_for(a.n_kv * (int)gridDim.z, ctx));
+    else if (a.min_chunk > 0) n_splits = min(n_splits, max(1, (ctx + a.min_chunk - 1) / a.min_chunk));
     if (split >= n_splits) return;
     const int chunk = (ctx + n_splits - 1) / n_splits;
     const int b0 = t_lo + split * chunk;
@@ -551,55 +609,35 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         if (n_splits == 1) {
             a.out[(long)seq * a.out_stride + (long)qh * HD + d] = osum / lsum;
         } else {
+            // agent-scope stores (sc1): they reach memory past this XCD's L2,
+            // so a block on another XCD reads them without the L2 write-back
+            // a device-scope release fence would cost
             const long pi = pbase + (long)qh * n_splits + split;
-            a.part_o[pi * HD + d] = osum;
-            if (d == 0) { a.part_m[pi] = mx; a.part_l[pi] = lsum; }
+            __hip_atomic_store(&a.part_o[pi * HD + d], osum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d == 0) {
+                __hip_atomic_store(&a.part_m[pi], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.part_l[pi], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     if (n_splits == 1) return;
     // ---- the last block of this (seq, kv head) merges the splits -------------
-    __threadfence();
+    // Every thread's partial stores have completed (vmcnt 0) before the block
+    // bumps the counter, so the block that sees n_splits - 1 earlier arrivals
+    // reads complete partials with agent-scope (sc1) loads.
+    __builtin_amdgcn_s_waitcnt(0x0F70);        // vmcnt(0)
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int prev = atomicAdd(&a.counters[seq * a.n_kv + kvh], 1);
+        const int prev = __hip_atomic_fetch_add(&a.counters[seq * a.n_kv + kvh], 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == n_splits - 1;
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    // Split weights of the G heads through LDS first; every (split, dim)
-    // partial is then an independent load.  Empty splits carry m = -inf and
-    // weigh exp2(-inf) = 0.
-    __shared__ float s_wt[G][kAttnFusedMaxSplits];
-    __shared__ float s_mx[G];
-    const long ph = pbase + (long)kvh * G * n_splits;     // head kvh*G, split 0
-    for (int i = threadIdx.x; i < G * n_splits; i += 64 * W)
-        s_wt[i / n_splits][i % n_splits] =
-            __hip_atomic_load(&a.part_m[ph + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (threadIdx.x < G) {
-        float mx = -INFINITY;
-        for (int s2 = 0; s2 < n_splits; ++s2) mx = fmaxf(mx, s_wt[threadIdx.x][s2]);
-        s_mx[threadIdx.x] = mx;
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < G * n_splits; i += 64 * W) {
-        const int h = i / n_splits, s2 = i % n_splits;
-        s_wt[h][s2] = exp2f(s_wt[h][s2] - s_mx[h]);
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < G * HD; e += 64 * W) {
-        const int h = e / HD, d = e % HD;
-        const long p0 = ph + (long)h * n_splits;
-        float lsum = 0.f, osum = 0.f;
-        for (int s2 = 0; s2 < n_splits; ++s2) {
-            const float w = s_wt[h][s2];
-            lsum += __hip_atomic_load(&a.part_l[p0 + s2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * w;
-            osum += __hip_atomic_load(&a.part_o[(p0 + s2) * HD + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * w;
-        }
-        a.out[(long)seq * a.out_stride + (long)(kvh * G + h) * HD + d] = osum / lsum;
-    }
-    if (threadIdx.x == 0) atomicExch(&a.counters[seq * a.n_kv + kvh], 0);
+    merge_splits<HD, G, 64 * W>(a.part_m + pbase, a.part_l + pbase, a.part_o + pbase * HD, n_splits,
+                                kvh, a.out + (long)seq * a.out_stride);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&a.counters[seq * a.n_kv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Waves per block.  Measured on MI355X at the 7B and GQA-32/8 shapes, ctx
@@ -653,22 +691,21 @@ int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream
 // ---------------------------------------------------------------------------
 
 int attn_max_splits(int n_kv) {
-    // Measured on MI355X (7B shapes, ctx 64..8192): the merge's device-scope
-    // release (an L2 write-back per block) makes grids beyond ~128 blocks
-    // slower, whatever the context; 8 splits of a GQA head already stream
-    // at the scan's rate.
-    int s = 128 / (n_kv > 0 ? n_kv : 1);
-    return s < 1 ? 1 : (s > 8 ? 8 : s);
+    // At most 256 blocks: with the partials published by sc1 stores (no L2
+    // write-back per block) the GQA 32/8/128 shape keeps gaining up to 32
+    // splits at ctx 16384, and no measured shape gains past 256 blocks.
+    const int s = 256 / (n_kv > 0 ? n_kv : 1);
+    return s < 1 ? 1 : (s > kAttnFusedMaxSplits ? kAttnFusedMaxSplits : s);
 }
 
 int attn_pick_splits_unfused(int n_kv, int ctx) { return attn_splits_for(n_kv, ctx); }
 
 int attn_pick_splits(int n_kv, int max_ctx) {
-    // one split per kAttnSplitChunk positions, within attn_max_splits
-    const int by_ctx = (max_ctx + kAttnSplitChunk - 1) / kAttnSplitChunk;
+    // the fused rule at the longest context (its split count only grows with
+    // ctx past the one-split range), within attn_max_splits
+    const int s = attn_fused_splits_for(n_kv, max_ctx);
     const int cap = attn_max_splits(n_kv);
-    const int s = by_ctx < cap ? by_ctx : cap;
-    return s < 1 ? 1 : s;
+    return s < cap ? s : cap;
 }
 
 template <int HD, int G>

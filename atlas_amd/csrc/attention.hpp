@@ -54,6 +54,8 @@ struct AttnFusedArgs {
     float* part_o;           // [n_seq][n_heads][n_splits][hd]
     int* counters;           // [n_seq][n_kv], zero before the first launch
     int min_chunk;           // > 0: active splits = min(grid, ceil(ctx / min_chunk))
+    int adaptive;            // 1 (min_chunk ignored): active splits = min(grid,
+                             // attn_fused_splits_for(n_kv * n_seq, ctx))
     int max_rows;            // cache rows per slot (max_seq), > 0
 };
 
@@ -93,6 +95,24 @@ __host__ __device__ inline int attn_batch_splits_for(int n_kv, int n_seq, int ct
     if (n_seq <= 1) return attn_splits_for(n_kv, ctx);
     const int streams = n_kv * n_seq;
     return streams >= 128 ? 1 : attn_splits_for(streams, ctx);
+}
+
+// Split count of the fused kernel for a live context ctx over `streams`
+// (sequence, KV head) pairs.  Fitted to a sweep on MI355X (the 7B shape
+// 32/32/128 at ctx 150..4000, GQA 32/8/128 at ctx 512..16384): one split
+// while 32+ streams each hold < 256 positions (the split merge then costs
+// more than the scan it shortens), else one split per 512 positions, raised
+// towards 128 blocks while splits keep >= 64 positions, at most 256 blocks.
+__host__ __device__ inline int attn_fused_splits_for(int streams, int ctx) {
+    const int ns = streams > 0 ? streams : 1;
+    if (ns >= 32 && ctx < 256) return 1;
+    int s = (ctx + kAttnSplitChunk - 1) / kAttnSplitChunk;
+    const int wide = 128 / ns < ctx / 64 ? 128 / ns : ctx / 64;
+    if (wide > s) s = wide;
+    const int cap = 256 / ns > 1 ? 256 / ns : 1;
+    if (s > cap) s = cap;
+    if (s > kAttnFusedMaxSplits) s = kAttnFusedMaxSplits;
+    return s < 1 ? 1 : s;
 }
 
 bool attn_fused_supported(int n_heads, int n_kv, int head_dim);

@@ -35,13 +35,15 @@ using namespace atlas;
 
 namespace {
 
-// Context length from which the fused step's attention (one launch per layer,
-// at most 128 blocks because of its in-kernel split merge) gives way to three
-// launches: QK-norm/RoPE/KV write, the split kernel over up to 256 blocks, and
-// the split merge (the two-kernel path of atlas_decode_attention).  Measured
-// on the 7B bf16 decode: 2.86 vs 2.99 ms/token at ctx 400, 3.12 vs 3.04 at
-// 656, 3.66 vs 3.34 at 2192 and 4.23 vs 3.65 at 4240 (fused vs long).
-constexpr int kLongAttnFrom = 512;
+// Context length from which decode steps give the fused attention (one
+// launch per layer, split merge inside the kernel) up for three launches:
+// QK-norm/RoPE/KV write, the split kernel and the split merge (the two-kernel
+// path of atlas_decode_attention).  With the fused kernel's partials published
+// by sc1 stores and its split count fitted per context it is the faster step
+// at every measured context of the 7B bf16 decode (2.89 vs 2.99 ms/token at
+// ctx 600, 2.93 vs 3.12 at 1200, 3.37 vs 3.52 at 4000), so the long-context
+// step runs only from a position the caller sets.
+constexpr int kLongAttnFrom = 1 << 30;
 // Rows of the multi-row step, and prompt tokens per prefill step: the
 // multi-row GEMV for 2-3 rows, the skinny MFMA kernel for 4-16.
 constexpr int kPrefillChunk = 16;
@@ -419,7 +421,7 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
             a.part_l = m->attn_part + (size_t)m->R * c.n_heads * m->attn_splits;
             a.part_o = m->attn_part + (size_t)2 * m->R * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
-            a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
+            a.adaptive = 1; a.max_rows = c.max_seq;
             TRY(attn_fused_launch(a, m->attn_splits, 1, m->st));
         }
         TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
@@ -1061,7 +1063,7 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             a.part_l = m->attn_part + (size_t)m->R * c.n_heads * m->attn_splits;
             a.part_o = m->attn_part + (size_t)2 * m->R * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
-            a.min_chunk = kAttnSplitChunk; a.max_rows = c.max_seq;
+            a.adaptive = 1; a.max_rows = c.max_seq;
             TRY(attn_fused_launch(a, m->attn_splits, n, m->st));
         }
         if (!m->fused) TRY(qkv_post_launch(q, n, m->st));
@@ -1314,9 +1316,9 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         }
     }
     // Split counts.  The fused kernel sizes its grid for the longest context
-    // and activates one split per kAttnSplitChunk positions of the live
-    // context, so short contexts run one block per KV head and merge nothing.
-    // The unfused kernel's count is fixed at launch.
+    // and activates attn_fused_splits_for(n_kv * n_seq, ctx) of its splits at
+    // the live context, so short contexts run one block per KV head and merge
+    // nothing.  The unfused kernel's count is fixed at launch.
     m->attn_splits = attn_pick_splits(c.n_kv_heads, c.max_seq);
     m->attn_splits_unfused = m->attn_splits;
     m->attn_splits_long = attn_splits_for(c.n_kv_heads, c.max_seq);

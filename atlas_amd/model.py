@@ -195,7 +195,8 @@ class OlmoModel:
 
     def set_long_context(self, from_pos: int) -> None:
         """Position from which decode steps use the long-context attention
-        path (extension; default 512)."""
+        path (extension; default: never, the fused step is faster at every
+        measured context)."""
         check(load().atlas_model_set_long_context(self._h, from_pos))
 
     def prefill(self, tokens: Sequence[int]) -> None:

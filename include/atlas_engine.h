@@ -182,8 +182,9 @@ int atlas_sample_device(const float* logits, int vocab, const uint32_t* hist, in
 
 /* Extension: position from which decode steps run the long-context attention
  * (QK-norm/RoPE/KV-write kernel, split kernel over up to 256 blocks, split
- * merge) instead of the one-launch fused attention; default 512.  Each path
- * is captured in its own graph; the choice is made per step on the host.  */
+ * merge) instead of the one-launch fused attention; default: never (the
+ * fused step is the faster one at every measured context).  Each path is
+ * captured in its own graph; the choice is made per step on the host.      */
 int atlas_model_set_long_context(atlas_model* m, int from_pos);
 
 /* Benchmark helper: greedy decode of n_steps tokens continuing from the
