@@ -471,6 +471,7 @@ int enqueue_step(atlas_model* m, int mode, bool long_ctx) {
 }
 
 void drop_graphs(atlas_model* m) {
+    if (m->st) (void)hipStreamSynchronize(m->st);   // no replay of them still running
     for (auto& g : m->gexec)
         if (g) {
             (void)hipGraphExecDestroy(g);
