@@ -128,6 +128,7 @@ SIGNATURES = {
                                            C.POINTER(C.c_int)]),
     "atlas_model_generate_batch": (I, [P, P, P, I, I, C.POINTER(SamplingC), P, P]),
     "atlas_model_decode_greedy": (I, [P, U32, I, P]),
+    "atlas_model_decode_greedy_timed": (I, [P, U32, I, P, P]),
     "atlas_model_set_long_context": (I, [P, I]),
     "atlas_model_prefill": (I, [P, P, I]),
     "atlas_model_set_prefill_chunk": (I, [P, I]),

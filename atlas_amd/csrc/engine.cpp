@@ -1760,8 +1760,8 @@ ATLAS_API int atlas_model_generate_hooked(atlas_model* m, const uint32_t* prompt
     return ATLAS_OK;
 }
 
-ATLAS_API int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, int n_steps,
-                                        uint32_t* tokens) {
+static int decode_greedy(atlas_model* m, uint32_t first_token, int n_steps, uint32_t* tokens,
+                         float* step_ms) {
     ATLAS_REQUIRE(m && n_steps >= 0, "decode_greedy: bad arguments");
     ATLAS_REQUIRE(m->pos + n_steps <= m->cfg.max_seq, "decode_greedy: exceeds max_seq");
     TRY(set_greedy_cfg(m, nullptr));
@@ -1770,11 +1770,41 @@ ATLAS_API int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, in
     ATLAS_HIP(hipMemcpyAsync(m->step_dev, &zero, 4, hipMemcpyHostToDevice, m->st));
     TRY(sync_pos(m));
     TRY(set_token(m, first_token));
-    for (int i = 0; i < n_steps; ++i) TRY(run_step(m, 1));
-    if (tokens && n_steps > 0)
-        ATLAS_HIP(hipMemcpyAsync(tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost, m->st));
-    ATLAS_HIP(hipStreamSynchronize(m->st));
-    return ATLAS_OK;
+    // step_ms: an event after every step (and one before the first), on the
+    // engine stream, so step i's GPU time is the span between two of them
+    std::vector<hipEvent_t> ev;
+    int rc = ATLAS_OK;
+    if (step_ms) {
+        ev.resize((size_t)n_steps + 1, nullptr);
+        for (auto& e : ev)
+            if (!rc && hipEventCreate(&e) != hipSuccess) rc = ATLAS_EHIP;
+        if (!rc && hipEventRecord(ev[0], m->st) != hipSuccess) rc = ATLAS_EHIP;
+    }
+    for (int i = 0; i < n_steps && !rc; ++i) {
+        rc = run_step(m, 1);
+        if (!rc && step_ms && hipEventRecord(ev[i + 1], m->st) != hipSuccess) rc = ATLAS_EHIP;
+    }
+    if (!rc && tokens && n_steps > 0 &&
+        hipMemcpyAsync(tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost, m->st) != hipSuccess)
+        rc = ATLAS_EHIP;
+    if (hipStreamSynchronize(m->st) != hipSuccess && !rc) rc = ATLAS_EHIP;
+    for (int i = 0; i < n_steps && !rc && step_ms; ++i)
+        if (hipEventElapsedTime(&step_ms[i], ev[i], ev[i + 1]) != hipSuccess) rc = ATLAS_EHIP;
+    for (auto e : ev)
+        if (e) (void)hipEventDestroy(e);
+    if (rc == ATLAS_EHIP) set_error(ATLAS_EHIP, "decode_greedy: HIP call failed");
+    return rc;
+}
+
+ATLAS_API int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, int n_steps,
+                                        uint32_t* tokens) {
+    return decode_greedy(m, first_token, n_steps, tokens, nullptr);
+}
+
+ATLAS_API int atlas_model_decode_greedy_timed(atlas_model* m, uint32_t first_token, int n_steps,
+                                              uint32_t* tokens, float* step_ms) {
+    ATLAS_REQUIRE(step_ms, "decode_greedy_timed: null step_ms");
+    return decode_greedy(m, first_token, n_steps, tokens, step_ms);
 }
 
 ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float* ms,

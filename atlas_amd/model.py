@@ -340,3 +340,11 @@ class OlmoModel:
         toks = np.empty(max(n_steps, 1), np.uint32)
         check(load().atlas_model_decode_greedy(self._h, first_token, n_steps, _p(toks)))
         return toks[:n_steps]
+
+    def decode_greedy_timed(self, first_token: int, n_steps: int):
+        """decode_greedy plus each step's GPU time in ms (HIP events on the
+        engine stream after every step): (tokens, step_ms)."""
+        toks = np.empty(max(n_steps, 1), np.uint32)
+        ms = np.zeros(max(n_steps, 1), np.float32)
+        check(load().atlas_model_decode_greedy_timed(self._h, first_token, n_steps, _p(toks), _p(ms)))
+        return toks[:n_steps], ms[:n_steps]

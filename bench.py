@@ -31,9 +31,10 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of each bf16 decode GEMV kernel: rocprofv3 FETCH_SIZE x 2
 # + WRITE_SIZE x 1 (the factors a 1 GiB copy reads on this part), measured by
-# `bench.py --pmc-probe` (profiles/gemv_bf16_7b_hbm_traffic.md).
-TRAFFIC = {"gate_up": 180976635, "qkv_wo_lm_head": 79177037, "w_down": 90670047}
+# `bench.py --pmc-probe` (profiles/gemv_7b_counters.md).
+TRAFFIC = {"gate_up": 180980000, "qkv_wo_lm_head": 79151230, "w_down": 90680000}
 ROOT = os.path.dirname(os.path.abspath(__file__))
+SPREAD: dict = {}
 
 
 def log(msg: str) -> None:
@@ -216,10 +217,57 @@ def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int
     PREFILL[fmt] = pre
     toks = m.decode_greedy(int(prompt[-1]), warmup)
     t0 = time.perf_counter()
-    toks2 = m.decode_greedy(int(toks[-1]) if warmup else int(prompt[-1]), steps)
+    toks2, step_ms = m.decode_greedy_timed(int(toks[-1]) if warmup else int(prompt[-1]), steps)
     dt = time.perf_counter() - t0
     assert len(toks2) == steps
+    SPREAD[fmt] = step_spread(step_ms)
     return m, dt
+
+
+def step_spread(step_ms) -> dict:
+    """Median and p10/p90 of the per-step GPU times (HIP events recorded on
+    the engine stream after every step of the timed run)."""
+    a = np.asarray(step_ms, np.float64)
+    return {"p10_ms": round(float(np.percentile(a, 10)), 4),
+            "median_ms": round(float(np.median(a)), 4),
+            "p90_ms": round(float(np.percentile(a, 90)), 4),
+            "mean_ms": round(float(a.mean()), 4), "steps": int(a.size)}
+
+
+def generate_rates(m, am) -> dict:
+    """Two end-to-end rates of the reference's own forms on the loaded 7B
+    model: n / elapsed(generate(&[1, 2, 3], n, 0.0)) with n = 30
+    (crates/atlas-model/src/lib.rs:4312-4316; prompt, host loop and logits
+    included) and the hooked generate (a host callback after every layer,
+    lib.rs:1452-1461), both greedy."""
+    from atlas_amd.model import SamplingConfig
+    m.reset()
+    m.generate([1, 2, 3], 4, 0.0)                   # captures, warm
+    n = 30
+    m.reset()
+    t0 = time.perf_counter()
+    out = m.generate([1, 2, 3], n, 0.0)
+    ref_style = n / (time.perf_counter() - t0)
+    assert len(out) == n
+    seen = [0]
+
+    def hook(li, h):
+        seen[0] += 1
+        return None
+
+    nh = 16
+    m.reset()
+    m.generate_with_sampling_hooked([1, 2, 3], 2, SamplingConfig.greedy(), hook)
+    m.reset()
+    seen[0] = 0
+    t0 = time.perf_counter()
+    outh, _ = m.generate_with_sampling_hooked([1, 2, 3], nh, SamplingConfig.greedy(), hook)
+    hooked = len(outh) / (time.perf_counter() - t0)
+    log(f"generate([1,2,3], {n}, 0.0): {ref_style:.1f} tok/s; hooked generate: {hooked:.1f} tok/s "
+        f"({seen[0]} hook calls for {len(outh)} tokens)")
+    return {"reference_style_tok_s": round(ref_style, 2),
+            "reference_style_form": "n / elapsed(generate([1,2,3], n=30, temperature 0.0))",
+            "hooked_generate_tok_s": round(hooked, 2), "hooked_tokens": len(outh)}
 
 
 def main() -> int:
@@ -320,10 +368,11 @@ def main() -> int:
     step_bytes = wbytes + kv_bytes + 100278 * 4
     step_floor_ms = step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
 
+    rates = generate_rates(m, am)
     # bench the GPU CPU-baseline inputs before freeing the model
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(m, am, prompt)
+        cpu = cpu_baseline(m, am, prompt, "bf16")
     m.close()
     del m
 
@@ -336,8 +385,11 @@ def main() -> int:
                        "ms_per_step": round(dtq * 1e3 / args.steps, 4),
                        "weight_bytes": int(wq),
                        "weight_GB_s": round(wq / (dtq / args.steps) / 1e9, 1)}
+        quant[name]["step_spread"] = SPREAD.get(fmt)
         log(f"{name} decode: {dtq * 1e3 / args.steps:.3f} ms/token, {args.steps / dtq:.1f} tok/s, "
             f"weights {wq / 1e9:.2f} GB")
+        if name == "int8" and cpu is not None:
+            cpu["int8"] = cpu_baseline(mq, am, prompt, "int8")
         mq.close()
         del mq
 
@@ -370,6 +422,8 @@ def main() -> int:
                      "bytes_per_launch": dom["bytes_per_launch"],
                      "us_per_launch": dom["us_per_launch"]},
         "gemv_kernels": kernels,
+        "step_spread": SPREAD.get(am.W_BF16),
+        "generate_rates": rates,
         "step_roofline": {"bytes_per_step": int(step_bytes),
                           "floor_ms": round(step_floor_ms, 4),
                           "frac_of_step_at_roofline": round(step_floor_ms / ms_step, 4),
@@ -544,32 +598,52 @@ def pmc_probe(torch, lib, am) -> int:
     return 0
 
 
-def cpu_baseline(m, am, prompt) -> dict:
-    """The oracle (restatement of the reference CPU path, one core) on one
-    7B decode step of the same bf16 weights, downloaded from the GPU."""
+def cpu_info() -> dict:
+    """The host the CPU baseline ran on: its CPU model and core counts."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(),
+            "cores_available": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline(m, am, prompt, fmt: str) -> dict:
+    """The oracle (restatement of the reference CPU path) on one 7B decode
+    step of the same weights (bf16, or int8 with its row scales), downloaded
+    from the GPU; the process is pinned to one host core for the timed step."""
     sys.path.insert(0, ROOT)
     import oracle as orc
-    cfg = am.ModelConfig.olmo3_actual_7b()
     d, V, L, f = 4096, 100278, 32, 11008
     t0 = time.perf_counter()
     shapes = {am.T_WQ: (d, d), am.T_WK: (d, d), am.T_WV: (d, d), am.T_WO: (d, d),
               am.T_W_GATE: (f, d), am.T_W_UP: (f, d), am.T_W_DOWN: (d, f)}
     names = {am.T_WQ: "wq", am.T_WK: "wk", am.T_WV: "wv", am.T_WO: "wo", am.T_W_GATE: "w_gate",
              am.T_W_UP: "w_up", am.T_W_DOWN: "w_down"}
+
+    def mat(k, li, shp):
+        if fmt == "bf16":
+            return orc.MatView.bf16(m.get_tensor(k, li, shp, np.uint16), *shp)
+        q, sc = m.get_tensor(k, li, shp, np.int8, n_scales=shp[0])
+        return orc.MatView.int8(q, sc)
+
     layers = []
     for li in range(L):
-        ld = {}
-        for k, shp in shapes.items():
-            ld[names[k]] = orc.MatView.bf16(m.get_tensor(k, li, shp, np.uint16), *shp)
+        ld = {names[k]: mat(k, li, shp) for k, shp in shapes.items()}
         ld["attn_norm"] = m.get_tensor(am.T_ATTN_NORM, li, (d,), np.float32)
         ld["ffn_norm"] = m.get_tensor(am.T_FFN_NORM, li, (d,), np.float32)
         ld["q_norm"] = m.get_tensor(am.T_Q_NORM, li, (d,), np.float32)
         ld["k_norm"] = m.get_tensor(am.T_K_NORM, li, (d,), np.float32)
         layers.append(ld)
     emb = orc.MatView.bf16(m.get_tensor(am.T_EMBED, 0, (V, d), np.uint16), V, d)
-    lm = orc.MatView.bf16(m.get_tensor(am.T_LM_HEAD, 0, (V, d), np.uint16), V, d)
+    lm = mat(am.T_LM_HEAD, 0, (V, d))
     fn = m.get_tensor(am.T_FINAL_NORM, 0, (d,), np.float32)
-    log(f"cpu baseline: weights downloaded in {time.perf_counter() - t0:.1f}s")
+    log(f"cpu baseline ({fmt}): weights downloaded in {time.perf_counter() - t0:.1f}s")
     ocfg = dict(vocab=V, d_model=d, n_layers=L, n_heads=32, n_kv_heads=32, ffn_hidden=f,
                 max_seq=8, rope_theta=500000.0, rms_eps=1e-6,
                 yarn=dict(factor=8.0, orig_max_pos=8192, attn_factor=1.2079441541679836,
@@ -577,19 +651,29 @@ def cpu_baseline(m, am, prompt) -> dict:
                 sliding_window=4096, layer_sliding=[0 if i % 4 == 3 else 1 for i in range(L)],
                 post_norm=True)
     om = orc.Model(ocfg, dict(embed=emb, lm_head=lm, final_norm=fn, layers=layers), threads=1)
-    t0 = time.perf_counter()
-    logits = om.forward_one(int(prompt[0]))
-    dt = time.perf_counter() - t0
+    info = cpu_info()
+    # one core for the timed step (in-process: the affinity of this thread,
+    # which runs the single-threaded oracle), restored afterwards
+    saved = os.sched_getaffinity(0)
+    core = min(saved)
+    os.sched_setaffinity(0, {core})
+    try:
+        t0 = time.perf_counter()
+        logits = om.forward_one(int(prompt[0]))
+        dt = time.perf_counter() - t0
+    finally:
+        os.sched_setaffinity(0, saved)
     # the same token through the GPU engine at pos 0 (sanity: top-1 agrees)
     m.reset()
     glog = m.forward_one(int(prompt[0]))
     agree = int(np.argmax(glog[::-1])) == int(np.argmax(logits[::-1]))
     rel = float(np.max(np.abs(glog - logits)) / np.max(np.abs(logits)))
-    log(f"cpu baseline: one 7B decode step on 1 core in {dt:.1f}s; GPU/CPU logits rel err "
-        f"{rel:.2e}, top-1 {'agrees' if agree else 'DIFFERS'}")
+    log(f"cpu baseline ({fmt}): one 7B decode step on core {core} of {info['cpu_model']} in "
+        f"{dt:.1f}s; GPU/CPU logits rel err {rel:.2e}, top-1 {'agrees' if agree else 'DIFFERS'}")
     return {"value": round(1.0 / dt, 5), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": "one OLMo-3-7B-shaped bf16 decode step (pos 0, all 32 layers + lm_head) "
-                      "of the same weights, oracle/oracle.c single-threaded",
+            "sample": f"one OLMo-3-7B-shaped {fmt} decode step (pos 0, all 32 layers + lm_head) "
+                      "of the same weights, oracle/oracle.c single-threaded, pinned to one core",
+            "pinned_core": core, **info,
             "seconds": round(dt, 2), "gpu_vs_cpu_logit_rel_err": rel, "top1_agrees": agree}
 
 

@@ -192,6 +192,11 @@ int atlas_model_set_long_context(atlas_model* m, int from_pos);
  * in between.  tokens (host, may be NULL) receives the chosen ids.          */
 int atlas_model_decode_greedy(atlas_model* m, uint32_t first_token, int n_steps,
                               uint32_t* tokens);
+/* Benchmark helper: atlas_model_decode_greedy that also writes each step's
+ * GPU time (ms, between HIP events recorded on the engine stream after
+ * every step) into step_ms[n_steps].                                       */
+int atlas_model_decode_greedy_timed(atlas_model* m, uint32_t first_token, int n_steps,
+                                    uint32_t* tokens, float* step_ms);
 /* Benchmark helper: enqueue `iters` copies of the weight GEMV launches of one
  * decode step (same kernels, shapes, prologues and weights; activations from
  * the engine's scratch) and time them with HIP events on the engine stream.
