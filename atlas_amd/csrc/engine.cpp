@@ -573,12 +573,15 @@ int upload_suppress(atlas_model* m, const atlas_sampling* s, int nsup) {
 
 // ---- device sampling: which configurations the sampler kernel takes ----------
 // temperature > 0 with 1 <= top_k <= SAMPLE_MAX_K (all of the vocabulary when
-// it is smaller), at most SAMPLE_MAX_HIST generated tokens when the frequency
-// or presence penalty is on, and a repetition window of at most SAMPLE_MAX_HIST
-// tokens.  Other configurations sample on the host.
+// it is smaller) or top_k = 0 with top_p off (the whole vocabulary), at most
+// SAMPLE_MAX_HIST generated tokens when the frequency or presence penalty is
+// on, and a repetition window of at most SAMPLE_MAX_HIST tokens.  Other
+// configurations (top_k = 0 with top_p < 1) sample on the host.
 bool sample_dev_ok(const atlas_sampling* s, int V, int max_hist) {
     if (!s || s->temperature <= 0.0f || s->temperature < 1e-6f) return false;
-    if (s->top_k < 1 || s->top_k > SAMPLE_MAX_K || (s->top_k >= V && V > SAMPLE_MAX_K)) return false;
+    const bool whole = s->top_k == 0 && !(s->top_p < 1.0f);
+    if (!whole && (s->top_k < 1 || s->top_k > SAMPLE_MAX_K || (s->top_k >= V && V > SAMPLE_MAX_K)))
+        return false;
     if ((s->frequency_penalty != 0.0f || s->presence_penalty != 0.0f) && max_hist > SAMPLE_MAX_HIST)
         return false;
     if (s->repetition_penalty != 1.0f && std::min(s->repetition_window, max_hist) > SAMPLE_MAX_HIST)
@@ -713,13 +716,25 @@ void top_p(std::vector<float>& lg, float p) {
     for (auto& e : pr) sum += e.second;
     if (sum <= 0.f) return;
     for (auto& e : pr) e.second /= sum;
-    std::stable_sort(pr.begin(), pr.end(),
-                     [](const auto& a, const auto& b) { return a.second > b.second; });
+    // The running sum goes over the probabilities in descending order (ties in
+    // index order, as a stable sort leaves them) until it reaches p.  Only
+    // that prefix is ordered: a selection brings the next largest entries to
+    // the front, a sort orders them, and the prefix grows 8x until it covers
+    // the cut (instead of sorting the whole vocabulary).
+    const auto before = [](const std::pair<size_t, float>& a, const std::pair<size_t, float>& b) {
+        return a.second > b.second || (a.second == b.second && a.first < b.first);
+    };
     float cum = 0.f;
-    size_t cut = n;
-    for (size_t i = 0; i < n; ++i) {
-        cum += pr[i].second;
-        if (cum >= p) { cut = i + 1; break; }
+    size_t cut = n, done = 0, k = std::min(n, (size_t)1024);
+    while (cut == n && done < n) {
+        if (k < n) std::nth_element(pr.begin() + done, pr.begin() + k, pr.end(), before);
+        std::sort(pr.begin() + done, pr.begin() + k, before);
+        for (size_t i = done; i < k; ++i) {
+            cum += pr[i].second;
+            if (cum >= p) { cut = i + 1; break; }
+        }
+        done = k;
+        k = std::min(n, k * 8);
     }
     for (size_t i = cut; i < n; ++i) lg[pr[i].first] = -INFINITY;
 }
@@ -1898,9 +1913,10 @@ ATLAS_API int atlas_sample_device(const float* logits, int vocab, const uint32_t
                   token && step >= 0 && (s->n_suppress <= 0 || s->suppress_initial_tokens),
                   "sample_device: bad arguments");
     if (!sample_dev_ok(s, vocab, n_hist)) {
-        set_error(ATLAS_EUNSUPPORTED, "sample_device: temperature %g, top_k %d, %d history tokens: "
-                  "the device sampler needs temperature > 0 and 1 <= top_k <= %d", s->temperature,
-                  s->top_k, n_hist, (int)SAMPLE_MAX_K);
+        set_error(ATLAS_EUNSUPPORTED, "sample_device: temperature %g, top_k %d, top_p %g, %d history "
+                  "tokens: the device sampler needs temperature > 0 and 1 <= top_k <= %d, or "
+                  "top_k = 0 with top_p = 1", s->temperature, s->top_k, s->top_p, n_hist,
+                  (int)SAMPLE_MAX_K);
         return ATLAS_EUNSUPPORTED;
     }
     const SampleCfg c = sample_cfg_of(s);

@@ -570,6 +570,374 @@ __device__ int sorted_tokens(const uint32_t* hist, int lo, int hi, uint32_t* s) 
     return len;
 }
 
+// ---- top_k = 0 with top_p off: the whole vocabulary samples ----------------
+// The reference sums p_i = exp(v_i - max) sequentially in f32, scales them by
+// inv = 1 / sum and takes the first i whose sequential f32 running sum of
+// p_i * inv exceeds the draw u (lib.rs:351-357, 2710-2717).  Here the running
+// sums are exact prefix sums C_j in double (a block scan over contiguous
+// segments, in index order), and the candidate j with C_{j-1} <= u < C_j is
+// the reference's choice whenever u clears both boundaries by what rounding
+// can move the f32 sums.  With g = gamma_{m-1} = (m-1)e / (1 - (m-1)e),
+// e = 2^-24, for the m non-zero terms (the error bound of recursive summation
+// of non-negative terms, Higham, "Accuracy and Stability of Numerical
+// Algorithms", 2nd ed., sec. 4.2), the reference's sum lies within S(1 +- g),
+// inv and each p_i * inv add one rounding each, and its running sum within
+// another factor (1 +- g): every running sum lies in
+// [C_j (1-e)^2 (1-g)/(1+g), C_j (1+e)^2 (1+g)/(1-g)], plus 2^-150 per term
+// where products or sums underflow.  When u falls inside that band (about 2g
+// of draws, g ~ 0.006 at a 100K vocabulary) the sums are redone sequentially
+// in f32, exactly as the reference does them.
+
+// exclusive prefix sums of v (double) over the 1024 threads into base[0..1024]
+// (base[1024] = the total)
+__device__ void block_scan1024_f64(double v, double* base, double* sh) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    double incl = v;
+    for (int off = 1; off < 64; off <<= 1) {
+        const double t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
+    }
+    double excl = __shfl_up(incl, 1, 64);
+    if (lane == 0) excl = 0.0;
+    if (lane == 63) sh[w] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double acc = 0.0;
+        for (int i = 0; i < 16; ++i) {
+            const double t = sh[i];
+            sh[i] = acc;
+            acc += t;
+        }
+        base[1024] = acc;
+    }
+    __syncthreads();
+    base[threadIdx.x] = sh[w] + excl;
+    __syncthreads();
+}
+
+constexpr int kSampleStage = 16384;      // floats staged per chunk (64 KB of LDS)
+
+// ---- the reference's sequential f32 running sums, computed in parallel -----
+// While the running sum s stays in one binade [2^E, 2^(E+1)), every float there
+// is a multiple of q = 2^(E-23), so fl(s + v) = s + r q with r = v / q rounded
+// to nearest: independent of s except at an exact tie, which rounds to the
+// even multiple and so depends on the parity of s / q.  Each value is thus a
+// map of the running parity b to (r(b), parity after); these maps compose
+// associatively, a block scan gives every running sum of a chunk exactly, up
+// to the first value whose sum leaves the binade.  Thread 0 adds that one in
+// f32 and the scan resumes after it with the new binade's grid.  The first
+// kRunSeq values, where a small running sum changes binade often, are added
+// by thread 0 in order.
+struct RunMap {
+    int r0, r1;              // units of q added from parity 0 / parity 1 (saturating at kRunSat)
+    int p;                   // bit 0: parity after from 0, bit 1: parity after from 1
+};
+constexpr int kRunSeq = 256;
+constexpr int kRunTop = 1 << 24;         // units of q at the binade's top
+constexpr int kRunSat = 1 << 30;         // sums saturate here (>= kRunTop: leaves anyway)
+
+__device__ __forceinline__ RunMap run_identity() { return {0, 0, 2}; }
+
+__device__ __forceinline__ int run_add(int a, int b) { return a + b < kRunSat ? a + b : kRunSat; }
+
+// a, then b
+__device__ __forceinline__ RunMap run_compose(const RunMap& a, const RunMap& b) {
+    const int a0 = a.p & 1, a1 = (a.p >> 1) & 1, b0 = b.p & 1, b1 = (b.p >> 1) & 1;
+    RunMap m;
+    m.r0 = run_add(a.r0, a0 ? b.r1 : b.r0);
+    m.r1 = run_add(a.r1, a1 ? b.r1 : b.r0);
+    m.p = (a0 ? b1 : b0) | ((a1 ? b1 : b0) << 1);
+    return m;
+}
+
+// adding v (>= 0, finite) on the grid q = 2^(E - 23), from v's bits: v = m 2^(ev - 23)
+// with m its 24-bit significand, so v / q = m 2^(ev - E)
+__device__ __forceinline__ RunMap run_map(float v, int E) {
+    const uint32_t u = __float_as_uint(v);
+    const int be = (int)(u >> 23);
+    const uint32_t m = be ? ((u & 0x7FFFFFu) | 0x800000u) : (u & 0x7FFFFFu);
+    const int ev = be ? be - 127 : -126;
+    const int d = E - ev;
+    RunMap r;
+    if (d <= 0) {                            // v / q is an integer, at least m
+        const int f = -d >= 7 ? kRunSat : (int)min((uint32_t)kRunSat, m << -d);
+        r.r0 = r.r1 = f;
+        r.p = (f & 1) | (((f + 1) & 1) << 1);
+        return r;
+    }
+    if (d > 25) {                            // v < q / 2: adds nothing
+        r.r0 = r.r1 = 0;
+        r.p = 2;
+        return r;
+    }
+    const int f = (int)(m >> d);
+    const uint32_t rem = m & ((1u << d) - 1), half = 1u << (d - 1);
+    if (rem == half) {                       // a tie: to the even multiple
+        r.r0 = f + (f & 1);
+        r.r1 = f + ((f + 1) & 1);
+        r.p = 0;
+        return r;
+    }
+    const int g = rem > half ? f + 1 : f;
+    r.r0 = r.r1 = g;
+    r.p = (g & 1) | (((g + 1) & 1) << 1);
+    return r;
+}
+
+// the binade of s (subnormals share the first normal binade's grid 2^-149)
+// and s in units of its grid
+__device__ __forceinline__ int run_binade(float s, int* K) {
+    const uint32_t u = __float_as_uint(s);
+    const int be = (int)(u >> 23);
+    if (be <= 1) {                           // s < 2^-125: grid 2^-149, s = bits
+        *K = (int)u;
+        return -126;
+    }
+    *K = (int)((u & 0x7FFFFFu) | 0x800000u);
+    return be - 127;
+}
+
+__device__ __forceinline__ float run_value(int K, int E) { return ldexpf((float)K, E - 23); }
+
+__device__ __forceinline__ RunMap run_shfl_up(const RunMap& m, int d) {
+    RunMap o;
+    o.r0 = __shfl_up(m.r0, d, 64);
+    o.r1 = __shfl_up(m.r1, d, 64);
+    o.p = __shfl_up(m.p, d, 64);
+    return o;
+}
+
+// the minima of a and of b over the block (sh: 32 ints)
+__device__ __forceinline__ void block_min2_1024(int a, int b, int* sh, int* oa, int* ob) {
+    for (int off = 32; off >= 1; off >>= 1) {
+        a = min(a, __shfl_xor(a, off, 64));
+        b = min(b, __shfl_xor(b, off, 64));
+    }
+    if ((threadIdx.x & 63) == 0) { sh[threadIdx.x >> 6] = a; sh[16 + (threadIdx.x >> 6)] = b; }
+    __syncthreads();
+    int ra = sh[0], rb = sh[16];
+    for (int i = 1; i < 16; ++i) { ra = min(ra, sh[i]); rb = min(rb, sh[16 + i]); }
+    __syncthreads();
+    *oa = ra;
+    *ob = rb;
+}
+
+// Running sums of v_i = x[i] (kind 0) or v_i = x[i] * inv (kind 1), i in [0, n),
+// in order in f32, exactly as a sequential loop gives them.  kind 0: returns
+// -1 and *sum the total.  kind 1: returns the first i with u < running sum
+// (n - 1 if there is none, as sample_from_probs).  Spans start at 1024 values
+// and double while no value leaves the binade (a small running sum changes
+// binade often; a restart only redoes the rest of its span).
+__device__ int exact_run(const float* x, int n, int kind, float inv, float u, float* buf, RunMap* sw,
+                         int* si, float* sf, float* sum) {
+#pragma clang fp contract(off)
+    constexpr int PMAX = kSampleStage / 1024;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n0 = n < kRunSeq ? n : kRunSeq;
+    for (int i = tid; i < n0; i += 1024) buf[i] = kind ? x[i] * inv : x[i];
+    __syncthreads();
+    if (tid == 0) {
+        float s = 0.0f;
+        int hit = -1;
+        for (int i = 0; i < n0; ++i) {
+            s += buf[i];
+            if (kind && u < s) { hit = i; break; }
+        }
+        sf[0] = s;
+        si[0] = hit;
+    }
+    __syncthreads();
+    if (kind && si[0] >= 0) return si[0];
+    int pos = n0, span = 1024;
+    while (pos < n) {
+        const int cnt = n - pos < span ? n - pos : span;
+        const int per = (cnt + 1023) / 1024;
+        for (int i = tid; i < cnt; i += 1024) buf[i] = kind ? x[pos + i] * inv : x[pos + i];
+        __syncthreads();
+        int K0;
+        const int E = run_binade(sf[0], &K0);
+        const int b0 = K0 & 1;
+        // this thread's values [tid * per, +per), their maps and their composition
+        RunMap mp[PMAX];
+        RunMap m = run_identity();
+#pragma unroll
+        for (int j = 0; j < PMAX; ++j) {
+            const int i = tid * per + j;
+            mp[j] = (j < per && i < cnt) ? run_map(buf[i], E) : run_identity();
+            m = run_compose(m, mp[j]);
+        }
+        // block scan: the map of every value before this thread's
+        RunMap inc = m;
+        for (int off = 1; off < 64; off <<= 1) {
+            const RunMap t = run_shfl_up(inc, off);
+            if (lane >= off) inc = run_compose(t, inc);
+        }
+        RunMap exc = run_shfl_up(inc, 1);
+        if (lane == 0) exc = run_identity();
+        if (lane == 63) sw[w] = inc;
+        __syncthreads();
+        if (tid == 0) {
+            RunMap acc = run_identity();
+            for (int i = 0; i < 16; ++i) {
+                const RunMap t = sw[i];
+                sw[i] = acc;
+                acc = run_compose(acc, t);
+            }
+            sw[16] = acc;
+        }
+        __syncthreads();
+        const RunMap pre = run_compose(sw[w], exc);
+        // every running sum of this thread's values, exact until one leaves the binade
+        int K = run_add(K0, b0 ? pre.r1 : pre.r0);
+        int b = b0 ? (pre.p >> 1) & 1 : pre.p & 1;
+        int cross = INT_MAX, hit = INT_MAX, Kc = 0;
+#pragma unroll
+        for (int j = 0; j < PMAX; ++j) {
+            const int i = tid * per + j;
+            if (j < per && i < cnt && cross == INT_MAX) {
+                const int Ka = run_add(K, b ? mp[j].r1 : mp[j].r0);
+                if (Ka >= kRunTop) {
+                    cross = i;
+                    Kc = K;
+                } else if (kind && hit == INT_MAX && u < run_value(Ka, E)) {
+                    hit = i;
+                }
+                K = Ka;
+                b = b ? (mp[j].p >> 1) & 1 : mp[j].p & 1;
+            }
+        }
+        int gc, gh;
+        block_min2_1024(cross, hit, si + 4, &gc, &gh);
+        if (gh < gc) return pos + gh;
+        if (gc == INT_MAX) {                     // no value leaves the binade: the span's total
+            if (tid == 0) {
+                const RunMap t = sw[16];
+                sf[0] = run_value(K0 + (b0 ? t.r1 : t.r0), E);
+            }
+            __syncthreads();
+            pos += cnt;
+            span = span * 2 < kSampleStage ? span * 2 : kSampleStage;
+            continue;
+        }
+        if (cross == gc) {                       // the value that leaves it, added in f32
+            const float sn = run_value(Kc, E) + buf[gc];
+            sf[0] = sn;
+            si[1] = kind && u < sn;
+        }
+        __syncthreads();
+        if (si[1]) return pos + gc;
+        pos += gc + 1;
+        __syncthreads();
+    }
+    *sum = sf[0];
+    return kind ? n - 1 : -1;
+}
+
+// One draw over the whole (penalised) vocabulary x[0..n); thread 0 returns it.
+// x is overwritten with the unnormalised probabilities p_i.
+__device__ uint32_t sample_all_vocab(float* x, int n, const SampleCfg& c, float u, float* buf,
+                                     double* base, double* sh, float* red, int* flag, RunMap* rmaps,
+                                     float* stmp) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x;
+    const float T = c.temperature;
+    // max of v = x / T (lib.rs:1684-1686): the max of x divided once (correctly
+    // rounded division by T > 0 is monotone), 16 coalesced loads in flight
+    float mxx = -INFINITY;
+    for (int b0 = tid; b0 < n; b0 += 1024 * 16) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = x[b0 + k * 1024 < n ? b0 + k * 1024 : n - 1];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) mxx = fmaxf(mxx, v[k]);
+    }
+    const float mx = block_max1024(mxx, red) / T;
+    const float th = c.min_p > 0.0f ? mx + c.log_min_p : -INFINITY;    // min-p's threshold
+    // p_i = exp(v_i - max) in place (0 below the threshold); their sum in
+    // double (any order: S is only compared to within 1e-12) and the non-zero count
+    double part = 0.0;
+    int nz = 0;
+    for (int b0 = tid; b0 < n; b0 += 1024 * 16) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = x[b0 + k * 1024 < n ? b0 + k * 1024 : n - 1];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int i = b0 + k * 1024;
+            const float vt = v[k] / T;
+            const float p = vt < th ? 0.0f : sample_exp(vt - mx);
+            if (i < n) {
+                x[i] = p;
+                part += (double)p;
+                nz += p != 0.0f;
+            }
+        }
+    }
+    int m;
+    (void)block_excl_scan1024(nz, flag + 2, &m);
+    block_scan1024_f64(part, base, sh);
+    const double S = base[1024];
+    const double target = (double)u * S;
+    if (tid == 0) { flag[0] = 0; flag[1] = -1; }
+    // the band's width at u (relative 2g + 4e): no interval C_j - C_(j-1) is
+    // wider than p_max / S = 1 / S, so when that is well inside the band the
+    // check cannot pass and the exact sums run at once
+    const double e = 0x1p-24;
+    const double kk = m > 1 ? (double)(m - 1) * e : 0.0;
+    const double g = kk / (1.0 - kk);
+    const double hi_f = (1.0 + e) * (1.0 + e) * (1.0 + g) / (1.0 - g) + 1e-12;
+    const double lo_f = (1.0 - e) * (1.0 - e) * (1.0 - g) / (1.0 + g) - 1e-12;
+    const bool try_band = 1.0 / S >= 0.5 * (double)u * (hi_f - lo_f);
+    // the exact prefix sums C_j in index order, chunk by chunk through LDS
+    // (each thread sums 16 consecutive values), up to the chunk holding the
+    // crossing; its owner finds j and checks the band
+    constexpr int PER = kSampleStage / 1024;
+    double cbase = 0.0;
+    for (int c0 = 0; c0 < n && try_band; c0 += kSampleStage) {
+        const int cnt = n - c0 < kSampleStage ? n - c0 : kSampleStage;
+        __syncthreads();
+        for (int i = tid; i < cnt; i += 1024) buf[i] = x[c0 + i];
+        __syncthreads();
+        double mine = 0.0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = tid * PER + j;
+            mine += i < cnt ? (double)buf[i] : 0.0;
+        }
+        block_scan1024_f64(mine, base, sh);
+        const double lo_c = cbase + base[tid], hi_c = cbase + base[tid + 1];
+        if (lo_c <= target && target < hi_c) {
+            double pre = lo_c;
+            for (int j = 0; j < PER; ++j) {
+                const int i = tid * PER + j;
+                if (i >= cnt) break;
+                const double prev = pre;
+                pre += (double)buf[i];
+                if (pre > target) {
+                    const double slack = 1e-35;
+                    const double uu = (double)u;
+                    flag[1] = c0 + i;
+                    if ((prev / S) * hi_f + slack <= uu && uu < (pre / S) * lo_f - slack) flag[0] = 1;
+                    break;
+                }
+            }
+        }
+        cbase += base[1024];
+        __syncthreads();
+        if (flag[1] >= 0 || cbase > target) break;
+    }
+    __syncthreads();
+    if (flag[0]) return (uint32_t)flag[1];
+    // ---- inside the band: the reference's sums, exactly (exact_run)
+    float sum, last;
+    (void)exact_run(x, n, 0, 0.0f, 0.0f, buf, rmaps, flag + 8, stmp, &sum);
+    const float inv = 1.0f / sum;
+    const int tok = exact_run(x, n, 1, inv, u, buf, rmaps, flag + 8, stmp, &last);
+    if (tid == 0) flag[1] = tok;
+    __syncthreads();
+    return (uint32_t)flag[1];       // n - 1 when no running sum exceeds u
+}
+
 __global__ __launch_bounds__(1024) void sample_kernel(SampleArgs a) {
 #pragma clang fp contract(off)
     __shared__ uint32_t s_hist[SAMPLE_MAX_HIST];
@@ -636,6 +1004,35 @@ __global__ __launch_bounds__(1024) void sample_kernel(SampleArgs a) {
             }
         }
         __syncthreads();
+    }
+
+    // ---- top_k = 0 (top_p off): every token competes
+    if (c.top_k == 0) {
+        __shared__ double s_base[1025];
+        __shared__ double s_dsh[16];
+        __shared__ float s_u;
+        __shared__ int s_flag[48];
+        __shared__ __attribute__((aligned(16))) float s_stage[kSampleStage];
+        __shared__ RunMap s_rmaps[17];
+        __shared__ float s_stmp[2];
+        if (tid == 0) {
+            unsigned long long r = *a.rng;
+            r ^= r << 13;
+            r ^= r >> 7;
+            r ^= r << 17;
+            *a.rng = r;
+            s_u = (float)(uint32_t)(r >> 33) / 2147483648.0f;
+        }
+        __syncthreads();
+        const uint32_t tok = sample_all_vocab(x, n, c, s_u, s_stage, s_base, s_dsh, s_red, s_flag,
+                                              s_rmaps, s_stmp);
+        if (tid == 0) {
+            if (a.out_u32) *a.out_u32 = tok;
+            if (a.record && a.hist && a.hist_len) { a.hist[len] = tok; *a.hist_len = len + 1; }
+            if (a.step) *a.step = step + 1;
+            if (a.pos_inc) *a.pos_inc += 1;
+        }
+        return;
     }
 
     // ---- top-k (x / T): threshold key th = the k-th largest, ties at th kept

@@ -52,7 +52,7 @@ struct SampleCfg {
     float top_p;                   // 1 = off
     float min_p, log_min_p;        // min_p > 0: threshold max + logf(min_p) (host logf)
     int window;                    // repetition window
-    int top_k;                     // 1 .. SAMPLE_MAX_K
+    int top_k;                     // 1 .. SAMPLE_MAX_K, or 0 (whole vocabulary; top_p off)
     int n_suppress;                // step-0 suppression list length
 };
 enum { SAMPLE_MAX_K = 1024, SAMPLE_MAX_HIST = 4096, SAMPLE_CAND = 4096 };

@@ -73,6 +73,34 @@ class ModelConfig:
                            sliding_window=4096, rope_scaling=RopeYarn())
 
     @staticmethod
+    def olmo3_1b() -> "ModelConfig":
+        """lib.rs:109-126."""
+        return ModelConfig(vocab_size=100352, d_model=2048, n_layers=16, n_heads=16, n_kv_heads=16,
+                           ffn_hidden=8192, max_seq_len=4096, rope_theta=500000.0,
+                           rms_norm_eps=1e-5)
+
+    @staticmethod
+    def llama32_1b() -> "ModelConfig":
+        """lib.rs:128-145."""
+        return ModelConfig(vocab_size=128256, d_model=2048, n_layers=16, n_heads=32, n_kv_heads=8,
+                           ffn_hidden=8192, max_seq_len=131072, rope_theta=500000.0,
+                           rms_norm_eps=1e-5)
+
+    @staticmethod
+    def smollm2_1b7() -> "ModelConfig":
+        """lib.rs:148-165."""
+        return ModelConfig(vocab_size=49152, d_model=2048, n_layers=24, n_heads=32, n_kv_heads=32,
+                           ffn_hidden=8192, max_seq_len=8192, rope_theta=130000.0,
+                           rms_norm_eps=1e-5)
+
+    @staticmethod
+    def smollm2_135m() -> "ModelConfig":
+        """lib.rs:188-205."""
+        return ModelConfig(vocab_size=49152, d_model=576, n_layers=30, n_heads=9, n_kv_heads=3,
+                           ffn_hidden=1536, max_seq_len=8192, rope_theta=10000.0,
+                           rms_norm_eps=1e-5)
+
+    @staticmethod
     def tiny() -> "ModelConfig":
         """lib.rs:312-328."""
         return ModelConfig(vocab_size=256, d_model=64, n_layers=2, n_heads=4, n_kv_heads=2,

@@ -235,11 +235,12 @@ def step_spread(step_ms) -> dict:
 
 
 def generate_rates(m, am) -> dict:
-    """Two end-to-end rates of the reference's own forms on the loaded 7B
-    model: n / elapsed(generate(&[1, 2, 3], n, 0.0)) with n = 30
+    """End-to-end rates of the reference's own forms on the loaded 7B model:
+    n / elapsed(generate(&[1, 2, 3], n, 0.0)) with n = 30
     (crates/atlas-model/src/lib.rs:4312-4316; prompt, host loop and logits
-    included) and the hooked generate (a host callback after every layer,
-    lib.rs:1452-1461), both greedy."""
+    included), the same with SamplingConfig::default() (lib.rs:1223-1276)
+    and SamplingConfig::olmo3() (lib.rs:1278-1294), and the greedy hooked
+    generate (a host callback after every layer, lib.rs:1452-1461)."""
     from atlas_amd.model import SamplingConfig
     m.reset()
     m.generate([1, 2, 3], 4, 0.0)                   # captures, warm
@@ -255,6 +256,16 @@ def generate_rates(m, am) -> dict:
         seen[0] += 1
         return None
 
+    # SamplingConfig::default() (temperature 1, top_k 0: the whole vocabulary)
+    # and the OLMo-3 preset, both sampled on the device inside the step
+    m.set_rng_seed(5)
+    m.generate_with_sampling([1, 2, 3], 4, SamplingConfig())
+    rates = {}
+    for name, sc in (("default", SamplingConfig()), ("olmo3", SamplingConfig.olmo3())):
+        m.set_rng_seed(7)
+        t0 = time.perf_counter()
+        got = m.generate_with_sampling([1, 2, 3], n, sc)
+        rates[name] = len(got) / (time.perf_counter() - t0)
     nh = 16
     m.reset()
     m.generate_with_sampling_hooked([1, 2, 3], 2, SamplingConfig.greedy(), hook)
@@ -263,10 +274,13 @@ def generate_rates(m, am) -> dict:
     t0 = time.perf_counter()
     outh, _ = m.generate_with_sampling_hooked([1, 2, 3], nh, SamplingConfig.greedy(), hook)
     hooked = len(outh) / (time.perf_counter() - t0)
-    log(f"generate([1,2,3], {n}, 0.0): {ref_style:.1f} tok/s; hooked generate: {hooked:.1f} tok/s "
-        f"({seen[0]} hook calls for {len(outh)} tokens)")
+    log(f"generate([1,2,3], {n}, 0.0): {ref_style:.1f} tok/s; sampled with SamplingConfig::default(): "
+        f"{rates['default']:.1f} tok/s, olmo3 preset: {rates['olmo3']:.1f} tok/s; hooked generate: "
+        f"{hooked:.1f} tok/s ({seen[0]} hook calls for {len(outh)} tokens)")
     return {"reference_style_tok_s": round(ref_style, 2),
             "reference_style_form": "n / elapsed(generate([1,2,3], n=30, temperature 0.0))",
+            "default_sampling_tok_s": round(rates["default"], 2),
+            "olmo3_sampling_tok_s": round(rates["olmo3"], 2),
             "hooked_generate_tok_s": round(hooked, 2), "hooked_tokens": len(outh)}
 
 

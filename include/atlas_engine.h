@@ -172,10 +172,14 @@ int atlas_sample_host(const float* logits, int vocab, const uint32_t* hist, int 
 /* The same token choice on the device, from device-resident logits (copied,
  * not modified): the sampler kernel the engine's generate loop replays for
  * temperature > 0 with 1 <= top_k <= 1024 (SamplingConfig::olmo3() among
- * them).  Every sum runs in the reference's order, so the choice equals the
- * host's except where glibc's expf and a correctly rounded exp differ (about
- * 1e-4 of arguments, 1 ulp) and that ulp moves a cumulative-probability
- * boundary across the random draw.  ATLAS_EUNSUPPORTED for other settings.
+ * them), or top_k = 0 with top_p = 1 (SamplingConfig::default()).  With
+ * top_k >= 1 every sum runs in the reference's order; with top_k = 0 the
+ * draw is placed by exact prefix sums and taken only where the reference's
+ * f32 rounding cannot move it, else the sums are redone in its order.  The
+ * choice equals the host's except where glibc's expf and a correctly rounded
+ * exp differ (about 1e-4 of arguments, 1 ulp) and that ulp moves a
+ * cumulative-probability boundary across the random draw.
+ * ATLAS_EUNSUPPORTED for other settings.
  * No reference counterpart (the reference samples on the host).             */
 int atlas_sample_device(const float* logits, int vocab, const uint32_t* hist, int n_hist,
                         int step, const atlas_sampling* s, uint64_t* rng_state, uint32_t* token);

@@ -1,6 +1,6 @@
 """The device sampler (atlas_sample_device, the kernel the engine's generate
-loop replays for temperature > 0 with 1 <= top_k <= 1024) against the host
-sampler atlas_sample_host, which tests/test_sampling.py pins bit for bit to the
+loop replays for temperature > 0 with 1 <= top_k <= 1024, or top_k = 0 with
+top_p = 1) against the host sampler atlas_sample_host, which tests/test_sampling.py pins bit for bit to the
 oracle's restatement of lib.rs:1623-1711.
 
 The two must choose the same token and leave the same RNG state.  Their only
@@ -80,9 +80,11 @@ def _random_case(rng, V):
                    frequency_penalty=float(rng.choice([0.0, 0.1, 0.5])),
                    presence_penalty=float(rng.choice([0.0, 0.2])),
                    top_p=float(rng.choice([1.0, 0.95, 0.8, 0.5])),
-                   top_k=int(rng.choice([1, 2, 5, 20, 50, 200, 1024])),
+                   top_k=int(rng.choice([0, 0, 1, 2, 5, 20, 50, 200, 1024])),
                    min_p=float(rng.choice([0.0, 0.02, 0.05, 0.2])),
                    suppress=[int(t) for t in rng.integers(0, V, rng.integers(0, 4))])
+    if s.top_k == 0:
+        s.top_p = 1.0                               # the device's whole-vocabulary path
     step = int(rng.choice([0, 0, 1, 7]))
     return lg, hist, step, s, keep
 
@@ -134,10 +136,52 @@ def test_device_sampler_top_k_covers_small_vocab_and_long_history():
         assert (td, sd) == (th, sh)
 
 
+def _xorshift_u(state):
+    """Rng::next_f32 after one step of XorShift64 (lib.rs:1190-1214)."""
+    m = (1 << 64) - 1
+    r = state
+    r ^= (r << 13) & m
+    r ^= r >> 7
+    r ^= (r << 17) & m
+    return np.float32(np.float32(r >> 33) / np.float32(2147483648.0)), r
+
+
+def test_device_sampler_whole_vocabulary_band_and_fast_path():
+    # top_k = 0 (SamplingConfig::default(): temperature 1, no top-k / top-p).
+    # Equal logits put a cumulative boundary every 1/V, inside the f32
+    # rounding band around any draw: every draw takes the sequential path.
+    # A peaked vocabulary leaves most draws outside the band (exact prefix
+    # sums decide).  Both must equal the host sampler, token and RNG state.
+    V = 100278
+    flat = np.zeros(V, np.float32)
+    s, keep = _cfg(top_k=0, temperature=1.0)
+    for seed in (3, 77, 0x9E3779B97F4A7C15 | 1, 2**62 + 1):
+        (th, sh), (td, sd) = _both(flat, [], 1, s, seed)
+        assert (td, sd) == (th, sh), seed
+        u, _ = _xorshift_u(seed)
+        # near u * V: the f32 running sum of 1/V drifts by ~1e-3 over 1e5 adds
+        assert abs(th - float(u) * V) <= 0.01 * V, (th, float(u))
+    rng = np.random.default_rng(11)
+    lg = (rng.standard_normal(V) * 1.5).astype(np.float32)
+    lg[rng.integers(0, V, 30)] += 9.0
+    state = 12345
+    for i in range(100):
+        (th, sh), (td, sd) = _both(lg, [], 1, s, state)
+        assert (td, sd) == (th, sh), i
+        state = sh
+    # min-p and penalties on the whole-vocabulary path
+    hist = [int(t) for t in rng.integers(0, V, 50)]
+    s2, keep2 = _cfg(top_k=0, temperature=0.8, min_p=0.01, repetition_penalty=1.2,
+                     frequency_penalty=0.2, presence_penalty=0.1, suppress=[int(lg.argmax())])
+    for seed in range(1, 60, 2):
+        (th, sh), (td, sd) = _both(lg, hist, 0, s2, seed)
+        assert (td, sd) == (th, sh), seed
+
+
 def test_device_sampler_rejects_what_it_does_not_cover():
     lg = Dev(np.zeros(2000, np.float32))
     st, tok = C.c_uint64(1), C.c_uint32(0)
-    for kw in (dict(top_k=0), dict(top_k=1025), dict(temperature=0.0)):
+    for kw in (dict(top_k=0, top_p=0.9), dict(top_k=1025), dict(temperature=0.0)):
         s, keep = _cfg(**kw)
         assert lib().atlas_sample_device(lg.ptr, 2000, None, 0, 0, C.byref(s), C.byref(st),
                                          C.byref(tok)) == -4
@@ -166,7 +210,8 @@ def test_generate_device_sampling_matches_host_sampling():
                               repetition_penalty=1.1, repetition_window=16,
                               frequency_penalty=0.1, presence_penalty=0.1,
                               suppress_initial_tokens=[7]),
-               SamplingConfig(temperature=1.3, top_k=5)):
+               SamplingConfig(temperature=1.3, top_k=5),
+               SamplingConfig()):                     # top_k = 0: the whole vocabulary
         for seed in (11, 12345):
             m.set_rng_seed(seed)
             dev = m.generate_with_sampling(prompt, 40, sc)
