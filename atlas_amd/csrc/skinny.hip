@@ -28,6 +28,11 @@
 // flight; the 16 waves' partial D meet in LDS (double-buffered, one barrier
 // per tile) and 128 threads apply the epilogue.  K > 4096 splits K across
 // blocks into fp32 partials summed by skinny_reduce_kernel in a fixed order.
+//
+// int4 with 2..8 rows takes skinny_i4d_kernel instead: weights go straight
+// from HBM into registers (a lane-row transpose gives the B layout), every
+// block's loads are in flight at once, and the nibbles become bf16 operands
+// by masks alone, with an exact offset correction per tile.
 #include <type_traits>
 
 #include "common.hpp"
@@ -464,6 +469,263 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_i4_kernel(GemvArgs a, float
         if (i + p < my_tiles) tile(i + p, pf[p]);
 }
 
+// ---------------------------------------------------------------------------
+// int4, N <= 8 rows, weights straight from HBM into registers.  A block owns
+// R <= RM 16-row groups (blockIdx.x + r * gridDim.x) of one K slice; wave w
+// owns the slice's 32-k tiles 8w .. 8w+7 as two 4-tile chunks, so each
+// (group, chunk) item is one 16-byte load per lane -- lane (j, n) takes tile
+// 4c + j of row n -- plus the row's scales of those four tiles.  All items
+// but the last U - 1 are in flight at once (x is issued before them), and a
+// 4 x 4 transpose across 16-lane rows turns lane (g, n)'s register j into
+// word g of tile 4c + j, the MFMA B operand; weights touch no LDS and the
+// waves meet once, to add their k partials.
+//
+// A operands: lanes 2s and 2s + 1 (sequence s, hi and lo bf16 parts) each
+// read four of the eight x values of a k group, split them into hi and lo,
+// and trade halves through a lane swap.
+//
+// B operands without conversions: a weight word (elements e0..e7, e_2b in
+// the high nibble of byte b) gives four bf16 pairs by one mask and XOR each
+// (plus three shifts).  With m = s ^ 8 = q + 8 for the stored nibble s of
+// the signed value q, (w & 0x000F000F) ^ 0x43084308 is (128 + m) for e1 and
+// e5, the same of w >> 8 for e3 and e7, and ((w >> 1) & 0x00780078) ^
+// 0x41C041C0 is (16 + m) for e0 and e4 (w >> 9: e2, e6) -- every value an
+// exact bf16.  So the k slots of a lane hold e1 e5 e3 e7 e0 e4 e2 e6 (the A
+// operands are built in that order) with offsets 136 on the first four and
+// 24 on the last four: a tile's product is sum_k A q + corr(i), where
+// corr(i) = sum_k off_k A(i, k) is one MFMA of the offsets against the A
+// operand (as B); the scaled corrections of a chunk's four tiles are then
+// one f32 MFMA (k = tile) subtracted from the accumulator.
+
+// afterwards register j of 16-lane row g holds what register g of row j held
+__device__ __forceinline__ void rows_transpose4(uint32_t& r0, uint32_t& r1, uint32_t& r2,
+                                                uint32_t& r3) {
+    const auto p02 = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+    const auto p13 = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+    const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+    const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+    r0 = q01[0];
+    r1 = q01[1];
+    r2 = q23[0];
+    r3 = q23[1];
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// packed bf16 of (a, b): hi = truncation, lo = the rounded remainder
+__device__ __forceinline__ uint32_t bf16_hi2(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+__device__ __forceinline__ uint32_t bf16_lo2(float a, float b) {
+    const float ra = a - __uint_as_float(__float_as_uint(a) & 0xFFFF0000u);
+    const float rb = b - __uint_as_float(__float_as_uint(b) & 0xFFFF0000u);
+    const bf16x2 v = {(__bf16)ra, (__bf16)rb};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+constexpr int SKD_KTW = 8;          // 32-k tiles per wave
+
+template <int RM, int U, bool SV>
+__global__ __launch_bounds__(1024) void skinny_i4d_kernel(GemvArgs a, float* __restrict__ partial,
+                                                          int kt_split, int cpb_shift) {
+    constexpr int NI = 2 * RM;                                  // items (group, chunk)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, li = lane & 15;
+    const int M = a.M, N = a.N;
+    const int kt_total = a.K / 32;
+    const int kt0 = blockIdx.y * kt_split;
+    const int nks = min(kt_total, kt0 + kt_split) - kt0;       // tiles of the slice (<= 128)
+    const int tw0 = wave * SKD_KTW;
+    const int ntw = max(0, min(SKD_KTW, nks - tw0));           // this wave's tiles (uniform)
+    const int n_groups = (M + 15) / 16;
+    const int gx = __builtin_amdgcn_readfirstlane((int)gridDim.x), bx = blockIdx.x;
+    const int R = bx < n_groups ? (n_groups - 1 - bx) / gx + 1 : 0;
+    __shared__ f32x4 red[RM][16][64];
+
+    // ---- x: lane (g, i), sequence s = i / 2, reads k = 8g + 4p .. + 3 (p = i & 1)
+    // of each of the wave's tiles (tiles past the slice read its last one);
+    // rows of sequences past N read sequence 0: they only reach D rows that
+    // are never stored
+    const int s = li >> 1, p = li & 1;
+    const float* xr = a.x + (s < N ? (long)s * a.x_stride_n : 0);
+    f32x4 xv[SKD_KTW];
+#pragma unroll
+    for (int j = 0; j < SKD_KTW; ++j) {
+        const long k = (long)(kt0 + min(tw0 + j, nks - 1)) * 32 + 8 * g + 4 * p;
+        if (a.x_vec) {
+            xv[j] = *reinterpret_cast<const f32x4*>(xr + k);
+        } else {
+            xv[j] = f32x4{xr[k * a.x_stride_k], xr[(k + 1) * a.x_stride_k], xr[(k + 2) * a.x_stride_k],
+                          xr[(k + 3) * a.x_stride_k]};
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- weights: item q = (group r = q / 2, chunk c = q % 2); past R the
+    // last group is re-read and not used.  The group's scales come with its
+    // chunk-0 item: lane (g, n) takes the four of chunk g & 1 (row n).
+    // buffer resources over the whole matrix and its scales (both < 2 GB:
+    // the launcher checks), 32-bit offsets
+    const uint32_t wstride = a.ldw > 0 ? (uint32_t)a.ldw : (uint32_t)a.K / 2;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a.w), (short)0, __builtin_amdgcn_readfirstlane((int)(M * wstride)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a.scales), (short)0, __builtin_amdgcn_readfirstlane(M * a.bpr * 4), 0x00020000);
+    auto load = [&](int q, u32x4& w, f32x4& sc) {
+        const int r = min(q >> 1, max(R - 1, 0)), c = q & 1;
+        const uint32_t row = (uint32_t)min((bx + r * gx) * 16 + li, M - 1);
+        const int kt = kt0 + min(tw0 + 4 * c + g, nks - 1);
+        w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          wres, (int)(row * wstride + (uint32_t)kt * 16u), 0, 2));
+        if (c == 0) {
+            const uint32_t so = row * (uint32_t)a.bpr;
+            if constexpr (SV) {                                 // nks % 4 == 0, one scale per tile
+                sc = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                    sres, (int)((so + kt0 + min(tw0 + 4 * (g & 1), nks - 4)) * 4u), 0, 0));
+            } else {
+                const int kc = kt0 + min(tw0 + 4 * (g & 1), nks - 1), kl = kt0 + nks - 1;
+                const float* sr = a.scales + so;
+                sc = f32x4{sr[min(kc, kl) >> cpb_shift], sr[min(kc + 1, kl) >> cpb_shift],
+                           sr[min(kc + 2, kl) >> cpb_shift], sr[min(kc + 3, kl) >> cpb_shift]};
+            }
+        }
+    };
+    if (ntw == 0) {                                             // a wave past the slice
+#pragma unroll
+        for (int r = 0; r < RM; ++r) red[r][wave][lane] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+    u32x4 wb[U];
+    f32x4 sb[(U + 1) / 2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load(u, wb[u], sb[(u >> 1) % ((U + 1) / 2)]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- A operands from x (zero on tiles past the slice), k slots in the
+    // B operands' order e1 e5 e3 e7 e0 e4 e2 e6
+    bf16x8 A[SKD_KTW];
+    // perm(own, other) selectors: lane 2s owns e0..e3 (bytes 4-7 of the
+    // pair), lane 2s + 1 owns e4..e7
+    const uint32_t sel_odd = p ? 0x07060302u : 0x03020706u;    // (e1, e5), (e3, e7)
+    const uint32_t sel_even = p ? 0x05040100u : 0x01000504u;   // (e0, e4), (e2, e6)
+#pragma unroll
+    for (int j = 0; j < SKD_KTW; ++j) {
+        f32x4 v = xv[j];
+        if (j >= ntw) v = f32x4{0.f, 0.f, 0.f, 0.f};             // uniform
+        const uint32_t h0 = bf16_hi2(v.x, v.y), h1 = bf16_hi2(v.z, v.w);
+        const uint32_t l0 = bf16_lo2(v.x, v.y), l1 = bf16_lo2(v.z, v.w);
+        // lane 2s keeps hi of its four and gets hi of the other four; lane
+        // 2s + 1 the lo parts (DPP quad_perm [1, 0, 3, 2]: the pair swaps)
+        const uint32_t o0 = p ? l0 : h0, o1 = p ? l1 : h1;
+        const uint32_t t0 = __builtin_amdgcn_update_dpp(0u, p ? h0 : l0, 0xB1, 0xF, 0xF, false);
+        const uint32_t t1 = __builtin_amdgcn_update_dpp(0u, p ? h1 : l1, 0xB1, 0xF, 0xF, false);
+        u32x4 o;
+        o.x = __builtin_amdgcn_perm(o0, t0, sel_odd);
+        o.y = __builtin_amdgcn_perm(o1, t1, sel_odd);
+        o.z = __builtin_amdgcn_perm(o0, t0, sel_even);
+        o.w = __builtin_amdgcn_perm(o1, t1, sel_even);
+        A[j] = __builtin_bit_cast(bf16x8, o);
+    }
+    // ---- offset corrections: lane (g, i) holds -corr of tile 4c + g, row i
+    float corr[2];
+    {
+        const bf16x8 offs = __builtin_bit_cast(bf16x8, u32x4{0x43084308u, 0x43084308u, 0x41C041C0u,
+                                                                0x41C041C0u});
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            float cg[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                cg[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(offs, A[4 * c + j],
+                                                                f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0)[0];
+            const float c01 = (g & 1) ? cg[1] : cg[0], c23 = (g & 1) ? cg[3] : cg[2];
+            corr[c] = -((g & 2) ? c23 : c01);
+        }
+    }
+
+    // ---- items in order; the group's partial goes to LDS after its chunk 1
+    constexpr int NS = (U + 1) / 2;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float sj1[4];                                               // chunk 1's scales
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+        const int u = q % U;
+        const u32x4 w = wb[u];
+        float sj[4];
+        const int c = q & 1;
+        if (c == 0) {
+            // rows g & 1 == 0 hold chunk 0's scales, the odd rows chunk 1's:
+            // one 16-lane row swap gives every lane both
+            const f32x4 sc = sb[(q >> 1) % NS];
+            const float sv[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const auto e = __builtin_amdgcn_permlane16_swap(__float_as_uint(sv[j]),
+                                                                __float_as_uint(sv[j]), false, false);
+                sj[j] = __uint_as_float(e[0]);
+                sj1[j] = __uint_as_float(e[1]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sj[j] = sj1[j];
+        }
+        if (q + U < NI) load(q + U, wb[u], sb[((q + U) >> 1) % NS]);
+        // no branches: A is zero on tiles past the slice, and groups past R
+        // (re-read copies) are computed but never stored
+        uint32_t wj[4] = {w.x, w.y, w.z, w.w};
+        rows_transpose4(wj[0], wj[1], wj[2], wj[3]);
+        f32x4 d[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w = wj[j], w8 = w >> 8;
+            const u32x4 b = {(w & 0x000F000Fu) ^ 0x43084308u, (w8 & 0x000F000Fu) ^ 0x43084308u,
+                             ((w >> 1) & 0x00780078u) ^ 0x41C041C0u,
+                             ((w >> 9) & 0x00780078u) ^ 0x41C041C0u};
+            d[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[4 * c + j], __builtin_bit_cast(bf16x8, b),
+                                                           f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc += d[j] * sj[j];
+        // minus sum over the four tiles of corr(tile, i) * scale(tile, n)
+        const float s01 = (g & 1) ? sj[1] : sj[0], s23 = (g & 1) ? sj[3] : sj[2];
+        const float sg = (g & 2) ? s23 : s01;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(corr[c], sg, acc, 0, 0, 0);
+        if (c == 1) {
+            red[q >> 1][wave][lane] = acc;
+            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    }
+    __syncthreads();
+
+    // ---- thread (r, h, l): group r, lane l's D rows 2h, 2h + 1 (sequence
+    // 2 (l / 16) + h: hi + lo) of weight row l % 16
+    const bool split_out = gridDim.y > 1;
+    for (int t = threadIdx.x; t < RM * 128; t += 1024) {
+        const int r = t >> 7, h = (t >> 6) & 1, l = t & 63;
+        float v = 0.f;
+        if (r < R) {
+#pragma unroll
+            for (int w = 0; w < 16; ++w) {
+                const f32x4 pr = red[r][w][l];
+                v += h ? pr.z + pr.w : pr.x + pr.y;
+            }
+        }
+        const int sq = 2 * (l >> 4) + h;
+        const int row = (bx + r * gx) * 16 + (l & 15);
+        const float up = __shfl_xor(v, 1, 64);                  // rows (2i, 2i + 1): (gate, up)
+        if (r >= R || sq >= N) continue;
+        if (split_out) {
+            if (row < M) partial[((long)blockIdx.y * N + sq) * M + row] = v;
+        } else if (a.epi == EPI_SILU_MUL) {
+            if ((row & 1) == 0 && row + 1 < M)
+                a.y[sq * a.y_stride_n + (long)(row >> 1) * a.y_stride_m] = v / (1.0f + expf(-v)) * up;
+        } else if (row < M) {
+            a.y[sq * a.y_stride_n + (long)row * a.y_stride_m] = v;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemvArgs a, const float* __restrict__ partial,
                                                             int splitk) {
     const int M = a.M, N = a.N;
@@ -507,15 +769,6 @@ static int skinny_na(int N) { return N > 8 ? 2 : 1; }
 static int skinny_splits(int K, int N) {
     const int kt_total = K / 32, kt_block = SK_KT_BLOCK / skinny_na(N);
     return (kt_total + kt_block - 1) / kt_block;
-}
-
-// Bytes of split-K partials an (M, N, K) launch needs; an N-row size
-// covers every smaller N.
-size_t skinny_partial_bytes(int M, int N, int K) {
-    int splits = skinny_splits(K, N);
-    if (N > 8) splits = std::max(splits, skinny_splits(K, 8));
-    if (splits <= 1) return 0;
-    return (size_t)splits * N * M * sizeof(float);
 }
 
 // blocks of 1024 threads one CU holds for kernel `kern` (cached per kernel)
@@ -567,6 +820,100 @@ static int launch_skinny(const GemvArgs& a, hipStream_t st) {
         if (rb > 4096) rb = 4096;
         hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a,
                            partial, splits);
+        ATLAS_LAUNCH_CHECK("skinny_reduce");
+    }
+    return ATLAS_OK;
+}
+
+// int4 with N <= 8 rows through skinny_i4d_kernel: a block per CU holding
+// RM <= 8 groups of 16 rows (a larger M takes more blocks than CUs), K in
+// slices of <= 128 tiles over blockIdx.y (a multiple of 4 tiles, so the
+// slices' scales load as 16-byte vectors when a block covers one tile).
+// Returns 1 when the shape does not fit (the caller takes skinny_i4_kernel).
+// K splits: the fewest whose grid (one block per CU) gives the smallest
+// per-block load (groups x tiles); a matrix too large for 8 groups per block
+// on every CU takes more blocks than CUs
+struct I4dPlan { int splits, kt_split, bx, rm; };
+static I4dPlan i4d_plan(int M, int K, int cus) {
+    const int kt_total = K / 32;
+    const int n_groups = (M + 15) / 16;
+    const int s_min = (kt_total + SK_KT_BLOCK - 1) / SK_KT_BLOCK;
+    I4dPlan p{0, 0, 0, 0};
+    long best = 0;
+    for (int sp = s_min; sp <= s_min + 3; ++sp) {
+        const int ks = ((kt_total + sp - 1) / sp + 3) & ~3;
+        if (ks > SK_KT_BLOCK || (kt_total + ks - 1) / ks != sp) continue;   // an empty split
+        const int b = std::min(n_groups, std::max(1, cus / sp));
+        const int r = (n_groups + b - 1) / b;
+        if (r > 8) continue;
+        const long cost = (long)r * ks;
+        if (p.splits == 0 || cost < best) {
+            p = I4dPlan{sp, ks, b, r};
+            best = cost;
+        }
+    }
+    if (p.splits == 0) {
+        p.splits = s_min;
+        p.kt_split = ((kt_total + s_min - 1) / s_min + 3) & ~3;
+        p.rm = 8;
+        p.bx = (n_groups + 7) / 8;
+    }
+    return p;
+}
+
+// Bytes of split-K partials an (M, N, K) launch needs; an N-row size
+// covers every smaller N.
+size_t skinny_partial_bytes(int M, int N, int K) {
+    int splits = skinny_splits(K, N);
+    if (N > 8) splits = std::max(splits, skinny_splits(K, 8));
+    else splits = std::max(splits, i4d_plan(M, K, device_cu_count()).splits);   // int4 rows
+    if (splits <= 1) return 0;
+    return (size_t)splits * N * M * sizeof(float);
+}
+
+template <int RM, int U>
+static void i4d_go(const GemvArgs& a, bool sv, dim3 grid, hipStream_t st, float* partial, int kt_split,
+                   int cpb_shift) {
+    if (sv)
+        hipLaunchKernelGGL((skinny_i4d_kernel<RM, U, true>), grid, dim3(1024), 0, st, a, partial,
+                           kt_split, cpb_shift);
+    else
+        hipLaunchKernelGGL((skinny_i4d_kernel<RM, U, false>), grid, dim3(1024), 0, st, a, partial,
+                           kt_split, cpb_shift);
+}
+
+static int launch_skinny_i4d(const GemvArgs& a, hipStream_t st) {
+    const long wstride = a.ldw > 0 ? a.ldw : a.K / 2;
+    if (a.N > 8 || ((uintptr_t)a.w & 15) || (wstride & 15) || (long)a.M * wstride >= (1L << 31) ||
+        (long)a.M * a.bpr * 4 >= (1L << 31))
+        return 1;
+    const int kt_total = a.K / 32;
+    const I4dPlan pl = i4d_plan(a.M, a.K, device_cu_count());
+    const int splits = pl.splits, kt_split = pl.kt_split, bx = pl.bx, rm = pl.rm;
+    const bool sv = a.cpb == 1 && a.bpr % 4 == 0 && kt_total % 4 == 0 && ((uintptr_t)a.scales & 15) == 0;
+    float* partial = nullptr;
+    if (splits > 1) {
+        const int rc = partial_for(a, (size_t)splits * a.N * a.M * sizeof(float), &partial);
+        if (rc) return rc;
+    }
+    int cpb_shift = 0;
+    while ((1 << cpb_shift) < a.cpb) ++cpb_shift;
+    const dim3 grid(bx, splits);
+    switch (rm) {
+    case 1: i4d_go<1, 2>(a, sv, grid, st, partial, kt_split, cpb_shift); break;
+    case 2: i4d_go<2, 4>(a, sv, grid, st, partial, kt_split, cpb_shift); break;
+    case 3: i4d_go<3, 6>(a, sv, grid, st, partial, kt_split, cpb_shift); break;
+    case 4: i4d_go<4, 4>(a, sv, grid, st, partial, kt_split, cpb_shift); break;
+    case 5: case 6: i4d_go<6, 4>(a, sv, grid, st, partial, kt_split, cpb_shift); break;
+    default: i4d_go<8, 4>(a, sv, grid, st, partial, kt_split, cpb_shift); break;
+    }
+    ATLAS_LAUNCH_CHECK("skinny int4");
+    if (splits > 1) {
+        const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
+        long rb = ((long)a.N * m_out + 255) / 256;
+        if (rb > 4096) rb = 4096;
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, partial,
+                           splits);
         ATLAS_LAUNCH_CHECK("skinny_reduce");
     }
     return ATLAS_OK;
@@ -859,11 +1206,18 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     if (a.M == 0) return ATLAS_OK;
     ATLAS_REQUIRE(a.K % 32 == 0 && a.K > 0, "skinny: K %% 32 != 0");
     ATLAS_REQUIRE(gemv_pitch_ok(a), "skinny: row pitch %ld bytes for K %d", a.ldw, a.K);
+    // int4 at 2-8 rows: the direct-load MFMA kernel (at the 7B shapes on
+    // MI355X 0.55-0.8x the multi-row GEMV's time at two and three rows, and
+    // 1.05-1.2x the batch-1 GEMV's from 11008 x 4096 up).
+    if (a.fmt == WF_I4 && a.N >= 2 && a.N <= 8 && a.block % 32 == 0 && (a.cpb & (a.cpb - 1)) == 0 &&
+        a.bpr > 0) {
+        const int rc = launch_skinny_i4d(a, st);
+        if (rc != 1) return rc;
+    }
     // Two or three rows stream the weights once through the multi-row GEMV:
     // at the 7B shapes on MI355X it takes 0.55-0.75x the MFMA kernel's time
-    // for two rows and 0.65-0.9x for three (int4 11008 x 4096 at three rows
-    // is within 3%); from four rows on, the LDS reads of the x rows per
-    // weight chunk make it no faster than the MFMA kernel.
+    // for two rows and 0.65-0.9x for three; from four rows on, the LDS reads
+    // of the x rows per weight chunk make it no faster than the MFMA kernel.
     if (a.N <= 3 && gemv_multi_ok(a)) return gemv_multi_launch(a, st);
     // One row is the batch-1 GEMV (int4 11008 x 4096: 10 us against 15.6 us
     // for the MFMA tiles, whose 16 rows would be 15 / 16 padding).

@@ -185,6 +185,39 @@ def attention_bench(torch, lib, rng, quick: bool) -> dict:
 PREFILL = {}      # weight format -> prompt prefill timings of decode_bench
 
 
+def host_slice_bench(rng) -> dict:
+    """GpuMatrix::sgemm, the reference's host-slice path (crates/atlas-tensor/
+    src/lib.rs:371-400): x uploaded, the GEMV, y downloaded, per call; beside
+    it sgemm_vec on device-resident x.  bf16 4096 x 4096."""
+    from atlas_amd.tensor import GpuMatrix, GpuVec
+    M = K = 4096
+    w = (rng.standard_normal(M * K) * 0.02).astype(np.float32)
+    g = GpuMatrix.upload_bf16(w, M, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    out = np.empty((M, 1), np.float32)
+    xv = GpuVec.from_slice(x)
+    for _ in range(5):
+        g.sgemm(x.reshape(K, 1), K, 1, out)
+        g.sgemm_vec(xv)
+    iters = 200
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        g.sgemm(x.reshape(K, 1), K, 1, out)
+    host_us = (time.perf_counter() - t0) / iters * 1e6
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        y = g.sgemm_vec(xv)
+    y.download() if hasattr(y, "download") else None
+    dev_us = (time.perf_counter() - t0) / iters * 1e6
+    wbytes = M * K * 2
+    log(f"GpuMatrix.sgemm (host slices in/out) bf16 4096x4096: {host_us:.1f} us/call "
+        f"({wbytes / (host_us * 1e-6) / 1e9:.0f} GB/s of weights); sgemm_vec (device x): "
+        f"{dev_us:.1f} us/call incl. host dispatch")
+    return {"shape": "bf16 4096x4096", "host_slices_us_per_call": round(host_us, 2),
+            "host_slices_weight_GB_s": round(wbytes / (host_us * 1e-6) / 1e9, 1),
+            "device_vec_us_per_call": round(dev_us, 2)}
+
+
 def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int):
     import dataclasses
     cfg = dataclasses.replace(model_mod.ModelConfig.olmo3_actual_7b(),
@@ -328,9 +361,11 @@ def main() -> int:
 
     micro = {}
     attn = {}
+    host_slice = None
     if not args.no_micro:
         micro = gemv_bench(torch, lib, rng, args.quick)
         attn = attention_bench(torch, lib, rng, args.quick)
+        host_slice = host_slice_bench(rng)
 
     # ---- headline: bf16 7B decode -------------------------------------------
     m, dt = decode_bench(am, am.W_BF16, prompt, args.steps, args.warmup, seed=7)
@@ -450,6 +485,7 @@ def main() -> int:
         "checkpoint_load": load_res,
         "gemv_microbench": micro,
         "attention_microbench": attn,
+        "host_slice_sgemm": host_slice,
         "reference_published": {"olmo3_7b_bf16_tok_s": 61.7, "hardware": "A100-SXM4-40GB"},
     }
     if cpu:
