@@ -619,7 +619,8 @@ def pmc_probe(torch, lib, am) -> int:
     plain copy of known size), then for the bf16, int8 and int4 7B models one
     launch of each GEMV set (bench_gemv which = 3 gate/up, 1 QKV + W_o +
     lm_head, 2 W_down) and two decode steps at positions 1 and 2 (attention,
-    argmax).  Kernels are told apart by name and grid size."""
+    argmax); last, int4 11008 x 4096 as one batch-1 GEMV and the skinny GEMM
+    at 4 and 8 rows.  Kernels are told apart by name and grid size."""
     n = 1 << 28
     src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
@@ -645,6 +646,23 @@ def pmc_probe(torch, lib, am) -> int:
         m.forward_one(3)
         torch.cuda.synchronize()
         m.close()
+    # int4 11008 x 4096 (block 32): batch-1 GEMV, then the skinny GEMM at 4
+    # and 8 rows, each on its own copy of the weights
+    M, K, bs = 11008, 4096, 32
+    rng = np.random.default_rng(5)
+    W = DevBufs(lib, rng.integers(0, 256, M * K // 2, dtype=np.uint8), 3)
+    S = DevBufs(lib, rng.uniform(1e-3, 2e-3, M * K // bs).astype(np.float32), 3)
+    X = DevBufs(lib, rng.standard_normal((8, K)).astype(np.float32), 1)
+    Y = DevBufs(lib, np.zeros((8, M), np.float32), 1)
+    assert lib.atlas_gemv_f32(3, W.ptrs[0], S.ptrs[0], bs, X.ptrs[0], Y.ptrs[0], M, K) == 0
+    for j, n in ((1, 4), (2, 8)):
+        assert lib.atlas_gemm_skinny_f32(3, W.ptrs[j], S.ptrs[j], bs, X.ptrs[0], Y.ptrs[0], M, n,
+                                         K) == 0
+    torch.cuda.synchronize()
+    log(f"pmc probe int4 {M}x{K}: GEMV, skinny n=4, skinny n=8 done "
+        f"({M * K // 2 + 4 * M * K // bs} algorithmic weight bytes each)")
+    for b in (W, S, X, Y):
+        b.free()
     return 0
 
 
