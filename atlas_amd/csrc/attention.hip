@@ -209,6 +209,63 @@ __device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long
     scan_run<HD, G, NG>(s, e1, q, m, l, o);
 }
 
+// Split merge of the fused kernel (and of the split kernel's one-launch
+// mode), run by the block that arrives last.  The
+// partials of query head qh, split s sit at index qh * n_splits + s (o: times
+// HD) of part_m / part_l / part_o; other XCDs wrote them, so they are read
+// with sc1 loads (past this XCD's L2, which can still hold an earlier
+// launch's lines).  A thread owns (head, dim) elements and reads the splits in
+// groups of 8, every load of a group issued before the first is used, with a
+// running maximum across groups: one memory round trip per 8 splits instead
+// of one per split.  Empty splits carry (m, l, o) = (-inf, 0, 0) and weigh 0;
+// the split holding pos is never empty, so the final maximum is finite.
+template <int HD, int G, int NT>
+__device__ __forceinline__ void merge_splits(const float* part_m, const float* part_l, const float* part_o,
+                                             int n_splits, int kvh, float* out) {
+    constexpr int SC1 = 16;                   // buffer cache policy: sc1
+    const int nh = n_splits * G;              // this kv head's (head, split) pairs
+    const long h0 = (long)kvh * G * n_splits;
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_m + h0), (short)0, nh * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rl =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_l + h0), (short)0, nh * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ro =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_o + h0 * HD), (short)0, nh * HD * 4, 0x00020000);
+    for (int e = threadIdx.x; e < G * HD; e += NT) {
+        const int h = e / HD, d = e % HD;
+        float M = -INFINITY, L = 0.f, O = 0.f;
+        for (int s0 = 0; s0 < n_splits; s0 += 8) {
+            float mv[8], lv[8], ov[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = h * n_splits + min(s0 + j, n_splits - 1);   // past the end: a copy
+                mv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, i * 4, 0, SC1));
+                lv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, i * 4, 0, SC1));
+                ov[j] = __builtin_bit_cast(float,
+                                           __builtin_amdgcn_raw_buffer_load_b32(ro, (i * HD + d) * 4, 0, SC1));
+            }
+            float cm = M;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (s0 + j >= n_splits) mv[j] = -INFINITY;                // ... which weighs 0
+                cm = fmaxf(cm, mv[j]);
+            }
+            if (cm == -INFINITY) continue;   // every split so far is empty
+            const float c = exp2f(M - cm);    // 0 while M = -inf
+            L *= c;
+            O *= c;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float w = exp2f(mv[j] - cm);
+                L += lv[j] * w;
+                O += ov[j] * w;
+            }
+            M = cm;
+        }
+        out[(long)(kvh * G + h) * HD + d] = O / L;
+    }
+}
+
 template <int HD, int G, int W>
 __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;              // dims per lane
@@ -287,12 +344,38 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
         const int qh = kvh * G + h;
         if (n_splits == 1) {
             out[(long)qh * HD + d] = osum / lsum;
+        } else if (a.counters) {
+            // agent-scope (sc1) stores for the merging block on any XCD
+            const long pi = pbase + (long)qh * n_splits + split;
+            __hip_atomic_store(&a.part_o[pi * HD + d], osum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d == 0) {
+                __hip_atomic_store(&a.part_m[pi], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.part_l[pi], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         } else {
             const long pi = pbase + (long)qh * n_splits + split;
             a.part_o[pi * HD + d] = osum;
             if (d == 0) { a.part_m[pi] = mx; a.part_l[pi] = lsum; }
         }
     }
+    if (n_splits == 1 || !a.counters) return;
+    // ---- one launch: the last block of this (seq, kv head) merges ------------
+    // (as in attn_fused_kernel: partial stores complete before the counter
+    // bump; the merging block resets the counter for the next launch)
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);        // vmcnt(0)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(&a.counters[seq * a.n_kv + kvh], 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == n_splits - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    merge_splits<HD, G, 64 * W>(a.part_m + pbase, a.part_l + pbase, a.part_o + pbase * HD, n_splits,
+                                kvh, out);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&a.counters[seq * a.n_kv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Split merge of the reference-ABI path: one block per query head.  The
@@ -387,61 +470,6 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
     }
 }
 
-// Split merge of the fused kernel, run by the block that arrives last.  The
-// partials of query head qh, split s sit at index qh * n_splits + s (o: times
-// HD) of part_m / part_l / part_o; other XCDs wrote them, so they are read
-// with sc1 loads (past this XCD's L2, which can still hold an earlier
-// launch's lines).  A thread owns (head, dim) elements and reads the splits in
-// groups of 8, every load of a group issued before the first is used, with a
-// running maximum across groups: one memory round trip per 8 splits instead
-// of one per split.  Empty splits carry (m, l, o) = (-inf, 0, 0) and weigh 0;
-// the split holding pos is never empty, so the final maximum is finite.
-template <int HD, int G, int NT>
-__device__ __forceinline__ void merge_splits(const float* part_m, const float* part_l, const float* part_o,
-                                             int n_splits, int kvh, float* out) {
-    constexpr int SC1 = 16;                   // buffer cache policy: sc1
-    const int nh = n_splits * G;              // this kv head's (head, split) pairs
-    const long h0 = (long)kvh * G * n_splits;
-    const __amdgpu_buffer_rsrc_t rm =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_m + h0), (short)0, nh * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rl =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_l + h0), (short)0, nh * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t ro =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_o + h0 * HD), (short)0, nh * HD * 4, 0x00020000);
-    for (int e = threadIdx.x; e < G * HD; e += NT) {
-        const int h = e / HD, d = e % HD;
-        float M = -INFINITY, L = 0.f, O = 0.f;
-        for (int s0 = 0; s0 < n_splits; s0 += 8) {
-            float mv[8], lv[8], ov[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = h * n_splits + min(s0 + j, n_splits - 1);   // past the end: a copy
-                mv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, i * 4, 0, SC1));
-                lv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, i * 4, 0, SC1));
-                ov[j] = __builtin_bit_cast(float,
-                                           __builtin_amdgcn_raw_buffer_load_b32(ro, (i * HD + d) * 4, 0, SC1));
-            }
-            float cm = M;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                if (s0 + j >= n_splits) mv[j] = -INFINITY;                // ... which weighs 0
-                cm = fmaxf(cm, mv[j]);
-            }
-            if (cm == -INFINITY) continue;   // every split so far is empty
-            const float c = exp2f(M - cm);    // 0 while M = -inf
-            L *= c;
-            O *= c;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float w = exp2f(mv[j] - cm);
-                L += lv[j] * w;
-                O += ov[j] * w;
-            }
-            M = cm;
-        }
-        out[(long)(kvh * G + h) * HD + d] = O / L;
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Fused decode attention for one layer: per-head QK-norm (eps 1e-6,
@@ -714,7 +742,7 @@ static int launch_split(AttnArgs a, int n_splits, hipStream_t st, int n_seq = 1)
     hipLaunchKernelGGL((attn_split_kernel<HD, G, W>), dim3(a.n_kv, n_splits, n_seq), dim3(64 * W),
                        0, st, a);
     ATLAS_LAUNCH_CHECK("attn_split");
-    if (n_splits > 1) {
+    if (n_splits > 1 && !a.counters) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3(a.n_heads, n_seq), dim3(HD < 256 ? HD : 256), 0, st,
                            a, n_splits, HD);
         ATLAS_LAUNCH_CHECK("attn_combine");
@@ -753,6 +781,8 @@ int attn_launch(AttnArgs a, int n_splits, hipStream_t st) {
         a.part_o = part + (size_t)2 * a.n_heads * n_splits;
     }
     ATLAS_REQUIRE(n_splits == 1 || (a.part_l && a.part_o), "attention: partial buffers missing");
+    ATLAS_REQUIRE(!a.counters || n_splits <= kAttnFusedMaxSplits,
+                  "attention: %d splits > %d for the one-launch merge", n_splits, kAttnFusedMaxSplits);
 #define ATLAS_ATTN_CASE(HDV, GV) \
     if (a.head_dim == HDV && G == GV) return launch_split<HDV, GV>(a, n_splits, st);
     ATLAS_ATTN_CASE(128, 1) ATLAS_ATTN_CASE(128, 2) ATLAS_ATTN_CASE(128, 4) ATLAS_ATTN_CASE(128, 8)

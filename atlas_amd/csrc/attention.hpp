@@ -28,6 +28,10 @@ struct AttnArgs {
     const int* slot_dev;
     long slot_stride;
     long q_stride, out_stride;
+    // [n_seq][n_kv] merge counters, zero before the first launch, or null:
+    // non-null, the splits merge in the block that finishes last (one launch,
+    // at most kAttnFusedMaxSplits splits); null, attn_combine_kernel merges
+    int* counters;
 };
 
 // Fused QK-norm + RoPE + KV write + split-K attention + split merge.

@@ -39,6 +39,7 @@ enum ScratchSlot {
     SCR_FUSED_PART,     // atlas_attention_fused_f32 split partials
     SCR_FUSED_CNT,      // ... its merge counters (kept at zero by the kernel)
     SCR_FUSED_POS,      // ... its position word
+    SCR_ATTN_CNT,       // atlas_decode_attention merge counters (kept at zero)
     SCR_N
 };
 int thread_scratch(int slot, size_t bytes, void** out, bool zero_new = false);

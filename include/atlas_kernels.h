@@ -78,7 +78,8 @@ void atlas_rope_precomputed(float* x, const float* cos_tab, const float* sin_tab
 void atlas_kv_cache_write(float* k_cache, float* v_cache, const float* new_k,
                           const float* new_v, int pos, int n_kv_heads, int head_dim);
 /* lib.rs:80-86 -> matmul.cu:786-933.  Split-K flash decode here; any
- * context length (no dynamic-LDS limit).                                    */
+ * context length (no dynamic-LDS limit).  Up to 8 splits merge in the block
+ * that finishes last (one launch), more in a second merge kernel.           */
 void atlas_decode_attention(const float* q, const float* k_cache, const float* v_cache,
                             float* out, int n_heads, int n_kv_heads, int head_dim, int pos,
                             float scale, int window_size);
@@ -206,8 +207,9 @@ int atlas_attention_fused_f32(const float* qkv, const float* q_norm, const float
 
 /* No counterpart in the reference.  atlas_decode_attention for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc): same arguments, same split count
- * and results, but the split partials live in a fixed 8 MiB device workspace
+ * loops, harnesses that forbid hipMalloc): same arguments and results (to
+ * float rounding: its splits always merge in a second kernel, with the
+ * two-kernel split count), but the split partials live in a fixed 8 MiB device workspace
  * of the library (one per GPU, held until the process ends); no hipMalloc or
  * hipFree is made.  Shapes whose partials (n_heads x splits x (head_dim + 2)
  * floats) exceed the workspace return ATLAS_EINVAL.  Calls that overlap on
