@@ -44,6 +44,9 @@ namespace {
 // ctx 600, 2.93 vs 3.12 at 1200, 3.37 vs 3.52 at 4000), so the long-context
 // step runs only from a position the caller sets.
 constexpr int kLongAttnFrom = 1 << 30;
+// The ragged batch's shared steps switch to the split kernel + merge from
+// this position of their longest row (or the caller's long_from, if lower).
+constexpr int kBatchLongAttnFrom = 512;
 // Rows of the multi-row step, and prompt tokens per prefill step: the
 // multi-row GEMV for 2-3 rows, the skinny MFMA kernel for 4-16.
 constexpr int kPrefillChunk = 16;
@@ -2089,7 +2092,8 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
         std::vector<int> sl(slots.begin(), slots.begin() + n);
         int max_pos = 0;
         for (int j = 0; j < n; ++j) max_pos = std::max(max_pos, poss[j]);
-        TRY(run_batch_step(m, n, sl, multi || max_pos >= m->long_from));
+        TRY(run_batch_step(m, n, sl,
+                           multi || max_pos >= std::min(m->long_from, kBatchLongAttnFrom)));
         // a row chooses a token when it consumes its last prompt token or
         // generates; steps inside every row's prompt need no host round trip
         const bool any_choice = any_choice_row;
