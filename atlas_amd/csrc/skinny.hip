@@ -32,7 +32,9 @@
 // int4 with 2..8 rows takes skinny_i4d_kernel instead: weights go straight
 // from HBM into registers (a lane-row transpose gives the B layout), every
 // block's loads are in flight at once, and the nibbles become bf16 operands
-// by masks alone, with an exact offset correction per tile.
+// by masks alone, with an exact offset correction per tile.  int8 (3..8
+// rows) and bf16 with K > 4096 (2..8 rows) take skinny_d_kernel, the same
+// scheme with the loads as B operands.
 #include <type_traits>
 
 #include "common.hpp"
@@ -726,6 +728,154 @@ __global__ __launch_bounds__(1024) void skinny_i4d_kernel(GemvArgs a, float* __r
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 / int8 with N <= 8 rows, the same direct-load scheme without the int4
+// layout work: a bf16 lane load (16 bytes = k 8g..8g+7 of one 32-k tile of
+// row n) already is the MFMA B operand, and an int8 lane load (16 bytes, k
+// 16g..16g+15 of a 64-k pair of tiles) is two B operands once converted --
+// any k order inside an MFMA is fine when the scale is per row, so the A
+// operands simply follow the loads.  The products accumulate in the MFMA
+// itself (two accumulators alternate); int8's row scale applies in the
+// epilogue.  Block / wave / group split, x handling and the epilogue are
+// those of skinny_i4d_kernel.
+
+// A operand of a lane pair from its four x values (lane 2s: k 0..3 of the
+// group, hi parts; lane 2s + 1: k 4..7, lo parts), natural k order
+__device__ __forceinline__ bf16x8 pair_operand(const f32x4 v, bool p) {
+    const uint32_t h0 = bf16_hi2(v.x, v.y), h1 = bf16_hi2(v.z, v.w);
+    const uint32_t l0 = bf16_lo2(v.x, v.y), l1 = bf16_lo2(v.z, v.w);
+    const uint32_t t0 = __builtin_amdgcn_update_dpp(0u, p ? h0 : l0, 0xB1, 0xF, 0xF, false);
+    const uint32_t t1 = __builtin_amdgcn_update_dpp(0u, p ? h1 : l1, 0xB1, 0xF, 0xF, false);
+    u32x4 o;
+    o.x = p ? t0 : h0;
+    o.y = p ? t1 : h1;
+    o.z = p ? l0 : t0;
+    o.w = p ? l1 : t1;
+    return __builtin_bit_cast(bf16x8, o);
+}
+
+template <int FMT, int RM, int U>
+__global__ __launch_bounds__(1024) void skinny_d_kernel(GemvArgs a, float* __restrict__ partial,
+                                                        int kt_split) {
+    static_assert(FMT == WF_BF16 || FMT == WF_I8, "bf16 or int8");
+    constexpr int IPG = FMT == WF_BF16 ? 8 : 4;                 // lane loads per group
+    constexpr int NI = RM * IPG;
+    constexpr int EB = FMT == WF_BF16 ? 2 : 1;                  // bytes per weight
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, li = lane & 15;
+    const int M = a.M, N = a.N;
+    const int kt_total = a.K / 32;
+    const int kt0 = blockIdx.y * kt_split;
+    const int nks = min(kt_total, kt0 + kt_split) - kt0;       // tiles of the slice (% 4 == 0)
+    const int tw0 = wave * SKD_KTW;
+    const int ntw = max(0, min(SKD_KTW, nks - tw0));           // 0, 4 or 8 (uniform)
+    const int n_groups = (M + 15) / 16;
+    const int gx = __builtin_amdgcn_readfirstlane((int)gridDim.x), bx = blockIdx.x;
+    const int R = bx < n_groups ? (n_groups - 1 - bx) / gx + 1 : 0;
+    __shared__ f32x4 red[RM][16][64];
+
+    // slice-relative k of this lane's first x value for MFMA t (0..7)
+    const int s = li >> 1, p = li & 1;
+    auto kofs = [&](int t) {
+        if constexpr (FMT == WF_BF16) return min(tw0 + t, nks - 1) * 32 + 8 * g + 4 * p;
+        else return min(tw0 + 2 * (t >> 1), nks - 2) * 32 + 16 * g + 8 * (t & 1) + 4 * p;
+    };
+    const float* xr = a.x + (s < N ? (long)s * a.x_stride_n : 0);   // rows past N: never stored
+    f32x4 xv[SKD_KTW];
+#pragma unroll
+    for (int t = 0; t < SKD_KTW; ++t) {
+        const long k = (long)kt0 * 32 + kofs(t);
+        if (a.x_vec) {
+            xv[t] = *reinterpret_cast<const f32x4*>(xr + k);
+        } else {
+            xv[t] = f32x4{xr[k * a.x_stride_k], xr[(k + 1) * a.x_stride_k], xr[(k + 2) * a.x_stride_k],
+                          xr[(k + 3) * a.x_stride_k]};
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const uint32_t wstride = a.ldw > 0 ? (uint32_t)a.ldw : (uint32_t)a.K * EB;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a.w), (short)0, __builtin_amdgcn_readfirstlane((int)(M * wstride)), 0x00020000);
+    // item q = (group r = q / IPG, load j = q % IPG)
+    auto load = [&](int q) {
+        const int r = min(q / IPG, max(R - 1, 0)), j = q % IPG;
+        const uint32_t row = (uint32_t)min((bx + r * gx) * 16 + li, M - 1);
+        uint32_t off;
+        if constexpr (FMT == WF_BF16) off = (uint32_t)(kt0 + min(tw0 + j, nks - 1)) * 64u + 16u * g;
+        else off = (uint32_t)(kt0 + min(tw0 + 2 * j, nks - 2)) * 32u + 16u * g;
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             wres, (int)(row * wstride + off), 0, 2));
+    };
+    if (ntw == 0) {                                             // a wave past the slice
+#pragma unroll
+        for (int r = 0; r < RM; ++r) red[r][wave][lane] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+    u32x4 wb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) wb[u] = load(u);
+    __builtin_amdgcn_sched_barrier(0);
+
+    bf16x8 A[SKD_KTW];
+#pragma unroll
+    for (int t = 0; t < SKD_KTW; ++t) {
+        f32x4 v = xv[t];
+        if (FMT == WF_BF16 ? t >= ntw : 2 * (t >> 1) >= ntw) v = f32x4{0.f, 0.f, 0.f, 0.f};
+        A[t] = pair_operand(v, p);
+    }
+
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+        const int u = q % U, j = q % IPG;
+        const u32x4 w = wb[u];
+        if (q + U < NI) wb[u] = load(q + U);
+        if constexpr (FMT == WF_BF16) {
+            if (j & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j], __builtin_bit_cast(bf16x8, w), acc1, 0, 0, 0);
+            else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j], __builtin_bit_cast(bf16x8, w), acc0, 0, 0, 0);
+        } else {
+            SkFrag<WF_I8> f0, f1;
+            f0.w0 = w.x; f0.w1 = w.y; f1.w0 = w.z; f1.w1 = w.w;
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2 * j], sk_operand<WF_I8>(f0), acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2 * j + 1], sk_operand<WF_I8>(f1), acc1, 0, 0, 0);
+        }
+        if (j == IPG - 1) {
+            red[q / IPG][wave][lane] = acc0 + acc1;
+            acc0 = f32x4{0.f, 0.f, 0.f, 0.f};
+            acc1 = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    }
+    __syncthreads();
+
+    const bool split_out = gridDim.y > 1;
+    for (int t = threadIdx.x; t < RM * 128; t += 1024) {
+        const int r = t >> 7, h = (t >> 6) & 1, l = t & 63;
+        const int sq = 2 * (l >> 4) + h;
+        const int row = (bx + r * gx) * 16 + (l & 15);
+        float v = 0.f;
+        if (r < R) {
+#pragma unroll
+            for (int w = 0; w < 16; ++w) {
+                const f32x4 pr = red[r][w][l];
+                v += h ? pr.z + pr.w : pr.x + pr.y;
+            }
+            if constexpr (FMT == WF_I8) v *= a.scales[min(row, M - 1)];
+        }
+        const float up = __shfl_xor(v, 1, 64);                  // rows (2i, 2i + 1): (gate, up)
+        if (r >= R || sq >= N) continue;
+        if (split_out) {
+            if (row < M) partial[((long)blockIdx.y * N + sq) * M + row] = v;
+        } else if (a.epi == EPI_SILU_MUL) {
+            if ((row & 1) == 0 && row + 1 < M)
+                a.y[sq * a.y_stride_n + (long)(row >> 1) * a.y_stride_m] = v / (1.0f + expf(-v)) * up;
+        } else if (row < M) {
+            a.y[sq * a.y_stride_n + (long)row * a.y_stride_m] = v;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemvArgs a, const float* __restrict__ partial,
                                                             int splitk) {
     const int M = a.M, N = a.N;
@@ -914,6 +1064,48 @@ static int launch_skinny_i4d(const GemvArgs& a, hipStream_t st) {
         if (rb > 4096) rb = 4096;
         hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, partial,
                            splits);
+        ATLAS_LAUNCH_CHECK("skinny_reduce");
+    }
+    return ATLAS_OK;
+}
+
+// bf16 / int8 with N <= 8 rows through skinny_d_kernel, with the int4
+// launcher's K splits and groups per block (K % 128 == 0: slices of whole
+// 4-tile steps).  Returns 1 when the shape does not fit.
+template <int FMT, int RM, int U>
+static void d_go(const GemvArgs& a, dim3 grid, hipStream_t st, float* partial, int kt_split) {
+    hipLaunchKernelGGL((skinny_d_kernel<FMT, RM, U>), grid, dim3(1024), 0, st, a, partial, kt_split);
+}
+
+template <int FMT>
+static int launch_skinny_d(const GemvArgs& a, hipStream_t st) {
+    constexpr long EB = FMT == WF_BF16 ? 2 : 1;
+    const long wstride = a.ldw > 0 ? a.ldw : (long)a.K * EB;
+    if (a.N > 8 || a.K % 128 || ((uintptr_t)a.w & 15) || (wstride & 15) ||
+        (long)a.M * wstride >= (1L << 31))
+        return 1;
+    const I4dPlan pl = i4d_plan(a.M, a.K, device_cu_count());
+    float* partial = nullptr;
+    if (pl.splits > 1) {
+        const int rc = partial_for(a, (size_t)pl.splits * a.N * a.M * sizeof(float), &partial);
+        if (rc) return rc;
+    }
+    const dim3 grid(pl.bx, pl.splits);
+    switch (pl.rm) {
+    case 1: d_go<FMT, 1, FMT == WF_BF16 ? 8 : 4>(a, grid, st, partial, pl.kt_split); break;
+    case 2: d_go<FMT, 2, 8>(a, grid, st, partial, pl.kt_split); break;
+    case 3: d_go<FMT, 3, 8>(a, grid, st, partial, pl.kt_split); break;
+    case 4: d_go<FMT, 4, 8>(a, grid, st, partial, pl.kt_split); break;
+    case 5: case 6: d_go<FMT, 6, 8>(a, grid, st, partial, pl.kt_split); break;
+    default: d_go<FMT, 8, 8>(a, grid, st, partial, pl.kt_split); break;
+    }
+    ATLAS_LAUNCH_CHECK(FMT == WF_BF16 ? "skinny bf16" : "skinny int8");
+    if (pl.splits > 1) {
+        const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
+        long rb = ((long)a.N * m_out + 255) / 256;
+        if (rb > 4096) rb = 4096;
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, partial,
+                           pl.splits);
         ATLAS_LAUNCH_CHECK("skinny_reduce");
     }
     return ATLAS_OK;
@@ -1212,6 +1404,16 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     if (a.fmt == WF_I4 && a.N >= 2 && a.N <= 8 && a.block % 32 == 0 && (a.cpb & (a.cpb - 1)) == 0 &&
         a.bpr > 0) {
         const int rc = launch_skinny_i4d(a, st);
+        if (rc != 1) return rc;
+    }
+    // int8 at 3-8 rows (2 when K > 4096) and bf16 at 2-8 rows with K > 4096:
+    // the direct-load MFMA kernel (MI355X, 7B shapes at 8 rows: int8 gate/up
+    // 26.7 vs 35.9 us, W_down 18.0 vs 33.1 us; bf16 W_down 25.0 vs 36.0 us).
+    // bf16 at K <= 4096 stays below: its 16-rows x 64-byte loads cap both
+    // kernels near 4.5 TB/s there, and the multi-row GEMV wins at 2-3 rows.
+    if (a.N >= 2 && a.N <= 8 &&
+        ((a.fmt == WF_I8 && (a.N >= 3 || a.K > 4096)) || (a.fmt == WF_BF16 && a.K > 4096))) {
+        const int rc = a.fmt == WF_I8 ? launch_skinny_d<WF_I8>(a, st) : launch_skinny_d<WF_BF16>(a, st);
         if (rc != 1) return rc;
     }
     // Two or three rows stream the weights once through the multi-row GEMV:

@@ -201,14 +201,29 @@ def test_skinny_7b_rows(orc, fmt, n, M, K):
     _skinny_check(orc, fmt, n, M, K, 32, seed=11)
 
 
+# The direct-load skinny kernels (int4 and int8 at 2-8 rows, bf16 at 2-8
+# rows with K > 4096): a ragged last 16-row group, K splits with a remainder
+# slice, and two rows of int8 with K > 4096.
+@pytest.mark.parametrize("fmt,n,M,K", [
+    ("int8", 8, 777, 4096), ("int8", 2, 1000, 8192), ("int8", 4, 300, 11008),
+    ("bf16", 8, 777, 8192), ("bf16", 5, 4096, 11008), ("bf16", 2, 100, 4224),
+    ("int4", 8, 777, 8192), ("int4", 6, 33, 4224)])
+def test_skinny_direct_loads(orc, fmt, n, M, K):
+    print(f"skinny direct {fmt} n={n} M={M} K={K}", flush=True)
+    _skinny_check(orc, fmt, n, M, K, 32, seed=13)
+
+
 # SwiGLU epilogue over n rows: one row (batch-1 GEMV), two (multi-row GEMV),
-# five (MFMA skinny tiles, split-K reduce applies SwiGLU), twenty rows at
+# five (MFMA skinny tiles, split-K reduce applies SwiGLU), the direct-load
+# kernels' own epilogue (int8 5 rows) and the split reduce after them (bf16
+# 4 rows at K = 4224, int8 8 rows at K = 8192), twenty rows at
 # K = 128 (the prompt GEMM's unsplit epilogue: gate/up pairs meet across
 # lanes) and at K = 4096 (split, SwiGLU in the reduce).
 @pytest.mark.parametrize("fmt,n,h,K", [
     ("bf16", 1, 1000, 512), ("int8", 2, 700, 1024), ("int4", 5, 512, 2048),
     ("bf16", 20, 640, 128), ("int8", 20, 640, 128), ("int4", 20, 640, 128),
-    ("bf16", 20, 2048, 4096), ("int4", 33, 1024, 4096)])
+    ("bf16", 20, 2048, 4096), ("int4", 33, 1024, 4096),
+    ("int8", 5, 512, 2048), ("bf16", 4, 256, 4224), ("int8", 8, 300, 8192)])
 def test_gemm_skinny_swiglu(orc, fmt, n, h, K):
     print(f"skinny swiglu {fmt} n={n} h={h} K={K}", flush=True)
     w = _w((2 * h, K), 97 + n)
