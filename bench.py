@@ -76,6 +76,27 @@ def time_launches(torch, fn, n_iter: int, warm: int = 3) -> float:
     return e0.elapsed_time(e1) / n_iter
 
 
+def launch_spread(torch, fn, n_iter: int) -> dict:
+    """p10 / median / p90 of the per-call time of fn(i) over n_iter >= 100
+    back-to-back calls, from a HIP event recorded after every call.  This is a
+    second pass: each event adds ~2.5 us to its call on MI355X (measured: the
+    median sits that far above the plain pass's mean), so the spread's width
+    is the information here and the plain pass's mean stays the time."""
+    n_iter = max(100, n_iter)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_iter + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(n_iter):
+        fn(i)
+        ev[i + 1].record()
+    ev[-1].synchronize()
+    d = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(n_iter)]) * 1e3
+    return {"p10_us": round(float(np.percentile(d, 10)), 2),
+            "median_us": round(float(np.median(d)), 2),
+            "p90_us": round(float(np.percentile(d, 90)), 2), "launches": n_iter,
+            "note": "an event after every call (~2.5 us each): read the width, not the level"}
+
+
 def gemv_bench(torch, lib, orc_free_rng, quick: bool) -> dict:
     """Configs 1-3: batch-1 GEMVs and the int4 skinny GEMM, GB/s."""
     out = {}
@@ -115,8 +136,11 @@ def gemv_bench(torch, lib, orc_free_rng, quick: bool) -> dict:
         ms = time_launches(torch, run, copies * (3 if quick else 10))
         gbs = alg / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 3), "bytes": alg, "rotating_copies": copies}
-        log(f"gemv {name}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+                     "frac": round(gbs / HBM_PEAK_GBS, 3), "bytes": alg, "rotating_copies": copies,
+                     "spread": launch_spread(torch, run, copies * (3 if quick else 10))}
+        sp = out[name]["spread"]
+        log(f"gemv {name}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}); "
+            f"per launch p10/median/p90 {sp['p10_us']}/{sp['median_us']}/{sp['p90_us']} us")
         W.free()
         if S:
             S.free()
@@ -143,8 +167,10 @@ def gemv_bench(torch, lib, orc_free_rng, quick: bool) -> dict:
         gbs = alg / (ms * 1e-3) / 1e9
         out[f"int4_skinny_n{n}_11008x4096_bs32"] = {
             "us": round(ms * 1e3, 2), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3),
-            "bytes": alg}
-        log(f"skinny int4 n={n}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+            "bytes": alg, "spread": launch_spread(torch, run, copies * (2 if quick else 6))}
+        sp = out[f"int4_skinny_n{n}_11008x4096_bs32"]["spread"]
+        log(f"skinny int4 n={n}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s; per launch p10/median/p90 "
+            f"{sp['p10_us']}/{sp['median_us']}/{sp['p90_us']} us")
         X.free()
         Y.free()
     W.free()
@@ -176,8 +202,11 @@ def attention_bench(torch, lib, rng, quick: bool) -> dict:
         gbs = alg / (ms * 1e-3) / 1e9
         key = f"ctx{ctx}" + (f"_w{window}" if window else "")
         out[key] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
-                    "frac": round(gbs / HBM_PEAK_GBS, 3), "bytes": alg}
-        log(f"attention {key}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+                    "frac": round(gbs / HBM_PEAK_GBS, 3), "bytes": alg,
+                    "spread": launch_spread(torch, run, copies * (3 if quick else 10))}
+        sp = out[key]["spread"]
+        log(f"attention {key}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s; per launch p10/median/p90 "
+            f"{sp['p10_us']}/{sp['median_us']}/{sp['p90_us']} us")
         Kc.free(); Vc.free(); Q.free(); O.free()
     return out
 
