@@ -32,9 +32,9 @@
 // int4 with 2..8 rows takes skinny_i4d_kernel instead: weights go straight
 // from HBM into registers (a lane-row transpose gives the B layout), every
 // block's loads are in flight at once, and the nibbles become bf16 operands
-// by masks alone, with an exact offset correction per tile.  int8 (3..8
-// rows) and bf16 with K > 4096 (2..8 rows) take skinny_d_kernel, the same
-// scheme with the loads as B operands.
+// by masks alone, with an exact offset correction per tile.  bf16 and int8
+// at 2..8 rows take skinny_lds_kernel (K <= 4096: GEMV-style row loads into
+// an LDS tile) or skinny_d_kernel (K > 4096: the loads are the B operands).
 #include <type_traits>
 
 #include "common.hpp"
@@ -876,6 +876,142 @@ __global__ __launch_bounds__(1024) void skinny_d_kernel(GemvArgs a, float* __res
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 / int8 with N <= 8 rows and K <= 4096 through LDS: the block loads a
+// 16-row group the way the batch-1 GEMV does (each wave instruction reads
+// 1 KB of one row), with PF groups in flight in registers, stores it in LDS
+// (rows padded by 16 bytes: the B reads of 16 rows at one offset fall on
+// distinct banks) and reads the MFMA B operands from there.  The direct-load
+// kernel's 16-rows x 64-byte instructions stream at ~4.5 TB/s at these
+// shapes; these run at the GEMV's rate.  x, A operands and the epilogue are
+// those of skinny_d_kernel; one barrier pair and one reduction per group.
+// (Two groups in flight need more than 128 VGPRs for bf16 and spill for
+// int8, so the launcher takes PF = 1.)
+constexpr int SKL_ROWB = 8192;                  // bytes of a row (K <= 4096 bf16)
+constexpr int SKL_ROWP = SKL_ROWB + 16;         // padded LDS row
+
+template <int FMT, int PF>
+__global__ __launch_bounds__(1024) void skinny_lds_kernel(GemvArgs a) {
+    static_assert(FMT == WF_BF16 || FMT == WF_I8, "bf16 or int8");
+    constexpr int EB = FMT == WF_BF16 ? 2 : 1;                  // bytes per weight
+    constexpr int NPC = 16 * (SKL_ROWB / (2 / EB)) / 16 / 1024; // pieces per thread per group
+    constexpr int ROWP = SKL_ROWB / (2 / EB) + 16;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, li = lane & 15;
+    const int M = a.M, N = a.N;
+    const int nks = a.K / 32;                                  // tiles (<= 128)
+    const int tw0 = wave * SKD_KTW;
+    const int ntw = max(0, min(SKD_KTW, nks - tw0));
+    const int n_groups = (M + 15) / 16;
+    const int gx = __builtin_amdgcn_readfirstlane((int)gridDim.x), bx = blockIdx.x;
+    const int R = bx < n_groups ? (n_groups - 1 - bx) / gx + 1 : 0;
+    const int dpr = nks * 2 * EB;                              // 16-byte pieces per row
+    __shared__ __align__(16) uint8_t wt[16 * ROWP];
+    __shared__ f32x4 red[16][64];
+
+    // A operands of the wave's 8 tiles (natural k order; zero past K)
+    const int s = li >> 1, p = li & 1;
+    const float* xr = a.x + (s < N ? (long)s * a.x_stride_n : 0);   // rows past N: never stored
+    bf16x8 A[SKD_KTW];
+    {
+        f32x4 xv[SKD_KTW];
+#pragma unroll
+        for (int t = 0; t < SKD_KTW; ++t) {
+            const long k = (long)min(tw0 + t, nks - 1) * 32 + 8 * g + 4 * p;
+            if (a.x_vec) {
+                xv[t] = *reinterpret_cast<const f32x4*>(xr + k);
+            } else {
+                xv[t] = f32x4{xr[k * a.x_stride_k], xr[(k + 1) * a.x_stride_k],
+                              xr[(k + 2) * a.x_stride_k], xr[(k + 3) * a.x_stride_k]};
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < SKD_KTW; ++t) {
+            f32x4 v = xv[t];
+            if (t >= ntw) v = f32x4{0.f, 0.f, 0.f, 0.f};
+            A[t] = pair_operand(v, p);
+        }
+    }
+
+    const uint32_t wstride = a.ldw > 0 ? (uint32_t)a.ldw : (uint32_t)a.K * EB;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a.w), (short)0, __builtin_amdgcn_readfirstlane((int)(M * wstride)), 0x00020000);
+    // piece q of this thread in a group: (row pc / dpr, 16-byte column pc % dpr);
+    // past the group's pieces, or past R, a copy is read and not stored
+    auto fetch = [&](int r, u32x4 (&f)[NPC]) {
+        const int grp = bx + min(r, max(R - 1, 0)) * gx;
+#pragma unroll
+        for (int q = 0; q < NPC; ++q) {
+            const int pc = min((int)threadIdx.x + 1024 * q, 16 * dpr - 1);
+            const uint32_t row = (uint32_t)min(grp * 16 + pc / dpr, M - 1);
+            f[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 wres, (int)(row * wstride + (uint32_t)(pc % dpr) * 16u), 0, 2));
+        }
+    };
+    u32x4 pf[PF][NPC];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) fetch(i, pf[i]);
+    for (int r0 = 0; r0 < R; r0 += PF) {                       // block-uniform
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+            const int r = r0 + i;
+            if (r >= R) break;
+            __syncthreads();                                   // the last group's B reads are done
+#pragma unroll
+            for (int q = 0; q < NPC; ++q) {
+                const int pc = (int)threadIdx.x + 1024 * q;
+                if (pc < 16 * dpr)
+                    *reinterpret_cast<u32x4*>(&wt[(pc / dpr) * ROWP + (pc % dpr) * 16]) = pf[i][q];
+            }
+            if (r + PF < R) fetch(r + PF, pf[i]);
+            __syncthreads();
+            f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < SKD_KTW; ++t) {
+                const int kt = min(tw0 + t, nks - 1);
+                bf16x8 b;
+                if constexpr (FMT == WF_BF16) {
+                    b = *reinterpret_cast<const bf16x8*>(&wt[li * ROWP + kt * 64 + 16 * g]);
+                } else {
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    const u32x2 w2 = *reinterpret_cast<const u32x2*>(&wt[li * ROWP + kt * 32 + 8 * g]);
+                    SkFrag<WF_I8> f;
+                    f.w0 = w2.x;
+                    f.w1 = w2.y;
+                    b = sk_operand<WF_I8>(f);
+                }
+                if (t & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[t], b, acc1, 0, 0, 0);
+                else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[t], b, acc0, 0, 0, 0);
+            }
+            red[wave][lane] = acc0 + acc1;
+            __syncthreads();
+            if (threadIdx.x < 128) {
+                const int h = threadIdx.x >> 6, l = threadIdx.x & 63;
+                const int sq = 2 * (l >> 4) + h;
+                const int row = (bx + r * gx) * 16 + (l & 15);
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < 16; ++w) {
+                    const f32x4 pr = red[w][l];
+                    v += h ? pr.z + pr.w : pr.x + pr.y;
+                }
+                if constexpr (FMT == WF_I8) v *= a.scales[min(row, M - 1)];
+                const float up = __shfl_xor(v, 1, 64);         // rows (2i, 2i + 1): (gate, up)
+                if (sq < N) {
+                    if (a.epi == EPI_SILU_MUL) {
+                        if ((row & 1) == 0 && row + 1 < M)
+                            a.y[sq * a.y_stride_n + (long)(row >> 1) * a.y_stride_m] =
+                                v / (1.0f + expf(-v)) * up;
+                    } else if (row < M) {
+                        a.y[sq * a.y_stride_n + (long)row * a.y_stride_m] = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemvArgs a, const float* __restrict__ partial,
                                                             int splitk) {
     const int M = a.M, N = a.N;
@@ -1108,6 +1244,23 @@ static int launch_skinny_d(const GemvArgs& a, hipStream_t st) {
                            pl.splits);
         ATLAS_LAUNCH_CHECK("skinny_reduce");
     }
+    return ATLAS_OK;
+}
+
+// bf16 / int8 with N <= 8 rows and K <= 4096 through skinny_lds_kernel: one
+// block of 1024 threads per CU (the LDS row tile), persistent over the
+// 16-row groups.  Returns 1 when the shape does not fit.
+template <int FMT>
+static int launch_skinny_lds(const GemvArgs& a, hipStream_t st) {
+    constexpr long EB = FMT == WF_BF16 ? 2 : 1;
+    const long wstride = a.ldw > 0 ? a.ldw : (long)a.K * EB;
+    if (a.N > 8 || a.K > 4096 || ((uintptr_t)a.w & 15) || (wstride & 15) ||
+        (long)a.M * wstride >= (1L << 31))
+        return 1;
+    const int n_groups = (a.M + 15) / 16;
+    const int bx = std::min(n_groups, device_cu_count());
+    hipLaunchKernelGGL((skinny_lds_kernel<FMT, 1>), dim3(bx), dim3(1024), 0, st, a);
+    ATLAS_LAUNCH_CHECK(FMT == WF_BF16 ? "skinny lds bf16" : "skinny lds int8");
     return ATLAS_OK;
 }
 
@@ -1406,14 +1559,19 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
         const int rc = launch_skinny_i4d(a, st);
         if (rc != 1) return rc;
     }
-    // int8 at 3-8 rows (2 when K > 4096) and bf16 at 2-8 rows with K > 4096:
-    // the direct-load MFMA kernel (MI355X, 7B shapes at 8 rows: int8 gate/up
-    // 26.7 vs 35.9 us, W_down 18.0 vs 33.1 us; bf16 W_down 25.0 vs 36.0 us).
-    // bf16 at K <= 4096 stays below: its 16-rows x 64-byte loads cap both
-    // kernels near 4.5 TB/s there, and the multi-row GEMV wins at 2-3 rows.
-    if (a.N >= 2 && a.N <= 8 &&
-        ((a.fmt == WF_I8 && (a.N >= 3 || a.K > 4096)) || (a.fmt == WF_BF16 && a.K > 4096))) {
-        const int rc = a.fmt == WF_I8 ? launch_skinny_d<WF_I8>(a, st) : launch_skinny_d<WF_BF16>(a, st);
+    // bf16 / int8 at 2-8 rows (MI355X, 7B shapes at 8 rows against the
+    // batch-1 GEMV's time over the same weights):
+    //  * K <= 4096: the LDS-staged kernel (bf16 gate/up 33.4 vs 29.1 us, QKV
+    //    20.7 vs 18.0; int8 gate/up 22.0 vs 17.6), except bf16 at two rows,
+    //    where the multi-row GEMV is faster (30.7 vs 33.2 us at gate/up);
+    //  * K > 4096: the direct-load kernel over K splits (bf16 W_down 25.0 us,
+    //    int8 17.9 us, against 36.0 and 33.1 for skinny_kernel).
+    if (a.N >= 2 && a.N <= 8 && (a.fmt == WF_I8 || a.fmt == WF_BF16)) {
+        int rc = 1;
+        if (a.K > 4096)
+            rc = a.fmt == WF_I8 ? launch_skinny_d<WF_I8>(a, st) : launch_skinny_d<WF_BF16>(a, st);
+        else if (a.fmt == WF_I8 || a.N >= 3)
+            rc = a.fmt == WF_I8 ? launch_skinny_lds<WF_I8>(a, st) : launch_skinny_lds<WF_BF16>(a, st);
         if (rc != 1) return rc;
     }
     // Two or three rows stream the weights once through the multi-row GEMV:

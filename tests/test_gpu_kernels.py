@@ -201,11 +201,13 @@ def test_skinny_7b_rows(orc, fmt, n, M, K):
     _skinny_check(orc, fmt, n, M, K, 32, seed=11)
 
 
-# The direct-load skinny kernels (int4 and int8 at 2-8 rows, bf16 at 2-8
-# rows with K > 4096): a ragged last 16-row group, K splits with a remainder
-# slice, and two rows of int8 with K > 4096.
+# The 2-8-row skinny kernels: direct loads (int4; bf16 and int8 with
+# K > 4096) and the LDS-staged tile (bf16 and int8 with K <= 4096): a ragged
+# last 16-row group, K splits with a remainder slice, and two rows of int8
+# on either side of K = 4096.
 @pytest.mark.parametrize("fmt,n,M,K", [
-    ("int8", 8, 777, 4096), ("int8", 2, 1000, 8192), ("int8", 4, 300, 11008),
+    ("int8", 8, 777, 4096), ("int8", 2, 1000, 8192), ("int8", 4, 300, 11008), ("int8", 2, 33, 2048),
+    ("bf16", 3, 1000, 4096),
     ("bf16", 8, 777, 8192), ("bf16", 5, 4096, 11008), ("bf16", 2, 100, 4224),
     ("int4", 8, 777, 8192), ("int4", 6, 33, 4224)])
 def test_skinny_direct_loads(orc, fmt, n, M, K):
