@@ -154,6 +154,8 @@ struct atlas_model {
     int* ring = nullptr;             // [kRing][3][kMaxRows]
     hipEvent_t ring_ev[kRing] = {};
     bool ring_used[kRing] = {};
+    // pinned [n_layers][d_model] of the hooked step's per-layer hidden states
+    float* hook_stage = nullptr;
     // greedy choice settings baked into the captured graph
     float g_theta = 1.f;
     int g_window = 0, g_nsup = 0;
@@ -1391,6 +1393,7 @@ ATLAS_API void atlas_model_destroy(atlas_model* m) {
     for (auto& e : m->ring_ev)
         if (e) (void)hipEventDestroy(e);
     if (m->ring) (void)hipHostFree(m->ring);
+    if (m->hook_stage) (void)hipHostFree(m->hook_stage);
     if (m->st) (void)hipStreamDestroy(m->st);
     delete m;
 }
@@ -1590,24 +1593,35 @@ ATLAS_API int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, flo
     TRY(sync_pos(m));
     TRY(set_token(m, token));
     TRY(embed_launch(m->embed, c.vocab, c.d_model, m->tok_dev, 0, m->x, c.d_model, 1, m->st));
-    std::vector<float> hbuf(hidden ? 0 : (size_t)c.d_model);
+    // The hook only reads the hidden states (StigmergicHook::on_layer returns
+    // a deposit; nothing flows back into the model), so the layers run back
+    // to back: each layer's hidden state is queued into pinned memory and the
+    // hooks run in layer order once the token's forward pass is done -- one
+    // host round trip per token instead of one per layer.
+    const bool keep = hidden || hook;
+    if (keep && !m->hook_stage)
+        ATLAS_HIP(hipHostMalloc((void**)&m->hook_stage, (size_t)c.n_layers * c.d_model * 4));
     for (int li = 0; li < c.n_layers; ++li) {
         TRY(layer_step(m, li));
-        float* dst = hidden ? hidden + (size_t)li * c.d_model : hbuf.data();
-        if (hidden || hook) {
-            ATLAS_HIP(hipMemcpyAsync(dst, m->x, (size_t)c.d_model * 4, hipMemcpyDeviceToHost, m->st));
-            ATLAS_HIP(hipStreamSynchronize(m->st));
-            if (hook) {
-                float delta = 0.f;
-                (void)hook(user, li, dst, c.d_model, &delta);
-            }
-        }
+        if (keep)
+            ATLAS_HIP(hipMemcpyAsync(m->hook_stage + (size_t)li * c.d_model, m->x,
+                                     (size_t)c.d_model * 4, hipMemcpyDeviceToHost, m->st));
     }
     TRY(head_step(m));
     TRY(add_int_launch(m->pos_dev, 1, 1, m->st));
     m->pos += 1;
     if (logits) TRY(download_logits(m, logits));
     else ATLAS_HIP(hipStreamSynchronize(m->st));
+    if (keep) {
+        ATLAS_HIP(hipStreamSynchronize(m->st));
+        if (hidden)
+            std::memcpy(hidden, m->hook_stage, (size_t)c.n_layers * c.d_model * 4);
+        if (hook)
+            for (int li = 0; li < c.n_layers; ++li) {
+                float delta = 0.f;
+                (void)hook(user, li, m->hook_stage + (size_t)li * c.d_model, c.d_model, &delta);
+            }
+    }
     return ATLAS_OK;
 }
 

@@ -120,7 +120,10 @@ float atlas_model_attn_scale(const atlas_model* m);
 int atlas_model_forward_one(atlas_model* m, uint32_t token, float* logits);
 /* forward_one_hooked: also downloads the post-residual hidden state after
  * every layer into hidden ([n_layers x d_model], may be NULL) and calls
- * hook (may be NULL) with it.                                               */
+ * hook (may be NULL) with it.  The hook only reads (StigmergicHook::on_layer
+ * returns a deposit, nothing flows back), so the layers run back to back and
+ * the hooks run in layer order after the token's forward pass: one host
+ * round trip per token.                                                     */
 int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits, float* hidden,
                                    atlas_hook_fn hook, void* user);
 
