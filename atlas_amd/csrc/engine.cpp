@@ -142,8 +142,10 @@ struct atlas_model {
     hipStream_t st = nullptr;
     bool use_graph = true;
     // captured decode steps per mode: 0 forward, 1 + greedy choice, 2 + sampled choice
-    hipGraphExec_t gexec[3] = {nullptr, nullptr, nullptr};
-    hipGraphExec_t gexec_long[3] = {nullptr, nullptr, nullptr};
+    // step modes: 0 logits, 1 greedy choice, 2 device sampling, 3 logits plus
+    // every layer's hidden state (hooked)
+    hipGraphExec_t gexec[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipGraphExec_t gexec_long[4] = {nullptr, nullptr, nullptr, nullptr};
     hipGraphExec_t bgexec[kMaxRows + 1] = {};       // multi-row step per row count
     hipGraphExec_t bgexec_long[kMaxRows + 1] = {};  // ... its two-kernel attention variant
     hipGraphExec_t pgexec[kMaxRows + 1] = {};       // prefill step (no lm_head) per row count
@@ -154,7 +156,9 @@ struct atlas_model {
     int* ring = nullptr;             // [kRing][3][kMaxRows]
     hipEvent_t ring_ev[kRing] = {};
     bool ring_used[kRing] = {};
-    // pinned [n_layers][d_model] of the hooked step's per-layer hidden states
+    // [n_layers][d_model] of the hooked step's per-layer hidden states: on the
+    // device (mode 3 copies them there) and pinned on the host
+    float* hook_dev = nullptr;
     float* hook_stage = nullptr;
     // greedy choice settings baked into the captured graph
     float g_theta = 1.f;
@@ -410,6 +414,9 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
         else
             TRY(gemv_launch(pro_args(L.qkv, m->xb, m->qkv, PRO_RESNORM, m->y2, m->L[li - 1].ffn_norm,
                                      eps, m->x), m->st));
+        // the QKV prologue wrote the hidden state after layer li - 1 into x
+        if (mode == 3 && li > 0)
+            TRY(ew_launch(EW_COPY, m->x, nullptr, m->hook_dev + (size_t)(li - 1) * d, 0.f, d, m->st));
         if (long_ctx) {
             TRY(enqueue_attn_long(m, L));
         } else {
@@ -435,6 +442,9 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
     }
     // x_L = x'_{L-1} + rmsnorm(y2) * ffn_norm_{L-1}, in place in xb
     TRY(residual_rmsnorm_launch(m->xb, m->y2, m->L[c.n_layers - 1].ffn_norm, d, 1, d, eps, m->st));
+    if (mode == 3)
+        TRY(ew_launch(EW_COPY, m->xb, nullptr, m->hook_dev + (size_t)(c.n_layers - 1) * d, 0.f, d,
+                      m->st));
     const bool penalties = m->g_nsup > 0 || m->g_theta != 1.0f;
     GemvArgs h = pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm, eps,
                           m->xn);
@@ -467,7 +477,12 @@ int enqueue_step(atlas_model* m, int mode, bool long_ctx) {
     if (m->fused) return enqueue_step_fused(m, mode, long_ctx);
     const atlas_model_config& c = m->cfg;
     TRY(embed_launch(m->embed, c.vocab, c.d_model, m->tok_dev, 0, m->x, c.d_model, 1, m->st));
-    for (int li = 0; li < c.n_layers; ++li) TRY(layer_step(m, li));
+    for (int li = 0; li < c.n_layers; ++li) {
+        TRY(layer_step(m, li));
+        if (mode == 3)
+            TRY(ew_launch(EW_COPY, m->x, nullptr, m->hook_dev + (size_t)li * c.d_model, 0.f,
+                          c.d_model, m->st));
+    }
     TRY(head_step(m));
     if (mode == 1) TRY(choose_step(m));
     if (mode == 2) TRY(sample_launch(sample_args(m, nullptr), m->st));
@@ -1589,39 +1604,28 @@ ATLAS_API int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, flo
                                              float* hidden, atlas_hook_fn hook, void* user) {
     ATLAS_REQUIRE(m, "forward_one_hooked: null model");
     const atlas_model_config& c = m->cfg;
-    ATLAS_REQUIRE(m->pos < c.max_seq, "position %d reaches max_seq %d", m->pos, c.max_seq);
+    const bool keep = hidden || hook;
+    if (!keep) return atlas_model_forward_one(m, token, logits);
+    // The hook only reads the hidden states (StigmergicHook::on_layer returns
+    // a deposit; nothing flows back into the model), so the token runs as one
+    // captured step that also copies every layer's hidden state aside (mode
+    // 3); the hooks run in layer order once it is done -- one host round
+    // trip per token instead of one per layer.
+    const size_t hb = (size_t)c.n_layers * c.d_model * 4;
+    if (!m->hook_dev) TRY(dalloc(m, (void**)&m->hook_dev, hb));
+    if (!m->hook_stage) ATLAS_HIP(hipHostMalloc((void**)&m->hook_stage, hb));
     TRY(sync_pos(m));
     TRY(set_token(m, token));
-    TRY(embed_launch(m->embed, c.vocab, c.d_model, m->tok_dev, 0, m->x, c.d_model, 1, m->st));
-    // The hook only reads the hidden states (StigmergicHook::on_layer returns
-    // a deposit; nothing flows back into the model), so the layers run back
-    // to back: each layer's hidden state is queued into pinned memory and the
-    // hooks run in layer order once the token's forward pass is done -- one
-    // host round trip per token instead of one per layer.
-    const bool keep = hidden || hook;
-    if (keep && !m->hook_stage)
-        ATLAS_HIP(hipHostMalloc((void**)&m->hook_stage, (size_t)c.n_layers * c.d_model * 4));
-    for (int li = 0; li < c.n_layers; ++li) {
-        TRY(layer_step(m, li));
-        if (keep)
-            ATLAS_HIP(hipMemcpyAsync(m->hook_stage + (size_t)li * c.d_model, m->x,
-                                     (size_t)c.d_model * 4, hipMemcpyDeviceToHost, m->st));
-    }
-    TRY(head_step(m));
-    TRY(add_int_launch(m->pos_dev, 1, 1, m->st));
-    m->pos += 1;
+    TRY(run_step(m, 3));
+    ATLAS_HIP(hipMemcpyAsync(m->hook_stage, m->hook_dev, hb, hipMemcpyDeviceToHost, m->st));
     if (logits) TRY(download_logits(m, logits));
     else ATLAS_HIP(hipStreamSynchronize(m->st));
-    if (keep) {
-        ATLAS_HIP(hipStreamSynchronize(m->st));
-        if (hidden)
-            std::memcpy(hidden, m->hook_stage, (size_t)c.n_layers * c.d_model * 4);
-        if (hook)
-            for (int li = 0; li < c.n_layers; ++li) {
-                float delta = 0.f;
-                (void)hook(user, li, m->hook_stage + (size_t)li * c.d_model, c.d_model, &delta);
-            }
-    }
+    if (hidden) std::memcpy(hidden, m->hook_stage, hb);
+    if (hook)
+        for (int li = 0; li < c.n_layers; ++li) {
+            float delta = 0.f;
+            (void)hook(user, li, m->hook_stage + (size_t)li * c.d_model, c.d_model, &delta);
+        }
     return ATLAS_OK;
 }
 
