@@ -866,8 +866,13 @@ __global__ __launch_bounds__(256) void gemv_v4_kernel(GemvArgs a) {
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
             if constexpr (FMT == WF_I8) {
+                // row scales through the constant address space: wave-uniform
+                // scalar loads (lgkmcnt), so no vector-memory wait here drains
+                // the next buffer's weight loads
+                const __attribute__((address_space(4))) float* cs =
+                    (const __attribute__((address_space(4))) float*)a.scales;
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r) acc[r] *= a.scales[r0 + r < M ? r0 + r : M - 1];
+                for (int r = 0; r < ROWS; ++r) acc[r] *= cs[r0 + r < M ? r0 + r : M - 1];
             }
             if (a.epi == EPI_SILU_MUL) {
                 if constexpr (ROWS % 2 == 0) {
@@ -896,13 +901,21 @@ __global__ __launch_bounds__(256) void gemv_v4_kernel(GemvArgs a) {
         }
     };
 
-    // two register buffers, renamed by unrolling the step loop by two
+    // Two register buffers, renamed by unrolling the step loop by two.  The
+    // prefetch is unconditional: past the wave's last step the cursor names
+    // rows >= M, whose buffer resources have size 0, so those loads return
+    // zeros without touching memory.  A conditional prefetch would give the
+    // compiler a path without the next buffer's loads, and the wait count it
+    // merges for both paths (the smaller one) would then drain the prefetch
+    // before every other step.
     for (int t = 0; t < total; t += 2) {
-        if (t + 1 < total) { load(cl, bufB, sB); advance(cl); }
+        load(cl, bufB, sB);
+        advance(cl);
         compute(cc, bufA, sA);
         advance(cc);
         if (t + 1 >= total) break;
-        if (t + 2 < total) { load(cl, bufA, sA); advance(cl); }
+        load(cl, bufA, sA);
+        advance(cl);
         compute(cc, bufB, sB);
         advance(cc);
     }
