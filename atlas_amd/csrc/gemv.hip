@@ -520,9 +520,12 @@ __global__ __launch_bounds__(256) void gemv_n1_kernel(GemvArgs a) {
                     for (int n = 0; n < NX; ++n) acc[r][n] *= 0.0625f;
             }
             if constexpr (FMT == WF_I8) {
+                // scalar loads (constant address space): no vector-memory wait
+                const __attribute__((address_space(4))) float* cs =
+                    (const __attribute__((address_space(4))) float*)a.scales;
 #pragma unroll
                 for (int r = 0; r < ROWS; ++r) {
-                    const float sc = a.scales[r0 + r < M ? r0 + r : M - 1];
+                    const float sc = cs[r0 + r < M ? r0 + r : M - 1];
 #pragma unroll
                     for (int n = 0; n < NX; ++n) acc[r][n] *= sc;
                 }
