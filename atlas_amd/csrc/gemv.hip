@@ -1120,35 +1120,38 @@ static bool v4_ok(const GemvArgs& a, int unroll) {
 }
 
 // Launch shape of the decode kernel per (format, role): rows per wave,
-// chunk unroll, blocks per CU.  From a sweep of rows 1/2/4, unroll 1-8 and
+// chunk unroll, blocks per CU.  From a sweep of rows 1/2/4, unroll 1-4 and
 // 2-8 blocks per CU at the 7B shapes on MI355X over >= 1.2 GB of rotating
-// weights (the best shapes of a role lie within 1-3% of each other).
+// weights, taken with the unconditional prefetch (the best shapes of a role
+// lie within 1-4% of each other, except int4 QKV and W_o, where 4 rows per
+// wave beat 2 by 7-9%).
 static N1Shape v4_shape(int fmt, int M, int K, int epi) {
     const bool gu = epi == EPI_SILU_MUL, wide = K > 4096, huge = M >= 65536, tall = M >= 8192;
     switch (fmt) {
     case WF_BF16:
-        if (gu || wide) return {2, 4, 4};
+        if (gu) return {2, 4, 4};
+        if (wide) return {1, 4, 3};
         if (huge) return {2, 4, 6};
         return tall ? N1Shape{2, 4, 3} : N1Shape{2, 4, 8};
     case WF_I8:
-        if (gu) return {2, 2, 4};
-        if (wide) return {1, 4, 8};
+        if (gu) return {2, 2, 6};
+        if (wide) return {1, 4, 2};
         if (huge) return {2, 4, 8};
-        return tall ? N1Shape{2, 2, 4} : N1Shape{1, 2, 4};
+        return tall ? N1Shape{2, 1, 4} : N1Shape{1, 2, 4};
     case WF_I4:
-        if (gu) return {2, 1, 3};
-        if (wide) return {2, 2, 4};
+        if (gu) return {2, 1, 2};
+        if (wide) return {2, 1, 3};
         if (huge) return {2, 1, 8};
-        return tall ? N1Shape{2, 2, 2} : N1Shape{2, 2, 8};
+        return {4, 1, 2};
     default:
         return {1, 4, 8};
     }
 }
 
 #define ATLAS_V4_LIST(X)                                                           \
-    X(WF_BF16, 2, 4)                                                               \
-    X(WF_I8, 1, 2) X(WF_I8, 1, 4) X(WF_I8, 2, 2) X(WF_I8, 2, 4)                    \
-    X(WF_I4, 2, 1) X(WF_I4, 2, 2)                                                  \
+    X(WF_BF16, 1, 4) X(WF_BF16, 2, 4)                                              \
+    X(WF_I8, 1, 2) X(WF_I8, 1, 4) X(WF_I8, 2, 1) X(WF_I8, 2, 2) X(WF_I8, 2, 4)     \
+    X(WF_I4, 2, 1) X(WF_I4, 4, 1)                                                  \
     X(WF_F32, 1, 4)
 
 static const void* v4_kernel(int fmt, int rows, int unroll) {

@@ -422,7 +422,7 @@ def main() -> int:
             (3, "gate_up", "gemv_v4_kernel<bf16, rows 2, unroll 4> (RMSNorm+residual prologue, "
                            "SwiGLU epilogue)"),
             (1, "qkv_wo_lm_head", "gemv_v4_kernel<bf16, rows 2, unroll 4> (RMSNorm prologues)"),
-            (2, "w_down", "gemv_v4_kernel<bf16, rows 2, unroll 4> (rows padded to 22272 B)")):
+            (2, "w_down", "gemv_v4_kernel<bf16, rows 1, unroll 4> (rows padded to 22272 B)")):
         per_ms, per_bytes, step_ms, n = gemv_set(which)
         gbs = per_bytes / (per_ms * 1e-3) / 1e9
         kernels[name] = {"kernel": kern, "launches_per_step": n, "ms_per_step": round(step_ms, 4),
