@@ -104,6 +104,7 @@ SIGNATURES = {
     "atlas_attention_fused_f32": (I, [P, P, P, F, P, P, P, P, P, I, I, I, I, F, I, I, I]),
     "atlas_decode_attention_noalloc": (I, [P, P, P, P, I, I, I, I, F, I]),
     "atlas_decode_attention_noalloc_max_bytes": (I64, []),
+    "atlas_bench_stream_floor": (I, [P, I64, I64, I, I, P]),
     "atlas_argmax_u32": (I, [P, I, P]),
     "atlas_quantize_int8_dev": (I, [P, I, I, I, P, P]),
     "atlas_quantize_int4_dev": (I, [P, I, I64, I, P, P]),

@@ -297,6 +297,12 @@ ATLAS_API int atlas_fill_random(int kind, void* out, int64_t n, uint64_t seed, f
     return init_launch(kind, out, (long)n, (unsigned long long)seed, a, b, stream());
 }
 
+ATLAS_API int atlas_bench_stream_floor(const void* buf, int64_t buf_bytes, int64_t bytes_per_launch,
+                                       int launches, int blocks_per_cu, float* us_per_launch) {
+    return stream_floor_bench(buf, (long)buf_bytes, (long)bytes_per_launch, launches, blocks_per_cu,
+                              us_per_launch, stream());
+}
+
 // ---- host quantisers (crates/atlas-quant/src/lib.rs:43-63, 113-145) --------------
 // Same arithmetic as the Rust: scale = absmax / 127 (or 7), 1.0 for an
 // all-zero row/block, value * (1/scale), clamp, round half away from zero.

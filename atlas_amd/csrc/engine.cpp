@@ -1845,7 +1845,7 @@ ATLAS_API int atlas_model_decode_greedy_timed(atlas_model* m, uint32_t first_tok
 
 ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float* ms,
                                      int* launches, int64_t* bytes) {
-    ATLAS_REQUIRE(m && iters > 0 && ms && launches && bytes && which >= 0 && which <= 3,
+    ATLAS_REQUIRE(m && iters > 0 && ms && launches && bytes && which >= 0 && which <= 6,
                   "bench_gemv: bad arguments");
     const float eps = m->cfg.rms_eps;
     auto mat_bytes = [](const DevMat& w, int64_t out) {
@@ -1853,12 +1853,17 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
     };
     const bool k_set = which == 0 || which == 1, down_set = which == 0 || which == 2,
                gu_set = which == 0 || which == 3;
+    const bool qkv_set = k_set || which == 4, wo_set = k_set || which == 5, lm_set = k_set || which == 6;
     int64_t b = 0;
     int n = 0;
     for (const auto& L : m->L) {
-        if (k_set) {
-            b += mat_bytes(L.qkv, L.qkv.rows) + mat_bytes(L.wo, L.wo.rows);
-            n += 2;
+        if (qkv_set) {
+            b += mat_bytes(L.qkv, L.qkv.rows);
+            n += 1;
+        }
+        if (wo_set) {
+            b += mat_bytes(L.wo, L.wo.rows);
+            n += 1;
         }
         if (gu_set) {
             b += mat_bytes(L.gu, L.gu.rows / 2);
@@ -1869,7 +1874,7 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
             n += 1;
         }
     }
-    if (k_set) {
+    if (lm_set) {
         b += mat_bytes(m->lm_head, m->lm_head.rows);
         n += 1;
     }
@@ -1880,13 +1885,13 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
     for (int it = 0; it < iters; ++it) {
         for (size_t li = 0; li < m->L.size(); ++li) {
             LayerW& L = m->L[li];
-            if (k_set) {
+            if (qkv_set) {
                 if (m->fused)
                     TRY(gemv_launch(pro_args(L.qkv, m->xb, m->qkv, PRO_RESNORM, m->y2, L.ffn_norm, eps, m->x), m->st));
                 else
                     TRY(gemv(m, L.qkv, m->x, m->qkv, EPI_STORE));
-                TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
             }
+            if (wo_set) TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
             if (gu_set) {
                 if (m->fused) TRY(enqueue_gu_fused(m, L));
                 else TRY(gemv(m, L.gu, m->x, m->h, EPI_SILU_MUL));
@@ -1896,7 +1901,7 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
                 else TRY(gemv(m, L.down, m->h, m->y, EPI_STORE));
             }
         }
-        if (k_set) {
+        if (lm_set) {
             if (m->fused)
                 TRY(gemv_launch(pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm, eps, m->xn), m->st));
             else

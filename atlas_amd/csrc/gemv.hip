@@ -1293,4 +1293,115 @@ int gemv_multi_launch(const GemvArgs& a_in, hipStream_t st) {
     return ATLAS_EUNSUPPORTED;
 }
 
+// ---------------------------------------------------------------------------
+// Measurement only: the streaming floor of a decode-GEMV-shaped launch.  The
+// kernel reads `bytes` from `src` with the bf16 decode GEMV's work split and
+// load pattern (8 KB rows in groups of two, groups round-robin over the
+// waves, 1 KB per load instruction, 4 KB per row per step, two register
+// buffers) and does no arithmetic on them beyond a checksum, so a graph of
+// such launches measures what a launch of that many bytes costs before any
+// GEMV work (launch gap, ramp, tail and streaming rate).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void stream_floor_kernel(const char* __restrict__ src, long bytes,
+                                                           float* __restrict__ sink) {
+    constexpr int U = 4, ROWS = 2;
+    constexpr long ROW = 8192;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const long n_groups = bytes / (ROW * ROWS);
+    const int S = gridDim.x * 4;
+    const int g0 = blockIdx.x * 4 + wave;
+    const int steps = g0 < n_groups ? (int)((n_groups - 1 - g0) / S + 1) * 2 : 0;   // 2 steps per group
+    auto load = [&](int t, u32x4 (&r)[U][ROWS]) {
+        const long g = g0 + (long)(t >> 1) * S;
+        const bool ok = t < steps;
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            const char* rp = src + (ok ? (g * ROWS + i) * ROW + (t & 1) * (ROW / 2) : 0);
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                uniform_ptr(rp), (short)0, __builtin_amdgcn_readfirstlane(ok ? (int)(ROW / 2) : 0),
+                0x00020000);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                r[u][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + u * 1024, 0, 2));
+        }
+    };
+    float acc = 0.f;
+    auto use = [&](const u32x4 (&r)[U][ROWS]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int i = 0; i < ROWS; ++i) acc += __uint_as_float(r[u][i].x & 0x3f800000u);
+    };
+    u32x4 A[U][ROWS], B[U][ROWS];
+    load(0, A);
+    for (int t = 0; t < steps; t += 2) {
+        load(t + 1, B);
+        use(A);
+        if (t + 1 >= steps) break;
+        load(t + 2, A);
+        use(B);
+    }
+    if (lane == 0) sink[blockIdx.x * 4 + wave] = acc;
+}
+
+int stream_floor_bench(const void* buf, long buf_bytes, long bytes_per_launch, int launches,
+                       int blocks_per_cu, float* us_per_launch, hipStream_t st) {
+    ATLAS_REQUIRE(buf && us_per_launch && launches > 0 && blocks_per_cu > 0,
+                  "stream_floor: bad arguments");
+    ATLAS_REQUIRE(bytes_per_launch >= 16384 && bytes_per_launch % 16384 == 0 &&
+                  bytes_per_launch <= buf_bytes, "stream_floor: %ld bytes per launch", bytes_per_launch);
+    ATLAS_REQUIRE(((uintptr_t)buf & 15) == 0, "stream_floor: 16-byte alignment");
+    const int blocks = blocks_per_cu * device_cu_count();
+    // captured and replayed on a stream of its own (the caller's may be the
+    // legacy default stream, which cannot be captured), after the caller's work
+    ATLAS_HIP(hipStreamSynchronize(st));
+    ATLAS_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    float* sink = nullptr;
+    if (hipMalloc(&sink, (size_t)blocks * 4 * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipStreamDestroy(st);
+        set_error(ATLAS_ENOMEM, "stream_floor: sink allocation");
+        return ATLAS_ENOMEM;
+    }
+    const long per = buf_bytes / bytes_per_launch;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t gx = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = ATLAS_OK;
+    if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) rc = ATLAS_EHIP;
+    for (int k = 0; rc == ATLAS_OK && k < launches; ++k)
+        hipLaunchKernelGGL(stream_floor_kernel, dim3(blocks), dim3(256), 0, st,
+                           static_cast<const char*>(buf) + (k % per) * bytes_per_launch, bytes_per_launch,
+                           sink);
+    if (rc == ATLAS_OK && hipStreamEndCapture(st, &g) != hipSuccess) rc = ATLAS_EHIP;
+    if (rc == ATLAS_OK && hipGraphInstantiate(&gx, g, nullptr, nullptr, 0) != hipSuccess) rc = ATLAS_EHIP;
+    if (rc == ATLAS_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+        rc = ATLAS_EHIP;
+    float best = 0.f;
+    for (int rep = 0; rc == ATLAS_OK && rep < 4; ++rep) {
+        float ms = 0.f;
+        if (hipEventRecord(e0, st) != hipSuccess || hipGraphLaunch(gx, st) != hipSuccess ||
+            hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+            hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+            rc = ATLAS_EHIP;
+            break;
+        }
+        if (rep == 1 || (rep > 1 && ms < best)) best = ms;   // replay 0 warms up
+    }
+    if (rc != ATLAS_OK) {
+        (void)hipGetLastError();
+        set_error(ATLAS_EHIP, "stream_floor: graph capture or replay failed");
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (gx) (void)hipGraphExecDestroy(gx);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(sink);
+    (void)hipStreamDestroy(st);
+    *us_per_launch = best * 1e3f / launches;
+    return rc;
+}
+
 }  // namespace atlas

@@ -86,4 +86,10 @@ inline void gemv_fill_int4_index(GemvArgs& a) {
     }
 }
 
+// Measurement only: per-launch time of a graph of `launches` read-only
+// launches of bytes_per_launch each with the bf16 decode GEMV's work split
+// (consecutive regions of buf, wrapping); best of three replays.
+int stream_floor_bench(const void* buf, long buf_bytes, long bytes_per_launch, int launches,
+                       int blocks_per_cu, float* us_per_launch, hipStream_t st);
+
 }  // namespace atlas

@@ -32,7 +32,8 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of each bf16 decode GEMV kernel: rocprofv3 FETCH_SIZE x 2
 # + WRITE_SIZE x 1 (the factors a 1 GiB copy reads on this part), measured by
 # `bench.py --pmc-probe` (profiles/gemv_7b_counters.md).
-TRAFFIC = {"gate_up": 180980000, "qkv_wo_lm_head": 79151230, "w_down": 90680000}
+TRAFFIC = {"gate_up": 180980000, "qkv": 101250000, "w_o": 33830000, "w_down": 90680000,
+           "lm_head": 822270000}
 ROOT = os.path.dirname(os.path.abspath(__file__))
 SPREAD: dict = {}
 
@@ -286,6 +287,46 @@ def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int
     return m, dt
 
 
+_FLOOR_BUF = []
+
+
+def stream_floor(lib, m) -> dict:
+    """Each decode GEMV role of model m (eager launches, atlas_model_bench_gemv)
+    beside the streaming floor of a launch of the same bytes: a graph of
+    read-only launches with the bf16 decode GEMV's work split and load pattern
+    (atlas_bench_stream_floor, best of 2-4 blocks per CU).  The difference is
+    what the GEMV's own work costs per launch."""
+    if not _FLOOR_BUF:
+        p = C.c_void_p()
+        nbytes = 2 << 30
+        assert lib.atlas_dev_malloc_sync(C.byref(p), nbytes) == 0
+        assert lib.atlas_fill_random(2, p.value, nbytes // 4, 11, 0.0, 1.0) == 0
+        _FLOOR_BUF.extend([p.value, nbytes])
+    buf, nbytes = _FLOOR_BUF
+    out = {}
+    for which, role in ((4, "qkv"), (5, "w_o"), (3, "gate_up"), (2, "w_down"), (6, "lm_head")):
+        ms, launches, b = C.c_float(), C.c_int(), C.c_int64()
+        iters = 32 if which == 6 else 8
+        assert lib.atlas_model_bench_gemv(m._h, 1, which, C.byref(ms), C.byref(launches), C.byref(b)) == 0
+        assert lib.atlas_model_bench_gemv(m._h, iters, which, C.byref(ms), C.byref(launches),
+                                          C.byref(b)) == 0
+        gemv_us = ms.value / launches.value * 1e3
+        per = b.value // (launches.value // iters)
+        size = max(16384, per // 16384 * 16384)
+        best = None
+        for bpc in (2, 3, 4):
+            us = C.c_float()
+            n = 16 if size > 400e6 else 64
+            assert lib.atlas_bench_stream_floor(C.c_void_p(buf), nbytes, size, n, bpc, C.byref(us)) == 0, \
+                lib.atlas_last_error()
+            best = us.value if best is None else min(best, us.value)
+        out[role] = {"MB": round(per / 1e6, 2), "gemv_us": round(gemv_us, 2), "floor_us": round(best, 2),
+                     "gemv_over_floor": round(gemv_us / best, 3)}
+        log(f"stream floor {role}: {per / 1e6:.1f} MB, GEMV {gemv_us:.2f} us, floor {best:.2f} us "
+            f"({gemv_us / best:.3f}x)")
+    return out
+
+
 def step_spread(step_ms) -> dict:
     """Median and p10/p90 of the per-step GPU times (HIP events recorded on
     the engine stream after every step of the timed run)."""
@@ -404,9 +445,10 @@ def main() -> int:
     log(f"bf16 decode: {ms_step:.3f} ms/token, {tok_s:.1f} tok/s, "
         f"weights {wbytes / 1e9:.2f} GB -> {wbytes / (ms_step * 1e-3) / 1e9:.0f} GB/s")
 
-    # The step's bf16 GEMVs run as three kernel instances; the roofline is
-    # reported for the one that takes the most time per step (gate/up: 42% of
-    # the weight bytes), the other two beside it.
+    # The step's bf16 GEMVs, role by role (QKV, W_o, gate/up, W_down and
+    # lm_head launch the same kernel template at different shapes); the
+    # roofline is reported for the role that takes the most time per step
+    # (gate/up: 42% of the weight bytes), the others beside it.
     def gemv_set(which, iters=8):
         ms, launches, nbytes = C.c_float(), C.c_int(), C.c_int64()
         assert lib.atlas_model_bench_gemv(m._h, 1, which, C.byref(ms), C.byref(launches),
@@ -421,9 +463,11 @@ def main() -> int:
     for which, name, kern in (
             (3, "gate_up", "gemv_v4_kernel<bf16, rows 2, unroll 4> (RMSNorm+residual prologue, "
                            "SwiGLU epilogue)"),
-            (1, "qkv_wo_lm_head", "gemv_v4_kernel<bf16, rows 2, unroll 4> (RMSNorm prologues)"),
-            (2, "w_down", "gemv_v4_kernel<bf16, rows 1, unroll 4> (rows padded to 22272 B)")):
-        per_ms, per_bytes, step_ms, n = gemv_set(which)
+            (4, "qkv", "gemv_v4_kernel<bf16, rows 2, unroll 4> (RMSNorm+residual prologue)"),
+            (5, "w_o", "gemv_v4_kernel<bf16, rows 2, unroll 4>"),
+            (2, "w_down", "gemv_v4_kernel<bf16, rows 1, unroll 4> (rows padded to 22272 B)"),
+            (6, "lm_head", "gemv_v4_kernel<bf16, rows 2, unroll 4> (RMSNorm prologue)")):
+        per_ms, per_bytes, step_ms, n = gemv_set(which, 8 if which != 6 else 32)
         gbs = per_bytes / (per_ms * 1e-3) / 1e9
         kernels[name] = {"kernel": kern, "launches_per_step": n, "ms_per_step": round(step_ms, 4),
                          "traffic": TRAFFIC.get(name),
@@ -446,6 +490,7 @@ def main() -> int:
     step_bytes = wbytes + kv_bytes + 100278 * 4
     step_floor_ms = step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
 
+    floor = {"bf16": stream_floor(lib, m)}
     rates = generate_rates(m, am)
     # bench the GPU CPU-baseline inputs before freeing the model
     cpu = None
@@ -468,6 +513,7 @@ def main() -> int:
             f"weights {wq / 1e9:.2f} GB")
         if name == "int8" and cpu is not None:
             cpu["int8"] = cpu_baseline(mq, am, prompt, "int8")
+        floor[name] = stream_floor(lib, mq)
         mq.close()
         del mq
 
@@ -500,6 +546,7 @@ def main() -> int:
                      "bytes_per_launch": dom["bytes_per_launch"],
                      "us_per_launch": dom["us_per_launch"]},
         "gemv_kernels": kernels,
+        "gemv_vs_stream_floor": floor,
         "step_spread": SPREAD.get(am.W_BF16),
         "generate_rates": rates,
         "step_roofline": {"bytes_per_step": int(step_bytes),

@@ -207,8 +207,9 @@ int atlas_model_decode_greedy_timed(atlas_model* m, uint32_t first_token, int n_
 /* Benchmark helper: enqueue `iters` copies of the weight GEMV launches of one
  * decode step (same kernels, shapes, prologues and weights; activations from
  * the engine's scratch) and time them with HIP events on the engine stream.
- * which: 0 = all of them, 1 = QKV, W_o and lm_head, 2 = W_down, 3 = gate/up
- * (for bf16 weights each of 1-3 is one kernel instance).  *ms = elapsed
+ * which: 0 = all of them, 1 = QKV, W_o and lm_head, 2 = W_down, 3 = gate/up,
+ * 4 = QKV, 5 = W_o, 6 = lm_head (for bf16 weights each of 1-3 is one kernel
+ * instance).  *ms = elapsed
  * milliseconds, *launches = GEMV launches issued, *bytes = algorithmic bytes
  * of one copy (weights + scales + x + y).                                    */
 int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float* ms, int* launches,

@@ -241,6 +241,16 @@ int atlas_quantize_int4_host(const float* w, int64_t rows, int64_t cols, int64_t
  * kind 0: N(a, b) f32; 1: N(a, b) bf16 by truncation; 2: U(a, b) f32.        */
 int atlas_fill_random(int kind, void* out, int64_t n, uint64_t seed, float a, float b);
 
+/* Measurement only (no reference counterpart): the streaming floor of a
+ * decode-GEMV-shaped launch.  Captures `launches` read-only launches of
+ * bytes_per_launch bytes each (consecutive regions of buf, wrapping; a
+ * multiple of 16 KiB, the bf16 decode GEMV's work split and load pattern,
+ * blocks_per_cu 4-wave blocks per CU) in one HIP graph on the library's
+ * stream, replays it and stores the best per-launch time in microseconds.
+ * What the decode GEMVs cost beyond it is their own work.                    */
+int atlas_bench_stream_floor(const void* buf, int64_t buf_bytes, int64_t bytes_per_launch,
+                             int launches, int blocks_per_cu, float* us_per_launch);
+
 #ifdef __cplusplus
 }
 #endif
