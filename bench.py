@@ -695,8 +695,11 @@ def pmc_probe(torch, lib, am) -> int:
     plain copy of known size), then for the bf16, int8 and int4 7B models one
     launch of each GEMV set (bench_gemv which = 3 gate/up, 1 QKV + W_o +
     lm_head, 2 W_down) and two decode steps at positions 1 and 2 (attention,
-    argmax); last, int4 11008 x 4096 as one batch-1 GEMV and the skinny GEMM
-    at 4 and 8 rows.  Kernels are told apart by name and grid size."""
+    argmax) and a 127-token prompt in one 128-row chunk (prompt GEMMs and
+    prompt attention); then int4 11008 x 4096 as one batch-1 GEMV and the
+    skinny GEMM at 4 and 8 rows; last, the reference-ABI decode attention of
+    BASELINE config 4 (GQA 32/8/128, f32 cache) at ctx 512, 4096 and 16384.
+    Kernels are told apart by name and grid size."""
     n = 1 << 28
     src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
@@ -721,6 +724,11 @@ def pmc_probe(torch, lib, am) -> int:
         m.forward_one(2)
         m.forward_one(3)
         torch.cuda.synchronize()
+        m.set_prefill_chunk(128)
+        m.reset()
+        m.prefill(list(range(100, 227)))
+        torch.cuda.synchronize()
+        log(f"pmc probe {name}: 127-token prompt chunk done")
         m.close()
     # int4 11008 x 4096 (block 32): batch-1 GEMV, then the skinny GEMM at 4
     # and 8 rows, each on its own copy of the weights
@@ -739,6 +747,21 @@ def pmc_probe(torch, lib, am) -> int:
         f"({M * K // 2 + 4 * M * K // bs} algorithmic weight bytes each)")
     for b in (W, S, X, Y):
         b.free()
+    H, KVH, hd = 32, 8, 128
+    for ctx in (512, 4096, 16384):
+        kv = rng.standard_normal((ctx, KVH, hd)).astype(np.float32)
+        Kc, Vc = DevBufs(lib, kv, 1), DevBufs(lib, kv, 1)
+        Q = DevBufs(lib, rng.standard_normal(H * hd).astype(np.float32), 1)
+        O = DevBufs(lib, np.zeros(H * hd, np.float32), 1)
+        for _ in range(2):
+            lib.atlas_decode_attention(Q.ptrs[0], Kc.ptrs[0], Vc.ptrs[0], O.ptrs[0], H, KVH, hd, ctx - 1,
+                                       C.c_float(0.1067), 0)
+        torch.cuda.synchronize()
+        assert lib.atlas_last_error_code() == 0, lib.atlas_last_error()
+        log(f"pmc probe: decode attention GQA {H}/{KVH}/{hd} ctx {ctx} x2 done "
+            f"({2 * ctx * KVH * hd * 4} K/V bytes each)")
+        for b in (Kc, Vc, Q, O):
+            b.free()
     return 0
 
 
