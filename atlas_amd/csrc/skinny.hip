@@ -583,8 +583,11 @@ __global__ __launch_bounds__(1024) void skinny_i4d_kernel(GemvArgs a, float* __r
         const int r = min(q >> 1, max(R - 1, 0)), c = q & 1;
         const uint32_t row = (uint32_t)min((bx + r * gx) * 16 + li, M - 1);
         const int kt = kt0 + min(tw0 + 4 * c + g, nks - 1);
+        // cached (policy 0): the two halves of each row's 128-byte line come
+        // from two items of the wave, and a non-temporal first half made the
+        // second fetch the line again
         w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          wres, (int)(row * wstride + (uint32_t)kt * 16u), 0, 2));
+                                          wres, (int)(row * wstride + (uint32_t)kt * 16u), 0, 0));
         if (c == 0) {
             const uint32_t so = row * (uint32_t)a.bpr;
             if constexpr (SV) {                                 // nks % 4 == 0, one scale per tile
@@ -810,8 +813,9 @@ __global__ __launch_bounds__(1024) void skinny_d_kernel(GemvArgs a, float* __res
         uint32_t off;
         if constexpr (FMT == WF_BF16) off = (uint32_t)(kt0 + min(tw0 + j, nks - 1)) * 64u + 16u * g;
         else off = (uint32_t)(kt0 + min(tw0 + 2 * j, nks - 2)) * 32u + 16u * g;
+        // cached, as in skinny_i4d_kernel: a load covers 16 rows x 64 bytes
         return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             wres, (int)(row * wstride + off), 0, 2));
+                                             wres, (int)(row * wstride + off), 0, 0));
     };
     if (ntw == 0) {                                             // a wave past the slice
 #pragma unroll
