@@ -1293,9 +1293,6 @@ static int launch_skinny_lds(const GemvArgs& a, hipStream_t st) {
 constexpr int GR_ROWS = 128;        // weight rows per block
 constexpr int GR_MAX_N = 128;       // activation rows per launch
 
-// 16-byte slot of MFMA lane L's A operand in a gemm_rows LDS tile
-__device__ __forceinline__ int gr_swz(int L) { return L ^ ((L >> 2) & 12); }
-
 // hi / lo bf16 parts of 8 floats, packed as MFMA operands
 __device__ __forceinline__ void split8(const f32x4 p0, const f32x4 p1, u32x4& hi, u32x4& lo) {
     const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
@@ -1318,7 +1315,6 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, li = lane & 15;
-    const int lane_swz = gr_swz(lane);
     const int M = a.M, N = a.N;
     const int s0 = blockIdx.y * steps_per_split;
     const int s1 = min(a.K / 32, s0 + steps_per_split);   // s1 - s0: a multiple of 4
@@ -1337,18 +1333,13 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
         p1 = *reinterpret_cast<const f32x4*>(xr + 4);
         if (n >= N) p0 = p1 = f32x4{0.f, 0.f, 0.f, 0.f};
     };
-    // MFMA lane L = 16 gg + ii keeps its operand in 16-byte slot gr_swz(L) of
-    // the tile: the stores (4 consecutive threads = 4 k groups of one row)
-    // and the operand reads (16 consecutive lanes = 16 rows) then both fall
-    // on 16 different bank groups (unswizzled, the stores of a k group's four
-    // threads shared one: 4.8 conflict cycles per LDS instruction)
     auto xstore = [&](int buf, int q, const f32x4& p0, const f32x4& p1) {
         const int it = (int)threadIdx.x + 256 * q;
         const int gg = it & 3, ii = (it >> 2) & 15, t = (it >> 6) % NT, st = it / (64 * NT);
         u32x4 hi, lo;
         split8(p0, p1, hi, lo);
-        As[buf][st][t][0][gr_swz(16 * gg + ii)] = hi;
-        As[buf][st][t][1][gr_swz(16 * gg + ii)] = lo;
+        As[buf][st][t][0][16 * gg + ii] = hi;
+        As[buf][st][t][1][16 * gg + ii] = lo;
     };
 
     const int nsteps = s1 - s0;                   // k steps of this split
@@ -1398,8 +1389,8 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __
             }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const bf16x8 ah = __builtin_bit_cast(bf16x8, As[buf][st][t][0][lane_swz]);
-                const bf16x8 al = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane_swz]);
+                const bf16x8 ah = __builtin_bit_cast(bf16x8, As[buf][st][t][0][lane]);
+                const bf16x8 al = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane]);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     if constexpr (FMT == WF_I4) {
