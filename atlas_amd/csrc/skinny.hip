@@ -1307,8 +1307,12 @@ __device__ __forceinline__ void split8(const f32x4 p0, const f32x4 p1, u32x4& hi
     lo = u32x4{pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])};
 }
 
+// int4 at eight tiles runs one block per CU: its per-step scaled products
+// need ~370 registers (spilled 27 at two blocks per CU), and one 128-row
+// launch that streams the weights once beats two 64-row launches that
+// stream them twice (127-token int4 prefill 14.1 -> 12.6 ms)
 template <int FMT, int NT>
-__global__ __launch_bounds__(256, 2) void gemm_rows_kernel(GemvArgs a, float* __restrict__ partial,
+__global__ __launch_bounds__(256, (FMT == WF_I4 && NT == 8) ? 1 : 2) void gemm_rows_kernel(GemvArgs a, float* __restrict__ partial,
                                                            int steps_per_split, int cpb_shift) {
     constexpr int ITEMS = 2 * NT * 64 / 256;      // A items (8 floats) per thread per chunk
     __shared__ u32x4 As[2][2][NT][2][64];         // [buf][k step][tile][hi/lo][lane]
@@ -1469,8 +1473,8 @@ bool gemm_rows_ok(const GemvArgs& a) {
            (a.epi == EPI_STORE || (a.epi == EPI_SILU_MUL && a.M % 2 == 0));
 }
 
-// int4 launches hold at most four 16-row tiles (gemm_rows_launch splits
-// larger chunks); anything else is refused rather than left unwritten
+// 2, 4 or 8 16-row tiles per launch; more are refused rather than left
+// unwritten (gemm_rows_launch splits chunks above 128 rows)
 template <int FMT>
 static int gemm_rows_go(const GemvArgs& a, float* partial, dim3 grid, int steps, int cpb_shift,
                         hipStream_t st) {
@@ -1479,10 +1483,10 @@ static int gemm_rows_go(const GemvArgs& a, float* partial, dim3 grid, int steps,
         hipLaunchKernelGGL((gemm_rows_kernel<FMT, 2>), grid, dim3(256), 0, st, a, partial, steps, cpb_shift);
     else if (nt <= 4)
         hipLaunchKernelGGL((gemm_rows_kernel<FMT, 4>), grid, dim3(256), 0, st, a, partial, steps, cpb_shift);
-    else if constexpr (FMT != WF_I4)
+    else if (nt <= 8)
         hipLaunchKernelGGL((gemm_rows_kernel<FMT, 8>), grid, dim3(256), 0, st, a, partial, steps, cpb_shift);
     else {
-        set_error(ATLAS_EUNSUPPORTED, "gemm rows: int4 launches take at most 64 rows (got %d)", a.N);
+        set_error(ATLAS_EUNSUPPORTED, "gemm rows: a launch takes at most 128 rows (got %d)", a.N);
         return ATLAS_EUNSUPPORTED;
     }
     return ATLAS_OK;
@@ -1527,10 +1531,7 @@ static int gemm_rows_part(const GemvArgs& a, hipStream_t st) {
 int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
     ATLAS_REQUIRE(gemm_rows_ok(a), "gemm rows: unsupported shape (fmt %d, n %d, k %d)", a.fmt, a.N,
                   a.K);
-    // int4 keeps at most four 16-row tiles per launch: its per-step scaled
-    // products need more registers than eight tiles leave (the weights then
-    // stream twice per 128-row chunk, at a quarter of bf16's bytes)
-    const int cap = a.fmt == WF_I4 ? 64 : GR_MAX_N;
+    const int cap = GR_MAX_N;
     for (int n0 = 0; n0 < a.N; n0 += cap) {
         GemvArgs p = a;
         p.N = std::min(cap, a.N - n0);
