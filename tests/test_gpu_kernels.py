@@ -585,6 +585,7 @@ def test_attention_fused(orc, H, KVH, hd, ctx, window, splits, chunk):
 # ---------------------------------------------------------------------------
 
 def test_bench_stream_floor_runs_and_rejects_bad_sizes():
+    lib().atlas_clear_error()                            # an earlier test's refusal may still be recorded
     buf = Dev.empty((16 << 20) // 4)                     # 16 MiB
     us = C.c_float(-1.0)
     # a graph of 8 launches of 4 MiB over the buffer, at 2 blocks per CU
@@ -592,7 +593,7 @@ def test_bench_stream_floor_runs_and_rejects_bad_sizes():
                                           C.byref(us)) == 0
     # 4 MiB at 8 TB/s would be 0.5 us; a launch also pays its fixed cost
     assert 0.5 < us.value < 1000.0, us.value
-    sync()
+    assert lib().atlas_last_error_code() == 0, lib().atlas_last_error()
     for nbytes in (4 << 20 | 4096, 0, 32 << 20):         # not whole 16 KiB groups, empty, past the buffer
         assert lib().atlas_bench_stream_floor(C.c_void_p(buf.ptr), 16 << 20, nbytes, 8, 2,
                                               C.byref(us)) < 0, nbytes
