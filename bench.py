@@ -278,12 +278,22 @@ def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int
         if f"chunk{chunk}_s" in pre:
             pre[f"chunk{chunk}_tok_s"] = round((len(prompt) - 1) / pre[f"chunk{chunk}_s"], 1)
     PREFILL[fmt] = pre
+    # the timed region: `steps` greedy steps, one graph replay each, with the
+    # stream idle on entry (the warm-up call synchronises) and synchronised on
+    # exit; no event between the steps (each costs 6-10 us of stream time)
     toks = m.decode_greedy(int(prompt[-1]), warmup)
+    first = int(toks[-1]) if warmup else int(prompt[-1])
     t0 = time.perf_counter()
-    toks2, step_ms = m.decode_greedy_timed(int(toks[-1]) if warmup else int(prompt[-1]), steps)
+    toks2 = m.decode_greedy(first, steps)
     dt = time.perf_counter() - t0
     assert len(toks2) == steps
+    # the per-step spread: the same positions again, an event after every step
+    m.reset()
+    m.prefill([int(t) for t in prompt[:-1]])
+    m.decode_greedy(int(prompt[-1]), warmup)
+    toks3, step_ms = m.decode_greedy_timed(first, steps)
     SPREAD[fmt] = step_spread(step_ms)
+    SPREAD[fmt]["same_tokens_as_timed_run"] = bool(np.array_equal(toks2, toks3))
     return m, dt
 
 
@@ -329,7 +339,8 @@ def stream_floor(lib, m) -> dict:
 
 def step_spread(step_ms) -> dict:
     """Median and p10/p90 of the per-step GPU times (HIP events recorded on
-    the engine stream after every step of the timed run)."""
+    the engine stream after every step of a second run over the timed run's
+    positions)."""
     a = np.asarray(step_ms, np.float64)
     return {"p10_ms": round(float(np.percentile(a, 10)), 4),
             "median_ms": round(float(np.median(a)), 4),
