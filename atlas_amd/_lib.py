@@ -86,8 +86,11 @@ SIGNATURES = {
     "atlas_memset_zero": (I, [P, SZ]),
     "atlas_set_device": (I, [I]),
     "atlas_set_stream": (I, [P]),
+    "atlas_set_thread_stream": (I, [P]),
+    "atlas_clear_thread_stream": (I, []),
     "atlas_get_stream": (P, []),
     "atlas_stream_sync": (I, []),
+    "atlas_thread_scratch_bytes": (I64, []),
     "atlas_device_cu_count": (I, []),
     # Part 3: extensions
     "atlas_gemv_f32": (I, [I, P, P, I, P, P, I, I]),
@@ -119,6 +122,8 @@ SIGNATURES = {
     "atlas_model_init_random": (I, [P, U64]),
     "atlas_model_reset": (I, [P]),
     "atlas_model_pos": (I, [P]),
+    "atlas_model_set_kv_rows": (I, [P, I, I, I, I, P, P]),
+    "atlas_model_set_pos": (I, [P, I]),
     "atlas_model_attn_scale": (F, [P]),
     "atlas_model_forward_one": (I, [P, U32, P]),
     "atlas_model_forward_one_hooked": (I, [P, U32, P, P, HOOK_FN, P]),

@@ -3,8 +3,9 @@
 // Error model: every C-ABI entry point returns 0 on success or a negative
 // ATLAS_E* code and records a message retrievable with atlas_last_error()
 // (thread-local).  Entry points that keep the reference's `void` signature
-// record the error the same way.  Launches go to the library's current
-// stream (atlas_set_stream; default: the null stream, as the reference uses).
+// record the error the same way.  Launches go to the library-wide stream
+// (atlas_set_stream; default: the null stream, as the reference uses) unless
+// the calling thread set its own (atlas_set_thread_stream).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -21,7 +22,7 @@ namespace atlas {
 
 void set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
-hipStream_t stream();          // the calling thread's launch stream
+hipStream_t stream();          // the calling thread's override, else the library-wide stream
 int device_cu_count();         // CUs of the current device (cached)
 
 // Device scratch owned by the calling thread on the current device, for entry
@@ -42,7 +43,11 @@ enum ScratchSlot {
     SCR_ATTN_CNT,       // atlas_decode_attention merge counters (kept at zero)
     SCR_N
 };
+// A slot that must grow while its stream is being captured is refused with
+// ATLAS_EUNSUPPORTED (no allocation is recorded into the caller's graph).  A
+// thread's slots are freed when the thread exits.
 int thread_scratch(int slot, size_t bytes, void** out, bool zero_new = false);
+size_t thread_scratch_bytes();   // bytes the calling thread holds on the current device
 
 // Check a HIP call; on failure record the error and return ATLAS_EHIP.
 #define ATLAS_HIP(call)                                                        \

@@ -1547,6 +1547,33 @@ ATLAS_API int atlas_model_get_config(const atlas_model* m, atlas_model_config* o
 }
 
 ATLAS_API int atlas_model_pos(const atlas_model* m) { return m ? m->pos : -1; }
+
+ATLAS_API int atlas_model_set_kv_rows(atlas_model* m, int seq, int layer, int pos0, int n,
+                                      const float* k, const float* v) {
+    ATLAS_REQUIRE(m && k && v, "set_kv_rows: null argument");
+    const atlas_model_config& c = m->cfg;
+    ATLAS_REQUIRE(seq >= 0 && seq < m->B, "set_kv_rows: sequence %d outside 0..%d", seq, m->B - 1);
+    ATLAS_REQUIRE(layer >= 0 && layer < c.n_layers, "set_kv_rows: layer %d", layer);
+    ATLAS_REQUIRE(pos0 >= 0 && n >= 0 && (long)pos0 + n <= c.max_seq,
+                  "set_kv_rows: rows [%d, %ld) outside the cache of %d", pos0, (long)pos0 + n,
+                  c.max_seq);
+    const size_t off = (size_t)seq * m->slot_stride + (size_t)pos0 * m->kvd;
+    const size_t bytes = (size_t)n * m->kvd * 4;
+    ATLAS_HIP(hipMemcpyAsync(m->L[layer].kc + off, k, bytes, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipMemcpyAsync(m->L[layer].vc + off, v, bytes, hipMemcpyHostToDevice, m->st));
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
+
+ATLAS_API int atlas_model_set_pos(atlas_model* m, int pos) {
+    ATLAS_REQUIRE(m, "set_pos: null model");
+    ATLAS_REQUIRE(pos >= 0 && pos < m->cfg.max_seq, "set_pos: %d outside [0, %d)", pos,
+                  m->cfg.max_seq);
+    m->pos = pos;
+    TRY(sync_pos(m));
+    ATLAS_HIP(hipStreamSynchronize(m->st));
+    return ATLAS_OK;
+}
 ATLAS_API float atlas_model_attn_scale(const atlas_model* m) { return m ? m->scale : 0.f; }
 ATLAS_API void* atlas_model_stream(atlas_model* m) { return m ? (void*)m->st : nullptr; }
 ATLAS_API const float* atlas_model_logits_dev(atlas_model* m) { return m ? m->logits : nullptr; }
@@ -1810,25 +1837,35 @@ static int decode_greedy(atlas_model* m, uint32_t first_token, int n_steps, uint
     // engine stream, so step i's GPU time is the span between two of them
     std::vector<hipEvent_t> ev;
     int rc = ATLAS_OK;
+    // this function's own HIP calls record what failed; an error from
+    // run_step keeps the message run_step recorded
+    auto hip_ok = [&rc](hipError_t e, const char* what) {
+        if (e == hipSuccess) return true;
+        set_error(ATLAS_EHIP, "decode_greedy: %s: %s", what, hipGetErrorString(e));
+        rc = ATLAS_EHIP;
+        return false;
+    };
     if (step_ms) {
         ev.resize((size_t)n_steps + 1, nullptr);
         for (auto& e : ev)
-            if (!rc && hipEventCreate(&e) != hipSuccess) rc = ATLAS_EHIP;
-        if (!rc && hipEventRecord(ev[0], m->st) != hipSuccess) rc = ATLAS_EHIP;
+            if (!rc) hip_ok(hipEventCreate(&e), "hipEventCreate");
+        if (!rc) hip_ok(hipEventRecord(ev[0], m->st), "hipEventRecord");
     }
     for (int i = 0; i < n_steps && !rc; ++i) {
         rc = run_step(m, 1);
-        if (!rc && step_ms && hipEventRecord(ev[i + 1], m->st) != hipSuccess) rc = ATLAS_EHIP;
+        if (!rc && step_ms) hip_ok(hipEventRecord(ev[i + 1], m->st), "hipEventRecord");
     }
-    if (!rc && tokens && n_steps > 0 &&
-        hipMemcpyAsync(tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost, m->st) != hipSuccess)
-        rc = ATLAS_EHIP;
-    if (hipStreamSynchronize(m->st) != hipSuccess && !rc) rc = ATLAS_EHIP;
+    if (!rc && tokens && n_steps > 0)
+        hip_ok(hipMemcpyAsync(tokens, m->hist, (size_t)n_steps * 4, hipMemcpyDeviceToHost, m->st),
+               "token download");
+    {
+        const hipError_t e = hipStreamSynchronize(m->st);
+        if (!rc) hip_ok(e, "hipStreamSynchronize");
+    }
     for (int i = 0; i < n_steps && !rc && step_ms; ++i)
-        if (hipEventElapsedTime(&step_ms[i], ev[i], ev[i + 1]) != hipSuccess) rc = ATLAS_EHIP;
+        hip_ok(hipEventElapsedTime(&step_ms[i], ev[i], ev[i + 1]), "hipEventElapsedTime");
     for (auto e : ev)
         if (e) (void)hipEventDestroy(e);
-    if (rc == ATLAS_EHIP) set_error(ATLAS_EHIP, "decode_greedy: HIP call failed");
     return rc;
 }
 

@@ -288,16 +288,21 @@ int softmax_rows_launch(const float* x, float* out, int rows, int cols, hipStrea
     return ATLAS_OK;
 }
 
-// AdamW (kernels/matmul.cu:138-161 contract; training, kept for ABI parity)
+// AdamW (kernels/matmul.cu:138-161 contract; training, kept for ABI parity).
+// bc1/bc2 are the reciprocal bias corrections 1/(1 - beta^t) that the caller
+// computes (crates/atlas-optim/src/lib.rs:203-204), so they multiply; weight
+// decay is decoupled: p * (1 - lr*wd) - lr * m_hat / (sqrt(v_hat) + eps).
 __global__ void adamw_kernel(float* p, float* m, float* v, const float* g, float lr, float b1,
                              float b2, float eps, float wd, float bc1, float bc2, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float gi = g[i];
-    m[i] = b1 * m[i] + (1.f - b1) * gi;
-    v[i] = b2 * v[i] + (1.f - b2) * gi * gi;
-    const float mh = m[i] / bc1, vh = v[i] / bc2;
-    p[i] -= lr * (mh / (sqrtf(vh) + eps) + wd * p[i]);
+    const float mi = b1 * m[i] + (1.f - b1) * gi;
+    const float vi = b2 * v[i] + (1.f - b2) * gi * gi;
+    m[i] = mi;
+    v[i] = vi;
+    const float mh = mi * bc1, vh = vi * bc2;
+    p[i] = p[i] * (1.f - lr * wd) - lr * mh / (sqrtf(vh) + eps);
 }
 
 int adamw_launch(float* p, float* m, float* v, const float* g, float lr, float b1, float b2,
@@ -307,6 +312,8 @@ int adamw_launch(float* p, float* m, float* v, const float* g, float lr, float b
     hipLaunchKernelGGL(adamw_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, m, v, g, lr, b1, b2,
                        eps, wd, bc1, bc2, n);
     ATLAS_LAUNCH_CHECK("adamw");
+    // the reference returns with the update complete (kernels/matmul.cu:555-556)
+    ATLAS_HIP(hipStreamSynchronize(st));
     return ATLAS_OK;
 }
 

@@ -213,6 +213,19 @@ class OlmoModel:
     def pos(self) -> int:
         return load().atlas_model_pos(self._h)
 
+    def set_kv_rows(self, layer: int, pos0: int, k, v, seq: int = 0) -> None:
+        """Test helper (no reference counterpart): cache rows pos0.. of one
+        layer of sequence slot seq; k, v are [n][n_kv * head_dim] f32."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        if k.shape != v.shape or k.ndim != 2:
+            raise ValueError("set_kv_rows: k and v must be [n][kv_dim] arrays of one shape")
+        check(load().atlas_model_set_kv_rows(self._h, seq, layer, pos0, k.shape[0], _p(k), _p(v)))
+
+    def set_pos(self, pos: int) -> None:
+        """Test helper: the position the next decode step writes."""
+        check(load().atlas_model_set_pos(self._h, pos))
+
     @property
     def attn_scale(self) -> float:
         return load().atlas_model_attn_scale(self._h)

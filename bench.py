@@ -791,10 +791,17 @@ def cpu_info() -> dict:
             "cores_available": len(os.sched_getaffinity(0))}
 
 
+CPU_POS = 140        # inside the timed decode's contexts (128-token prompt + steps)
+
+
 def cpu_baseline(m, am, prompt, fmt: str) -> dict:
     """The oracle (restatement of the reference CPU path) on one 7B decode
     step of the same weights (bf16, or int8 with its row scales), downloaded
-    from the GPU; the process is pinned to one host core for the timed step."""
+    from the GPU, at position CPU_POS: the oracle and the engine get the same
+    seeded KV-cache rows for positions 0..CPU_POS-1, so the timed CPU step
+    includes attention over CPU_POS + 1 positions in every layer, and the
+    GPU step over the same state is compared with it.  The process is pinned
+    to one host core for the timed step."""
     sys.path.insert(0, ROOT)
     import oracle as orc
     d, V, L, f = 4096, 100278, 32, 11008
@@ -823,12 +830,23 @@ def cpu_baseline(m, am, prompt, fmt: str) -> dict:
     fn = m.get_tensor(am.T_FINAL_NORM, 0, (d,), np.float32)
     log(f"cpu baseline ({fmt}): weights downloaded in {time.perf_counter() - t0:.1f}s")
     ocfg = dict(vocab=V, d_model=d, n_layers=L, n_heads=32, n_kv_heads=32, ffn_hidden=f,
-                max_seq=8, rope_theta=500000.0, rms_eps=1e-6,
+                max_seq=CPU_POS + 8, rope_theta=500000.0, rms_eps=1e-6,
                 yarn=dict(factor=8.0, orig_max_pos=8192, attn_factor=1.2079441541679836,
                           beta_fast=32.0, beta_slow=1.0),
                 sliding_window=4096, layer_sliding=[0 if i % 4 == 3 else 1 for i in range(L)],
                 post_norm=True)
     om = orc.Model(ocfg, dict(embed=emb, lm_head=lm, final_norm=fn, layers=layers), threads=1)
+    # the same cache rows in both (K, V ~ N(0, 1)), then both at CPU_POS
+    krng = np.random.default_rng(140)
+    m.reset()
+    for li in range(L):
+        k = krng.standard_normal((CPU_POS, 32 * 128), dtype=np.float32)
+        v = krng.standard_normal((CPU_POS, 32 * 128), dtype=np.float32)
+        m.set_kv_rows(li, 0, k, v)
+        om.set_kv_rows(li, 0, k, v)
+    m.set_pos(CPU_POS)
+    om.set_pos(CPU_POS)
+    tok = int(prompt[0])
     info = cpu_info()
     # one core for the timed step (in-process: the affinity of this thread,
     # which runs the single-threaded oracle), restored afterwards
@@ -837,21 +855,23 @@ def cpu_baseline(m, am, prompt, fmt: str) -> dict:
     os.sched_setaffinity(0, {core})
     try:
         t0 = time.perf_counter()
-        logits = om.forward_one(int(prompt[0]))
+        logits = om.forward_one(tok)
         dt = time.perf_counter() - t0
     finally:
         os.sched_setaffinity(0, saved)
-    # the same token through the GPU engine at pos 0 (sanity: top-1 agrees)
-    m.reset()
-    glog = m.forward_one(int(prompt[0]))
+    # the same token and state through the GPU engine (a sanity line; the
+    # parity tests carry the parity claims)
+    glog = m.forward_one(tok)
     agree = int(np.argmax(glog[::-1])) == int(np.argmax(logits[::-1]))
     rel = float(np.max(np.abs(glog - logits)) / np.max(np.abs(logits)))
-    log(f"cpu baseline ({fmt}): one 7B decode step on core {core} of {info['cpu_model']} in "
-        f"{dt:.1f}s; GPU/CPU logits rel err {rel:.2e}, top-1 {'agrees' if agree else 'DIFFERS'}")
+    log(f"cpu baseline ({fmt}): one 7B decode step at pos {CPU_POS} on core {core} of "
+        f"{info['cpu_model']} in {dt:.1f}s; GPU/CPU logits rel err {rel:.2e}, top-1 "
+        f"{'agrees' if agree else 'DIFFERS'}")
     return {"value": round(1.0 / dt, 5), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"one OLMo-3-7B-shaped {fmt} decode step (pos 0, all 32 layers + lm_head) "
-                      "of the same weights, oracle/oracle.c single-threaded, pinned to one core",
-            "pinned_core": core, **info,
+            "sample": f"one OLMo-3-7B-shaped {fmt} decode step at position {CPU_POS} (all 32 "
+                      f"layers with attention over {CPU_POS + 1} cached positions, lm_head) of "
+                      "the same weights, oracle/oracle.c single-threaded, pinned to one core",
+            "pinned_core": core, "position": CPU_POS, **info,
             "seconds": round(dt, 2), "gpu_vs_cpu_logit_rel_err": rel, "top1_agrees": agree}
 
 

@@ -114,6 +114,15 @@ int atlas_model_init_random(atlas_model* m, uint64_t seed);
 
 int atlas_model_reset(atlas_model* m);
 int atlas_model_pos(const atlas_model* m);
+/* Test helpers, no reference counterpart: write n rows of one layer's KV
+ * cache of sequence slot seq (rows pos0.., each n_kv_heads * head_dim f32
+ * for K and for V, from host memory; the layout of GpuKvCache,
+ * crates/atlas-model/src/lib.rs:557-596), and set the decode position.
+ * Parity tests use them to start decoding at a long position with the same
+ * cache rows in the engine and in the CPU oracle.                          */
+int atlas_model_set_kv_rows(atlas_model* m, int seq, int layer, int pos0, int n,
+                            const float* k, const float* v);
+int atlas_model_set_pos(atlas_model* m, int pos);
 float atlas_model_attn_scale(const atlas_model* m);
 /* forward_one_gpu: one token at the current position; pos += 1.  logits
  * (host, [vocab]) may be NULL (they stay on the device).                    */

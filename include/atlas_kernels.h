@@ -19,9 +19,21 @@
  * atlas_last_error() report the most recent failure on the calling thread
  * (cleared by atlas_clear_error()).
  *
- * Streams: every launch goes to the library's current stream
- * (atlas_set_stream; default = the null stream, as in the reference,
- * kernels/matmul.cu:17-23).  Launches are asynchronous.
+ * Streams: every launch, stream-ordered allocation and copy goes to the
+ * library-wide stream set by atlas_set_stream (default = the null stream, as
+ * in the reference, kernels/matmul.cu:17-23), from whichever thread it is
+ * called.  A thread may override it for its own calls only
+ * (atlas_set_thread_stream, undone by atlas_clear_thread_stream).  Launches
+ * are asynchronous.
+ *
+ * Library scratch: entry points that need device scratch and are not handed
+ * a workspace (atlas_decode_attention, atlas_gpu_argmax,
+ * atlas_gemm_skinny_f32, atlas_attention_fused_f32) keep it per calling
+ * thread, grow it on first use of a larger shape and free it when the
+ * thread exits.  A call that would grow it while its stream is being
+ * captured into a graph returns / records ATLAS_EUNSUPPORTED instead: warm
+ * up with one call of the same shape before the capture, or use
+ * atlas_decode_attention_noalloc.
  */
 #ifndef ATLAS_KERNELS_H
 #define ATLAS_KERNELS_H
@@ -58,7 +70,11 @@ void atlas_rope_apply_f32(float* x, int pos, int head_dim, float theta_base);
 void atlas_silu_mul_f32(const float* gate, const float* up, float* out, int n);
 /* lib.rs:36 -> matmul.cu:620-626 */
 void atlas_vram_copy_f32(const float* src, float* dst, int n);
-/* lib.rs:37-41 -> matmul.cu:546-557 (training; kept for ABI completeness) */
+/* lib.rs:37-41 -> matmul.cu:138-161, 546-557 (training; kept for ABI
+ * completeness).  bc1/bc2 are 1/(1 - beta^t) as the caller passes them
+ * (crates/atlas-optim/src/lib.rs:203-204) and multiply the moments;
+ * param = param*(1 - lr*wd) - lr*m_hat/(sqrt(v_hat) + eps).  Returns with
+ * the update complete (the current stream is synchronised).                 */
 void atlas_adamw_step(float* param, float* m, float* v, const float* grad, float lr,
                       float beta1, float beta2, float eps, float wd, float bc1, float bc2,
                       int n);
@@ -117,9 +133,13 @@ int atlas_memcpy_d2d(void* dst, const void* src, size_t bytes);
 int atlas_memset_zero(void* dst, size_t bytes);     /* fill kernel, graph-safe */
 
 int atlas_set_device(int device);
-int atlas_set_stream(void* hip_stream);               /* NULL = null stream */
-void* atlas_get_stream(void);
-int atlas_stream_sync(void);
+int atlas_set_stream(void* hip_stream);               /* library-wide; NULL = null stream */
+int atlas_set_thread_stream(void* hip_stream);        /* this thread only (NULL = null stream) */
+int atlas_clear_thread_stream(void);                  /* back to the library-wide stream */
+void* atlas_get_stream(void);                         /* the calling thread's effective stream */
+int atlas_stream_sync(void);                          /* waits for that stream */
+/* Bytes of library scratch the calling thread holds on the current device. */
+int64_t atlas_thread_scratch_bytes(void);
 int atlas_device_cu_count(void);
 
 /* ===== Part 3: decode hot-path extensions (no reference counterpart) ===== */

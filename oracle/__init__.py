@@ -118,6 +118,8 @@ def _declare(L):
         "orc_model_attn_scale": (F, [P]),
         "orc_model_forward_one": (None, [P, C.c_uint32, P, P]),
         "orc_model_select_slot": (None, [P, I]),
+        "orc_model_set_kv_rows": (I, [P, I, I, I, P, P]),
+        "orc_model_set_pos": (I, [P, I]),
         "orc_argmax": (I, [P, I]),
         "orc_repetition_penalty": (None, [P, I, P, I, F]),
         "orc_generate_greedy": (I, [P, P, I, I, P, I, F, I, I64, P, I, P]),
@@ -439,6 +441,18 @@ class Model:
     @property
     def pos(self) -> int:
         return lib().orc_model_pos(self.h)
+
+    def set_kv_rows(self, layer: int, pos0: int, k, v) -> None:
+        """Test seeding: cache rows pos0.. of one layer (k, v: [n][n_kv*hd] f32)."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        assert k.shape == v.shape and k.ndim == 2
+        if lib().orc_model_set_kv_rows(self.h, layer, pos0, k.shape[0], _p(k), _p(v)) != 0:
+            raise ValueError("set_kv_rows: rows outside the cache")
+
+    def set_pos(self, pos: int) -> None:
+        if lib().orc_model_set_pos(self.h, pos) != 0:
+            raise ValueError(f"set_pos: {pos} outside the cache")
 
     @property
     def attn_scale(self) -> float:

@@ -429,6 +429,27 @@ void orc_model_select_slot(orc_model* m, int slot) {
 /* reset(): pos = 0, caches not zeroed (lib.rs:1389-1392, 872-880) */
 void orc_model_reset(orc_model* m) { m->pos[m->slot] = 0; }
 int orc_model_pos(const orc_model* m) { return m->pos[m->slot]; }
+
+/* Test seeding (no reference counterpart): cache rows [pos0, pos0 + n) of one
+ * layer of the current slot, [n][n_kv * hd] each, copied in; then the
+ * position.  Lets a parity test start decoding at a long position without
+ * feeding every earlier token through both models. */
+int orc_model_set_kv_rows(orc_model* m, int layer, int pos0, int n, const float* k,
+                          const float* v) {
+    int hd = m->cfg.d_model / m->cfg.n_heads, kvd = m->cfg.n_kv_heads * hd;
+    if (layer < 0 || layer >= m->cfg.n_layers || pos0 < 0 || n < 0 || pos0 + n > m->cfg.max_seq)
+        return -1;
+    orc_kv* c = &m->kv[m->slot * m->cfg.n_layers + layer];
+    memcpy(c->k + (size_t)pos0 * kvd, k, (size_t)n * kvd * 4);
+    memcpy(c->v + (size_t)pos0 * kvd, v, (size_t)n * kvd * 4);
+    return 0;
+}
+
+int orc_model_set_pos(orc_model* m, int pos) {
+    if (pos < 0 || pos >= m->cfg.max_seq) return -1;
+    m->pos[m->slot] = pos;
+    return 0;
+}
 float orc_model_attn_scale(const orc_model* m) { return m->scale; }
 
 static void lin(orc_model* m, const orc_mat* w, const float* x, float* y) {

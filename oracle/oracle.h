@@ -141,6 +141,12 @@ orc_model* orc_model_new_slots(const orc_config* cfg, const orc_mat* embed,
                                const orc_layer* layers, const float* final_norm,
                                const orc_mat* lm_head, int threads, int n_slots);
 void  orc_model_select_slot(orc_model* m, int slot);
+/* Test seeding: copy n cache rows ([n][n_kv*hd] K and V) of one layer of the
+ * current slot in at positions pos0.., and set the position; -1 when out of
+ * range.  No reference counterpart. */
+int   orc_model_set_kv_rows(orc_model* m, int layer, int pos0, int n, const float* k,
+                            const float* v);
+int   orc_model_set_pos(orc_model* m, int pos);
 
 /* ---- token choice / greedy loop ----------------------------------------- */
 /* argmax with Rust max_by semantics (last maximal index): lib.rs:2701-2706  */

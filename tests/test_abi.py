@@ -101,3 +101,32 @@ def test_model_config_presets():
     assert [i for i, t in enumerate(c.layer_types) if t == "full"] == [3, 7, 11, 15, 19, 23, 27, 31]
     s = SamplingConfig.olmo3()
     assert s.suppress_initial_tokens == [14023] and s.top_k == 50
+
+
+def test_stream_rule_library_wide_with_thread_override(lib):
+    """atlas_set_stream is library-wide: another thread without an override
+    sees it; atlas_set_thread_stream overrides it for the calling thread only.
+    The handles are never used for work here (no HIP call takes them)."""
+    import ctypes as C
+    import threading
+    a, b = C.c_void_p(0x1000), C.c_void_p(0x2000)
+    seen = {}
+
+    def other():
+        seen["before"] = lib.atlas_get_stream()
+        lib.atlas_set_thread_stream(b)
+        seen["override"] = lib.atlas_get_stream()
+        lib.atlas_clear_thread_stream()
+        seen["cleared"] = lib.atlas_get_stream()
+
+    try:
+        assert lib.atlas_set_stream(a) == 0
+        assert lib.atlas_get_stream() == 0x1000
+        t = threading.Thread(target=other)
+        t.start()
+        t.join()
+        assert seen == {"before": 0x1000, "override": 0x2000, "cleared": 0x1000}
+        assert lib.atlas_get_stream() == 0x1000          # the override stayed on its thread
+    finally:
+        lib.atlas_set_stream(None)
+    assert not lib.atlas_get_stream()

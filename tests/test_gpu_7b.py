@@ -5,15 +5,17 @@ and 32 KV heads of dim 128, MLP 11008 (SwiGLU), post-norm RMSNorm, per-head
 QK-norm, YaRN RoPE, layers i % 4 != 3 sliding with window 4096
 (crates/atlas-model/src/lib.rs:253-269 plus the OLMo-3 config.json
 fields, lib.rs:2367-2432).  Weights are random-initialised on the device
-(N(0, 0.02) projections, U(0.5, 1.5) norms), in bf16 and separately int8,
-then downloaded to build the oracle model of the same weights.
+(N(0, 0.02) projections, U(0.5, 1.5) norms), in bf16 and separately int8
+and int4, then downloaded to build the oracle model of the same weights.
 
-* Teacher forcing past position 0: a 40-token prompt goes through the
-  engine's prompt-chunk path (39 rows in one chunk, then the last token as a
-  decode step), followed by 8 decode steps.  At each of those 9 positions
-  the logits must be within 1e-3 * max|logit| of the oracle (the reference's
-  CPU path restated, row-threaded) and top-1 must agree (a near-tie of the
-  oracle's own top two is reported instead).
+* Teacher forcing past position 0 in bf16, int8 and int4 (blocks of 32): a
+  40-token prompt goes through the engine's prompt-chunk path (39 rows in one
+  chunk, then the last token as a decode step), followed by 8 decode steps.
+  At each of those 9 positions the logits must be within 1e-3 * max|logit|
+  of the oracle (the reference's CPU path restated, row-threaded) and top-1
+  must agree (a near-tie of the oracle's own top two is reported instead).
+* Long positions: both models get the same seeded KV-cache rows and decode
+  8 teacher-forced steps from position 300 and from 4100 (bf16 and int4).
 * The ragged batch of 8 sequences with prompts of 16..2048 tokens and 256
   greedy tokens each: every sequence's tokens equal its own single-sequence
   greedy run (a divergence is accepted only at a near-tie, checked on the
@@ -46,7 +48,8 @@ def _engine(fmt: str, max_seq: int, max_batch: int = 1, seed: int = 2024):
     from atlas_amd import model as am
     cfg = am.ModelConfig.olmo3_actual_7b()
     cfg.max_seq_len = max_seq
-    m = am.OlmoModel(cfg, weight_format={"bf16": am.W_BF16, "int8": am.W_INT8}[fmt],
+    m = am.OlmoModel(cfg, weight_format={"bf16": am.W_BF16, "int8": am.W_INT8,
+                                         "int4": am.W_INT4}[fmt],
                      int4_block=32, max_batch=max_batch)
     m.init_random(seed)
     return m
@@ -64,6 +67,13 @@ def _oracle_of(m, fmt: str, max_seq: int):
     def mat(kind, li, shp):
         if fmt == "bf16":
             return orc.MatView.bf16(m.get_tensor(kind, li, shp, np.uint16), *shp)
+        if fmt == "int4":
+            # Int4Tensor: two weights per byte, one f32 scale per 32-weight
+            # block of the flattened matrix (crates/atlas-quant/src/lib.rs:113-168)
+            rows, cols = shp
+            q, s = m.get_tensor(kind, li, (rows * cols // 2,), np.uint8,
+                                n_scales=rows * cols // 32)
+            return orc.MatView.int4(q, s, rows, cols, 32)
         q, s = m.get_tensor(kind, li, shp, np.int8, n_scales=shp[0])
         return orc.MatView.int8(q, s)
 
@@ -99,7 +109,7 @@ def _margin(lg):
     return float(s[-1] - s[-2])
 
 
-@pytest.mark.parametrize("fmt", ["bf16", "int8"])
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
 def test_7b_teacher_forced(orc, fmt):
     max_seq = 64
     m = _engine(fmt, max_seq)
@@ -125,6 +135,43 @@ def test_7b_teacher_forced(orc, fmt):
         tok = _top1(ref)                         # teacher: the oracle's choice
     assert m.pos == o.pos == 48
     print(f"7B {fmt}: worst rel logit err {worst:.2e} over positions 39..47", flush=True)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "int4"])
+def test_7b_long_positions(orc, fmt):
+    """Decode steps at positions 300..307 (four attention splits merged by the
+    last block) and 4100..4107 (eight splits; the sliding layers' window of
+    4096 masks cache rows 4..11), teacher-forced against the oracle.  Both
+    models get the same seeded cache rows (K, V ~ N(0, 1)) for every earlier
+    position instead of a 4100-token prefill through the CPU path."""
+    max_seq = 4120
+    m = _engine(fmt, max_seq)
+    o = _oracle_of(m, fmt, max_seq)
+    kvd = 32 * 128
+    rng = np.random.default_rng(31)
+    for p0 in (300, 4100):
+        for li in range(L):
+            k = rng.standard_normal((p0, kvd), dtype=np.float32)
+            v = rng.standard_normal((p0, kvd), dtype=np.float32)
+            m.set_kv_rows(li, 0, k, v)
+            o.set_kv_rows(li, 0, k, v)
+        m.set_pos(p0)
+        o.set_pos(p0)
+        tok = int(rng.integers(0, V))
+        worst = 0.0
+        for step in range(8):
+            lg, ref = m.forward_one(tok), o.forward_one(tok)
+            err = _rel(lg, ref)
+            worst = max(worst, err)
+            print(f"7B {fmt} pos {m.pos - 1}: rel logit err {err:.2e}, top-1 {_top1(lg)} / "
+                  f"{_top1(ref)}, oracle margin {_margin(ref):.3g}", flush=True)
+            assert err <= LOGIT_TOL, (p0, step, err)
+            if _top1(lg) != _top1(ref):
+                assert _margin(ref) <= 2 * LOGIT_TOL * np.max(np.abs(ref)), (p0, step)
+            tok = _top1(ref)
+        assert m.pos == o.pos == p0 + 8
+        print(f"7B {fmt}: worst rel logit err {worst:.2e} over positions {p0}..{p0 + 7}",
+              flush=True)
 
 
 def test_7b_ragged_batch_matches_single(orc):

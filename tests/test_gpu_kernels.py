@@ -10,6 +10,7 @@ import math
 import numpy as np
 import pytest
 
+from atlas_amd._lib import check_void
 from tests.gpu_util import Dev, lib, rel_err, sync
 
 pytestmark = pytest.mark.gpu
@@ -191,10 +192,11 @@ def test_skinny_multi_row(orc, fmt, n, M, K, block):
     _skinny_check(orc, fmt, n, M, K, block, seed=7)
 
 
-# The ragged batch's three- and five-row GEMMs at the 7B decode shapes
-# (BASELINE.json configs[2] asks for 1/3/5/8 rows of 11008 x 4096).
+# The ragged batch's 1/3/5/8-row GEMMs at the 7B decode shapes (BASELINE.json
+# configs[2] asks for 1/3/5/8 rows of 11008 x 4096; at that shape the int4
+# kernel hands 688 row groups to 256 blocks).
 @pytest.mark.parametrize("M,K", [(4096, 4096), (11008, 4096)])
-@pytest.mark.parametrize("n", [3, 5])
+@pytest.mark.parametrize("n", [1, 3, 5, 8])
 @pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
 def test_skinny_7b_rows(orc, fmt, n, M, K):
     print(f"skinny 7B {fmt} n={n} M={M} K={K}", flush=True)
@@ -429,6 +431,144 @@ def test_reference_tensor_ops():
 
 
 # ---------------------------------------------------------------------------
+# the remaining reference-FFI exports (crates/atlas-tensor/src/lib.rs:17-92)
+# ---------------------------------------------------------------------------
+
+def _adamw_ref(p, m, v, g, lr, b1, b2, eps, wd, bc1, bc2):
+    """kernels/matmul.cu:138-161 restated in float64 from float32 inputs.  The
+    coefficients the kernel forms in float32 (1 - beta, 1 - lr * wd) are
+    rounded to float32 first: 1 - 0.999f is 0.00099998713, not 0.001."""
+    f = np.float32
+    p, m, v, g = (np.asarray(a, np.float64) for a in (p, m, v, g))
+    b1, b2, lr, eps = float(f(b1)), float(f(b2)), float(f(lr)), float(f(eps))
+    c1, c2 = float(f(1) - f(b1)), float(f(1) - f(b2))
+    decay = float(f(1) - f(lr) * f(wd))
+    m = b1 * m + c1 * g
+    v = b2 * v + c2 * g * g
+    mh, vh = m * bc1, v * bc2
+    return p * decay - lr * mh / (np.sqrt(vh) + eps), m, v
+
+
+def test_adamw_step_reference_contract():
+    # The caller passes bc = 1/(1 - beta^t) (crates/atlas-optim/src/lib.rs:203-204),
+    # which the kernel multiplies by; decay is decoupled (p * (1 - lr*wd)).
+    print("adamw_step", flush=True)
+    rng = np.random.default_rng(17)
+    n = 70001
+    lr, b1, b2, eps, wd = 1e-3, 0.9, 0.999, 1e-8, 0.01
+    p = rng.standard_normal(n).astype(np.float32)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    dp, dm, dv = Dev(p), Dev(m), Dev(v)
+    for t in range(1, 4):
+        g = rng.standard_normal(n).astype(np.float32)
+        bc1 = np.float32(1.0 / (1.0 - np.float32(b1) ** np.float32(t)))
+        bc2 = np.float32(1.0 / (1.0 - np.float32(b2) ** np.float32(t)))
+        dg = Dev(g)
+        lib().atlas_adamw_step(dp.ptr, dm.ptr, dv.ptr, dg.ptr, lr, b1, b2, eps, wd,
+                               float(bc1), float(bc2), n)
+        check_void()
+        p_ref, m_ref, v_ref = _adamw_ref(p, m, v, g, lr, b1, b2, eps, wd, float(bc1), float(bc2))
+        gp, gm, gv = dp.get(), dm.get(), dv.get()
+        assert np.max(np.abs(gm - m_ref)) <= 1e-6 * np.max(np.abs(m_ref))
+        assert np.max(np.abs(gv - v_ref)) <= 1e-6 * np.max(np.abs(v_ref))
+        assert np.max(np.abs(gp - p_ref)) <= 2e-6 * np.max(np.abs(p_ref))
+        if t == 1:
+            # closed form at step 1 from zero moments: m_hat = g, v_hat = g^2, so
+            # every parameter moves by lr * sign(g) after decay (|g| >> eps)
+            step = p.astype(np.float64) * (1 - lr * wd) - gp
+            big = np.abs(g) > 1e-3
+            # (a few float32 ulps of |p| <= 5; a divided bias correction is off by 9 lr)
+            assert np.max(np.abs(step[big] - lr * np.sign(g[big]))) < 2e-6
+        p, m, v = gp, gm, gv
+
+
+def test_softmax_scale_relu_copy():
+    print("softmax/scale/relu/vram_copy", flush=True)
+    # crates/atlas-tensor/src/lib.rs:1109-1114 and 1132-1138 literals
+    x = Dev(np.array([1.0, 2.0, 3.0], np.float32))
+    o = Dev.empty(3)
+    lib().atlas_softmax_f32(x.ptr, o.ptr, 1, 3)
+    s = o.get()
+    e = np.exp(np.array([1.0, 2.0, 3.0]) - 3.0)
+    assert abs(float(np.sum(s)) - 1.0) < 1e-6
+    assert np.max(np.abs(s - e / e.sum())) < 1e-7
+    t = Dev(np.array([-2.0, -1.0, 0.0, 1.0, 2.0], np.float32))
+    o5 = Dev.empty(5)
+    lib().atlas_scale_f32(t.ptr, 2.0, o5.ptr, 5)
+    assert np.array_equal(o5.get(), [-4.0, -2.0, 0.0, 2.0, 4.0])
+    lib().atlas_relu_f32(t.ptr, o5.ptr, 5)
+    assert np.array_equal(o5.get(), [0.0, 0.0, 0.0, 1.0, 2.0])
+    rng = np.random.default_rng(23)
+    # row softmax: against float64, rows summing to one, shift invariance
+    for rows, cols in ((7, 100278), (33, 5), (4, 257), (1, 1)):
+        a = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+        da, do = Dev(a), Dev.empty((rows, cols))
+        lib().atlas_softmax_f32(da.ptr, do.ptr, rows, cols)
+        got = do.get().astype(np.float64)
+        a64 = a.astype(np.float64)
+        ex = np.exp(a64 - a64.max(axis=1, keepdims=True))
+        ref = ex / ex.sum(axis=1, keepdims=True)
+        assert np.max(np.abs(got - ref)) <= 1e-6 * np.max(ref)
+        assert np.max(np.abs(got.sum(axis=1) - 1.0)) < 1e-5
+        da2 = Dev(a + np.float32(8.0))
+        lib().atlas_softmax_f32(da2.ptr, do.ptr, rows, cols)
+        assert np.max(np.abs(do.get() - got)) <= 2e-6 * np.max(ref)
+    # scale and relu are one rounding each: bit-exact with numpy float32
+    n = 1 << 20 | 3
+    a = rng.standard_normal(n).astype(np.float32)
+    da, do = Dev(a), Dev.empty(n)
+    lib().atlas_scale_f32(da.ptr, np.float32(-0.3125), do.ptr, n)
+    assert np.array_equal(do.get(), a * np.float32(-0.3125))
+    lib().atlas_relu_f32(da.ptr, do.ptr, n)
+    assert np.array_equal(do.get(), np.where(a > 0, a, np.float32(0)))
+    # vram_copy is a bit copy (NaN payloads and -0.0 included)
+    bits = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
+    bits[:4] = [0x7FC01234, 0xFF800001, 0x80000000, 0x00000001]
+    db, dc = Dev(bits), Dev.empty(n, np.uint32)
+    lib().atlas_vram_copy_f32(db.ptr, dc.ptr, n)
+    assert np.array_equal(dc.get(), bits)
+    check_void()
+
+
+def _rope_apply_ref(x, pos, hd, theta):
+    """crates/atlas-tensor/src/lib.rs:570-587 CPU form (float32 throughout)."""
+    x = np.array(x, np.float32)
+    half = hd // 2
+    i = np.arange(half)
+    freq = np.float32(1.0) / np.power(np.float32(theta), (2 * i).astype(np.float32) / np.float32(hd))
+    ang = np.float32(pos) * freq.astype(np.float32)
+    c, s = np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))
+    x0, x1 = x[:half].astype(np.float64), x[half:].astype(np.float64)
+    return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c])
+
+
+@pytest.mark.parametrize("hd,theta", [(128, 500000.0), (64, 10000.0), (6, 10000.0)])
+def test_rope_apply_positions(hd, theta):
+    print(f"rope_apply hd={hd}", flush=True)
+    rng = np.random.default_rng(hd)
+    for pos in (1, 3, 17, 63):
+        x = rng.standard_normal(hd).astype(np.float32)
+        d = Dev(x)
+        lib().atlas_rope_apply_f32(d.ptr, pos, hd, theta)
+        got = d.get().astype(np.float64)
+        ref = _rope_apply_ref(x, pos, hd, theta)
+        assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref)), pos
+        # rotate-half pairs (i, i + hd/2) keep their norm; adjacent pairs would not
+        half = hd // 2
+        n_in = x[:half].astype(np.float64) ** 2 + x[half:].astype(np.float64) ** 2
+        n_out = got[:half] ** 2 + got[half:] ** 2
+        assert np.max(np.abs(n_out - n_in)) <= 1e-5 * np.max(n_in)
+    # position 1, dimension pair 0 turns by exactly one radian (freq_0 = 1)
+    x = np.zeros(hd, np.float32)
+    x[0] = 1.0
+    d = Dev(x)
+    lib().atlas_rope_apply_f32(d.ptr, 1, hd, theta)
+    g = d.get()
+    assert abs(g[0] - math.cos(1.0)) < 1e-6 and abs(g[hd // 2] - math.sin(1.0)) < 1e-6
+
+
+# ---------------------------------------------------------------------------
 # argmax, quantisers, initialisers
 # ---------------------------------------------------------------------------
 
@@ -600,3 +740,102 @@ def test_bench_stream_floor_runs_and_rejects_bad_sizes():
     assert lib().atlas_bench_stream_floor(C.c_void_p(buf.ptr), 16 << 20, 4 << 20, 0, 2,
                                           C.byref(us)) < 0
     lib().atlas_clear_error()                            # the refusals above recorded errors
+
+
+# ---------------------------------------------------------------------------
+# library scratch and graph capture
+# ---------------------------------------------------------------------------
+
+def _hip_runtime():
+    """The HIP runtime this process's atlas library uses (the same loaded
+    copy, found in /proc/self/maps), for stream capture from the test."""
+    path = None
+    with open("/proc/self/maps") as f:
+        for line in f:
+            if "libamdhip64.so" in line:
+                path = line.split()[-1]
+                break
+    assert path, "libamdhip64 is not loaded"
+    hip = C.CDLL(path)
+    for name in ("hipStreamCreate", "hipStreamDestroy", "hipStreamBeginCapture",
+                 "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
+                 "hipStreamSynchronize", "hipGraphExecDestroy", "hipGraphDestroy"):
+        getattr(hip, name).restype = C.c_int
+    return hip
+
+
+def test_scratch_growth_refused_under_capture():
+    """A fresh thread's first atlas_gpu_argmax needs library scratch; under a
+    stream capture that growth is refused (ATLAS_EUNSUPPORTED) instead of
+    recording an allocation into the caller's graph.  After one eager call
+    of the same shape the captured call works, and every replay matches the
+    eager result."""
+    import threading
+    hip = _hip_runtime()
+    n = 100278
+    x = np.random.default_rng(41).standard_normal(n).astype(np.float32)
+    x[777] = 9.0
+    res = {}
+
+    def capture(st, fn):
+        """Capture fn() on stream st (global mode); returns the graph exec."""
+        graph, exe = C.c_void_p(), C.c_void_p()
+        assert hip.hipStreamBeginCapture(st, 0) == 0
+        fn()
+        assert hip.hipStreamEndCapture(st, C.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, C.c_size_t(0)) == 0
+        return graph, exe
+
+    def worker():
+        st = C.c_void_p()
+        try:
+            dx, d_eager, d_graph = Dev(x), Dev.empty(2), Dev.empty(2)
+            assert hip.hipStreamCreate(C.byref(st)) == 0
+            lib().atlas_set_thread_stream(st)
+            res["bytes_before"] = lib().atlas_thread_scratch_bytes()
+            g1, e1 = capture(st, lambda: lib().atlas_gpu_argmax(dx.ptr, d_graph.ptr, n))
+            res["code"] = lib().atlas_last_error_code()
+            res["msg"] = lib().atlas_last_error().decode()
+            lib().atlas_clear_error()
+            res["bytes_refused"] = lib().atlas_thread_scratch_bytes()
+            hip.hipGraphExecDestroy(e1)
+            hip.hipGraphDestroy(g1)
+            # warm-up on the same thread, then capture
+            lib().atlas_gpu_argmax(dx.ptr, d_eager.ptr, n)
+            lib().atlas_stream_sync()
+            check_void()
+            res["bytes_warm"] = lib().atlas_thread_scratch_bytes()
+            eager = d_eager.get()
+            g2, e2 = capture(st, lambda: lib().atlas_gpu_argmax(dx.ptr, d_graph.ptr, n))
+            check_void()
+            replays = []
+            for _ in range(3):
+                lib().atlas_memset_zero(d_graph.ptr, 8)        # eager work between replays
+                lib().atlas_stream_sync()
+                assert hip.hipGraphLaunch(e2, st) == 0
+                assert hip.hipStreamSynchronize(st) == 0
+                replays.append(d_graph.get())
+            hip.hipGraphExecDestroy(e2)
+            hip.hipGraphDestroy(g2)
+            res["eager"], res["replays"] = eager, replays
+        except BaseException as e:          # reported on the main thread
+            res["exc"] = e
+        finally:
+            lib().atlas_clear_thread_stream()
+            if st.value:
+                hip.hipStreamSynchronize(st)
+                hip.hipStreamDestroy(st)
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    if "exc" in res:
+        raise res["exc"]
+    assert res["bytes_before"] == 0
+    assert res["code"] == -4, res          # ATLAS_EUNSUPPORTED
+    assert "captured" in res["msg"]
+    assert res["bytes_refused"] == 0
+    assert res["bytes_warm"] > 0
+    assert res["eager"][0] == 777.0          # the index, as a float (lib.rs:107-126)
+    for r in res["replays"]:
+        assert np.array_equal(r, res["eager"])

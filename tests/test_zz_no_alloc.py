@@ -4,11 +4,13 @@ atlas_decode_attention_noalloc takes the arguments of atlas_decode_attention
 (crates/atlas-tensor/src/lib.rs:80-86) and the same split count, with its
 split partials in the library's fixed device workspace.  Two calls in a row,
 the second with a smaller input (the workspace keeps the first call's
-contents), must match the allocating entry point within the attention
+contents), made first and from a fresh thread that must end them holding no
+library scratch, must match the allocating entry point within the attention
 tolerance (2e-3 * max|o|) and the oracle; a shape whose partials exceed the
 workspace is refused with ATLAS_EINVAL.
 """
 import math
+import threading
 
 import numpy as np
 import pytest
@@ -40,16 +42,37 @@ def test_decode_attention_noalloc_matches_allocating_entry(orc):
     H, KVH, hd = 32, 8, 128
     scale = 1.2079441541679836 / math.sqrt(hd)
     # the second call is smaller: fewer positions and a window
-    for pos, window, seed in ((16383, 0, 1), (700, 256, 2)):
-        print(f"noalloc attention pos={pos} window={window}", flush=True)
+    cases = ((16383, 0, 1), (700, 256, 2))
+    bufs = []
+    for pos, window, seed in cases:
         q, kc, vc = _case(H, KVH, hd, pos + 1, seed)
-        dq, dk, dv = Dev(q), Dev(kc), Dev(vc)
-        da, db = Dev.empty(H * hd), Dev.empty(H * hd)
+        bufs.append((q, kc, vc, Dev(q), Dev(kc), Dev(vc), Dev.empty(H * hd), Dev.empty(H * hd)))
+    # The no-allocation calls come first, from a fresh thread with no library
+    # scratch: they must leave it without any (nothing allocated on its behalf).
+    res = {}
+
+    def worker():
+        try:
+            res["before"] = lib().atlas_thread_scratch_bytes()
+            for (pos, window, _), (_, _, _, dq, dk, dv, _, db) in zip(cases, bufs):
+                print(f"noalloc attention pos={pos} window={window}", flush=True)
+                res[pos] = lib().atlas_decode_attention_noalloc(dq.ptr, dk.ptr, dv.ptr, db.ptr,
+                                                                H, KVH, hd, pos, scale, window)
+            lib().atlas_stream_sync()
+            res["after"] = lib().atlas_thread_scratch_bytes()
+        except BaseException as e:          # reported on the main thread
+            res["exc"] = e
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    if "exc" in res:
+        raise res["exc"]
+    assert res["before"] == 0 and res["after"] == 0, res
+    for (pos, window, _), (q, kc, vc, dq, dk, dv, da, db) in zip(cases, bufs):
+        assert res[pos] == 0, pos
         lib().atlas_decode_attention(dq.ptr, dk.ptr, dv.ptr, da.ptr, H, KVH, hd, pos, scale,
                                      window)
-        sync()
-        assert lib().atlas_decode_attention_noalloc(dq.ptr, dk.ptr, dv.ptr, db.ptr, H, KVH, hd,
-                                                    pos, scale, window) == 0
         sync()
         a, b = da.get(), db.get()
         assert rel_err(b, a) <= ATTN_TOL
