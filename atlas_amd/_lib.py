@@ -91,6 +91,7 @@ SIGNATURES = {
     "atlas_get_stream": (P, []),
     "atlas_stream_sync": (I, []),
     "atlas_thread_scratch_bytes": (I64, []),
+    "atlas_debug_fail_allocations": (I, [I, I]),
     "atlas_device_cu_count": (I, []),
     # Part 3: extensions
     "atlas_gemv_f32": (I, [I, P, P, I, P, P, I, I]),
@@ -190,10 +191,15 @@ def load():
 
 
 def check(rc: int) -> int:
-    """Raise AtlasError for a negative status code."""
+    """Raise AtlasError for a negative status code.  The library's recorded
+    error is cleared once it is raised, so a later `void` call's check_void
+    does not report it again."""
     if rc is not None and rc < 0:
-        msg = load().atlas_last_error()
-        raise AtlasError(rc, msg.decode() if msg else "")
+        lib = load()
+        msg = lib.atlas_last_error()
+        text = msg.decode() if msg else ""
+        lib.atlas_clear_error()
+        raise AtlasError(rc, text)
     return rc
 
 

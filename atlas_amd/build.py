@@ -21,8 +21,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libatlas_kernels.so")
 
-SOURCES = ["gemv.hip", "skinny.hip", "attention.hip", "fused.hip", "runtime.cpp", "capi.cpp",
-           "engine.cpp", "loader.cpp"]
+SOURCES = ["gemv.hip", "skinny.hip", "attention.hip", "fused.hip", "errors.cpp", "runtime.cpp",
+           "capi.cpp", "engine.cpp", "st_format.cpp", "loader.cpp"]
 
 
 def hipcc() -> str:

@@ -1,9 +1,8 @@
 // common.hpp -- shared helpers for the gfx950 decode kernels.
 //
-// Error model: every C-ABI entry point returns 0 on success or a negative
-// ATLAS_E* code and records a message retrievable with atlas_last_error()
-// (thread-local).  Entry points that keep the reference's `void` signature
-// record the error the same way.  Launches go to the library-wide stream
+// Error model (errors.hpp): every C-ABI entry point returns 0 on success or a
+// negative ATLAS_E* code and records a message retrievable with
+// atlas_last_error() (thread-local).  Launches go to the library-wide stream
 // (atlas_set_stream; default: the null stream, as the reference uses) unless
 // the calling thread set its own (atlas_set_thread_stream).
 #pragma once
@@ -14,14 +13,10 @@
 #include <cstdio>
 #include <cstring>
 
-#include "../../include/atlas_kernels.h"   // ATLAS_OK / ATLAS_E* codes
-
-#define ATLAS_API extern "C" __attribute__((visibility("default")))
+#include "errors.hpp"
 
 namespace atlas {
 
-void set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-void clear_error();
 hipStream_t stream();          // the calling thread's override, else the library-wide stream
 int device_cu_count();         // CUs of the current device (cached)
 
@@ -30,7 +25,7 @@ int device_cu_count();         // CUs of the current device (cached)
 // attention, split-K partials of the skinny GEMMs, argmax partials).  Each
 // slot grows stream-ordered on the thread's current stream (the old buffer is
 // freed after the work already queued there; a thread that switched streams
-// waits for the previous one first) and is kept until the process ends.  Two
+// waits for the previous one first) and is kept until the thread exits.  Two
 // threads never share a slot; calls of one thread on two streams at once do.
 // zero_new: a grown slot is cleared (fill kernel) before it is returned.
 enum ScratchSlot {
@@ -71,13 +66,24 @@ size_t thread_scratch_bytes();   // bytes the calling thread holds on the curren
         }                                                                      \
     } while (0)
 
-#define ATLAS_REQUIRE(cond, ...)                                               \
-    do {                                                                       \
-        if (!(cond)) {                                                         \
-            ::atlas::set_error(ATLAS_EINVAL, __VA_ARGS__);                     \
-            return ATLAS_EINVAL;                                               \
-        }                                                                      \
-    } while (0)
+// Every device and pinned-host allocation of the library goes through these:
+// they fail with hipErrorOutOfMemory while the allocation-failure switch says
+// so (atlas_debug_fail_allocations), and otherwise call HIP.
+template <typename T>
+inline hipError_t dev_malloc(T** p, size_t bytes) {
+    if (alloc_should_fail()) { *p = nullptr; return hipErrorOutOfMemory; }
+    return hipMalloc(reinterpret_cast<void**>(p), bytes);
+}
+template <typename T>
+inline hipError_t dev_malloc_async(T** p, size_t bytes, hipStream_t st) {
+    if (alloc_should_fail()) { *p = nullptr; return hipErrorOutOfMemory; }
+    return hipMallocAsync(reinterpret_cast<void**>(p), bytes, st);
+}
+template <typename T>
+inline hipError_t host_malloc_pinned(T** p, size_t bytes, unsigned flags = hipHostMallocDefault) {
+    if (alloc_should_fail()) { *p = nullptr; return hipErrorOutOfMemory; }
+    return hipHostMalloc(reinterpret_cast<void**>(p), bytes, flags);
+}
 
 // ---------------------------------------------------------------------------
 // device helpers

@@ -172,7 +172,7 @@ namespace {
 int dalloc(atlas_model* m, void** p, size_t bytes) {
     *p = nullptr;
     if (bytes == 0) return ATLAS_OK;
-    if (hipMalloc(p, bytes) != hipSuccess || !*p) {
+    if (dev_malloc(p, bytes) != hipSuccess || !*p) {
         (void)hipGetLastError();
         *p = nullptr;
         set_error(ATLAS_ENOMEM, "engine: device allocation of %zu bytes failed", bytes);
@@ -970,7 +970,7 @@ int grow(void** p, size_t* have, size_t need) {
         *p = nullptr;
         *have = 0;
     }
-    if (hipMalloc(p, need) != hipSuccess) {
+    if (dev_malloc(p, need) != hipSuccess) {
         (void)hipGetLastError();
         *p = nullptr;
         set_error(ATLAS_ENOMEM, "load scratch: %zu bytes", need);
@@ -1468,11 +1468,15 @@ ATLAS_API int atlas_model_init_random(atlas_model* m, uint64_t seed) {
     float* tmp = nullptr;
     void* qd = nullptr;
     float* qs = nullptr;
-    ATLAS_HIP(hipMalloc((void**)&tmp, max_el * 4));
+    if (dev_malloc(&tmp, max_el * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(ATLAS_ENOMEM, "init_random: temporaries");
+        return ATLAS_ENOMEM;
+    }
     int rc = ATLAS_OK;
     const int fmt = c.weight_format;
     if (fmt != WF_BF16) {
-        if (hipMalloc(&qd, max_el) != hipSuccess || hipMalloc((void**)&qs, max_el / 8 * 4 + 64) != hipSuccess) {
+        if (dev_malloc(&qd, max_el) != hipSuccess || dev_malloc(&qs, max_el / 8 * 4 + 64) != hipSuccess) {
             (void)hipGetLastError();
             (void)hipFree(tmp);
             if (qd) (void)hipFree(qd);
@@ -1640,7 +1644,12 @@ ATLAS_API int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, flo
     // trip per token instead of one per layer.
     const size_t hb = (size_t)c.n_layers * c.d_model * 4;
     if (!m->hook_dev) TRY(dalloc(m, (void**)&m->hook_dev, hb));
-    if (!m->hook_stage) ATLAS_HIP(hipHostMalloc((void**)&m->hook_stage, hb));
+    if (!m->hook_stage && host_malloc_pinned(&m->hook_stage, hb) != hipSuccess) {
+        (void)hipGetLastError();
+        m->hook_stage = nullptr;
+        set_error(ATLAS_ENOMEM, "forward_one_hooked: pinned staging of %zu bytes", hb);
+        return ATLAS_ENOMEM;
+    }
     TRY(sync_pos(m));
     TRY(set_token(m, token));
     TRY(run_step(m, 3));
@@ -1990,7 +1999,11 @@ ATLAS_API int atlas_sample_device(const float* logits, int vocab, const uint32_t
     const size_t off_i = (off_c + sizeof(SampleCfg) + 7) & ~(size_t)7;
     const size_t bytes = off_i + 32;
     char* d = nullptr;
-    ATLAS_HIP(hipMalloc((void**)&d, bytes));
+    if (dev_malloc(&d, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(ATLAS_ENOMEM, "sample_device: %zu bytes", bytes);
+        return ATLAS_ENOMEM;
+    }
     int rc = ATLAS_OK;
     const int ints[4] = {n_hist, step, 0, 0};
     if (hipMemcpyAsync(d, logits, (size_t)vocab * 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
@@ -2066,7 +2079,12 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
     std::vector<int> rows_of(n_seqs);
     std::vector<float> lg;
     if (!m->ring) {
-        ATLAS_HIP(hipHostMalloc((void**)&m->ring, sizeof(int) * 3 * kMaxRows * atlas_model::kRing));
+        if (host_malloc_pinned(&m->ring, sizeof(int) * 3 * kMaxRows * atlas_model::kRing) != hipSuccess) {
+            (void)hipGetLastError();
+            m->ring = nullptr;
+            set_error(ATLAS_ENOMEM, "generate_batch: pinned staging ring");
+            return ATLAS_ENOMEM;
+        }
         for (auto& e : m->ring_ev) ATLAS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     int ring_next = 0;

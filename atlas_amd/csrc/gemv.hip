@@ -1358,7 +1358,7 @@ int stream_floor_bench(const void* buf, long buf_bytes, long bytes_per_launch, i
     ATLAS_HIP(hipStreamSynchronize(st));
     ATLAS_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
     float* sink = nullptr;
-    if (hipMalloc(&sink, (size_t)blocks * 4 * sizeof(float)) != hipSuccess) {
+    if (dev_malloc(&sink, (size_t)blocks * 4 * sizeof(float)) != hipSuccess) {
         (void)hipGetLastError();
         (void)hipStreamDestroy(st);
         set_error(ATLAS_ENOMEM, "stream_floor: sink allocation");

@@ -5,29 +5,12 @@
 // cudaMallocAsync, cudaFreeAsync) and the device queries of
 // kernels/matmul.cu:580-595.
 #include <atomic>
-#include <cstdarg>
 #include <mutex>
 
 #include "common.hpp"
 #include "fused.hpp"
 
 namespace atlas {
-
-static thread_local int t_err_code = ATLAS_OK;
-static thread_local char t_err_msg[512] = "";
-
-void set_error(int code, const char* fmt, ...) {
-    t_err_code = code;
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(t_err_msg, sizeof(t_err_msg), fmt, ap);
-    va_end(ap);
-}
-
-void clear_error() {
-    t_err_code = ATLAS_OK;
-    t_err_msg[0] = 0;
-}
 
 // The launch stream: one library-wide stream (atlas_set_stream; the null
 // stream until set, as in the reference), which a thread may override for
@@ -109,7 +92,7 @@ int thread_scratch(int slot, size_t bytes, void** out, bool zero_new) {
         }
         const size_t cap = (bytes + 65535) / 65536 * 65536;
         void* p = nullptr;
-        if (hipMallocAsync(&p, cap, st) != hipSuccess || !p) {
+        if (dev_malloc_async(&p, cap, st) != hipSuccess || !p) {
             (void)hipGetLastError();
             set_error(ATLAS_ENOMEM, "scratch: device allocation of %zu bytes failed", cap);
             return ATLAS_ENOMEM;
@@ -147,10 +130,6 @@ int device_cu_count() {
 }  // namespace atlas
 
 using namespace atlas;
-
-ATLAS_API int atlas_last_error_code(void) { return t_err_code; }
-ATLAS_API const char* atlas_last_error(void) { return t_err_msg; }
-ATLAS_API void atlas_clear_error(void) { clear_error(); }
 
 ATLAS_API int atlas_cuda_device_count(void) {
     int n = 0;
@@ -202,6 +181,12 @@ ATLAS_API int atlas_dev_malloc(void** ptr, size_t bytes) {
     ATLAS_REQUIRE(ptr, "atlas_dev_malloc: null out pointer");
     *ptr = nullptr;
     if (bytes == 0) return ATLAS_OK;
+    // one allocation: the switch is asked once, then stream-ordered with a
+    // plain hipMalloc as the fallback
+    if (alloc_should_fail()) {
+        set_error(ATLAS_ENOMEM, "device allocation of %zu bytes failed (injected)", bytes);
+        return ATLAS_ENOMEM;
+    }
     if (hipMallocAsync(ptr, bytes, stream()) == hipSuccess && *ptr) return ATLAS_OK;
     (void)hipGetLastError();
     if (hipMalloc(ptr, bytes) != hipSuccess || !*ptr) {
@@ -225,7 +210,7 @@ ATLAS_API int atlas_dev_malloc_sync(void** ptr, size_t bytes) {
     ATLAS_REQUIRE(ptr, "atlas_dev_malloc_sync: null out pointer");
     *ptr = nullptr;
     if (bytes == 0) return ATLAS_OK;
-    if (hipMalloc(ptr, bytes) != hipSuccess || !*ptr) {
+    if (dev_malloc(ptr, bytes) != hipSuccess || !*ptr) {
         (void)hipGetLastError();
         *ptr = nullptr;
         set_error(ATLAS_ENOMEM, "device allocation of %zu bytes failed", bytes);

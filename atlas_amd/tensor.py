@@ -55,7 +55,11 @@ class _DevMem:
         fn = load().atlas_dev_malloc_sync if sync_alloc else load().atlas_dev_malloc
         rc = fn(C.byref(p), nbytes)
         if rc < 0:
-            raise MemoryError(load().atlas_last_error().decode())
+            # delivered here (GpuBuf.alloc turns it into None): not left
+            # recorded for the next call's check
+            msg = load().atlas_last_error().decode()
+            load().atlas_clear_error()
+            raise MemoryError(msg)
         self.ptr = p.value or 0
 
     def free(self):

@@ -140,6 +140,12 @@ void* atlas_get_stream(void);                         /* the calling thread's ef
 int atlas_stream_sync(void);                          /* waits for that stream */
 /* Bytes of library scratch the calling thread holds on the current device. */
 int64_t atlas_thread_scratch_bytes(void);
+/* Test hook, no reference counterpart: after `skip` more device or pinned-host
+ * allocations of the library succeed, the next `count` fail as if the device
+ * were out of memory (ATLAS_ENOMEM; the reference's Option/bool fallback
+ * contract, crates/atlas-tensor/src/lib.rs:193-207, is tested with it).
+ * count = 0 turns it off.  Process-wide.                                     */
+int atlas_debug_fail_allocations(int skip, int count);
 int atlas_device_cu_count(void);
 
 /* ===== Part 3: decode hot-path extensions (no reference counterpart) ===== */

@@ -16,7 +16,9 @@
  * a data_offsets array with fewer than two entries, a byte range outside the
  * data section, a tensor whose element count does not match the model, and
  * QK-norm weights present for only some layers are errors (ATLAS_EINVAL)
- * instead of a panic or a silently inconsistent model.
+ * instead of a panic or a silently inconsistent model, and so is JSON nested
+ * deeper than 512 levels (the reference's recursive parser has no bound and
+ * would overflow its stack).
  *
  * All entry points return 0 or a negative ATLAS_E* code (atlas_kernels.h);
  * atlas_last_error() has the message.

@@ -196,20 +196,34 @@ def _hdr(obj_text: str, data=b""):
     return struct.pack("<Q", len(h)) + h + data
 
 
+def header_error_cases():
+    """Files SafetensorsFile.from_bytes rejects, with the message each gives
+    (also the corpus of the sanitizer run, tests/test_loader_sanitize.py)."""
+    raw = b'{"\xff": 1}'
+    return [(b"\x01\x00", "too short"),
+            (struct.pack("<Q", 100) + b"{}", "truncated"),
+            (struct.pack("<Q", 2**64 - 1) + b"{}", "truncated"),
+            (struct.pack("<Q", len(raw)) + raw, "UTF-8"),
+            (_hdr('{"a": {"dtype": "F32",}}'), "JSON"),
+            (_hdr('{"a": 1} x'), "JSON"),
+            (_hdr('{"a": {"dtype": "F32", "shape": [1]}}'), "missing data_offsets"),
+            (_hdr('{"a": {"data_offsets": [0]}}'), "two entries"),
+            (_hdr("[" * 600 + "]" * 600), "nesting")]
+
+
+def range_error_file():
+    """A file that parses, whose tensors fail on read: an unsupported dtype, a
+    range past the data section and a reversed range."""
+    return _hdr('{"a": {"dtype": "I8", "shape": [4], "data_offsets": [0, 4]},'
+                ' "b": {"dtype": "F32", "shape": [1], "data_offsets": [0, 8]},'
+                ' "c": {"dtype": "F32", "shape": [1], "data_offsets": [4, 2]}}', b"\0" * 4)
+
+
 def test_safetensors_errors(ld):
     fb = ld.SafetensorsFile.from_bytes
-    assert "too short" in _err(fb, b"\x01\x00")
-    assert "truncated" in _err(fb, struct.pack("<Q", 100) + b"{}")
-    assert "truncated" in _err(fb, struct.pack("<Q", 2**64 - 1) + b"{}")
-    raw = b'{"\xff": 1}'
-    assert "UTF-8" in _err(fb, struct.pack("<Q", len(raw)) + raw)
-    assert "JSON" in _err(fb, _hdr('{"a": {"dtype": "F32",}}'))
-    assert "JSON" in _err(fb, _hdr('{"a": 1} x'))
-    assert "missing data_offsets" in _err(fb, _hdr('{"a": {"dtype": "F32", "shape": [1]}}'))
-    assert "two entries" in _err(fb, _hdr('{"a": {"data_offsets": [0]}}'))
-    st = fb(_hdr('{"a": {"dtype": "I8", "shape": [4], "data_offsets": [0, 4]},'
-                 ' "b": {"dtype": "F32", "shape": [1], "data_offsets": [0, 8]},'
-                 ' "c": {"dtype": "F32", "shape": [1], "data_offsets": [4, 2]}}', b"\0" * 4))
+    for blob, msg in header_error_cases():
+        assert msg in _err(fb, blob), msg
+    st = fb(range_error_file())
     assert "unsupported dtype: I8" in _err(st.get_f32, "a")
     assert "not BF16" in _err(st.get_bf16, "a")
     assert "outside" in _err(st.get_f32, "b") and "outside" in _err(st.get_f32, "c")
