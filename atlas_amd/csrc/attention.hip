@@ -58,6 +58,13 @@ template <int HD> struct ScanShape {
     static constexpr int DPL = HD / 16;
     static constexpr int P = HD == 64 ? 8 : 2;
 };
+// Steps each scan keeps in flight (register buffers of 2 * P * HD / 16 floats
+// each): the split kernel's, and the fused decode kernel's.
+constexpr int kScanDepth = 2;
+#ifndef ATLAS_FUSED_SCAN_DEPTH
+#define ATLAS_FUSED_SCAN_DEPTH 3
+#endif
+constexpr int kFusedScanDepth = ATLAS_FUSED_SCAN_DEPTH;
 
 // A lane of a 16-lane position group owns DPL = HD/16 dims in chunks of 4:
 // chunk c holds dims c*64 + dl*4 .. +3.  One 16-byte load per chunk then
@@ -149,64 +156,123 @@ __device__ __forceinline__ void scan_update(const float (&q)[G][HD / 16], float 
     }
 }
 
+// Merge the online-softmax states of a wave's four 16-lane rows (lanes with
+// the same dl hold the same dims in every row) by lane shuffles across rows;
+// afterwards every row holds the wave's state.  An empty state (m = -inf)
+// weighs 0.
+template <int HD, int G>
+__device__ __forceinline__ void merge_rows(float (&m)[G], float (&l)[G], float (&o)[G][HD / 16]) {
+    constexpr int DPL = HD / 16;
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float m2 = __shfl_xor(m[h], sh, 64);
+            const float l2 = __shfl_xor(l[h], sh, 64);
+            const float mn = fmaxf(m[h], m2);
+            const float c1 = m[h] == -INFINITY ? 0.f : exp2f(m[h] - mn);
+            const float c2 = m2 == -INFINITY ? 0.f : exp2f(m2 - mn);
+            l[h] = l[h] * c1 + l2 * c2;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                const float o2 = __shfl_xor(o[h][d], sh, 64);
+                o[h][d] = o[h][d] * c1 + o2 * c2;
+            }
+            m[h] = mn;
+        }
+    }
+}
+
+// States a block merges through LDS: its W waves' when the rows of each wave
+// were merged by shuffles first (G <= 2: 10 shuffles per head and stage),
+// else all 4 W (wave, row) states (at G = 4 the shuffle chains cost more
+// than the LDS reads they save: the GQA 32/8/128 split kernel at ctx 512 /
+// 4096 ran 0.8 / 0.7 us slower with them on MI355X).
+template <int G, int W> constexpr int block_states() { return G <= 2 ? W : 4 * W; }
+
+// Writes the block's states for the LDS merge: (m, l) per head and the
+// partial output of every dim.
+template <int HD, int G, int W, int NS = block_states<G, W>()>
+__device__ __forceinline__ void stage_block_states(float (&m)[G], float (&l)[G], float (&o)[G][HD / 16],
+                                                   int wave, int row, int dl, float (&s_m)[NS][G],
+                                                   float (&s_l)[NS][G], float (&s_o)[NS][G][HD]) {
+    constexpr int DPL = HD / 16;
+    if constexpr (NS == W) merge_rows<HD, G>(m, l, o);
+    const int st = NS == W ? wave : wave * 4 + row;
+    if (NS == W && row != 0) return;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        if (dl == 0) { s_m[st][h] = m[h]; s_l[st][h] = l[h]; }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) s_o[st][h][lane_dim(dl, d)] = o[h][d];
+    }
+}
+
 // Scan cache rows [b0, e1) into the (wave, row) group's state (NG groups per
 // block).  kb/vb: dim 0 of the KV head in row 0, lane_dims: the lane's
-// first dim (lane_dim(dl, 0)).  scan_start issues the first step's loads;
-// scan_run scores everything.  A caller can put independent work (the fused
+// first dim (lane_dim(dl, 0)).  scan_start issues the first PD - 1 steps'
+// loads; scan_run scores everything, issuing each step's loads PD - 1 steps
+// ahead of its scoring.  A caller can put independent work (the fused
 // kernel's QK-norm/RoPE prep) between them, so that work and the first
-// load's latency overlap.
-template <int HD>
+// loads' latency overlap.
+template <int HD, int PD>
 struct ScanState {
     static constexpr int P = ScanShape<HD>::P, DPL = HD / 16;
     ScanBufs b;
     int t, steps;
-    float ka[P][DPL], va[P][DPL];
+    float k[PD][P][DPL], v[PD][P][DPL];
 };
 
-template <int HD, int NG>
-__device__ __forceinline__ void scan_start(ScanState<HD>& s, const float* kb, const float* vb,
+template <int HD, int NG, int PD>
+__device__ __forceinline__ void scan_start(ScanState<HD, PD>& s, const float* kb, const float* vb,
                                            long kv_stride, int lane_dims, int b0, int e1,
                                            int group) {
     constexpr int S = NG * ScanShape<HD>::P;
     // Block-uniform trip count and one exit, at the bottom of the loop: with a
-    // divergent or mid-body exit the compiler must assume the other buffer's
+    // divergent or mid-body exit the compiler must assume the other buffers'
     // loads may still be in flight at the loop head and waits for them there,
-    // serialising the two buffers again.
+    // serialising the buffers again.
     s.steps = __builtin_amdgcn_readfirstlane(e1 > b0 ? (e1 - b0 + S - 1) / S : 0);
     s.t = b0 + group * ScanShape<HD>::P;
-    if (s.steps == 0) return;
-    s.b = scan_bufs(kb, vb, kv_stride, e1, lane_dims);
-    scan_load<HD>(s.b, s.t, s.ka, s.va);
+    // Unconditional, also for a slice with no rows (those loads lie past the
+    // buffer's end: zeros, no traffic).  A return here would join two paths
+    // with different loads in flight, and the wait count merged at the join
+    // would make the caller's next use of its own, earlier loads wait for
+    // every K/V load issued here.
+    s.b = scan_bufs(kb, vb, kv_stride, e1 > 0 ? e1 : 0, lane_dims);
+#pragma unroll
+    for (int i = 0; i < PD - 1; ++i) scan_load<HD>(s.b, s.t + i * S, s.k[i], s.v[i]);
 }
 
-template <int HD, int G, int NG>
-__device__ __forceinline__ void scan_run(ScanState<HD>& s, int e1, const float (&q)[G][HD / 16],
+template <int HD, int G, int NG, int PD>
+__device__ __forceinline__ void scan_run(ScanState<HD, PD>& s, int e1, const float (&q)[G][HD / 16],
                                          float (&m)[G], float (&l)[G], float (&o)[G][HD / 16]) {
-    constexpr int P = ScanShape<HD>::P, DPL = HD / 16, S = NG * P;
+    constexpr int S = NG * ScanShape<HD>::P;
     if (s.steps == 0) return;
     int t = s.t;
-    float kn[P][DPL], vn[P][DPL];
-    for (int pair = 0; pair < s.steps / 2; ++pair) {
-        scan_load<HD>(s.b, t + S, kn, vn);
-        __builtin_amdgcn_sched_barrier(0);
-        scan_update<HD, G>(q, m, l, o, s.ka, s.va, t, e1);
-        t += S;
-        scan_load<HD>(s.b, t + S, s.ka, s.va);       // past the end: zeros, no traffic
-        __builtin_amdgcn_sched_barrier(0);
-        scan_update<HD, G>(q, m, l, o, kn, vn, t, e1);
-        t += S;
+    // step j lives in buffer j % PD; before step j is scored, step j + PD - 1
+    // goes out into the buffer step j - 1 has freed (past the end: zeros, no
+    // traffic), then a scheduling barrier keeps those loads ahead of the
+    // scoring
+    const int full = s.steps / PD;
+    for (int it = 0; it < full; ++it) {
+#pragma unroll
+        for (int i = 0; i < PD; ++i) {
+            const int nb = (i + PD - 1) % PD;
+            scan_load<HD>(s.b, t + (PD - 1) * S, s.k[nb], s.v[nb]);
+            __builtin_amdgcn_sched_barrier(0);
+            scan_update<HD, G>(q, m, l, o, s.k[i], s.v[i], t, e1);
+            t += S;
+        }
     }
-    if (s.steps & 1) scan_update<HD, G>(q, m, l, o, s.ka, s.va, t, e1);
-}
-
-template <int HD, int G, int NG>
-__device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long kv_stride,
-                                          int lane_dims, int b0, int e1, int group,
-                                          const float (&q)[G][HD / 16], float (&m)[G],
-                                          float (&l)[G], float (&o)[G][HD / 16]) {
-    ScanState<HD> s;
-    scan_start<HD, NG>(s, kb, vb, kv_stride, lane_dims, b0, e1, group);
-    scan_run<HD, G, NG>(s, e1, q, m, l, o);
+    const int rem = s.steps - full * PD;
+#pragma unroll
+    for (int i = 0; i < PD - 1; ++i) {
+        if (i < rem) {
+            scan_update<HD, G>(q, m, l, o, s.k[i], s.v[i], t, e1);
+            t += S;
+        }
+    }
 }
 
 // Split merge of the fused kernel (and of the split kernel's one-launch
@@ -215,14 +281,15 @@ __device__ __forceinline__ void attn_scan(const float* kb, const float* vb, long
 // HD) of part_m / part_l / part_o; other XCDs wrote them, so they are read
 // with sc1 loads (past this XCD's L2, which can still hold an earlier
 // launch's lines).  A thread owns (head, dim) elements and reads the splits in
-// groups of 8, every load of a group issued before the first is used, with a
-// running maximum across groups: one memory round trip per 8 splits instead
-// of one per split.  Empty splits carry (m, l, o) = (-inf, 0, 0) and weigh 0;
+// groups of 8, every load of a group -- for all of its elements -- issued
+// before the first is used, with a running maximum across groups: one memory
+// round trip per 8 splits instead of one per split and element.  Empty splits carry (m, l, o) = (-inf, 0, 0) and weigh 0;
 // the split holding pos is never empty, so the final maximum is finite.
 template <int HD, int G, int NT>
 __device__ __forceinline__ void merge_splits(const float* part_m, const float* part_l, const float* part_o,
                                              int n_splits, int kvh, float* out) {
     constexpr int SC1 = 16;                   // buffer cache policy: sc1
+    constexpr int NE = (G * HD + NT - 1) / NT;   // (head, dim) elements per thread
     const int nh = n_splits * G;              // this kv head's (head, split) pairs
     const long h0 = (long)kvh * G * n_splits;
     const __amdgpu_buffer_rsrc_t rm =
@@ -231,38 +298,51 @@ __device__ __forceinline__ void merge_splits(const float* part_m, const float* p
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_l + h0), (short)0, nh * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t ro =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(part_o + h0 * HD), (short)0, nh * HD * 4, 0x00020000);
-    for (int e = threadIdx.x; e < G * HD; e += NT) {
-        const int h = e / HD, d = e % HD;
-        float M = -INFINITY, L = 0.f, O = 0.f;
-        for (int s0 = 0; s0 < n_splits; s0 += 8) {
-            float mv[8], lv[8], ov[8];
+    float M[NE], L[NE], O[NE];
+#pragma unroll
+    for (int k = 0; k < NE; ++k) { M[k] = -INFINITY; L[k] = 0.f; O[k] = 0.f; }
+    for (int s0 = 0; s0 < n_splits; s0 += 8) {
+        // every load of this round, for all of the thread's elements, goes out
+        // before the first is used: one memory round trip per 8 splits
+        float mv[NE][8], lv[NE][8], ov[NE][8];
+#pragma unroll
+        for (int k = 0; k < NE; ++k) {
+            const int e = min((int)threadIdx.x + k * NT, G * HD - 1);   // past the end: a copy
+            const int h = e / HD, d = e % HD;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int i = h * n_splits + min(s0 + j, n_splits - 1);   // past the end: a copy
-                mv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, i * 4, 0, SC1));
-                lv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, i * 4, 0, SC1));
-                ov[j] = __builtin_bit_cast(float,
-                                           __builtin_amdgcn_raw_buffer_load_b32(ro, (i * HD + d) * 4, 0, SC1));
+                mv[k][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, i * 4, 0, SC1));
+                lv[k][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, i * 4, 0, SC1));
+                ov[k][j] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(ro, (i * HD + d) * 4, 0, SC1));
             }
-            float cm = M;
+        }
+#pragma unroll
+        for (int k = 0; k < NE; ++k) {
+            float cm = M[k];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                if (s0 + j >= n_splits) mv[j] = -INFINITY;                // ... which weighs 0
-                cm = fmaxf(cm, mv[j]);
+                if (s0 + j >= n_splits) mv[k][j] = -INFINITY;               // ... which weighs 0
+                cm = fmaxf(cm, mv[k][j]);
             }
             if (cm == -INFINITY) continue;   // every split so far is empty
-            const float c = exp2f(M - cm);    // 0 while M = -inf
-            L *= c;
-            O *= c;
+            const float c = exp2f(M[k] - cm);    // 0 while M = -inf
+            L[k] *= c;
+            O[k] *= c;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float w = exp2f(mv[j] - cm);
-                L += lv[j] * w;
-                O += ov[j] * w;
+                const float w = exp2f(mv[k][j] - cm);
+                L[k] += lv[k][j] * w;
+                O[k] += ov[k][j] * w;
             }
-            M = cm;
+            M[k] = cm;
         }
-        out[(long)(kvh * G + h) * HD + d] = O / L;
+    }
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int e = threadIdx.x + k * NT;
+        if (e < G * HD) out[(long)(kvh * G + e / HD) * HD + e % HD] = O[k] / L[k];
     }
 }
 
@@ -288,10 +368,11 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
     const int b1 = min(pos + 1, b0 + chunk);
     const long kv_stride = (long)a.n_kv * HD;
     const float sc = a.scale * LOG2E;
-    // the scan's first K/V step goes out before q's loads
-    ScanState<HD> scan;
-    scan_start<HD, 4 * W>(scan, a.k_cache + cache0 + (long)kvh * HD, a.v_cache + cache0 + (long)kvh * HD,
-                          kv_stride, lane_dim(dl, 0), b0, b1, wave * 4 + row);
+    // the scan's first K/V steps go out before q's loads
+    ScanState<HD, kScanDepth> scan;
+    scan_start<HD, 4 * W, kScanDepth>(scan, a.k_cache + cache0 + (long)kvh * HD,
+                                      a.v_cache + cache0 + (long)kvh * HD, kv_stride, lane_dim(dl, 0),
+                                      b0, b1, wave * 4 + row);
     __builtin_amdgcn_sched_barrier(0);
 
     // q for the G heads of this group, this lane's dims
@@ -313,29 +394,25 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(AttnArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    scan_run<HD, G, 4 * W>(scan, b1, q, m, l, o);
+    scan_run<HD, G, 4 * W, kScanDepth>(scan, b1, q, m, l, o);
 
-    // ---- merge the 16 (wave,row) states of this block through LDS ---------
-    __shared__ float s_m[4 * W][G], s_l[4 * W][G];
-    __shared__ float s_o[4 * W][G][HD];
-    const int st = wave * 4 + row;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        if (dl == 0) { s_m[st][h] = m[h]; s_l[st][h] = l[h]; }
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) s_o[st][h][lane_dim(dl, d)] = o[h][d];
-    }
+    // ---- merge the block's 16 (wave, row) states (first by lane shuffles
+    // within each wave when G is small) through LDS ------------------------------
+    constexpr int NS = block_states<G, W>();
+    __shared__ float s_m[NS][G], s_l[NS][G];
+    __shared__ float s_o[NS][G][HD];
+    stage_block_states<HD, G, W>(m, l, o, wave, row, dl, s_m, s_l, s_o);
     __syncthreads();
     // thread -> (head, dim) pairs
     for (int e = threadIdx.x; e < G * HD; e += 64 * W) {
         const int h = e / HD, d = e % HD;
         float mx = -INFINITY;
 #pragma unroll
-        for (int s2 = 0; s2 < 4 * W; ++s2) mx = fmaxf(mx, s_m[s2][h]);
+        for (int s2 = 0; s2 < NS; ++s2) mx = fmaxf(mx, s_m[s2][h]);
         float lsum = 0.f, osum = 0.f;
         if (mx != -INFINITY) {
 #pragma unroll
-            for (int s2 = 0; s2 < 4 * W; ++s2) {
+            for (int s2 = 0; s2 < NS; ++s2) {
                 const float w = exp2f(s_m[s2][h] - mx);   // 0 for empty states
                 lsum += s_l[s2][h] * w;
                 osum += s_o[s2][h][d] * w;
@@ -487,7 +564,7 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
 //    block that sees n_splits - 1 merges and resets the counter to 0 (no
 //    waiting anywhere, and the counters are clean for the next launch).
 // ---------------------------------------------------------------------------
-template <int HD, int G, int W>
+template <int HD, int G, int W, int PD>
 __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     constexpr int DPL = HD / 16;
     constexpr int EPL = HD / 64;              // head elements per lane in the prep
@@ -517,47 +594,80 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     float* kc = a.k_cache + (long)slot * a.slot_stride;
     float* vc = a.v_cache + (long)slot * a.slot_stride;
 
-    // the first step of the history scan (rows < pos, untouched by this
-    // launch) goes out before the prep, whose latency it then overlaps
-    ScanState<HD> scan;
-    scan_start<HD, 4 * W>(scan, kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride, lane_dim(dl, 0),
-                          b0, e1, wave * 4 + row);
+    // ---- loads first: the prep's inputs (q / k / v of the raw GEMV output,
+    // their QK-norm weights, the RoPE row of pos), then the first PD steps of
+    // the history scan (rows < pos, untouched by this launch).  Vector loads
+    // return in order, so the prep waits only for its own small loads and
+    // computes while the K/V steps are in flight.
+    constexpr int NV = (G + 1 + W - 1) / W;   // prep vectors per wave
+    const float* cr = a.cos_tab + (long)pos * (HD / 2);
+    const float* sr = a.sin_tab + (long)pos * (HD / 2);
+    float pv[NV][EPL], pn[NV][EPL], rc[EPL], rs[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        const int ei = e < HD / 2 ? e : e - HD / 2;     // rotate-half partner table index
+        rc[j] = cr[ei];
+        rs[j] = sr[ei];
+    }
+    // Branch-free: every lane loads (a wave past the G + 1 vectors reloads k;
+    // without norm weights the vector itself is loaded and ignored), so the
+    // wait counts before the prep cover these loads only, not the K/V steps
+    // issued after them.
+    const float* nq = a.q_norm, *nk = a.k_norm;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int vi = min(wave + n * W, G);            // wave-uniform
+        const bool isq = vi < G;
+        const float* src = qkv + (isq ? (long)(kvh * G + vi) * HD : (long)(a.n_heads + kvh) * HD);
+        const float* nw = isq ? (nq ? nq + (long)(kvh * G + vi) * HD : nullptr)
+                              : (nk ? nk + (long)kvh * HD : nullptr);
+        const float* nsrc = nw ? nw : src;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            pv[n][j] = src[lane + 64 * j];
+            const float w = nsrc[lane + 64 * j];
+            pn[n][j] = nw ? w : 1.f;
+        }
+    }
+    const float vnew = qkv[(long)(a.n_heads + a.n_kv + kvh) * HD + (threadIdx.x & (HD - 1))];
+    __builtin_amdgcn_sched_barrier(0);
+    ScanState<HD, PD> scan;
+    scan_start<HD, 4 * W, PD>(scan, kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride,
+                              lane_dim(dl, 0), b0, e1, wave * 4 + row);
     __builtin_amdgcn_sched_barrier(0);
 
     __shared__ float sq[G][HD], sk[HD], sv[HD];
     // ---- prep: QK-norm + RoPE of the G q heads and k, wave per vector -----
-    const float* cr = a.cos_tab + (long)pos * (HD / 2);
-    const float* sr = a.sin_tab + (long)pos * (HD / 2);
-    for (int vi = wave; vi < G + 1; vi += W) {
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int vi = wave + n * W;
+        if (vi >= G + 1) continue;                     // wave-uniform
         const bool isq = vi < G;
-        const int head = isq ? kvh * G + vi : kvh;
-        const float* src = qkv + (isq ? (long)head * HD : (long)(a.n_heads + kvh) * HD);
-        const float* nw = isq ? (a.q_norm ? a.q_norm + (long)head * HD : nullptr)
-                              : (a.k_norm ? a.k_norm + (long)kvh * HD : nullptr);
+        const bool normed = isq ? nq != nullptr : nk != nullptr;
         float v[EPL];
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
-            v[j] = src[lane + 64 * j];
+            v[j] = pv[n][j];
             ss += v[j] * v[j];
         }
-        if (nw) {
+        if (normed) {
             ss = wave_sum(ss);
             const float inv = 1.0f / sqrtf(ss / (float)HD + a.qk_eps);
 #pragma unroll
-            for (int j = 0; j < EPL; ++j) v[j] = v[j] * inv * nw[lane + 64 * j];
+            for (int j = 0; j < EPL; ++j) v[j] = v[j] * inv * pn[n][j];
         }
         float r[EPL];
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
-            const int e = lane + 64 * j;
             if constexpr (HD == 64) {
                 const float other = __shfl_xor(v[j], 32, 64);   // partner e +- 32
-                r[j] = e < 32 ? v[j] * cr[e] - other * sr[e] : other * sr[e - 32] + v[j] * cr[e - 32];
+                r[j] = lane < 32 ? v[j] * rc[j] - other * rs[j] : other * rs[j] + v[j] * rc[j];
             } else {
                 constexpr int HJ = EPL / 2;                     // partner is j +- HJ
-                r[j] = j < HJ ? v[j] * cr[e] - v[j + HJ] * sr[e]
-                              : v[j - HJ] * sr[e - HD / 2] + v[j] * cr[e - HD / 2];
+                r[j] = j < HJ ? v[j] * rc[j] - v[j + HJ] * rs[j]
+                              : v[j - HJ] * rs[j] + v[j] * rc[j];
             }
         }
 #pragma unroll
@@ -567,7 +677,7 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
             else sk[e] = r[j];
         }
     }
-    for (int e = threadIdx.x; e < HD; e += 64 * W) sv[e] = qkv[(long)(a.n_heads + a.n_kv + kvh) * HD + e];
+    if (threadIdx.x < HD) sv[threadIdx.x] = vnew;
     __syncthreads();
     if (owner) {
         for (int e = threadIdx.x; e < HD; e += 64 * W) {
@@ -589,7 +699,7 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
-    scan_run<HD, G, 4 * W>(scan, e1, q, m, l, o);
+    scan_run<HD, G, 4 * W, PD>(scan, e1, q, m, l, o);
     if (owner && wave == 0 && row == 0) {
         // position pos from LDS (the 16 lanes of row 0 of wave 0)
         constexpr int P = ScanShape<HD>::P;
@@ -604,17 +714,13 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         scan_update<HD, G>(q, m, l, o, kf, vf, 0, 1);
     }
 
-    // ---- merge the 16 (wave,row) states of this block ------------------------
-    __shared__ float s_m[4 * W][G], s_l[4 * W][G];
-    __shared__ float s_o[4 * W][G][HD];
+    // ---- merge the block's 16 (wave, row) states (first by lane shuffles
+    // within each wave when G is small) through LDS ------------------------------
+    constexpr int NS = block_states<G, W>();
+    __shared__ float s_m[NS][G], s_l[NS][G];
+    __shared__ float s_o[NS][G][HD];
     __shared__ int s_last;
-    const int st = wave * 4 + row;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        if (dl == 0) { s_m[st][h] = m[h]; s_l[st][h] = l[h]; }
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) s_o[st][h][lane_dim(dl, d)] = o[h][d];
-    }
+    stage_block_states<HD, G, W>(m, l, o, wave, row, dl, s_m, s_l, s_o);
     __syncthreads();
     // each sequence owns n_heads * gridDim.y partial slots (its active split
     // count may be smaller and differs between sequences)
@@ -623,11 +729,11 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         const int h = e / HD, d = e % HD;
         float mx = -INFINITY;
 #pragma unroll
-        for (int s2 = 0; s2 < 4 * W; ++s2) mx = fmaxf(mx, s_m[s2][h]);
+        for (int s2 = 0; s2 < NS; ++s2) mx = fmaxf(mx, s_m[s2][h]);
         float lsum = 0.f, osum = 0.f;
         if (mx != -INFINITY) {
 #pragma unroll
-            for (int s2 = 0; s2 < 4 * W; ++s2) {
+            for (int s2 = 0; s2 < NS; ++s2) {
                 const float w = exp2f(s_m[s2][h] - mx);
                 lsum += s_l[s2][h] * w;
                 osum += s_o[s2][h][d] * w;
@@ -676,8 +782,8 @@ template <int HD, int G> constexpr int attn_waves() { return 4; }
 template <int HD, int G>
 static int launch_fused(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st) {
     constexpr int W = attn_waves<HD, G>();
-    hipLaunchKernelGGL((attn_fused_kernel<HD, G, W>), dim3(a.n_kv, n_splits, n_seq), dim3(64 * W),
-                       0, st, a);
+    hipLaunchKernelGGL((attn_fused_kernel<HD, G, W, kFusedScanDepth>), dim3(a.n_kv, n_splits, n_seq),
+                       dim3(64 * W), 0, st, a);
     ATLAS_LAUNCH_CHECK("attn_fused");
     return ATLAS_OK;
 }

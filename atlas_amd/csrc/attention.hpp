@@ -64,8 +64,11 @@ struct AttnFusedArgs {
 };
 
 // The scan addresses one KV head's rows with 32-bit byte offsets.
+// Cache byte offsets are 32-bit.  A scan prefetches up to a few steps past
+// its last row (those loads lie past the buffer's end and read zeros); the
+// 1024 rows of headroom keep every such offset from wrapping around.
 inline bool attn_rows_fit(long max_rows, int n_kv, int head_dim) {
-    return max_rows > 0 && max_rows * (long)n_kv * head_dim * 4 <= 0xFFFFFFFFL;
+    return max_rows > 0 && (max_rows + 1024) * (long)n_kv * head_dim * 4 <= 0xFFFFFFFFL;
 }
 
 // Positions per split below which another split costs more than it saves
