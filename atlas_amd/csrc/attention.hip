@@ -156,6 +156,59 @@ __device__ __forceinline__ void scan_update(const float (&q)[G][HD / 16], float 
     }
 }
 
+// scan_update for rows loaded before the live range was known: positions
+// outside [lo, end) are masked and their V rows zeroed first (rows past the
+// live position may hold anything a previous sequence left there).
+template <int HD, int G>
+__device__ __forceinline__ void scan_update_masked(const float (&q)[G][HD / 16], float (&m)[G],
+                                                   float (&l)[G], float (&o)[G][HD / 16],
+                                                   const float (&kf)[ScanShape<HD>::P][HD / 16],
+                                                   float (&vf)[ScanShape<HD>::P][HD / 16], int t,
+                                                   int lo, int end) {
+    constexpr int P = ScanShape<HD>::P, DPL = HD / 16;
+    float kk[P][DPL];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const bool ok = t + i >= lo && t + i < end;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) {
+            kk[i][d] = ok ? kf[i][d] : 0.f;
+            vf[i][d] = ok ? vf[i][d] : 0.f;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float s[P];
+        float smax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            float acc = 0.f;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) acc += q[h][d] * kk[i][d];
+            acc = row16_sum(acc);
+            s[i] = (t + i >= lo && t + i < end) ? acc : -INFINITY;
+            smax = fmaxf(smax, s[i]);
+        }
+        const float mn = fmaxf(m[h], smax);
+        const float corr = m[h] == -INFINITY ? 0.f : exp2f(m[h] - mn);
+        float psum = 0.f, p[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            p[i] = (t + i >= lo && t + i < end) ? exp2f(s[i] - mn) : 0.f;
+            psum += p[i];
+        }
+        l[h] = l[h] * corr + psum;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) {
+            float acc = o[h][d] * corr;
+#pragma unroll
+            for (int i = 0; i < P; ++i) acc += p[i] * vf[i][d];
+            o[h][d] = acc;
+        }
+        m[h] = mn;
+    }
+}
+
 // Merge the online-softmax states of a wave's four 16-lane rows (lanes with
 // the same dl hold the same dims in every row) by lane shuffles across rows;
 // afterwards every row holds the wave's state.  An empty state (m = -inf)
@@ -564,52 +617,40 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a, int hd) {
 //    block that sees n_splits - 1 merges and resets the counter to 0 (no
 //    waiting anywhere, and the counters are clean for the next launch).
 // ---------------------------------------------------------------------------
-template <int HD, int G, int W, int PD>
+// LIVE: the step provides its RoPE row (a.rope_row) and the launch is one
+// sequence in slot 0; the prep then needs no position, and split 0 loads its
+// first steps before the position arrives (the pre-scan).
+template <int HD, int G, int W, int PD, bool LIVE>
 __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
     constexpr int DPL = HD / 16;
     constexpr int EPL = HD / 64;              // head elements per lane in the prep
     constexpr float LOG2E = 1.4426950408889634f;
+    constexpr int S = 4 * W * ScanShape<HD>::P;   // positions per scan step
+    if constexpr (LIVE) {
+        // the arguments the loads before pos and the split rule after it
+        // need, in SGPRs now, in one round of argument loads: fetched where
+        // first used, they cost further dependent rounds between the prep's
+        // loads and the pre-scan's, and after pos
+        asm volatile("" ::"s"(a.k_cache), "s"(a.v_cache), "s"(a.max_rows), "s"(gridDim.y),
+                     "s"(a.window), "s"(a.adaptive), "s"(a.qk_eps), "s"(a.scale));
+    }
     const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = lane >> 4, dl = lane & 15;
-    const int pos = a.pos_dev[seq];
-    const int slot = a.slot_dev ? a.slot_dev[seq] : 0;
-    const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
-    const int ctx = pos - t_lo + 1;
-    // active splits: all gridDim.y, the measured rule for the live context,
-    // or one per min_chunk positions of it (the grid is fixed when a decode
-    // step is captured once and replayed at every position; surplus blocks
-    // leave here)
-    int n_splits = gridDim.y;
-    if (a.adaptive) n_splits = min(n_splits, attn_fused_splits_for(a.n_kv * (int)gridDim.z, ctx));
-    else if (a.min_chunk > 0) n_splits = min(n_splits, max(1, (ctx + a.min_chunk - 1) / a.min_chunk));
-    if (split >= n_splits) return;
-    const int chunk = (ctx + n_splits - 1) / n_splits;
-    const int b0 = t_lo + split * chunk;
-    const int b1 = min(pos + 1, b0 + chunk);
-    const bool owner = b0 <= pos && pos < b0 + chunk;
-    const int e1 = min(b1, pos);              // cache rows [b0, e1) are read here
     const long kv_stride = (long)a.n_kv * HD;
     const float* qkv = a.qkv + (long)seq * a.qkv_stride;
-    float* kc = a.k_cache + (long)slot * a.slot_stride;
-    float* vc = a.v_cache + (long)slot * a.slot_stride;
 
-    // ---- loads first: the prep's inputs (q / k / v of the raw GEMV output,
-    // their QK-norm weights, the RoPE row of pos), then the first PD steps of
-    // the history scan (rows < pos, untouched by this launch).  Vector loads
-    // return in order, so the prep waits only for its own small loads and
-    // computes while the K/V steps are in flight.
+    // ---- loads that need no position, first: the prep's inputs (q / k / v
+    // of the raw GEMV output and their QK-norm weights) and, when LIVE, the
+    // step's RoPE row and -- for split 0, whose history always starts at row
+    // 0 or later -- the first PD - 1 steps of rows from row 0 (the pre-scan;
+    // rows outside the live range are masked once it is known).  The
+    // position is a dependent device load (~1 us); everything that needs it
+    // follows.  Vector loads return in order, so the prep waits only for the
+    // loads issued before its own last one: without LIVE its table row goes
+    // out after pos, and there is no pre-scan for it to wait behind.
     constexpr int NV = (G + 1 + W - 1) / W;   // prep vectors per wave
-    const float* cr = a.cos_tab + (long)pos * (HD / 2);
-    const float* sr = a.sin_tab + (long)pos * (HD / 2);
     float pv[NV][EPL], pn[NV][EPL], rc[EPL], rs[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-        const int e = lane + 64 * j;
-        const int ei = e < HD / 2 ? e : e - HD / 2;     // rotate-half partner table index
-        rc[j] = cr[ei];
-        rs[j] = sr[ei];
-    }
     // Branch-free: every lane loads (a wave past the G + 1 vectors reloads k;
     // without norm weights the vector itself is loaded and ignored), so the
     // wait counts before the prep cover these loads only, not the K/V steps
@@ -631,10 +672,72 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         }
     }
     const float vnew = qkv[(long)(a.n_heads + a.n_kv + kvh) * HD + (threadIdx.x & (HD - 1))];
+    // the rotate-half partner table index of each of the lane's elements
+    auto rope_idx = [&](int j) {
+        const int e = lane + 64 * j;
+        return e < HD / 2 ? e : e - HD / 2;
+    };
+    const bool pre_on = LIVE && split == 0;
+    const int pre_rows = pre_on ? min((PD - 1) * S, a.max_rows) : 0;
+    ScanState<HD, PD> pre;
+    int pos;
+    if constexpr (LIVE) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            rc[j] = a.rope_row[rope_idx(j)];
+            rs[j] = a.rope_row[HD / 2 + rope_idx(j)];
+        }
+        // pos as a vector load behind the prep's loads and ahead of the
+        // pre-scan's (loads return in order: it arrives before the K/V rows);
+        // a scalar load would make the next scalar wait cover it
+        const __amdgpu_buffer_rsrc_t pb =
+            __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.pos_dev), (short)0, 4, 0x00020000);
+        const int pos_v = __builtin_amdgcn_raw_buffer_load_b32(pb, 0, 0, 0);
+        // unconditional (split > 0: an empty range, zeros, no traffic)
+        __builtin_amdgcn_sched_barrier(0);
+        scan_start<HD, 4 * W, PD>(pre, a.k_cache + (long)kvh * HD, a.v_cache + (long)kvh * HD,
+                                  kv_stride, lane_dim(dl, 0), 0, pre_rows, wave * 4 + row);
+        __builtin_amdgcn_sched_barrier(0);
+        pos = __builtin_amdgcn_readfirstlane(pos_v);
+    } else {
+        pos = a.pos_dev[seq];
+    }
+
+    const int slot = LIVE ? 0 : (a.slot_dev ? a.slot_dev[seq] : 0);
+    const int t_lo = (a.window > 0 && pos >= a.window) ? pos - a.window + 1 : 0;
+    const int ctx = pos - t_lo + 1;
+    // active splits: all gridDim.y, the measured rule for the live context,
+    // or one per min_chunk positions of it (the grid is fixed when a decode
+    // step is captured once and replayed at every position; surplus blocks
+    // leave here)
+    int n_splits = gridDim.y;
+    if (a.adaptive)
+        n_splits = min(n_splits, attn_fused_splits_for(a.n_kv * (LIVE ? 1 : (int)gridDim.z), ctx));
+    else if (a.min_chunk > 0) n_splits = min(n_splits, max(1, (ctx + a.min_chunk - 1) / a.min_chunk));
+    if (split >= n_splits) return;
+    const int chunk = (ctx + n_splits - 1) / n_splits;
+    const int b0 = t_lo + split * chunk;
+    const int b1 = min(pos + 1, b0 + chunk);
+    const bool owner = b0 <= pos && pos < b0 + chunk;
+    const int e1 = min(b1, pos);              // cache rows [b0, e1) are read here
+    float* kc = a.k_cache + (long)slot * a.slot_stride;
+    float* vc = a.v_cache + (long)slot * a.slot_stride;
+
+    if constexpr (!LIVE) {
+        // the RoPE row of pos
+        const float* cr = a.cos_tab + (long)pos * (HD / 2);
+        const float* sr = a.sin_tab + (long)pos * (HD / 2);
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            rc[j] = cr[rope_idx(j)];
+            rs[j] = sr[rope_idx(j)];
+        }
+    }
+    // the history scan proper: rows [b0, e1), less the pre-scan's
     __builtin_amdgcn_sched_barrier(0);
     ScanState<HD, PD> scan;
     scan_start<HD, 4 * W, PD>(scan, kc + (long)kvh * HD, vc + (long)kvh * HD, kv_stride,
-                              lane_dim(dl, 0), b0, e1, wave * 4 + row);
+                              lane_dim(dl, 0), pre_on ? max(b0, pre_rows) : b0, e1, wave * 4 + row);
     __builtin_amdgcn_sched_barrier(0);
 
     __shared__ float sq[G][HD], sk[HD], sv[HD];
@@ -699,6 +802,11 @@ __global__ __launch_bounds__(64 * W) void attn_fused_kernel(AttnFusedArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
 
+    if (LIVE && pre_on) {
+#pragma unroll
+        for (int i = 0; i < PD - 1; ++i)
+            scan_update_masked<HD, G>(q, m, l, o, pre.k[i], pre.v[i], pre.t + i * S, b0, e1);
+    }
     scan_run<HD, G, 4 * W, PD>(scan, e1, q, m, l, o);
     if (owner && wave == 0 && row == 0) {
         // position pos from LDS (the 16 lanes of row 0 of wave 0)
@@ -782,8 +890,12 @@ template <int HD, int G> constexpr int attn_waves() { return 4; }
 template <int HD, int G>
 static int launch_fused(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream_t st) {
     constexpr int W = attn_waves<HD, G>();
-    hipLaunchKernelGGL((attn_fused_kernel<HD, G, W, kFusedScanDepth>), dim3(a.n_kv, n_splits, n_seq),
-                       dim3(64 * W), 0, st, a);
+    if (a.rope_row)
+        hipLaunchKernelGGL((attn_fused_kernel<HD, G, W, kFusedScanDepth, true>),
+                           dim3(a.n_kv, n_splits, n_seq), dim3(64 * W), 0, st, a);
+    else
+        hipLaunchKernelGGL((attn_fused_kernel<HD, G, W, kFusedScanDepth, false>),
+                           dim3(a.n_kv, n_splits, n_seq), dim3(64 * W), 0, st, a);
     ATLAS_LAUNCH_CHECK("attn_fused");
     return ATLAS_OK;
 }
@@ -803,6 +915,8 @@ int attn_fused_launch(const AttnFusedArgs& a, int n_splits, int n_seq, hipStream
     ATLAS_REQUIRE(n_splits == 1 || (a.part_m && a.part_l && a.part_o && a.counters),
                   "attention: split partials missing");
     ATLAS_REQUIRE(n_seq >= 1 && n_splits >= 1, "attention: empty grid");
+    ATLAS_REQUIRE(!a.rope_row || (n_seq == 1 && !a.slot_dev),
+                  "attention: a live RoPE row serves one sequence in slot 0");
     ATLAS_REQUIRE(n_splits <= kAttnFusedMaxSplits, "attention: %d splits > %d", n_splits,
                   kAttnFusedMaxSplits);
     ATLAS_REQUIRE(attn_rows_fit(a.max_rows, a.n_kv, a.head_dim),

@@ -61,6 +61,8 @@ struct AttnFusedArgs {
     int adaptive;            // 1 (min_chunk ignored): active splits = min(grid,
                              // attn_fused_splits_for(n_kv * n_seq, ctx))
     int max_rows;            // cache rows per slot (max_seq), > 0
+    const float* rope_row;   // [hd]: cos (hd/2) then sin (hd/2) at pos_dev[0], or null (the
+                             // tables); one sequence in slot 0 only
 };
 
 // The scan addresses one KV head's rows with 32-bit byte offsets.

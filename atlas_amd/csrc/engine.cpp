@@ -114,6 +114,7 @@ struct atlas_model {
     DevMat lm_head;
     float* final_norm = nullptr;
     float *cos_tab = nullptr, *sin_tab = nullptr;
+    float* rope_row = nullptr;           // the fused step's RoPE row at pos (embed writes it)
     float *x = nullptr, *xn = nullptr, *y = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr,
           *logits = nullptr;
     // fused step: residual ping-pong partner of x, the W_down output, split
@@ -406,7 +407,10 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
     const atlas_model_config& c = m->cfg;
     const int d = c.d_model;
     const float eps = c.rms_eps;
-    TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, 1, m->st));
+    RopeRowArgs rr;
+    rr.pos_dev = m->pos_dev; rr.cos_tab = m->cos_tab; rr.sin_tab = m->sin_tab; rr.half = m->hd / 2;
+    rr.out = long_ctx ? nullptr : m->rope_row;
+    TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, 1, m->st, rr));
     for (int li = 0; li < c.n_layers; ++li) {
         LayerW& L = m->L[li];
         if (li == 0)
@@ -434,6 +438,7 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
             a.part_o = m->attn_part + (size_t)2 * m->R * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
             a.adaptive = 1; a.max_rows = c.max_seq;
+            a.rope_row = m->rope_row;
             TRY(attn_fused_launch(a, m->attn_splits, 1, m->st));
         }
         TRY(gemv(m, L.wo, m->att, m->y, EPI_STORE));
@@ -1343,7 +1348,8 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         std::vector<float> cs, sn;
         rope_tables(c, hd, cs, sn);
         if (dalloc(m, (void**)&m->cos_tab, cs.size() * 4) ||
-            dalloc(m, (void**)&m->sin_tab, sn.size() * 4))
+            dalloc(m, (void**)&m->sin_tab, sn.size() * 4) ||
+            dalloc(m, (void**)&m->rope_row, (size_t)hd * 4))
             return fail(m);
         if (hipMemcpy(m->cos_tab, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemcpy(m->sin_tab, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {

@@ -1326,7 +1326,7 @@ int sample_launch(const SampleArgs& a, hipStream_t st) {
 // ---- embedding gather -----------------------------------------------------------
 __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__ table, int vocab,
                                                     int d, const uint32_t* tok_dev, uint32_t tok,
-                                                    float* __restrict__ out, long ld) {
+                                                    float* __restrict__ out, long ld, RopeRowArgs r) {
     const int s = blockIdx.y;
     uint32_t t = tok_dev ? tok_dev[s] : tok;
     if (t >= (uint32_t)vocab) t = (uint32_t)vocab - 1;
@@ -1334,14 +1334,24 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
     float* o = out + (long)s * ld;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < d; i += gridDim.x * 256)
         o[i] = __uint_as_float((uint32_t)row[i] << 16);
+    // the step's RoPE row: cos then sin at the live position
+    if (r.out && blockIdx.x == 0 && s == 0) {
+        const long p = *r.pos_dev;
+        for (int i = threadIdx.x; i < r.half; i += 256) {
+            r.out[i] = r.cos_tab[p * r.half + i];
+            r.out[r.half + i] = r.sin_tab[p * r.half + i];
+        }
+    }
 }
 
 int embed_launch(const uint16_t* table, int vocab, int d, const uint32_t* tok_dev, uint32_t tok,
-                 float* out, long ld, int n_seq, hipStream_t st) {
+                 float* out, long ld, int n_seq, hipStream_t st, const RopeRowArgs& rope) {
     ATLAS_REQUIRE(table && out && vocab > 0 && d > 0 && n_seq > 0, "embed: bad arguments");
+    ATLAS_REQUIRE(!rope.out || (rope.pos_dev && rope.cos_tab && rope.sin_tab && rope.half > 0),
+                  "embed: RoPE row needs the position and the tables");
     const int bx = (d + 255) / 256 < 16 ? (d + 255) / 256 : 16;
     hipLaunchKernelGGL(embed_kernel, dim3(bx, n_seq), dim3(256), 0, st, table, vocab, d, tok_dev, tok,
-                       out, ld);
+                       out, ld, rope);
     ATLAS_LAUNCH_CHECK("embed");
     return ATLAS_OK;
 }

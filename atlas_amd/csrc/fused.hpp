@@ -89,8 +89,18 @@ int adamw_launch(float* p, float* m, float* v, const float* g, float lr, float b
 int argmax_launch(const ArgmaxArgs& a, hipStream_t st);
 // one token of generate_with_sampling (temperature > 0, 1 <= top_k <= 1024)
 int sample_launch(const SampleArgs& a, hipStream_t st);
+// Optional copy of the RoPE tables' row at *pos_dev into out (cos[half] then
+// sin[half]), made by the embedding gather that starts a decode step, so the
+// step's attention launches read their rotation without waiting on pos.
+struct RopeRowArgs {
+    const int* pos_dev = nullptr;
+    const float* cos_tab = nullptr;   // [max_seq x half]
+    const float* sin_tab = nullptr;
+    int half = 0;
+    float* out = nullptr;             // null: no copy
+};
 int embed_launch(const uint16_t* table, int vocab, int d, const uint32_t* tok_dev, uint32_t tok,
-                 float* out, long ld, int n_seq, hipStream_t st);
+                 float* out, long ld, int n_seq, hipStream_t st, const RopeRowArgs& rope = RopeRowArgs{});
 int add_int_launch(int* p, int n, int v, hipStream_t st);
 int init_launch(int kind, void* out, long n, unsigned long long seed, float a, float b,
                 hipStream_t st);

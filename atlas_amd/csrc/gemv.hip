@@ -98,11 +98,15 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const f32x4* __restric
 // residual x + normed (lib.rs:985-993); PRO_SILU is FeedForward's
 // silu(gate) * up (lib.rs:918-921) over interleaved (gate, up) pairs.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float block_sum256(float v, float* red4) {
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return red4[0] + red4[1] + red4[2] + red4[3];
+    float s = red[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) s += red[i];
+    return s;
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
@@ -119,7 +123,7 @@ template <int PPT>
 struct XRegs { f32x4 x[PPT], y[PPT], w[PPT]; };
 
 // guarded loads: only the vectors the prologue uses, only pieces below K
-template <int PPT>
+template <int PPT, int NT = 256>
 __device__ __forceinline__ void stage_regs_issue(const GemvArgs& a, XRegs<PPT>& r, int K) {
     const int np = K >> 2;
     const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
@@ -128,7 +132,7 @@ __device__ __forceinline__ void stage_regs_issue(const GemvArgs& a, XRegs<PPT>& 
     const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-        const int p = threadIdx.x + 256 * j;
+        const int p = threadIdx.x + NT * j;
         if (p < np) {
             r.x[j] = xin[p];
             if (res) r.y[j] = yin[p];
@@ -142,7 +146,7 @@ __device__ __forceinline__ void stage_regs_issue(const GemvArgs& a, XRegs<PPT>& 
 // K.  Guarded loads split the issue into branches, after which the compiler
 // waits for every load in flight, including weight loads issued between
 // the two halves.
-template <int PPT>
+template <int PPT, int NT = 256>
 __device__ __forceinline__ void stage_regs_issue_buf(const GemvArgs& a, XRegs<PPT>& r, int K) {
     const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
     const __amdgpu_buffer_rsrc_t xb =
@@ -154,16 +158,16 @@ __device__ __forceinline__ void stage_regs_issue_buf(const GemvArgs& a, XRegs<PP
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
         const int off = (int)threadIdx.x * 16;
-        r.x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xb, off, 4096 * j, 0));
-        r.y[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(yb, off, 4096 * j, 0));
-        r.w[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wb, off, 4096 * j, 0));
+        r.x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xb, off, NT * 16 * j, 0));
+        r.y[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(yb, off, NT * 16 * j, 0));
+        r.w[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wb, off, NT * 16 * j, 0));
     }
 }
 
-template <bool SWZ, int PPT>
+template <bool SWZ, int PPT, int NT = 256>
 __device__ __forceinline__ void stage_regs_finish(const GemvArgs& a, XRegs<PPT>& r, f32x4* xs,
                                                   int K) {
-    __shared__ float red4[4];
+    __shared__ float red[NT / 64];
     const int np = K >> 2;
     const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
     const f32x4 (&xv)[PPT] = r.x;
@@ -174,7 +178,7 @@ __device__ __forceinline__ void stage_regs_finish(const GemvArgs& a, XRegs<PPT>&
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < PPT; ++j) {
-            if (threadIdx.x + 256 * j < np) {
+            if (threadIdx.x + NT * j < np) {
                 const f32x4 t = res ? yv[j] : xv[j];
                 ss += t.x * t.x;
                 ss += t.y * t.y;
@@ -182,13 +186,13 @@ __device__ __forceinline__ void stage_regs_finish(const GemvArgs& a, XRegs<PPT>&
                 ss += t.w * t.w;
             }
         }
-        ss = block_sum256(ss, red4);
+        ss = block_sum<NT / 64>(ss, red);
         inv = 1.0f / sqrtf(ss / (float)K + a.pro_eps);
     }
     const bool write_out = a.pro_out && blockIdx.x == 0 && norm;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-        const int p = threadIdx.x + 256 * j;
+        const int p = threadIdx.x + NT * j;
         if (p < np) {
             f32x4 v;
             if (res) v = xv[j] + (yv[j] * inv) * wv[j];
@@ -204,22 +208,22 @@ __device__ __forceinline__ void stage_regs_finish(const GemvArgs& a, XRegs<PPT>&
 // the registers hold (PPT = 12: K <= 12288).  Buffer loads address all
 // pieces from one VGPR offset (the piece stride goes in the SGPR offset),
 // and reads past the end of x return zeros that are never stored.
-template <int PPT>
+template <int PPT, int NT = 256>
 __device__ __forceinline__ void stage_plain_issue(const GemvArgs& a, f32x4 (&xv)[PPT], int K) {
     const __amdgpu_buffer_rsrc_t xb =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.x), (short)0, K * 4, 0x00020000);
 #pragma unroll
     for (int j = 0; j < PPT; ++j)
         xv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              xb, (int)threadIdx.x * 16, 4096 * j, 0));
+                                              xb, (int)threadIdx.x * 16, NT * 16 * j, 0));
 }
 
-template <bool SWZ, int PPT>
+template <bool SWZ, int PPT, int NT = 256>
 __device__ __forceinline__ void stage_plain_finish(const f32x4 (&xv)[PPT], f32x4* xs, int K) {
     const int np = K >> 2;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-        const int p = threadIdx.x + 256 * j;
+        const int p = threadIdx.x + NT * j;
         if (p < np) xs[SWZ ? xpad(p) : p] = xv[j];
     }
 }
@@ -235,28 +239,28 @@ __device__ __forceinline__ int stage_kind(const GemvArgs& a, int K) {
 }
 
 // Looped staging: any K the LDS holds, and the SwiGLU prologue.
-template <bool SWZ>
+template <bool SWZ, int NT = 256>
 __device__ __forceinline__ void stage_x_loop(const GemvArgs& a, f32x4* xs, int K) {
-    __shared__ float red4[4];
+    __shared__ float red[NT / 64];
     const int np = K >> 2;
     const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
     float inv = 1.0f;
     if (a.pro == PRO_RESNORM || a.pro == PRO_RMSNORM) {
         const f32x4* v = reinterpret_cast<const f32x4*>(a.pro == PRO_RESNORM ? a.pro_y : a.x);
         float ss = 0.f;
-        for (int p = threadIdx.x; p < np; p += 256) {
+        for (int p = threadIdx.x; p < np; p += NT) {
             const f32x4 t = v[p];
             ss += t.x * t.x;
             ss += t.y * t.y;
             ss += t.z * t.z;
             ss += t.w * t.w;
         }
-        ss = block_sum256(ss, red4);
+        ss = block_sum<NT / 64>(ss, red);
         inv = 1.0f / sqrtf(ss / (float)K + a.pro_eps);
     }
     const bool write_out = a.pro_out && blockIdx.x == 0 &&
                            (a.pro == PRO_RESNORM || a.pro == PRO_RMSNORM);
-    for (int p = threadIdx.x; p < np; p += 256) {
+    for (int p = threadIdx.x; p < np; p += NT) {
         f32x4 r;
         if (a.pro == PRO_X) {
             r = xin[p];
@@ -698,9 +702,13 @@ inline size_t v4_lds_bytes(int fmt, int K, int U) {
     return b;
 }
 
-template <int FMT, int ROWS, int U>
-__global__ __launch_bounds__(256) void gemv_v4_kernel(GemvArgs a) {
+template <int FMT, int ROWS, int U, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_v4_kernel(GemvArgs a) {
     extern __shared__ f32x4 xs[];
+    constexpr int NT = 64 * NW;               // threads per block
+    constexpr int PR = 1024 / NT;             // register staging: 16-byte pieces per thread (K <= 4096)
+    constexpr int PP = 3072 / NT;             // plain staging: pieces per thread (K <= 12288)
+    static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves per block");
     constexpr int EPC = WT<FMT>::EPC;
     constexpr int PPC = EPC / 4;
     constexpr int STEP = 64 * U;
@@ -715,8 +723,8 @@ __global__ __launch_bounds__(256) void gemv_v4_kernel(GemvArgs a) {
     const char* Wb = static_cast<const char*>(a.w);
     const int SEQ = (ROWS == 1 && a.epi == EPI_SILU_MUL) ? 2 : 1;
     const int n_groups = ((M + ROWS - 1) / ROWS + SEQ - 1) / SEQ;
-    const int S = gridDim.x * 4;
-    const int g0 = blockIdx.x * 4 + wave;
+    const int S = gridDim.x * NW;
+    const int g0 = blockIdx.x * NW + wave;
     const int my_groups = g0 < n_groups ? (n_groups - 1 - g0) / S + 1 : 0;
     const int total = my_groups * SEQ * iters;
     // int4 block-scale indexing inside a row (K % block == 0, block = 32 * 2^sh):
@@ -775,44 +783,44 @@ __global__ __launch_bounds__(256) void gemv_v4_kernel(GemvArgs a) {
     const int kind = stage_kind(a, K);
     if constexpr (FMT == WF_I4) {
         if (kind == STAGE_REGS) {
-            XRegs<4> r;
-            stage_regs_issue_buf<4>(a, r, K);
+            XRegs<PR> r;
+            stage_regs_issue_buf<PR, NT>(a, r, K);
             __builtin_amdgcn_sched_barrier(0);
             load(cl, bufA, sA);
-            stage_regs_finish<true, 4>(a, r, xs, K);
+            stage_regs_finish<true, PR, NT>(a, r, xs, K);
         } else if (kind == STAGE_PLAIN) {
-            f32x4 xv[12];
-            stage_plain_issue<12>(a, xv, K);
+            f32x4 xv[PP];
+            stage_plain_issue<PP, NT>(a, xv, K);
             __builtin_amdgcn_sched_barrier(0);
             load(cl, bufA, sA);
-            stage_plain_finish<true, 12>(xv, xs, K);
+            stage_plain_finish<true, PP, NT>(xv, xs, K);
         } else {
             load(cl, bufA, sA);
-            stage_x_loop<true>(a, xs, K);
+            stage_x_loop<true, NT>(a, xs, K);
         }
     } else {
         load(cl, bufA, sA);
         if (kind == STAGE_REGS) {
-            XRegs<4> r;
-            stage_regs_issue<4>(a, r, K);
-            stage_regs_finish<true, 4>(a, r, xs, K);
+            XRegs<PR> r;
+            stage_regs_issue<PR, NT>(a, r, K);
+            stage_regs_finish<true, PR, NT>(a, r, xs, K);
         } else if (kind == STAGE_PLAIN) {
-            f32x4 xv[12];
-            stage_plain_issue<12>(a, xv, K);
-            stage_plain_finish<true, 12>(xv, xs, K);
+            f32x4 xv[PP];
+            stage_plain_issue<PP, NT>(a, xv, K);
+            stage_plain_finish<true, PP, NT>(xv, xs, K);
         } else {
-            stage_x_loop<true>(a, xs, K);
+            stage_x_loop<true, NT>(a, xs, K);
         }
     }
     advance(cl);
     const int np = K >> 2;
     const int np_all = iters * STEP * PPC;
-    for (int p = np + (int)threadIdx.x; p < np_all; p += 256) xs[xpad(p)] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int p = np + (int)threadIdx.x; p < np_all; p += NT) xs[xpad(p)] = f32x4{0.f, 0.f, 0.f, 0.f};
     float* corr = nullptr;
     if constexpr (FMT == WF_I4) {
         __syncthreads();
         corr = reinterpret_cast<float*>(xs + (np_all + (np_all + 15) / 16));
-        for (int c = threadIdx.x; c < iters * STEP; c += 256) {
+        for (int c = threadIdx.x; c < iters * STEP; c += NT) {
             const int b = xpad(c * PPC);
             float se = 0.f, so = 0.f;
 #pragma unroll
@@ -922,7 +930,7 @@ __global__ __launch_bounds__(256) void gemv_v4_kernel(GemvArgs a) {
         compute(cc, bufB, sB);
         advance(cc);
     }
-    if (a.epi == EPI_ARGMAX && lane == 0) a.arg_part[blockIdx.x * 4 + wave] = best;
+    if (a.epi == EPI_ARGMAX && lane == 0) a.arg_part[blockIdx.x * NW + wave] = best;
 }
 
 // Any-shape fallback (K not a multiple of the chunk width, tiny matrices):
@@ -1002,9 +1010,9 @@ int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m,
 // ---------------------------------------------------------------------------
 
 // Allow `kern` up to 160 KB of dynamic LDS (once per kernel) and return the
-// blocks of it (256 threads, `lds` dynamic LDS bytes) one CU holds at once;
-// cached per (kernel, LDS size).
-static int resident_per_cu(const void* kern, size_t lds) {
+// blocks of it (`threads` threads, `lds` dynamic LDS bytes) one CU holds at
+// once; cached per (kernel, LDS size).
+static int resident_per_cu(const void* kern, size_t lds, int threads = 256) {
     struct Entry { const void* k; size_t lds; int n; };
     static std::mutex mu;
     static Entry cache[64];
@@ -1027,7 +1035,7 @@ static int resident_per_cu(const void* kern, size_t lds) {
         }
     }
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, lds) != hipSuccess) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) != hipSuccess) {
         (void)hipGetLastError();
         return 0;
     }
@@ -1035,13 +1043,13 @@ static int resident_per_cu(const void* kern, size_t lds) {
     return n;
 }
 
-// Persistent grid of the LDS-staged kernel: every block resident at once
-// (LDS and register occupancy bound the blocks per CU), at most
-// blocks_per_cu of them per CU.  0 if the kernel cannot run at this K.
-static int n1_blocks(const void* kern, int M, size_t lds, int rows, int blocks_per_cu) {
+// Persistent grid of the LDS-staged kernel (nw waves per block): every block
+// resident at once (LDS and register occupancy bound the blocks per CU), at
+// most blocks_per_cu of them per CU.  0 if the kernel cannot run at this K.
+static int n1_blocks(const void* kern, int M, size_t lds, int rows, int blocks_per_cu, int nw = 4) {
     const int n_groups = (M + rows - 1) / rows;
-    const int blocks = (n_groups + 3) / 4;
-    const int fit = resident_per_cu(kern, lds);
+    const int blocks = (n_groups + nw - 1) / nw;
+    const int fit = resident_per_cu(kern, lds, 64 * nw);
     if (fit < 1) return 0;
     const int bpc = blocks_per_cu < fit ? blocks_per_cu : fit;
     const int cap = bpc * device_cu_count();
@@ -1081,7 +1089,7 @@ int gemv_fast_ok(int fmt, int K, int block) {
 // Chosen by sweeping the 7B decode shapes on MI355X over >= 1.1 GB of
 // rotating weights (rows = 1 wins at K = 4096: more waves in flight per CU;
 // the bf16 W_down, 4096 x 11008 with padded rows, prefers two-row waves).
-struct N1Shape { int rows, unroll, bpc; };
+struct N1Shape { int rows, unroll, bpc, nw = 4; };
 static N1Shape n1_shape(int fmt, int K, int epi) {
     // SwiGLU epilogue: bf16 and int4 two-row waves hold the (gate, up) pair;
     // int8 one-row waves take the pair in sequence (its two-row variant
@@ -1148,15 +1156,18 @@ static N1Shape v4_shape(int fmt, int M, int K, int epi) {
     }
 }
 
-#define ATLAS_V4_LIST(X)                                                           \
-    X(WF_BF16, 1, 4) X(WF_BF16, 2, 4)                                              \
-    X(WF_I8, 1, 2) X(WF_I8, 1, 4) X(WF_I8, 2, 1) X(WF_I8, 2, 2) X(WF_I8, 2, 4)     \
-    X(WF_I4, 2, 1) X(WF_I4, 4, 1)                                                  \
-    X(WF_F32, 1, 4)
+// (format, rows per wave, unroll, waves per block)
+#ifndef ATLAS_V4_LIST
+#define ATLAS_V4_LIST(X)                                                                  \
+    X(WF_BF16, 1, 4, 4) X(WF_BF16, 2, 4, 4)                                               \
+    X(WF_I8, 1, 2, 4) X(WF_I8, 1, 4, 4) X(WF_I8, 2, 1, 4) X(WF_I8, 2, 2, 4) X(WF_I8, 2, 4, 4) \
+    X(WF_I4, 2, 1, 4) X(WF_I4, 4, 1, 4)                                                   \
+    X(WF_F32, 1, 4, 4)
+#endif
 
-static const void* v4_kernel(int fmt, int rows, int unroll) {
-#define ATLAS_V4_PTR(F, R, U) \
-    if (fmt == F && rows == R && unroll == U) return (const void*)gemv_v4_kernel<F, R, U>;
+static const void* v4_kernel(int fmt, int rows, int unroll, int nw) {
+#define ATLAS_V4_PTR(F, R, U, W) \
+    if (fmt == F && rows == R && unroll == U && nw == W) return (const void*)gemv_v4_kernel<F, R, U, W>;
     ATLAS_V4_LIST(ATLAS_V4_PTR)
 #undef ATLAS_V4_PTR
     return nullptr;
@@ -1168,9 +1179,9 @@ int gemv_waves(const GemvArgs& a_in) {
     gemv_fill_int4_index(a);
     const N1Shape v4 = v4_shape(a.fmt, a.M, a.K, a.epi);
     if (v4_ok(a, v4.unroll)) {
-        const void* kern = v4_kernel(a.fmt, v4.rows, v4.unroll);
-        return kern ? 4 * n1_blocks(kern, a.M, v4_lds_bytes(a.fmt, a.K, v4.unroll),
-                                    n1_group_rows(a, v4.rows), v4.bpc)
+        const void* kern = v4_kernel(a.fmt, v4.rows, v4.unroll, v4.nw);
+        return kern ? v4.nw * n1_blocks(kern, a.M, v4_lds_bytes(a.fmt, a.K, v4.unroll),
+                                        n1_group_rows(a, v4.rows), v4.bpc, v4.nw)
                     : 0;
     }
     const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
@@ -1179,15 +1190,16 @@ int gemv_waves(const GemvArgs& a_in) {
                 : 0;
 }
 
-template <int FMT, int ROWS, int UNROLL>
+template <int FMT, int ROWS, int UNROLL, int NW>
 int launch_v4(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
     const size_t lds = v4_lds_bytes(FMT, a.K, UNROLL);
-    auto kern = gemv_v4_kernel<FMT, ROWS, UNROLL>;
-    const int blocks = n1_blocks((const void*)kern, a.M, lds, n1_group_rows(a, ROWS), blocks_per_cu);
+    auto kern = gemv_v4_kernel<FMT, ROWS, UNROLL, NW>;
+    const int blocks =
+        n1_blocks((const void*)kern, a.M, lds, n1_group_rows(a, ROWS), blocks_per_cu, NW);
     ATLAS_REQUIRE(blocks > 0, "gemv: the kernel does not fit a CU at K=%d", a.K);
     if (a.epi == EPI_ARGMAX)
-        ATLAS_REQUIRE(blocks * 4 <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a);
+        ATLAS_REQUIRE(blocks * NW <= GEMV_MAX_WAVES, "gemv: too many waves for argmax partials");
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * NW), lds, st, a);
     ATLAS_LAUNCH_CHECK("gemv_v4");
     return ATLAS_OK;
 }
@@ -1220,8 +1232,9 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     if (fast) {
         const N1Shape v4 = v4_shape(a.fmt, a.M, a.K, a.epi);
         if (v4_ok(a, v4.unroll)) {
-#define ATLAS_V4(F, R, U) \
-            if (a.fmt == F && v4.rows == R && v4.unroll == U) return launch_v4<F, R, U>(a, st, v4.bpc);
+#define ATLAS_V4(F, R, U, W) \
+            if (a.fmt == F && v4.rows == R && v4.unroll == U && v4.nw == W) \
+                return launch_v4<F, R, U, W>(a, st, v4.bpc);
             ATLAS_V4_LIST(ATLAS_V4)
 #undef ATLAS_V4
         }
@@ -1345,35 +1358,28 @@ __global__ __launch_bounds__(256) void stream_floor_kernel(const char* __restric
     if (lane == 0) sink[blockIdx.x * 4 + wave] = acc;
 }
 
-int stream_floor_bench(const void* buf, long buf_bytes, long bytes_per_launch, int launches,
-                       int blocks_per_cu, float* us_per_launch, hipStream_t st) {
-    ATLAS_REQUIRE(buf && us_per_launch && launches > 0 && blocks_per_cu > 0,
-                  "stream_floor: bad arguments");
-    ATLAS_REQUIRE(bytes_per_launch >= 16384 && bytes_per_launch % 16384 == 0 &&
-                  bytes_per_launch <= buf_bytes, "stream_floor: %ld bytes per launch", bytes_per_launch);
-    ATLAS_REQUIRE(((uintptr_t)buf & 15) == 0, "stream_floor: 16-byte alignment");
-    const int blocks = blocks_per_cu * device_cu_count();
-    // captured and replayed on a stream of its own (the caller's may be the
-    // legacy default stream, which cannot be captured), after the caller's work
-    ATLAS_HIP(hipStreamSynchronize(st));
-    ATLAS_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
-    float* sink = nullptr;
-    if (dev_malloc(&sink, (size_t)blocks * 4 * sizeof(float)) != hipSuccess) {
-        (void)hipGetLastError();
-        (void)hipStreamDestroy(st);
-        set_error(ATLAS_ENOMEM, "stream_floor: sink allocation");
-        return ATLAS_ENOMEM;
-    }
-    const long per = buf_bytes / bytes_per_launch;
+__global__ __launch_bounds__(256) void empty_launch_kernel(float* __restrict__ sink, int never) {
+    if (never == 1) sink[blockIdx.x] = 0.f;   // the host passes 0: no work, no memory access
+}
+
+// Best replay time (ms) of a graph of `n` floor launches (empty kernels when
+// bytes_per_launch is 0) on stream st.
+static int floor_graph_ms(const void* buf, long buf_bytes, long bytes_per_launch, int n, int blocks,
+                          float* sink, hipStream_t st, float* best_ms) {
+    const long per = bytes_per_launch > 0 ? buf_bytes / bytes_per_launch : 1;
     hipGraph_t g = nullptr;
     hipGraphExec_t gx = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     int rc = ATLAS_OK;
     if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) rc = ATLAS_EHIP;
-    for (int k = 0; rc == ATLAS_OK && k < launches; ++k)
-        hipLaunchKernelGGL(stream_floor_kernel, dim3(blocks), dim3(256), 0, st,
-                           static_cast<const char*>(buf) + (k % per) * bytes_per_launch, bytes_per_launch,
-                           sink);
+    for (int k = 0; rc == ATLAS_OK && k < n; ++k) {
+        if (bytes_per_launch > 0)
+            hipLaunchKernelGGL(stream_floor_kernel, dim3(blocks), dim3(256), 0, st,
+                               static_cast<const char*>(buf) + (k % per) * bytes_per_launch,
+                               bytes_per_launch, sink);
+        else
+            hipLaunchKernelGGL(empty_launch_kernel, dim3(blocks), dim3(256), 0, st, sink, 0);
+    }
     if (rc == ATLAS_OK && hipStreamEndCapture(st, &g) != hipSuccess) rc = ATLAS_EHIP;
     if (rc == ATLAS_OK && hipGraphInstantiate(&gx, g, nullptr, nullptr, 0) != hipSuccess) rc = ATLAS_EHIP;
     if (rc == ATLAS_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
@@ -1389,18 +1395,49 @@ int stream_floor_bench(const void* buf, long buf_bytes, long bytes_per_launch, i
         }
         if (rep == 1 || (rep > 1 && ms < best)) best = ms;   // replay 0 warms up
     }
-    if (rc != ATLAS_OK) {
-        (void)hipGetLastError();
-        set_error(ATLAS_EHIP, "stream_floor: graph capture or replay failed");
-    }
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     if (gx) (void)hipGraphExecDestroy(gx);
     if (g) (void)hipGraphDestroy(g);
+    *best_ms = best;
+    return rc;
+}
+
+int stream_floor_bench(const void* buf, long buf_bytes, long bytes_per_launch, int launches,
+                       int blocks_per_cu, float* us_per_launch, hipStream_t st) {
+    ATLAS_REQUIRE(us_per_launch && launches > 0 && blocks_per_cu > 0, "stream_floor: bad arguments");
+    ATLAS_REQUIRE(bytes_per_launch == 0 || (buf && bytes_per_launch >= 16384 &&
+                                            bytes_per_launch % 16384 == 0 &&
+                                            bytes_per_launch <= buf_bytes),
+                  "stream_floor: %ld bytes per launch", bytes_per_launch);
+    ATLAS_REQUIRE(((uintptr_t)buf & 15) == 0, "stream_floor: 16-byte alignment");
+    const int blocks = blocks_per_cu * device_cu_count();
+    // captured and replayed on a stream of its own (the caller's may be the
+    // legacy default stream, which cannot be captured), after the caller's work
+    ATLAS_HIP(hipStreamSynchronize(st));
+    ATLAS_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    float* sink = nullptr;
+    if (dev_malloc(&sink, (size_t)blocks * 4 * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipStreamDestroy(st);
+        set_error(ATLAS_ENOMEM, "stream_floor: sink allocation");
+        return ATLAS_ENOMEM;
+    }
+    // graphs of n and 2n launches: the difference is n launches without the
+    // graph launch's own fixed cost (~10 us, which a short graph would spread
+    // over few launches)
+    float t1 = 0.f, t2 = 0.f;
+    int rc = floor_graph_ms(buf, buf_bytes, bytes_per_launch, launches, blocks, sink, st, &t1);
+    if (rc == ATLAS_OK)
+        rc = floor_graph_ms(buf, buf_bytes, bytes_per_launch, 2 * launches, blocks, sink, st, &t2);
+    if (rc != ATLAS_OK) {
+        (void)hipGetLastError();
+        set_error(ATLAS_EHIP, "stream_floor: graph capture or replay failed");
+    }
     (void)hipStreamSynchronize(st);
     (void)hipFree(sink);
     (void)hipStreamDestroy(st);
-    *us_per_launch = best * 1e3f / launches;
+    *us_per_launch = (t2 - t1) * 1e3f / launches;
     return rc;
 }
 

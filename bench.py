@@ -337,6 +337,48 @@ def stream_floor(lib, m) -> dict:
     return out
 
 
+def launch_floor(lib) -> dict:
+    """What any launch costs in a graph of back-to-back launches on this part,
+    before GEMV work: an empty kernel of a decode GEMV's grid, and read-only
+    launches with the GEMV's work split at 10.5-180 MB, with a line fitted
+    through the sizes from 33.6 MB (fixed microseconds + bytes / streaming
+    rate).  A single launch of B bytes can reach at most B / floor(B) of HBM
+    bandwidth; the 75% target needs launches of about 80 MB or more."""
+    if not _FLOOR_BUF:
+        p = C.c_void_p()
+        nbytes = 2 << 30
+        assert lib.atlas_dev_malloc_sync(C.byref(p), nbytes) == 0
+        assert lib.atlas_fill_random(2, p.value, nbytes // 4, 11, 0.0, 1.0) == 0
+        _FLOOR_BUF.extend([p.value, nbytes])
+    buf, nbytes = _FLOOR_BUF
+    us = C.c_float()
+    empty = None
+    for bpc in (2, 4):
+        assert lib.atlas_bench_stream_floor(None, 0, 0, 64, bpc, C.byref(us)) == 0, lib.atlas_last_error()
+        empty = us.value if empty is None else min(empty, us.value)
+    sizes = (10518528, 33587200, 100728832, 180355072)
+    pts = []
+    for size in sizes:
+        best = None
+        for bpc in (2, 3, 4):
+            assert lib.atlas_bench_stream_floor(C.c_void_p(buf), nbytes, size, 16, bpc, C.byref(us)) == 0, \
+                lib.atlas_last_error()
+            best = us.value if best is None else min(best, us.value)
+        pts.append((size, best))
+    xs = np.array([p[0] for p in pts if p[0] >= 30e6], dtype=np.float64)
+    ys = np.array([p[1] for p in pts if p[0] >= 30e6], dtype=np.float64)
+    slope, fixed = np.polyfit(xs, ys, 1)        # us per byte, us
+    out = {"empty_kernel_us": round(empty, 3),
+           "fit": {"fixed_us": round(float(fixed), 3), "stream_TB_s": round(1e-6 / float(slope), 3),
+                   "from_MB": [round(x / 1e6, 2) for x in xs]},
+           "by_size": {f"{s / 1e6:.2f}MB": {"us": round(t, 3), "GB_s": round(s / t / 1e3, 1),
+                                            "max_frac_of_peak": round(s / t / 1e3 / HBM_PEAK_GBS, 3)}
+                       for s, t in pts}}
+    log(f"launch floor: empty kernel {empty:.2f} us; read floor {fixed:.2f} us + bytes / "
+        f"{1e-6 / slope:.2f} TB/s; " + ", ".join(f"{s / 1e6:.1f} MB {t:.2f} us" for s, t in pts))
+    return out
+
+
 def step_spread(step_ms) -> dict:
     """Median and p10/p90 of the per-step GPU times (HIP events recorded on
     the engine stream after every step of a second run over the timed run's
@@ -502,6 +544,7 @@ def main() -> int:
     step_floor_ms = step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
 
     floor = {"bf16": stream_floor(lib, m)}
+    lfloor = launch_floor(lib)
     rates = generate_rates(m, am)
     # bench the GPU CPU-baseline inputs before freeing the model
     cpu = None
@@ -558,6 +601,7 @@ def main() -> int:
                      "us_per_launch": dom["us_per_launch"]},
         "gemv_kernels": kernels,
         "gemv_vs_stream_floor": floor,
+        "launch_floor": lfloor,
         "step_spread": SPREAD.get(am.W_BF16),
         "generate_rates": rates,
         "step_roofline": {"bytes_per_step": int(step_bytes),

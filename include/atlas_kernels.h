@@ -268,12 +268,15 @@ int atlas_quantize_int4_host(const float* w, int64_t rows, int64_t cols, int64_t
 int atlas_fill_random(int kind, void* out, int64_t n, uint64_t seed, float a, float b);
 
 /* Measurement only (no reference counterpart): the streaming floor of a
- * decode-GEMV-shaped launch.  Captures `launches` read-only launches of
+ * decode-GEMV-shaped launch.  Captures read-only launches of
  * bytes_per_launch bytes each (consecutive regions of buf, wrapping; a
  * multiple of 16 KiB, the bf16 decode GEMV's work split and load pattern,
- * blocks_per_cu 4-wave blocks per CU) in one HIP graph on the library's
- * stream, replays it and stores the best per-launch time in microseconds.
- * What the decode GEMVs cost beyond it is their own work.                    */
+ * blocks_per_cu 4-wave blocks per CU) in HIP graphs of `launches` and
+ * 2 * `launches` kernels on the library's stream, replays them and stores
+ * the difference of the best replay times per launch in microseconds (the
+ * graph launch's own cost cancels).  bytes_per_launch 0 times an empty
+ * kernel of the same grid (buf may be null): the launch floor itself.
+ * What the decode GEMVs cost beyond the streaming floor is their own work. */
 int atlas_bench_stream_floor(const void* buf, int64_t buf_bytes, int64_t bytes_per_launch,
                              int launches, int blocks_per_cu, float* us_per_launch);
 

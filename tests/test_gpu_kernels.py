@@ -734,7 +734,12 @@ def test_bench_stream_floor_runs_and_rejects_bad_sizes():
     # 4 MiB at 8 TB/s would be 0.5 us; a launch also pays its fixed cost
     assert 0.5 < us.value < 1000.0, us.value
     assert lib().atlas_last_error_code() == 0, lib().atlas_last_error()
-    for nbytes in (4 << 20 | 4096, 0, 32 << 20):         # not whole 16 KiB groups, empty, past the buffer
+    # 0 bytes: an empty kernel of the same grid (the launch floor), cheaper
+    # than a launch that streams 4 MiB; buf may be null
+    empty = C.c_float(-1.0)
+    assert lib().atlas_bench_stream_floor(None, 0, 0, 8, 2, C.byref(empty)) == 0
+    assert 0.0 < empty.value < us.value, (empty.value, us.value)
+    for nbytes in (4 << 20 | 4096, 32 << 20):            # not whole 16 KiB groups, past the buffer
         assert lib().atlas_bench_stream_floor(C.c_void_p(buf.ptr), 16 << 20, nbytes, 8, 2,
                                               C.byref(us)) < 0, nbytes
     assert lib().atlas_bench_stream_floor(C.c_void_p(buf.ptr), 16 << 20, 4 << 20, 0, 2,
