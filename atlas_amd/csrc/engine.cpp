@@ -445,14 +445,21 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
         TRY(enqueue_gu_fused(m, L));
         TRY(enqueue_down_fused(m, L));
     }
-    // x_L = x'_{L-1} + rmsnorm(y2) * ffn_norm_{L-1}, in place in xb
-    TRY(residual_rmsnorm_launch(m->xb, m->y2, m->L[c.n_layers - 1].ffn_norm, d, 1, d, eps, m->st));
-    if (mode == 3)
-        TRY(ew_launch(EW_COPY, m->xb, nullptr, m->hook_dev + (size_t)(c.n_layers - 1) * d, 0.f, d,
-                      m->st));
+    // lm_head with the last layer's residual and the final norm in its prologue:
+    // x_L = x'_{L-1} + rmsnorm(y2) * ffn_norm_{L-1} (into the hook's last slot in
+    // mode 3), logits = W_lm rmsnorm(x_L) * final_norm.  Shapes the decode GEMV
+    // does not cover keep a residual launch and the final norm prologue.
     const bool penalties = m->g_nsup > 0 || m->g_theta != 1.0f;
-    GemvArgs h = pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm, eps,
-                          m->xn);
+    float* hook_last = mode == 3 ? m->hook_dev + (size_t)(c.n_layers - 1) * d : nullptr;
+    GemvArgs h = pro_args(m->lm_head, m->xb, m->logits, PRO_RESNORM_NORM, m->y2,
+                          m->L[c.n_layers - 1].ffn_norm, eps, hook_last);
+    h.pro_w2 = m->final_norm;
+    if (!gemv_resnorm_norm_ok(h)) {
+        TRY(residual_rmsnorm_launch(m->xb, m->y2, m->L[c.n_layers - 1].ffn_norm, d, 1, d, eps,
+                                    m->st));
+        if (hook_last) TRY(ew_launch(EW_COPY, m->xb, nullptr, hook_last, 0.f, d, m->st));
+        h = pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm, eps, m->xn);
+    }
     const bool fused_choice = mode == 1 && !penalties;
     if (fused_choice) {
         h.epi = EPI_ARGMAX;
@@ -1954,8 +1961,15 @@ ATLAS_API int atlas_model_bench_gemv(atlas_model* m, int iters, int which, float
             }
         }
         if (lm_set) {
-            if (m->fused)
-                TRY(gemv_launch(pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm, eps, m->xn), m->st));
+            if (m->fused) {
+                GemvArgs h = pro_args(m->lm_head, m->xb, m->logits, PRO_RESNORM_NORM, m->y2,
+                                      m->L.back().ffn_norm, eps, nullptr);
+                h.pro_w2 = m->final_norm;
+                if (!gemv_resnorm_norm_ok(h))
+                    h = pro_args(m->lm_head, m->xb, m->logits, PRO_RMSNORM, nullptr, m->final_norm,
+                                 eps, m->xn);
+                TRY(gemv_launch(h, m->st));
+            }
             else
                 TRY(gemv(m, m->lm_head, m->xn, m->logits, EPI_STORE));
         }

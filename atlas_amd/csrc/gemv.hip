@@ -123,13 +123,14 @@ template <int PPT>
 struct XRegs { f32x4 x[PPT], y[PPT], w[PPT]; };
 
 // guarded loads: only the vectors the prologue uses, only pieces below K
-template <int PPT, int NT = 256>
+template <int PPT, int NT = 256, bool N2 = false>
 __device__ __forceinline__ void stage_regs_issue(const GemvArgs& a, XRegs<PPT>& r, int K) {
     const int np = K >> 2;
     const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
     const f32x4* yin = reinterpret_cast<const f32x4*>(a.pro_y);
     const f32x4* win = reinterpret_cast<const f32x4*>(a.pro_w);
-    const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
+    const bool norm2 = N2 && a.pro == PRO_RESNORM_NORM;
+    const bool res = a.pro == PRO_RESNORM || norm2, norm = res || a.pro == PRO_RMSNORM;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
         const int p = threadIdx.x + NT * j;
@@ -146,9 +147,10 @@ __device__ __forceinline__ void stage_regs_issue(const GemvArgs& a, XRegs<PPT>& 
 // K.  Guarded loads split the issue into branches, after which the compiler
 // waits for every load in flight, including weight loads issued between
 // the two halves.
-template <int PPT, int NT = 256>
+template <int PPT, int NT = 256, bool N2 = false>
 __device__ __forceinline__ void stage_regs_issue_buf(const GemvArgs& a, XRegs<PPT>& r, int K) {
-    const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
+    const bool norm2 = N2 && a.pro == PRO_RESNORM_NORM;
+    const bool res = a.pro == PRO_RESNORM || norm2, norm = res || a.pro == PRO_RMSNORM;
     const __amdgpu_buffer_rsrc_t xb =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.x), (short)0, K * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t yb = __builtin_amdgcn_make_buffer_rsrc(
@@ -164,12 +166,13 @@ __device__ __forceinline__ void stage_regs_issue_buf(const GemvArgs& a, XRegs<PP
     }
 }
 
-template <bool SWZ, int PPT, int NT = 256>
+template <bool SWZ, int PPT, int NT = 256, bool N2 = false>
 __device__ __forceinline__ void stage_regs_finish(const GemvArgs& a, XRegs<PPT>& r, f32x4* xs,
                                                   int K) {
-    __shared__ float red[NT / 64];
+    __shared__ float red[NT / 64], red2[NT / 64];
     const int np = K >> 2;
-    const bool res = a.pro == PRO_RESNORM, norm = res || a.pro == PRO_RMSNORM;
+    const bool norm2 = N2 && a.pro == PRO_RESNORM_NORM;
+    const bool res = a.pro == PRO_RESNORM || norm2, norm = res || a.pro == PRO_RMSNORM;
     const f32x4 (&xv)[PPT] = r.x;
     const f32x4 (&yv)[PPT] = r.y;
     const f32x4 (&wv)[PPT] = r.w;
@@ -190,16 +193,48 @@ __device__ __forceinline__ void stage_regs_finish(const GemvArgs& a, XRegs<PPT>&
         inv = 1.0f / sqrtf(ss / (float)K + a.pro_eps);
     }
     const bool write_out = a.pro_out && blockIdx.x == 0 && norm;
+    f32x4 v[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+        if (res) v[j] = xv[j] + (yv[j] * inv) * wv[j];
+        else if (norm) v[j] = (xv[j] * inv) * wv[j];
+        else v[j] = xv[j];
+    }
+    // RESNORM_NORM: the final norm of the residual-updated h (second reduction).
+    // Its weight is loaded only now, into registers the first norm's inputs
+    // have freed: loaded with them, it cost the kernel a block per CU of
+    // occupancy (+16 VGPRs), more than this round trip costs the one launch.
+    float inv2 = 1.0f;
+    f32x4 w2[N2 ? PPT : 1];
+    if constexpr (N2) {
+        const __amdgpu_buffer_rsrc_t w2b = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr(norm2 ? a.pro_w2 : a.x), (short)0, norm2 ? K * 4 : 0, 0x00020000);
+#pragma unroll
+        for (int j = 0; j < PPT; ++j)
+            w2[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  w2b, (int)threadIdx.x * 16, NT * 16 * j, 0));
+    }
+    if constexpr (N2) if (norm2) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) {
+            if (threadIdx.x + NT * j < np) {
+                ss += v[j].x * v[j].x;
+                ss += v[j].y * v[j].y;
+                ss += v[j].z * v[j].z;
+                ss += v[j].w * v[j].w;
+            }
+        }
+        ss = block_sum<NT / 64>(ss, red2);
+        inv2 = 1.0f / sqrtf(ss / (float)K + a.pro_eps);
+    }
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
         const int p = threadIdx.x + NT * j;
         if (p < np) {
-            f32x4 v;
-            if (res) v = xv[j] + (yv[j] * inv) * wv[j];
-            else if (norm) v = (xv[j] * inv) * wv[j];
-            else v = xv[j];
-            xs[SWZ ? xpad(p) : p] = v;
-            if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = v;
+            if constexpr (N2) xs[SWZ ? xpad(p) : p] = norm2 ? (v[j] * inv2) * w2[j] : v[j];
+            else xs[SWZ ? xpad(p) : p] = v[j];
+            if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = v[j];
         }
     }
 }
@@ -239,14 +274,16 @@ __device__ __forceinline__ int stage_kind(const GemvArgs& a, int K) {
 }
 
 // Looped staging: any K the LDS holds, and the SwiGLU prologue.
-template <bool SWZ, int NT = 256>
+template <bool SWZ, int NT = 256, bool N2 = false>
 __device__ __forceinline__ void stage_x_loop(const GemvArgs& a, f32x4* xs, int K) {
-    __shared__ float red[NT / 64];
+    __shared__ float red[NT / 64], red2[NT / 64];
     const int np = K >> 2;
     const f32x4* xin = reinterpret_cast<const f32x4*>(a.x);
+    const bool norm2 = N2 && a.pro == PRO_RESNORM_NORM;
+    const bool res = a.pro == PRO_RESNORM || norm2;
     float inv = 1.0f;
-    if (a.pro == PRO_RESNORM || a.pro == PRO_RMSNORM) {
-        const f32x4* v = reinterpret_cast<const f32x4*>(a.pro == PRO_RESNORM ? a.pro_y : a.x);
+    if (res || a.pro == PRO_RMSNORM) {
+        const f32x4* v = reinterpret_cast<const f32x4*>(res ? a.pro_y : a.x);
         float ss = 0.f;
         for (int p = threadIdx.x; p < np; p += NT) {
             const f32x4 t = v[p];
@@ -258,13 +295,13 @@ __device__ __forceinline__ void stage_x_loop(const GemvArgs& a, f32x4* xs, int K
         ss = block_sum<NT / 64>(ss, red);
         inv = 1.0f / sqrtf(ss / (float)K + a.pro_eps);
     }
-    const bool write_out = a.pro_out && blockIdx.x == 0 &&
-                           (a.pro == PRO_RESNORM || a.pro == PRO_RMSNORM);
+    const bool write_out = a.pro_out && blockIdx.x == 0 && (res || a.pro == PRO_RMSNORM);
+    float ss2 = 0.f;
     for (int p = threadIdx.x; p < np; p += NT) {
         f32x4 r;
         if (a.pro == PRO_X) {
             r = xin[p];
-        } else if (a.pro == PRO_RESNORM) {
+        } else if (res) {
             const f32x4 yi = reinterpret_cast<const f32x4*>(a.pro_y)[p];
             const f32x4 wi = reinterpret_cast<const f32x4*>(a.pro_w)[p];
             r = xin[p] + (yi * inv) * wi;
@@ -279,6 +316,15 @@ __device__ __forceinline__ void stage_x_loop(const GemvArgs& a, f32x4* xs, int K
         }
         xs[SWZ ? xpad(p) : p] = r;
         if (write_out) reinterpret_cast<f32x4*>(a.pro_out)[p] = r;
+        if (norm2) ss2 += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
+    }
+    if (norm2) {
+        // the final norm of h, over the pieces this thread staged
+        ss2 = block_sum<NT / 64>(ss2, red2);
+        const float inv2 = 1.0f / sqrtf(ss2 / (float)K + a.pro_eps);
+        for (int p = threadIdx.x; p < np; p += NT)
+            xs[SWZ ? xpad(p) : p] = (xs[SWZ ? xpad(p) : p] * inv2) *
+                                    reinterpret_cast<const f32x4*>(a.pro_w2)[p];
     }
 }
 
@@ -702,7 +748,7 @@ inline size_t v4_lds_bytes(int fmt, int K, int U) {
     return b;
 }
 
-template <int FMT, int ROWS, int U, int NW>
+template <int FMT, int ROWS, int U, int NW, bool N2>
 __global__ __launch_bounds__(64 * NW) void gemv_v4_kernel(GemvArgs a) {
     extern __shared__ f32x4 xs[];
     constexpr int NT = 64 * NW;               // threads per block
@@ -784,10 +830,10 @@ __global__ __launch_bounds__(64 * NW) void gemv_v4_kernel(GemvArgs a) {
     if constexpr (FMT == WF_I4) {
         if (kind == STAGE_REGS) {
             XRegs<PR> r;
-            stage_regs_issue_buf<PR, NT>(a, r, K);
+            stage_regs_issue_buf<PR, NT, N2>(a, r, K);
             __builtin_amdgcn_sched_barrier(0);
             load(cl, bufA, sA);
-            stage_regs_finish<true, PR, NT>(a, r, xs, K);
+            stage_regs_finish<true, PR, NT, N2>(a, r, xs, K);
         } else if (kind == STAGE_PLAIN) {
             f32x4 xv[PP];
             stage_plain_issue<PP, NT>(a, xv, K);
@@ -796,20 +842,20 @@ __global__ __launch_bounds__(64 * NW) void gemv_v4_kernel(GemvArgs a) {
             stage_plain_finish<true, PP, NT>(xv, xs, K);
         } else {
             load(cl, bufA, sA);
-            stage_x_loop<true, NT>(a, xs, K);
+            stage_x_loop<true, NT, N2>(a, xs, K);
         }
     } else {
         load(cl, bufA, sA);
         if (kind == STAGE_REGS) {
             XRegs<PR> r;
-            stage_regs_issue<PR, NT>(a, r, K);
-            stage_regs_finish<true, PR, NT>(a, r, xs, K);
+            stage_regs_issue<PR, NT, N2>(a, r, K);
+            stage_regs_finish<true, PR, NT, N2>(a, r, xs, K);
         } else if (kind == STAGE_PLAIN) {
             f32x4 xv[PP];
             stage_plain_issue<PP, NT>(a, xv, K);
             stage_plain_finish<true, PP, NT>(xv, xs, K);
         } else {
-            stage_x_loop<true, NT>(a, xs, K);
+            stage_x_loop<true, NT, N2>(a, xs, K);
         }
     }
     advance(cl);
@@ -1165,12 +1211,26 @@ static N1Shape v4_shape(int fmt, int M, int K, int epi) {
     X(WF_F32, 1, 4, 4)
 #endif
 
-static const void* v4_kernel(int fmt, int rows, int unroll, int nw) {
-#define ATLAS_V4_PTR(F, R, U, W) \
-    if (fmt == F && rows == R && unroll == U && nw == W) return (const void*)gemv_v4_kernel<F, R, U, W>;
+static const void* v4_kernel(int fmt, int rows, int unroll, int nw, bool n2) {
+#define ATLAS_V4_PTR(F, R, U, W)                                                            \
+    if (fmt == F && rows == R && unroll == U && nw == W)                                    \
+        return n2 ? (const void*)gemv_v4_kernel<F, R, U, W, true>                           \
+                  : (const void*)gemv_v4_kernel<F, R, U, W, false>;
     ATLAS_V4_LIST(ATLAS_V4_PTR)
 #undef ATLAS_V4_PTR
     return nullptr;
+}
+
+bool gemv_resnorm_norm_ok(const GemvArgs& a_in) {
+    GemvArgs a = a_in;
+    gemv_fill_int4_index(a);
+    const uintptr_t align = (uintptr_t)a.w | (uintptr_t)a.x | (uintptr_t)a.pro_y |
+                            (uintptr_t)a.pro_w | (uintptr_t)a.pro_w2 | (uintptr_t)a.pro_out;
+    if ((align & 15) || a.K % 4 || !gemv_fast_ok(a.fmt, a.K, a.block) ||
+        gemv_x_lds_bytes(a.K) > 160 * 1024)
+        return false;
+    const N1Shape v4 = v4_shape(a.fmt, a.M, a.K, a.epi);
+    return v4_ok(a, v4.unroll) && v4_kernel(a.fmt, v4.rows, v4.unroll, v4.nw, true) != nullptr;
 }
 
 // number of persistent waves gemv_launch uses (argmax partial count)
@@ -1179,7 +1239,7 @@ int gemv_waves(const GemvArgs& a_in) {
     gemv_fill_int4_index(a);
     const N1Shape v4 = v4_shape(a.fmt, a.M, a.K, a.epi);
     if (v4_ok(a, v4.unroll)) {
-        const void* kern = v4_kernel(a.fmt, v4.rows, v4.unroll, v4.nw);
+        const void* kern = v4_kernel(a.fmt, v4.rows, v4.unroll, v4.nw, a.pro == PRO_RESNORM_NORM);
         return kern ? v4.nw * n1_blocks(kern, a.M, v4_lds_bytes(a.fmt, a.K, v4.unroll),
                                         n1_group_rows(a, v4.rows), v4.bpc, v4.nw)
                     : 0;
@@ -1190,10 +1250,10 @@ int gemv_waves(const GemvArgs& a_in) {
                 : 0;
 }
 
-template <int FMT, int ROWS, int UNROLL, int NW>
+template <int FMT, int ROWS, int UNROLL, int NW, bool N2>
 int launch_v4(const GemvArgs& a, hipStream_t st, int blocks_per_cu) {
     const size_t lds = v4_lds_bytes(FMT, a.K, UNROLL);
-    auto kern = gemv_v4_kernel<FMT, ROWS, UNROLL, NW>;
+    auto kern = gemv_v4_kernel<FMT, ROWS, UNROLL, NW, N2>;
     const int blocks =
         n1_blocks((const void*)kern, a.M, lds, n1_group_rows(a, ROWS), blocks_per_cu, NW);
     ATLAS_REQUIRE(blocks > 0, "gemv: the kernel does not fit a CU at K=%d", a.K);
@@ -1213,6 +1273,8 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     ATLAS_REQUIRE(a.pro == PRO_SILU || a.x, "gemv: null x");
     ATLAS_REQUIRE(a.pro != PRO_RESNORM || (a.pro_y && a.pro_w), "gemv: residual norm needs y and w");
     ATLAS_REQUIRE(a.pro != PRO_RMSNORM || a.pro_w, "gemv: rmsnorm prologue needs w");
+    ATLAS_REQUIRE(a.pro != PRO_RESNORM_NORM || (a.pro_y && a.pro_w && a.pro_w2),
+                  "gemv: residual + final norm prologue needs y, w and w2");
     ATLAS_REQUIRE(a.pro != PRO_SILU || a.pro_y, "gemv: silu prologue needs the gate/up pairs");
     ATLAS_REQUIRE(a.pro_out == nullptr || (a.pro_out != a.x && a.pro_out != a.pro_y),
                   "gemv: the materialised x must not alias the prologue inputs");
@@ -1226,18 +1288,21 @@ int gemv_launch(const GemvArgs& a_in, hipStream_t st) {
     }
     ATLAS_REQUIRE(gemv_pitch_ok(a), "gemv: row pitch %ld bytes for K %d", a.ldw, a.K);
     const uintptr_t align = (uintptr_t)a.w | (uintptr_t)a.x | (uintptr_t)a.pro_y |
-                            (uintptr_t)a.pro_w | (uintptr_t)a.pro_out;
+                            (uintptr_t)a.pro_w | (uintptr_t)a.pro_w2 | (uintptr_t)a.pro_out;
     const bool fast = (align & 15) == 0 && a.K % 4 == 0 && gemv_fast_ok(a.fmt, a.K, a.block) &&
                       gemv_x_lds_bytes(a.K) <= 160 * 1024;
     if (fast) {
         const N1Shape v4 = v4_shape(a.fmt, a.M, a.K, a.epi);
         if (v4_ok(a, v4.unroll)) {
-#define ATLAS_V4(F, R, U, W) \
-            if (a.fmt == F && v4.rows == R && v4.unroll == U && v4.nw == W) \
-                return launch_v4<F, R, U, W>(a, st, v4.bpc);
+#define ATLAS_V4(F, R, U, W)                                                          \
+            if (a.fmt == F && v4.rows == R && v4.unroll == U && v4.nw == W)                 \
+                return a.pro == PRO_RESNORM_NORM ? launch_v4<F, R, U, W, true>(a, st, v4.bpc) \
+                                                 : launch_v4<F, R, U, W, false>(a, st, v4.bpc);
             ATLAS_V4_LIST(ATLAS_V4)
 #undef ATLAS_V4
         }
+        ATLAS_REQUIRE(a.pro != PRO_RESNORM_NORM,
+                      "gemv: the residual + final norm prologue needs the decode kernel's shapes");
         const N1Shape sh = n1_shape(a.fmt, a.K, a.epi);
 #define ATLAS_N1(F, R, U) \
         if (a.fmt == F && sh.rows == R && sh.unroll == U) return launch_n1<F, R, U>(a, st, sh.bpc);

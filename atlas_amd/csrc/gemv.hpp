@@ -11,7 +11,9 @@ enum {
     PRO_X = 0,        // x as given
     PRO_RESNORM = 1,  // x = x_in + (y * inv(y)) * w   (post-norm residual; materialised)
     PRO_RMSNORM = 2,  // x = (x_in * inv(x_in)) * w
-    PRO_SILU = 3      // x[k] = silu(y[2k]) * y[2k+1]   (SwiGLU of interleaved gate/up)
+    PRO_SILU = 3,     // x[k] = silu(y[2k]) * y[2k+1]   (SwiGLU of interleaved gate/up)
+    PRO_RESNORM_NORM = 4   // h = x_in + (y * inv(y)) * w; x = (h * inv(h)) * w2 (the last
+                           // layer's residual and the final norm; h materialised)
 };
 
 struct GemvArgs {
@@ -31,9 +33,11 @@ struct GemvArgs {
     int x_vec;               // skinny: x rows 16-byte aligned with x_stride_k == 1
     int pro;                 // PRO_*
     const float* pro_y;      // RESNORM: normalised addend [K]; SILU: pairs [2K]
-    const float* pro_w;      // RESNORM / RMSNORM: norm weight [K]
+    const float* pro_w;      // RESNORM / RMSNORM / RESNORM_NORM: norm weight [K]
+    const float* pro_w2;     // RESNORM_NORM: the second norm's weight [K]
     float pro_eps;
-    float* pro_out;          // RESNORM / RMSNORM: x written out by block 0 (nullable)
+    float* pro_out;          // RESNORM / RMSNORM: x, RESNORM_NORM: h, written out by block 0
+                             // (nullable)
     unsigned long long* arg_part;   // EPI_ARGMAX: per-wave (value, index) keys
     long ldw;                // bytes between weight rows (multiple of 16); 0 = packed rows
     float* partial;          // skinny / prompt GEMM split-K partials (null: the thread's scratch)
@@ -45,6 +49,7 @@ enum { GEMV_MAX_WAVES = 16384 };    // bound on persistent waves (argmax partial
 int gemv_fast_ok(int fmt, int K, int block);
 int gemv_launch(const GemvArgs& a, hipStream_t st);     // N == 1
 int gemv_waves(const GemvArgs& a);                       // persistent waves of gemv_launch
+bool gemv_resnorm_norm_ok(const GemvArgs& a);             // PRO_RESNORM_NORM available for a
 int skinny_launch(const GemvArgs& a, hipStream_t st);   // 1 <= N <= 8
 // N = 2..kGemvMaxNx rows through the batch-1 GEMV (every weight load feeds
 // all N rows); plain x, store / SwiGLU epilogues

@@ -392,6 +392,25 @@ def test_padded_rows_wide_ffn(orc):
         assert b == m2.generate_with_sampling(p, 6, am.SamplingConfig.greedy()), p
 
 
+def test_wide_model_prologue_loops(orc):
+    # d_model 4608 (> 4096): the decode GEMVs stage x through the looped
+    # prologue, including the lm_head's residual + final-norm prologue, and the
+    # hooked step's last hidden state comes out of that prologue
+    cfg = modelgen.olmo3_small_config(n_layers=2, d_model=4608, n_heads=36, n_kv_heads=36,
+                                      ffn_hidden=512, max_seq=32)
+    W = modelgen.make_weights(cfg, seed=41, fmt="bf16")
+    toks = np.random.default_rng(4).integers(0, cfg["vocab"], 6)
+    assert _teacher_forced(W, toks) <= LOGIT_TOL
+    m = modelgen.engine_model(W)
+    o = modelgen.oracle_model(W, threads=4)
+    for t in toks[:3]:
+        lg, hidden = m.forward_one_hidden(int(t))
+        ref_lg, ref = o.forward_one(int(t), hidden=True)
+        assert hidden.shape == ref.shape
+        assert _rel(hidden[-1], ref[-1]) <= LOGIT_TOL
+        assert _rel(lg, ref_lg) <= LOGIT_TOL
+
+
 def test_init_random_weights_roundtrip(orc):
     from atlas_amd import model as am
     cfg = am.ModelConfig(vocab_size=300, d_model=128, n_layers=2, n_heads=2, n_kv_heads=1,
