@@ -3,7 +3,8 @@
 The reference compiles kernels/matmul.cu with nvcc from build.rs
 (crates/atlas-tensor/build.rs:19-107); this is the hipcc equivalent: one
 shared library with the extern "C" ABI of include/atlas_kernels.h and
-include/atlas_engine.h, linked against the HIP runtime only.
+include/atlas_engine.h, linked against the HIP runtime and hipBLASLt (the
+bf16 prompt GEMM of 17..128 rows; every other kernel is hand-written HIP).
 
 Usage: python -m atlas_amd.build   (or atlas_amd.build.build())
 Environment: ATLAS_HIP_ARCH overrides the target (default gfx950).
@@ -22,7 +23,7 @@ OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libatlas_kernels.so")
 
 SOURCES = ["gemv.hip", "skinny.hip", "attention.hip", "fused.hip", "errors.cpp", "runtime.cpp",
-           "capi.cpp", "engine.cpp", "st_format.cpp", "loader.cpp"]
+           "capi.cpp", "engine.cpp", "st_format.cpp", "loader.cpp", "blas.cpp"]
 
 
 def hipcc() -> str:
@@ -60,7 +61,7 @@ def build(verbose: bool = False) -> str:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={os.environ.get('ATLAS_HIP_ARCH', 'gfx950')}", "-shared",
-           "-fPIC", "-o", tmp] + objs + ["-lpthread"]
+           "-fPIC", "-o", tmp] + objs + ["-lhipblaslt", "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

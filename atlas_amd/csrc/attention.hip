@@ -1140,7 +1140,17 @@ __global__ __launch_bounds__(1024) void attn_prefill_kernel(AttnArgs a, int n) {
             lsum += s_l[k2][r] * w;
             osum += s_o[k2][r][d] * w;
         }
-        a.out[(long)jr * a.out_stride + (long)qh * HD + d] = osum / lsum;
+        const float v = osum / lsum;
+        const long off = (long)jr * a.out_stride + (long)qh * HD + d;
+        if (a.out_split) {
+            // bf16 hi = the top 16 bits, lo = the rest rounded to nearest even
+            const uint32_t u = __float_as_uint(v);
+            const uint32_t ur = __float_as_uint(v - __uint_as_float(u & 0xFFFF0000u));
+            a.out_split[off] = (uint16_t)(u >> 16);
+            a.out_split[a.split_lo + off] = (uint16_t)((ur + 0x7FFFu + ((ur >> 16) & 1u)) >> 16);
+        } else {
+            a.out[off] = v;
+        }
     }
 }
 

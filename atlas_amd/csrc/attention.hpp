@@ -32,6 +32,11 @@ struct AttnArgs {
     // non-null, the splits merge in the block that finishes last (one launch,
     // at most kAttnFusedMaxSplits splits); null, attn_combine_kernel merges
     int* counters;
+    // attn_prefill_launch only: non-null, row j's output goes instead to
+    // out_split + j * out_stride (its bf16 hi part) and + split_lo (its lo
+    // part), the input rows of the library GEMM that follows
+    uint16_t* out_split;
+    long split_lo;
 };
 
 // Fused QK-norm + RoPE + KV write + split-K attention + split merge.

@@ -1,0 +1,230 @@
+// blas.cpp -- the bf16 prompt GEMM (17..128 activation rows) through hipBLASLt.
+//
+// Y[n, m] = sum_k W[m, k] X[n, k] with W bf16 [M x K] (row pitch ldw) and X
+// f32, as the tiled kernel gemm_rows_kernel computes it (the prompt-chunk
+// form of Linear::forward, crates/atlas-model/src/lib.rs:487-499): X's rows
+// are split into bf16 hi and lo rows (split_rows_kernel, the tiled kernel's
+// split), one library GEMM multiplies the weights with all 2N rows at f32
+// accumulation (the weights stream once), and combine_rows_kernel adds the hi
+// and lo products and applies the store or SwiGLU epilogue.  A plain library
+// GEMM of bf16 operands: the hand-written kernel keeps the int8/int4 formats
+// (dequantisation fused) and every shape this path does not take.
+//
+// Layouts in the library's column-major terms: W is K x M with leading
+// dimension ldw / 2 and is transposed (op T), the split rows are K x 2N, and
+// D = W^T X' is M x 2N f32 (row j of the row-major view = product row j).
+#include <hipblaslt/hipblaslt.h>
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+#include "gemv.hpp"
+
+namespace atlas {
+
+namespace {
+
+struct Plan {
+    int M, K, lda, N2;
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+
+void destroy_plan(Plan& p) {
+    if (p.la) (void)hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb) (void)hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.lc) (void)hipblasLtMatrixLayoutDestroy(p.lc);
+    if (p.desc) (void)hipblasLtMatmulDescDestroy(p.desc);
+    p = Plan{};
+}
+
+constexpr size_t kWorkspace = 32u << 20;
+constexpr size_t kMaxPlans = 64;
+
+#define TRY_RC(expr)              \
+    do {                          \
+        const int rc_ = (expr);   \
+        if (rc_) return rc_;      \
+    } while (0)
+
+}  // namespace
+
+struct BlasRows {
+    hipblasLtHandle_t h = nullptr;
+    int max_n = 0, max_m = 0, max_k = 0;
+    void* ws = nullptr;           // library workspace
+    uint16_t* xs = nullptr;       // split rows [2 max_n][max_k] bf16
+    float* d = nullptr;           // products [2 max_n][max_m] f32
+    std::vector<Plan> plans;
+    size_t next = 0;              // plan slot reused once kMaxPlans are held
+    std::mutex mu;
+};
+
+int blas_rows_create(BlasRows** out, int max_n, int max_m, int max_k) {
+    ATLAS_REQUIRE(out && max_n > 0 && max_m > 0 && max_k > 0, "blas rows: bad arguments");
+    *out = nullptr;
+    BlasRows* b = new BlasRows();
+    b->max_n = max_n;
+    b->max_m = max_m;
+    b->max_k = max_k;
+    if (hipblasLtCreate(&b->h) != HIPBLAS_STATUS_SUCCESS) {
+        delete b;
+        set_error(ATLAS_EUNSUPPORTED, "blas rows: hipBLASLt handle creation failed");
+        return ATLAS_EUNSUPPORTED;
+    }
+    if (dev_malloc(&b->ws, kWorkspace) != hipSuccess ||
+        dev_malloc(&b->xs, (size_t)2 * max_n * max_k * sizeof(uint16_t)) != hipSuccess ||
+        dev_malloc(&b->d, (size_t)2 * max_n * max_m * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        blas_rows_destroy(b);
+        set_error(ATLAS_ENOMEM, "blas rows: staging buffers");
+        return ATLAS_ENOMEM;
+    }
+    *out = b;
+    return ATLAS_OK;
+}
+
+void blas_rows_destroy(BlasRows* b) {
+    if (!b) return;
+    for (Plan& p : b->plans) destroy_plan(p);
+    if (b->ws) (void)hipFree(b->ws);
+    if (b->xs) (void)hipFree(b->xs);
+    if (b->d) (void)hipFree(b->d);
+    if (b->h) (void)hipblasLtDestroy(b->h);
+    delete b;
+}
+
+// The plan of (M, K, lda, 2N): descriptors and the fastest of the library's
+// first candidates, timed once on the caller's stream with the caller's
+// weights w (the prompt GEMMs run eagerly, never under capture).
+static int get_plan(BlasRows* b, const void* w, int M, int K, int lda, int N2, hipStream_t st,
+                    Plan** out) {
+    for (Plan& p : b->plans)
+        if (p.M == M && p.K == K && p.lda == lda && p.N2 == N2) {
+            *out = &p;
+            return ATLAS_OK;
+        }
+    Plan p{};
+    p.M = M; p.K = K; p.lda = lda; p.N2 = N2;
+    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, M, lda) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, N2, K) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, M, N2, M) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+    const uint64_t wsz = kWorkspace;
+    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                     &wsz, sizeof(wsz)) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulHeuristicResult_t res[8];
+    int n_res = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(b->h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 8, res,
+                                               &n_res) == HIPBLAS_STATUS_SUCCESS &&
+         n_res > 0;
+    if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+    if (!ok) {
+        destroy_plan(p);
+        set_error(ATLAS_EUNSUPPORTED, "blas rows: no hipBLASLt algorithm for %d x %d x %d", M, N2, K);
+        return ATLAS_EUNSUPPORTED;
+    }
+    // time up to four candidates on the staging buffers (their contents are
+    // overwritten by the real call that follows)
+    int best = 0;
+    if (n_res > 1) {
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        ATLAS_HIP(hipEventCreate(&e0));
+        if (hipEventCreate(&e1) != hipSuccess) {
+            (void)hipEventDestroy(e0);
+            (void)hipGetLastError();
+            set_error(ATLAS_EHIP, "blas rows: event creation failed");
+            return ATLAS_EHIP;
+        }
+        const float alpha = 1.f, beta = 0.f;
+        float best_ms = 0.f;
+        for (int i = 0; i < n_res && i < 4; ++i) {
+            bool run_ok = true;
+            for (int r = 0; r < 4 && run_ok; ++r) {
+                if (r == 1) run_ok = hipEventRecord(e0, st) == hipSuccess;
+                run_ok = run_ok && hipblasLtMatmul(b->h, p.desc, &alpha, w, p.la, b->xs, p.lb, &beta,
+                                                   b->d, p.lc, b->d, p.lc, &res[i].algo, b->ws,
+                                                   kWorkspace, st) == HIPBLAS_STATUS_SUCCESS;
+            }
+            float ms = 0.f;
+            run_ok = run_ok && hipEventRecord(e1, st) == hipSuccess &&
+                     hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+            if (run_ok && (i == 0 || ms < best_ms)) {
+                best_ms = ms;
+                best = i;
+            }
+            (void)hipGetLastError();
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+    }
+    p.algo = res[best].algo;
+    if (b->plans.size() < kMaxPlans) {
+        b->plans.push_back(p);
+        *out = &b->plans.back();
+    } else {
+        Plan& slot = b->plans[b->next++ % kMaxPlans];
+        destroy_plan(slot);
+        slot = p;
+        *out = &slot;
+    }
+    return ATLAS_OK;
+}
+
+// D[0 .. 2n) = W . xs[0 .. 2n)^T for the 2n split rows already in b->xs
+static int matmul(BlasRows* b, const GemvArgs& a, int n, hipStream_t st) {
+    const long pitch = a.ldw > 0 ? a.ldw : (long)a.K * 2;
+    ATLAS_REQUIRE(pitch % 2 == 0 && pitch / 2 >= a.K, "blas rows: row pitch %ld", pitch);
+    Plan* p = nullptr;
+    TRY_RC(get_plan(b, a.w, a.M, a.K, (int)(pitch / 2), 2 * n, st, &p));
+    const float alpha = 1.f, beta = 0.f;
+    if (hipblasLtMatmul(b->h, p->desc, &alpha, a.w, p->la, b->xs, p->lb, &beta, b->d, p->lc, b->d,
+                        p->lc, &p->algo, b->ws, kWorkspace, st) != HIPBLAS_STATUS_SUCCESS) {
+        (void)hipGetLastError();
+        set_error(ATLAS_EHIP, "blas rows: hipBLASLt matmul failed (%d x %d x %d)", a.M, 2 * n, a.K);
+        return ATLAS_EHIP;
+    }
+    return ATLAS_OK;
+}
+
+int blas_rows_launch(BlasRows* b, const GemvArgs& a, hipStream_t st) {
+    ATLAS_REQUIRE(b && a.fmt == WF_BF16 && a.N > 0 && a.M > 0 && a.K > 0, "blas rows: bad arguments");
+    ATLAS_REQUIRE(a.M <= b->max_m && a.K <= b->max_k, "blas rows: %d x %d beyond the staging buffers",
+                  a.M, a.K);
+    ATLAS_REQUIRE(a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0,
+                  "blas rows: x rows must be contiguous and 16-byte aligned");
+    std::lock_guard<std::mutex> lock(b->mu);     // one set of staging buffers
+    for (int n0 = 0; n0 < a.N; n0 += b->max_n) {
+        const int n = std::min(b->max_n, a.N - n0);
+        TRY_RC(split_rows_launch(a.x + (long)n0 * a.x_stride_n, a.x_stride_n, n, a.K, b->xs, st));
+        TRY_RC(matmul(b, a, n, st));
+        TRY_RC(combine_rows_launch(b->d, n, a.M, a.epi, a.y + (long)n0 * a.y_stride_n, a.y_stride_n,
+                                   a.y_stride_m, st));
+    }
+    return ATLAS_OK;
+}
+
+int blas_rows_gemm(BlasRows* b, const GemvArgs& a, int n, hipStream_t st) {
+    ATLAS_REQUIRE(b && a.fmt == WF_BF16 && n > 0 && n <= b->max_n && a.M > 0 && a.K > 0,
+                  "blas rows: bad arguments");
+    ATLAS_REQUIRE(a.M <= b->max_m && a.K <= b->max_k, "blas rows: %d x %d beyond the staging buffers",
+                  a.M, a.K);
+    std::lock_guard<std::mutex> lock(b->mu);
+    return matmul(b, a, n, st);
+}
+
+uint16_t* blas_rows_xs(BlasRows* b) { return b ? b->xs : nullptr; }
+float* blas_rows_d(BlasRows* b) { return b ? b->d : nullptr; }
+int blas_rows_max_n(const BlasRows* b) { return b ? b->max_n : 0; }
+
+}  // namespace atlas

@@ -63,6 +63,52 @@ __global__ __launch_bounds__(1024) void residual_rmsnorm_kernel(float* __restric
     for (int i = threadIdx.x; i < n; i += blockDim.x) xb[i] += yb[i] * inv * w[i];
 }
 
+// The prompt chunk's form of residual_rmsnorm_kernel: y = d_hi + d_lo (the
+// two product rows of the library GEMM, n wide, row b at d + b*n and
+// d + lo_off + b*n), the same sums and order as residual_rmsnorm_kernel reading
+// that y; the updated x row is also written as the bf16 hi / lo split rows of
+// the next GEMM's input (xs rows b and rows + b, n wide) when xs is non-null.
+__global__ __launch_bounds__(1024) void residual_rmsnorm_rows_kernel(
+    float* __restrict__ x, const float* __restrict__ d, long lo_off, const float* __restrict__ w, int n,
+    long ld, float eps, uint16_t* __restrict__ xs) {
+    const int b = blockIdx.x;
+    float* xb = x + b * ld;
+    const float* dh = d + (long)b * n;
+    const float* dl = dh + lo_off;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float y = dh[i] + dl[i];
+        ss += y * y;
+    }
+    ss = block_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    uint16_t* sh = xs ? xs + (long)b * n : nullptr;
+    uint16_t* sl = xs ? xs + (long)(gridDim.x + b) * n : nullptr;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float y = dh[i] + dl[i];
+        const float v = xb[i] + y * inv * w[i];
+        xb[i] = v;
+        if (xs) {
+            const uint32_t u = __float_as_uint(v);
+            const float r = v - __uint_as_float(u & 0xFFFF0000u);
+            const uint32_t ur = __float_as_uint(r);
+            sh[i] = (uint16_t)(u >> 16);
+            sl[i] = (uint16_t)((ur + 0x7FFFu + ((ur >> 16) & 1u)) >> 16);
+        }
+    }
+}
+
+int residual_rmsnorm_rows_launch(float* x, const float* d, long lo_off, const float* w, int n, int rows,
+                                 long ld, float eps, uint16_t* xs, hipStream_t st) {
+    ATLAS_REQUIRE(x && d && w && n > 0 && rows > 0 && lo_off >= (long)rows * n,
+                  "residual_rmsnorm_rows: bad arguments");
+    const int threads = n >= 1024 ? 1024 : ((n + 63) / 64) * 64;
+    hipLaunchKernelGGL(residual_rmsnorm_rows_kernel, dim3(rows), dim3(threads), 0, st, x, d, lo_off, w,
+                       n, ld, eps, xs);
+    ATLAS_LAUNCH_CHECK("residual_rmsnorm_rows");
+    return ATLAS_OK;
+}
+
 int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, long ld, float eps,
                    hipStream_t st) {
     ATLAS_REQUIRE(x && w && out && n > 0 && rows > 0, "rmsnorm: bad arguments");
@@ -96,13 +142,15 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
     const int nq = a.n_heads, nkv = a.n_kv;
     const int slot = a.slot_dev ? a.slot_dev[s] : 0;
     const long cache_off = (long)slot * a.slot_stride + ((long)pos * nkv) * HD;
+    // element off of this sequence's q|k|v: in place, or hi + lo product rows
+    const long src_off = a.src ? (long)s * a.src_stride : 0;
+    auto in = [&](long off) { return a.src ? a.src[off] + a.src[a.src_lo + off] : qkv[off]; };
 
     if (hidx >= nq + nkv) {
         // V head: copy into the cache
         const int vh = hidx - nq - nkv;
-        const float* src = qkv + (long)(nq + nkv + vh) * HD;
         float* dst = a.v_cache + cache_off + (long)vh * HD;
-        for (int e = lane; e < HD; e += 64) dst[e] = src[e];
+        for (int e = lane; e < HD; e += 64) dst[e] = in(src_off + (long)(nq + nkv + vh) * HD + e);
         return;
     }
     const bool is_q = hidx < nq;
@@ -114,7 +162,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int e = lane + 64 * j;
-        v[j] = e < HD ? xh[e] : 0.f;
+        v[j] = e < HD ? in(src_off + (long)hidx * HD + e) : 0.f;
         ss += v[j] * v[j];
     }
     if (nw) {

@@ -24,6 +24,10 @@ struct QkvPostArgs {
     const int* pos_dev;      // [n_seq] position per sequence, or null (use pos)
     int pos;
     int n_heads, n_kv, head_dim;
+    // non-null: sequence s's q|k|v is src[s*src_stride + e] + src[src_lo + s*src_stride + e]
+    // (the library GEMM's hi and lo product rows); q is written to qkv
+    const float* src;
+    long src_stride, src_lo;
 };
 
 struct ArgmaxArgs {
@@ -75,6 +79,11 @@ int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, 
                    hipStream_t st);
 int residual_rmsnorm_launch(float* x, const float* y, const float* w, int n, int rows, long ld,
                             float eps, hipStream_t st);
+// x += rmsnorm(d_hi + d_lo) * w from the library GEMM's product rows (row b at
+// d + b*n, its lo row lo_off further); with xs non-null the new x rows are
+// also written as bf16 hi rows (xs row b) and lo rows (xs row rows + b)
+int residual_rmsnorm_rows_launch(float* x, const float* d, long lo_off, const float* w, int n, int rows,
+                                 long ld, float eps, uint16_t* xs, hipStream_t st);
 int qkv_post_launch(const QkvPostArgs& a, int n_seq, hipStream_t st);
 int qk_norm_launch(float* x, const float* w, int n_heads, int hd, float eps, hipStream_t st);
 int rope_tab_launch(float* x, const float* c, const float* s, int n_heads, int hd, int pos,

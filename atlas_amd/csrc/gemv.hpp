@@ -42,6 +42,8 @@ struct GemvArgs {
     long ldw;                // bytes between weight rows (multiple of 16); 0 = packed rows
     float* partial;          // skinny / prompt GEMM split-K partials (null: the thread's scratch)
     size_t partial_bytes;    // ... their size
+    struct BlasRows* blas;   // 17..128 rows of bf16 weights: the caller's hipBLASLt context, or
+                             // null (the tiled MFMA kernel)
 };
 
 enum { GEMV_MAX_WAVES = 16384 };    // bound on persistent waves (argmax partials)
@@ -61,6 +63,32 @@ size_t skinny_partial_bytes(int M, int N, int K);    // split-K partials of (M, 
 bool gemm_rows_ok(const GemvArgs& a);
 int gemm_rows_launch(const GemvArgs& a, hipStream_t st);
 size_t gemm_rows_partial_bytes(int M, int N, int K);
+// The bf16 prompt GEMM through hipBLASLt (blas.cpp): X's rows split into bf16
+// hi and lo rows, one library GEMM of the weights against all 2N rows (the
+// weights stream once), then y = hi + lo products with the store or SwiGLU
+// epilogue.  A context holds the library handle, its workspace and the
+// staging buffers for up to max_n rows of K <= max_k, M <= max_m.
+struct BlasRows;
+int blas_rows_create(BlasRows** out, int max_n, int max_m, int max_k);
+void blas_rows_destroy(BlasRows* b);
+int blas_rows_launch(BlasRows* b, const GemvArgs& a, hipStream_t st);   // bf16, gemm_rows_ok(a)
+// The library GEMM alone, for callers that fuse the split and the combine into
+// their neighbouring kernels: blas_rows_xs(b) holds the 2n split rows of X (K
+// wide: hi rows 0..n-1, lo rows n..2n-1), blas_rows_d(b) receives the 2n
+// product rows (M wide, f32).  n <= blas_rows_max_n(b).
+int blas_rows_gemm(BlasRows* b, const GemvArgs& a, int n, hipStream_t st);
+uint16_t* blas_rows_xs(BlasRows* b);
+float* blas_rows_d(BlasRows* b);
+int blas_rows_max_n(const BlasRows* b);
+// the two element-wise halves (skinny.hip): rows n of x (f32, stride sn) ->
+// out rows n (bf16 hi) and N + n (bf16 lo); y[n, m] = d[n, m] + d[N + n, m]
+// (d rows of M f32) or the SwiGLU of the (gate, up) column pairs
+int split_rows_launch(const float* x, long sn, int N, int K, uint16_t* out, hipStream_t st);
+int combine_rows_launch(const float* d, int N, int M, int epi, float* y, long ysn, long ysm,
+                        hipStream_t st);
+// the SwiGLU of the (gate, up) pairs of d = hi + lo product rows, written
+// straight as the split rows (M / 2 wide) of the next GEMM's input
+int combine_split_launch(const float* d, int N, int M, uint16_t* out, hipStream_t st);
 int gemm_generic_launch(int fmt, const void* A, const float* B, float* C, int m, int n, int k,
                         hipStream_t st);
 

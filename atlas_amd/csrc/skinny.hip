@@ -1528,6 +1528,94 @@ static int gemm_rows_part(const GemvArgs& a, hipStream_t st) {
     return ATLAS_OK;
 }
 
+// ---- the element-wise halves of the hipBLASLt prompt GEMM ---------------------
+// Thread per 8 consecutive k of one row: the split of the tiled kernel
+// (hi = the top 16 bits, lo = the rest rounded to nearest even).
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ x, long sn, int N,
+                                                         int K, uint16_t* __restrict__ out) {
+    const int n = blockIdx.y;
+    const int k8 = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (k8 >= K) return;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + (long)n * sn + k8);
+    u32x4 hi, lo;
+    split8(xr[0], xr[1], hi, lo);
+    *reinterpret_cast<u32x4*>(out + (long)n * K + k8) = hi;
+    *reinterpret_cast<u32x4*>(out + (long)(N + n) * K + k8) = lo;
+}
+
+// Thread per output element (or per (gate, up) pair with SwiGLU).
+__global__ __launch_bounds__(256) void combine_rows_kernel(const float* __restrict__ d, int N, int M,
+                                                           int epi, float* __restrict__ y, long ysn,
+                                                           long ysm) {
+    const int n = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const float* dh = d + (long)n * M;
+    const float* dl = d + (long)(N + n) * M;
+    if (epi == EPI_SILU_MUL) {
+        if (2 * i + 1 >= M) return;
+        const float g = dh[2 * i] + dl[2 * i], u = dh[2 * i + 1] + dl[2 * i + 1];
+        y[n * ysn + (long)i * ysm] = g / (1.0f + expf(-g)) * u;
+    } else {
+        if (i >= M) return;
+        y[n * ysn + (long)i * ysm] = dh[i] + dl[i];
+    }
+}
+
+// Thread per two (gate, up) pairs: h = SwiGLU(hi + lo products) as the
+// combine kernel computes it, then split as split_rows_kernel does.
+__global__ __launch_bounds__(256) void combine_split_kernel(const float* __restrict__ d, int N, int M,
+                                                            uint16_t* __restrict__ out) {
+    const int n = blockIdx.y;
+    const int j = (blockIdx.x * 256 + threadIdx.x) * 2;        // first of two outputs
+    const int K2 = M / 2;
+    if (j >= K2) return;
+    const f32x4 ph = *reinterpret_cast<const f32x4*>(d + (long)n * M + 2 * j);
+    const f32x4 pl = *reinterpret_cast<const f32x4*>(d + (long)(N + n) * M + 2 * j);
+    const float g0 = ph.x + pl.x, u0 = ph.y + pl.y, g1 = ph.z + pl.z, u1 = ph.w + pl.w;
+    const float h[2] = {g0 / (1.0f + expf(-g0)) * u0, g1 / (1.0f + expf(-g1)) * u1};
+    uint32_t hb[2], lb[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t u = __float_as_uint(h[e]);
+        hb[e] = u >> 16;
+        lb[e] = bf16_rne_bits(h[e] - __uint_as_float(u & 0xFFFF0000u));
+    }
+    *reinterpret_cast<uint32_t*>(out + (long)n * K2 + j) = pack2(hb[0], hb[1]);
+    *reinterpret_cast<uint32_t*>(out + (long)(N + n) * K2 + j) = pack2(lb[0], lb[1]);
+}
+
+int combine_split_launch(const float* d, int N, int M, uint16_t* out, hipStream_t st) {
+    ATLAS_REQUIRE(d && out && N > 0 && N <= 65535 && M > 0 && M % 4 == 0 && ((uintptr_t)d & 15) == 0 &&
+                      ((uintptr_t)out & 3) == 0,
+                  "combine split: N %d M %d", N, M);
+    hipLaunchKernelGGL(combine_split_kernel, dim3((M / 4 + 255) / 256, N), dim3(256), 0, st, d, N, M,
+                       out);
+    ATLAS_LAUNCH_CHECK("combine_split");
+    return ATLAS_OK;
+}
+
+int split_rows_launch(const float* x, long sn, int N, int K, uint16_t* out, hipStream_t st) {
+    ATLAS_REQUIRE(x && out && N > 0 && N <= 65535 && K > 0 && K % 8 == 0 && sn % 4 == 0 &&
+                      ((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0,
+                  "split rows: N %d K %d", N, K);
+    hipLaunchKernelGGL(split_rows_kernel, dim3((K / 8 + 255) / 256, N), dim3(256), 0, st, x, sn, N, K,
+                       out);
+    ATLAS_LAUNCH_CHECK("split_rows");
+    return ATLAS_OK;
+}
+
+int combine_rows_launch(const float* d, int N, int M, int epi, float* y, long ysn, long ysm,
+                        hipStream_t st) {
+    ATLAS_REQUIRE(d && y && N > 0 && N <= 65535 && M > 0 && (epi == EPI_STORE ||
+                                                             (epi == EPI_SILU_MUL && M % 2 == 0)),
+                  "combine rows: N %d M %d epi %d", N, M, epi);
+    const int cols = epi == EPI_SILU_MUL ? M / 2 : M;
+    hipLaunchKernelGGL(combine_rows_kernel, dim3((cols + 255) / 256, N), dim3(256), 0, st, d, N, M, epi,
+                       y, ysn, ysm);
+    ATLAS_LAUNCH_CHECK("combine_rows");
+    return ATLAS_OK;
+}
+
 int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
     ATLAS_REQUIRE(gemm_rows_ok(a), "gemm rows: unsupported shape (fmt %d, n %d, k %d)", a.fmt, a.N,
                   a.K);
@@ -1552,7 +1640,8 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     GemvArgs a = a_in;
     gemv_fill_int4_index(a);
     a.x_vec = a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0;
-    if (a.N > 16 && gemm_rows_ok(a)) return gemm_rows_launch(a, st);
+    if (a.N > 16 && gemm_rows_ok(a))
+        return a.blas && a.fmt == WF_BF16 ? blas_rows_launch(a.blas, a, st) : gemm_rows_launch(a, st);
     ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17..128 rows need K %% 128 == 0 "
                   "and, for int4, blocks of 32 * 2^j)", a.N);
     ATLAS_REQUIRE(a.w && a.x && a.y, "skinny: null pointer");
