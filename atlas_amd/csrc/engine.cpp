@@ -1449,10 +1449,10 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         }
         if (need && dalloc(m, (void**)&m->gemm_part, need)) return fail(m);
         m->gemm_part_bytes = need;
-        // bf16 prompt chunks through hipBLASLt (1.5-1.8x the tiled kernel's rate
-        // at 127 rows of the 7B shapes); without a library context the tiled
-        // kernel serves them
-        if (m->big_prefill && fmt == WF_BF16) {
+        // bf16 and int8 prompt chunks through hipBLASLt (bf16 1.6x the tiled
+        // kernel's rate at 127 rows of the 7B shapes); without a library
+        // context the tiled kernel serves them, as it serves int4
+        if (m->big_prefill && (fmt == WF_BF16 || fmt == WF_I8)) {
             int max_m = 0, max_k = 0;
             for (const auto& sh : shapes) {
                 max_m = std::max(max_m, sh[0]);

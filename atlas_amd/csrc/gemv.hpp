@@ -63,15 +63,16 @@ size_t skinny_partial_bytes(int M, int N, int K);    // split-K partials of (M, 
 bool gemm_rows_ok(const GemvArgs& a);
 int gemm_rows_launch(const GemvArgs& a, hipStream_t st);
 size_t gemm_rows_partial_bytes(int M, int N, int K);
-// The bf16 prompt GEMM through hipBLASLt (blas.cpp): X's rows split into bf16
-// hi and lo rows, one library GEMM of the weights against all 2N rows (the
-// weights stream once), then y = hi + lo products with the store or SwiGLU
+// The bf16 and int8 prompt GEMMs through hipBLASLt (blas.cpp): X's rows split
+// into bf16 hi and lo rows (bf16 weights) or three int8 digit rows (int8
+// weights), one library GEMM of the weights against all of them (the weights
+// stream once), then y = the recombined products with the store or SwiGLU
 // epilogue.  A context holds the library handle, its workspace and the
 // staging buffers for up to max_n rows of K <= max_k, M <= max_m.
 struct BlasRows;
 int blas_rows_create(BlasRows** out, int max_n, int max_m, int max_k);
 void blas_rows_destroy(BlasRows* b);
-int blas_rows_launch(BlasRows* b, const GemvArgs& a, hipStream_t st);   // bf16, gemm_rows_ok(a)
+int blas_rows_launch(BlasRows* b, const GemvArgs& a, hipStream_t st);   // bf16/int8, gemm_rows_ok(a)
 // The library GEMM alone, for callers that fuse the split and the combine into
 // their neighbouring kernels: blas_rows_xs(b) holds the 2n split rows of X (K
 // wide: hi rows 0..n-1, lo rows n..2n-1), blas_rows_d(b) receives the 2n
@@ -86,6 +87,13 @@ int blas_rows_max_n(const BlasRows* b);
 int split_rows_launch(const float* x, long sn, int N, int K, uint16_t* out, hipStream_t st);
 int combine_rows_launch(const float* d, int N, int M, int epi, float* y, long ysn, long ysm,
                         hipStream_t st);
+// int8 weights: rows n of x -> three int8 digit rows (n, N + n, 2N + n; K
+// wide) and the row scale xscale[n] = max|x[n]| / 127; y from the int32
+// product rows d (M wide) times the weight row scales, store or SwiGLU
+int digits_rows_launch(const float* x, long sn, int N, int K, int8_t* out, float* xscale,
+                       hipStream_t st);
+int combine_digits_launch(const int* d, int N, int M, const float* wscale, const float* xscale, int epi,
+                          float* y, long ysn, long ysm, hipStream_t st);
 // the SwiGLU of the (gate, up) pairs of d = hi + lo product rows, written
 // straight as the split rows (M / 2 wide) of the next GEMM's input
 int combine_split_launch(const float* d, int N, int M, uint16_t* out, hipStream_t st);

@@ -1594,6 +1594,86 @@ int combine_split_launch(const float* d, int N, int M, uint16_t* out, hipStream_
     return ATLAS_OK;
 }
 
+// int8 weights (W8A32): each activation row n becomes three int8 digit rows,
+// x[n, k] = s_n (d0 + d1 / 128 + d2 / 16384) + e with s_n = max_k |x[n, k]| / 127
+// and |e| <= s_n / 32768 (2^-22 of the row's largest element); the library's
+// int8 GEMM sums q * d exactly in int32.  Block per row.
+__global__ __launch_bounds__(256) void digits_rows_kernel(const float* __restrict__ x, long sn, int N,
+                                                          int K, int8_t* __restrict__ out,
+                                                          float* __restrict__ xscale) {
+    __shared__ float red[4];
+    const int n = blockIdx.x;
+    const float* xr = x + (long)n * sn;
+    float mx = 0.f;
+    for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float inv = mx > 0.f ? 127.0f / mx : 0.f;
+    if (threadIdx.x == 0) xscale[n] = mx / 127.0f;
+    int8_t* o0 = out + (long)n * K;
+    int8_t* o1 = out + (long)(N + n) * K;
+    int8_t* o2 = out + (long)(2 * N + n) * K;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const float u = xr[k] * inv;
+        const float d0 = fminf(fmaxf(rintf(u), -127.f), 127.f);
+        const float r1 = (u - d0) * 128.f;
+        const float d1 = fminf(fmaxf(rintf(r1), -127.f), 127.f);
+        const float r2 = (r1 - d1) * 128.f;
+        const float d2 = fminf(fmaxf(rintf(r2), -127.f), 127.f);
+        o0[k] = (int8_t)(int)d0;
+        o1[k] = (int8_t)(int)d1;
+        o2[k] = (int8_t)(int)d2;
+    }
+}
+
+// y[n, m] = wscale[m] * s_n * (D0 + D1 / 128 + D2 / 16384) from the int32
+// product rows of the three digit rows (M wide), with the store or SwiGLU
+// epilogue; thread per output element (or per (gate, up) pair).
+__global__ __launch_bounds__(256) void combine_digits_kernel(const int* __restrict__ d, int N, int M,
+                                                             const float* __restrict__ wscale,
+                                                             const float* __restrict__ xscale, int epi,
+                                                             float* __restrict__ y, long ysn, long ysm) {
+    const int n = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const long plane = (long)N * M;
+    const int* dr = d + (long)n * M;
+    const float s = xscale[n];
+    auto val = [&](int m) {
+        const float lo = (float)dr[m + plane] + (float)dr[m + 2 * plane] * (1.0f / 128.f);
+        return ((float)dr[m] + lo * (1.0f / 128.f)) * s * wscale[m];
+    };
+    if (epi == EPI_SILU_MUL) {
+        if (2 * i + 1 >= M) return;
+        const float g = val(2 * i), u = val(2 * i + 1);
+        y[n * ysn + (long)i * ysm] = g / (1.0f + expf(-g)) * u;
+    } else {
+        if (i >= M) return;
+        y[n * ysn + (long)i * ysm] = val(i);
+    }
+}
+
+int digits_rows_launch(const float* x, long sn, int N, int K, int8_t* out, float* xscale,
+                       hipStream_t st) {
+    ATLAS_REQUIRE(x && out && xscale && N > 0 && N <= 65535 && K > 0, "digit rows: N %d K %d", N, K);
+    hipLaunchKernelGGL(digits_rows_kernel, dim3(N), dim3(256), 0, st, x, sn, N, K, out, xscale);
+    ATLAS_LAUNCH_CHECK("digits_rows");
+    return ATLAS_OK;
+}
+
+int combine_digits_launch(const int* d, int N, int M, const float* wscale, const float* xscale, int epi,
+                          float* y, long ysn, long ysm, hipStream_t st) {
+    ATLAS_REQUIRE(d && wscale && xscale && y && N > 0 && N <= 65535 && M > 0 &&
+                      (epi == EPI_STORE || (epi == EPI_SILU_MUL && M % 2 == 0)),
+                  "combine digits: N %d M %d epi %d", N, M, epi);
+    const int cols = epi == EPI_SILU_MUL ? M / 2 : M;
+    hipLaunchKernelGGL(combine_digits_kernel, dim3((cols + 255) / 256, N), dim3(256), 0, st, d, N, M,
+                       wscale, xscale, epi, y, ysn, ysm);
+    ATLAS_LAUNCH_CHECK("combine_digits");
+    return ATLAS_OK;
+}
+
 int split_rows_launch(const float* x, long sn, int N, int K, uint16_t* out, hipStream_t st) {
     ATLAS_REQUIRE(x && out && N > 0 && N <= 65535 && K > 0 && K % 8 == 0 && sn % 4 == 0 &&
                       ((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0,
@@ -1636,12 +1716,37 @@ static int launch_skinny_n(const GemvArgs& a, hipStream_t st) {
     return a.N > 8 ? launch_skinny<FMT, 2>(a, st) : launch_skinny<FMT, 1>(a, st);
 }
 
+// Whether 9..16 rows run faster as two launches of the 2..8-row kernels
+// (the weights stream twice) than through the 16-row MFMA tiles.  Measured at
+// the 7B shapes on MI355X (us, 16 rows: MFMA tiles against two 8-row launches):
+// int4 QKV 28.0 / 21.5, W_o 18.6 / 13.6, gate/up 40.2 / 32.2, W_down 49.6 /
+// 27.3; int8 W_o 17.8 / 14.7, W_down 46.0 / 32.3, but gate/up 40.6 / 46.0 and
+// QKV even; bf16 W_down 48.0 / 43.8, but QKV 31.9 / 40.6, gate/up 46.3 / 68.
+static bool halves_pay(const GemvArgs& a) {
+    if (a.N < 9 || a.N > 16) return false;
+    if (a.fmt == WF_I4) return a.block % 32 == 0 && (a.cpb & (a.cpb - 1)) == 0 && a.bpr > 0;
+    if (a.fmt == WF_I8) return a.K > 4096 || a.M <= 8192;
+    return a.fmt == WF_BF16 && a.K > 4096;
+}
+
 int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     GemvArgs a = a_in;
     gemv_fill_int4_index(a);
+    if (halves_pay(a)) {
+        const int n0 = (a.N + 1) / 2;
+        GemvArgs h = a;
+        h.N = n0;
+        const int rc = skinny_launch(h, st);
+        if (rc) return rc;
+        h.N = a.N - n0;
+        h.x = a.x + (long)n0 * a.x_stride_n;
+        h.y = a.y + (long)n0 * a.y_stride_n;
+        return skinny_launch(h, st);
+    }
     a.x_vec = a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0;
     if (a.N > 16 && gemm_rows_ok(a))
-        return a.blas && a.fmt == WF_BF16 ? blas_rows_launch(a.blas, a, st) : gemm_rows_launch(a, st);
+        return a.blas && (a.fmt == WF_BF16 || a.fmt == WF_I8) ? blas_rows_launch(a.blas, a, st)
+                                                               : gemm_rows_launch(a, st);
     ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17..128 rows need K %% 128 == 0 "
                   "and, for int4, blocks of 32 * 2^j)", a.N);
     ATLAS_REQUIRE(a.w && a.x && a.y, "skinny: null pointer");

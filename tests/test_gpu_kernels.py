@@ -153,11 +153,13 @@ def test_skinny(orc, fmt, n):
 
 
 # 9-16 rows: two MFMA A tiles share each weight tile (half the k tiles per
-# wave, so K = 4096 already splits across blocks)
+# wave, so K = 4096 already splits across blocks) -- bf16 with K <= 4096 and
+# int8 with K <= 4096 and M > 8192 -- or two launches of the 2-8-row kernels
+# (int4, int8 otherwise, bf16 with K > 4096), the second half's rows offset
 @pytest.mark.parametrize("fmt,n,M,K", [
     ("bf16", 9, 1000, 512), ("bf16", 16, 4096, 4096), ("bf16", 13, 777, 11008),
-    ("int8", 16, 1000, 4096), ("int8", 9, 4096, 11008),
-    ("int4", 16, 2048, 4096), ("int4", 12, 1000, 11008)])
+    ("int8", 16, 1000, 4096), ("int8", 9, 4096, 11008), ("int8", 12, 9000, 1024),
+    ("int4", 16, 2048, 4096), ("int4", 12, 1000, 11008), ("int4", 9, 4096, 4096)])
 def test_skinny_two_a_tiles(orc, fmt, n, M, K):
     print(f"skinny two tiles {fmt} n={n} M={M} K={K}", flush=True)
     _skinny_check(orc, fmt, n, M, K, 32, seed=3)
@@ -222,12 +224,15 @@ def test_skinny_direct_loads(orc, fmt, n, M, K):
 # kernels' own epilogue (int8 5 rows) and the split reduce after them (bf16
 # 4 rows at K = 4224, int8 8 rows at K = 8192), twenty rows at
 # K = 128 (the prompt GEMM's unsplit epilogue: gate/up pairs meet across
-# lanes) and at K = 4096 (split, SwiGLU in the reduce).
+# lanes) and at K = 4096 (split, SwiGLU in the reduce); 9-16 rows as two
+# launches (int4 12 rows, int8 13 rows at K = 8192) and as 16-row MFMA tiles
+# (int8, 2h = 10 000 weight rows).
 @pytest.mark.parametrize("fmt,n,h,K", [
     ("bf16", 1, 1000, 512), ("int8", 2, 700, 1024), ("int4", 5, 512, 2048),
     ("bf16", 20, 640, 128), ("int8", 20, 640, 128), ("int4", 20, 640, 128),
     ("bf16", 20, 2048, 4096), ("int4", 33, 1024, 4096),
-    ("int8", 5, 512, 2048), ("bf16", 4, 256, 4224), ("int8", 8, 300, 8192)])
+    ("int8", 5, 512, 2048), ("bf16", 4, 256, 4224), ("int8", 8, 300, 8192),
+    ("int4", 12, 512, 2048), ("int8", 13, 600, 8192), ("int8", 16, 5000, 1024)])
 def test_gemm_skinny_swiglu(orc, fmt, n, h, K):
     print(f"skinny swiglu {fmt} n={n} h={h} K={K}", flush=True)
     w = _w((2 * h, K), 97 + n)

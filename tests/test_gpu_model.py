@@ -289,13 +289,16 @@ def test_prefill_chunks_match_token_by_token(orc):
         assert _top2_margin(lg) <= 2 * LOGIT_TOL * np.max(np.abs(lg)), k
 
 
-def test_prefill_chunks_head_dim_128(orc):
+@pytest.mark.parametrize("fmt", ["bf16", "int8"])
+def test_prefill_chunks_head_dim_128(orc, fmt):
     # head_dim 128 takes the query-tiled prompt attention (16 rows per K/V
     # tile): chunks of 128 with sliding-window layers (window 16 < chunk),
     # ragged last row blocks and a later chunk that starts mid-window; the
-    # next token's logits agree with the oracle
+    # next token's logits agree with the oracle.  The chunks' GEMMs go through
+    # the library: bf16 hi/lo rows with the split and combine fused into the
+    # neighbouring kernels, int8 digit rows with their own split and combine.
     cfg = modelgen.olmo3_small_config(n_heads=2, n_kv_heads=2, max_seq=320)
-    W = modelgen.make_weights(cfg, seed=73)
+    W = modelgen.make_weights(cfg, seed=73, fmt=fmt)
     toks = [int(t) for t in np.random.default_rng(14).integers(0, cfg["vocab"], 300)]
     m = modelgen.engine_model(W)
     o = modelgen.oracle_model(W, threads=8)
@@ -306,7 +309,7 @@ def test_prefill_chunks_head_dim_128(orc):
         if i + 1 in (20, 129, 150, 300):
             ref[i + 1] = lg
     for n, r in ref.items():
-        print(f"prefill hd128: {n - 1} prompt tokens", flush=True)
+        print(f"prefill hd128 {fmt}: {n - 1} prompt tokens", flush=True)
         m.reset()
         m.prefill(toks[:n - 1])
         assert _rel(m.forward_one(toks[n - 1]), r) <= LOGIT_TOL, n
