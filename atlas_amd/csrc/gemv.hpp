@@ -90,6 +90,7 @@ int combine_rows_launch(const float* d, int N, int M, int epi, float* y, long ys
 // int8 weights: rows n of x -> three int8 digit rows (n, N + n, 2N + n; K
 // wide) and the row scale xscale[n] = max|x[n]| / 127; y from the int32
 // product rows d (M wide) times the weight row scales, store or SwiGLU
+constexpr int kDigitsMaxK = 12288;      // digits_rows_launch: K <= this, K % 4 == 0
 int digits_rows_launch(const float* x, long sn, int N, int K, int8_t* out, float* xscale,
                        hipStream_t st);
 int combine_digits_launch(const int* d, int N, int M, const float* wscale, const float* xscale, int epi,

@@ -1597,34 +1597,59 @@ int combine_split_launch(const float* d, int N, int M, uint16_t* out, hipStream_
 // int8 weights (W8A32): each activation row n becomes three int8 digit rows,
 // x[n, k] = s_n (d0 + d1 / 128 + d2 / 16384) + e with s_n = max_k |x[n, k]| / 127
 // and |e| <= s_n / 32768 (2^-22 of the row's largest element); the library's
-// int8 GEMM sums q * d exactly in int32.  Block per row.
-__global__ __launch_bounds__(256) void digits_rows_kernel(const float* __restrict__ x, long sn, int N,
-                                                          int K, int8_t* __restrict__ out,
-                                                          float* __restrict__ xscale) {
-    __shared__ float red[4];
+// int8 GEMM sums q * d exactly in int32.  A 1024-thread block per row; a
+// thread holds up to DR_PT groups of four consecutive elements in registers
+// between the row maximum and the digits (K <= 4 * 1024 * DR_PT), and stores
+// each digit plane's four bytes as one word.
+constexpr int DR_PT = kDigitsMaxK / 4096;
+__global__ __launch_bounds__(1024) void digits_rows_kernel(const float* __restrict__ x, long sn, int N,
+                                                           int K, int8_t* __restrict__ out,
+                                                           float* __restrict__ xscale) {
+    __shared__ float red[16];
     const int n = blockIdx.x;
-    const float* xr = x + (long)n * sn;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + (long)n * sn);
+    const int ng = K >> 2;
+    f32x4 v[DR_PT];
     float mx = 0.f;
-    for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+#pragma unroll
+    for (int j = 0; j < DR_PT; ++j) {
+        const int g = threadIdx.x + 1024 * j;
+        v[j] = g < ng ? xr[g] : f32x4{0.f, 0.f, 0.f, 0.f};
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
     mx = wave_max(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, red[i]);
     const float inv = mx > 0.f ? 127.0f / mx : 0.f;
     if (threadIdx.x == 0) xscale[n] = mx / 127.0f;
-    int8_t* o0 = out + (long)n * K;
-    int8_t* o1 = out + (long)(N + n) * K;
-    int8_t* o2 = out + (long)(2 * N + n) * K;
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const float u = xr[k] * inv;
-        const float d0 = fminf(fmaxf(rintf(u), -127.f), 127.f);
-        const float r1 = (u - d0) * 128.f;
-        const float d1 = fminf(fmaxf(rintf(r1), -127.f), 127.f);
-        const float r2 = (r1 - d1) * 128.f;
-        const float d2 = fminf(fmaxf(rintf(r2), -127.f), 127.f);
-        o0[k] = (int8_t)(int)d0;
-        o1[k] = (int8_t)(int)d1;
-        o2[k] = (int8_t)(int)d2;
+    uint32_t* o0 = reinterpret_cast<uint32_t*>(out + (long)n * K);
+    uint32_t* o1 = reinterpret_cast<uint32_t*>(out + (long)(N + n) * K);
+    uint32_t* o2 = reinterpret_cast<uint32_t*>(out + (long)(2 * N + n) * K);
+    auto digit = [](float f) { return (uint32_t)((int)fminf(fmaxf(rintf(f), -127.f), 127.f) & 0xFF); };
+#pragma unroll
+    for (int j = 0; j < DR_PT; ++j) {
+        const int g = threadIdx.x + 1024 * j;
+        if (g >= ng) break;
+        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float u = e[c] * inv;
+            const uint32_t b0 = digit(u);
+            const float r1 = (u - (float)(int8_t)b0) * 128.f;
+            const uint32_t b1 = digit(r1);
+            const float r2 = (r1 - (float)(int8_t)b1) * 128.f;
+            const uint32_t b2 = digit(r2);
+            w0 |= b0 << (8 * c);
+            w1 |= b1 << (8 * c);
+            w2 |= b2 << (8 * c);
+        }
+        o0[g] = w0;
+        o1[g] = w1;
+        o2[g] = w2;
     }
 }
 
@@ -1656,8 +1681,11 @@ __global__ __launch_bounds__(256) void combine_digits_kernel(const int* __restri
 
 int digits_rows_launch(const float* x, long sn, int N, int K, int8_t* out, float* xscale,
                        hipStream_t st) {
-    ATLAS_REQUIRE(x && out && xscale && N > 0 && N <= 65535 && K > 0, "digit rows: N %d K %d", N, K);
-    hipLaunchKernelGGL(digits_rows_kernel, dim3(N), dim3(256), 0, st, x, sn, N, K, out, xscale);
+    ATLAS_REQUIRE(x && out && xscale && N > 0 && N <= 65535 && K > 0 && K % 4 == 0 &&
+                      K <= kDigitsMaxK && sn % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
+                      ((uintptr_t)out & 3) == 0,
+                  "digit rows: N %d K %d", N, K);
+    hipLaunchKernelGGL(digits_rows_kernel, dim3(N), dim3(1024), 0, st, x, sn, N, K, out, xscale);
     ATLAS_LAUNCH_CHECK("digits_rows");
     return ATLAS_OK;
 }
@@ -1745,8 +1773,9 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     }
     a.x_vec = a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0;
     if (a.N > 16 && gemm_rows_ok(a))
-        return a.blas && (a.fmt == WF_BF16 || a.fmt == WF_I8) ? blas_rows_launch(a.blas, a, st)
-                                                               : gemm_rows_launch(a, st);
+        return a.blas && (a.fmt == WF_BF16 || (a.fmt == WF_I8 && a.K <= kDigitsMaxK))
+                   ? blas_rows_launch(a.blas, a, st)
+                   : gemm_rows_launch(a, st);
     ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17..128 rows need K %% 128 == 0 "
                   "and, for int4, blocks of 32 * 2^j)", a.N);
     ATLAS_REQUIRE(a.w && a.x && a.y, "skinny: null pointer");

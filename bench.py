@@ -77,6 +77,37 @@ def time_launches(torch, fn, n_iter: int, warm: int = 3) -> float:
     return e0.elapsed_time(e1) / n_iter
 
 
+def time_graph(torch, lib, fn, n_launch: int, replays: int = 5) -> float:
+    """Average ms per call of fn(i), i < n_launch, captured into one HIP graph on
+    a torch capture stream (the library's launches follow it through
+    atlas_set_thread_stream) and replayed: the launch gaps of a graph, as the
+    decode step runs its kernels, without the host's per-call enqueue cost."""
+    s = torch.cuda.Stream()
+    fn(0)                                   # any first-use work outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        assert lib.atlas_set_thread_stream(C.c_void_p(s.cuda_stream)) == 0
+        try:
+            for i in range(n_launch):
+                fn(i)
+        finally:
+            lib.atlas_clear_thread_stream()
+    g.replay()
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(replays):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / n_launch
+        best = ms if best is None else min(best, ms)
+    del g
+    return best
+
+
 def launch_spread(torch, fn, n_iter: int) -> dict:
     """p10 / median / p90 of the per-call time of fn(i) over n_iter >= 100
     back-to-back calls, from a HIP event recorded after every call.  This is a
@@ -136,11 +167,16 @@ def gemv_bench(torch, lib, orc_free_rng, quick: bool) -> dict:
 
         ms = time_launches(torch, run, copies * (3 if quick else 10))
         gbs = alg / (ms * 1e-3) / 1e9
+        ms_g = time_graph(torch, lib, run, copies * 2)
+        gbs_g = alg / (ms_g * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
                      "frac": round(gbs / HBM_PEAK_GBS, 3), "bytes": alg, "rotating_copies": copies,
+                     "graph_us": round(ms_g * 1e3, 2), "graph_GB_s": round(gbs_g, 1),
+                     "graph_frac": round(gbs_g / HBM_PEAK_GBS, 3),
                      "spread": launch_spread(torch, run, copies * (3 if quick else 10))}
         sp = out[name]["spread"]
         log(f"gemv {name}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}); "
+            f"in a graph {ms_g * 1e3:.2f} us ({gbs_g / HBM_PEAK_GBS:.1%}); "
             f"per launch p10/median/p90 {sp['p10_us']}/{sp['median_us']}/{sp['p90_us']} us")
         W.free()
         if S:
@@ -260,7 +296,7 @@ def decode_bench(model_mod, fmt: int, prompt, steps: int, warmup: int, seed: int
     # the prompt: token by token (the reference's loop), then through the
     # multi-row prefill step; the second leaves the state the decode continues
     pre = {}
-    # 128-row chunks take the tiled MFMA GEMM
+    # 128-row chunks take hipBLASLt (bf16, int8) or the tiled MFMA GEMM (int4)
     for chunk in (1, 16, 128):
         m.reset()
         m.set_prefill_chunk(chunk)
@@ -613,6 +649,8 @@ def main() -> int:
         "int4": quant["int4"],
         "ragged_batch": ragged,
         "prefill_bf16": PREFILL.get(am.W_BF16),
+        "prefill_int8": PREFILL.get(am.W_INT8),
+        "prefill_int4": PREFILL.get(am.W_INT4),
         "checkpoint_load": load_res,
         "gemv_microbench": micro,
         "attention_microbench": attn,
