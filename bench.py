@@ -97,10 +97,11 @@ def time_graph(torch, lib, fn, n_launch: int, replays: int = 5) -> float:
     torch.cuda.synchronize()
     best = None
     for _ in range(replays):
+        # replay() launches on the current stream: the events go there too
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
+        e0.record()
         g.replay()
-        e1.record(s)
+        e1.record()
         e1.synchronize()
         ms = e0.elapsed_time(e1) / n_launch
         best = ms if best is None else min(best, ms)
