@@ -159,38 +159,47 @@ static int get_plan(BlasRows* b, const void* w, int fmt, int M, int K, int lda, 
         return ATLAS_EUNSUPPORTED;
     }
     // time up to four candidates on the staging buffers (their contents are
-    // overwritten by the real call that follows)
+    // overwritten by the real call that follows): two warm-up calls (the first
+    // loads the candidate's kernels), then the fastest of five single calls
     int best = 0;
     if (n_res > 1) {
-        hipEvent_t e0 = nullptr, e1 = nullptr;
-        ATLAS_HIP(hipEventCreate(&e0));
-        if (hipEventCreate(&e1) != hipSuccess) {
-            (void)hipEventDestroy(e0);
+        constexpr int kRuns = 5;
+        hipEvent_t ev[kRuns + 1] = {};
+        bool ev_ok = true;
+        for (hipEvent_t& e : ev) ev_ok = ev_ok && hipEventCreate(&e) == hipSuccess;
+        if (!ev_ok) {
+            for (hipEvent_t e : ev)
+                if (e) (void)hipEventDestroy(e);
             (void)hipGetLastError();
+            destroy_plan(p);
             set_error(ATLAS_EHIP, "blas rows: event creation failed");
             return ATLAS_EHIP;
         }
         const Scalars sc;
-        float best_ms = 0.f;
+        float best_ms = -1.f;
         for (int i = 0; i < n_res && i < 4; ++i) {
-            bool run_ok = true;
-            for (int r = 0; r < 4 && run_ok; ++r) {
-                if (r == 1) run_ok = hipEventRecord(e0, st) == hipSuccess;
-                run_ok = run_ok && hipblasLtMatmul(b->h, p.desc, sc.one(fmt), w, p.la, b->xs, p.lb,
-                                                   sc.zero(fmt), b->d, p.lc, b->d, p.lc, &res[i].algo,
-                                                   b->ws, kWorkspace, st) == HIPBLAS_STATUS_SUCCESS;
+            auto run = [&] {
+                return hipblasLtMatmul(b->h, p.desc, sc.one(fmt), w, p.la, b->xs, p.lb, sc.zero(fmt),
+                                       b->d, p.lc, b->d, p.lc, &res[i].algo, b->ws, kWorkspace,
+                                       st) == HIPBLAS_STATUS_SUCCESS;
+            };
+            bool ok_i = run() && run();
+            for (int r = 0; r < kRuns && ok_i; ++r) ok_i = hipEventRecord(ev[r], st) == hipSuccess && run();
+            ok_i = ok_i && hipEventRecord(ev[kRuns], st) == hipSuccess &&
+                   hipEventSynchronize(ev[kRuns]) == hipSuccess;
+            float ms = 1e30f;
+            for (int r = 0; r < kRuns && ok_i; ++r) {
+                float t = 0.f;
+                ok_i = hipEventElapsedTime(&t, ev[r], ev[r + 1]) == hipSuccess;
+                ms = std::min(ms, t);
             }
-            float ms = 0.f;
-            run_ok = run_ok && hipEventRecord(e1, st) == hipSuccess &&
-                     hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
-            if (run_ok && (i == 0 || ms < best_ms)) {
+            if (ok_i && (best_ms < 0.f || ms < best_ms)) {
                 best_ms = ms;
                 best = i;
             }
             (void)hipGetLastError();
         }
-        (void)hipEventDestroy(e0);
-        (void)hipEventDestroy(e1);
+        for (hipEvent_t e : ev) (void)hipEventDestroy(e);
     }
     p.algo = res[best].algo;
     if (b->plans.size() < kMaxPlans) {
