@@ -260,7 +260,8 @@ int blas_rows_launch(BlasRows* b, const GemvArgs& a, hipStream_t st) {
 }
 
 int blas_rows_gemm(BlasRows* b, const GemvArgs& a, int n, hipStream_t st) {
-    ATLAS_REQUIRE(b && a.fmt == WF_BF16 && n > 0 && n <= b->max_n && a.M > 0 && a.K > 0,
+    ATLAS_REQUIRE(b && (a.fmt == WF_BF16 || a.fmt == WF_I8) && n > 0 && n <= b->max_n && a.M > 0 &&
+                      a.K > 0,
                   "blas rows: bad arguments");
     ATLAS_REQUIRE(a.M <= b->max_m && a.K <= b->max_k, "blas rows: %d x %d beyond the staging buffers",
                   a.M, a.K);
@@ -270,6 +271,7 @@ int blas_rows_gemm(BlasRows* b, const GemvArgs& a, int n, hipStream_t st) {
 
 uint16_t* blas_rows_xs(BlasRows* b) { return b ? b->xs : nullptr; }
 float* blas_rows_d(BlasRows* b) { return b ? b->d : nullptr; }
+float* blas_rows_xscale(BlasRows* b) { return b ? b->xscale : nullptr; }
 int blas_rows_max_n(const BlasRows* b) { return b ? b->max_n : 0; }
 
 }  // namespace atlas

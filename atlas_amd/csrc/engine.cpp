@@ -1052,27 +1052,34 @@ int bmm(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int ep
 }
 
 // A prompt chunk of 17..128 rows whose four GEMMs per layer all take the
-// hipBLASLt path (bf16, post-norm): their activation split and product
-// combine then live in the neighbouring kernels instead of kernels of their
-// own -- the split of x in the residual RMSNorm that produces it (and once
-// after the embedding), the QKV combine in qkv_post, the W_o / W_down combine
-// in the residual RMSNorm that consumes it, and the gate/up combine with its
-// SwiGLU in one kernel that writes the W_down input split.  Same values as
-// the separate kernels: every sum, product and rounding is the same.
-bool blas_chunk(atlas_model* m, int n) {
+// hipBLASLt path (post-norm): their activation split and product combine then
+// live in the neighbouring kernels where those see whole rows -- the split of
+// x in the residual RMSNorm that produces it (and once after the embedding),
+// the QKV combine in qkv_post, the W_o / W_down combine in the residual
+// RMSNorm that consumes it; for bf16 also the attention output's split in the
+// prompt attention and the gate/up combine with its SwiGLU in one kernel that
+// writes the W_down input split (int8 digits need a whole row's maximum, so
+// those two keep their own split).  Same values as the separate kernels:
+// every sum, product and rounding is the same.  Returns the weight format
+// (WF_BF16 or WF_I8), or 0 when the chunk takes the unfused path.
+int blas_chunk(atlas_model* m, int n) {
     if (!m->blas || !m->fused || !m->cfg.post_norm || n <= 16 || n > blas_rows_max_n(m->blas))
-        return false;
+        return 0;
+    const int fmt = m->L[0].qkv.fmt;
+    if (fmt != WF_BF16 && fmt != WF_I8) return 0;
     for (const LayerW& L : m->L)
         for (const DevMat* w : {&L.qkv, &L.wo, &L.gu, &L.down}) {
             GemvArgs a = gemv_args(*w, m->x, m->y, w == &L.gu ? EPI_SILU_MUL : EPI_STORE);
             a.N = n;
             a.x_stride_n = w->cols;
             a.x_stride_k = 1;
-            if (w->fmt != WF_BF16 || !gemm_rows_ok(a)) return false;
+            if (w->fmt != fmt || !gemm_rows_ok(a) || (fmt == WF_I8 && w->cols > kDigitsMaxK))
+                return 0;
         }
-    return m->L[0].qkv.rows == m->qkv_rows && m->L[0].wo.rows == m->cfg.d_model &&
-           m->L[0].down.rows == m->cfg.d_model && m->L[0].gu.rows % 4 == 0 &&
-           m->cfg.d_model % 8 == 0;
+    const bool ok = m->L[0].qkv.rows == m->qkv_rows && m->L[0].wo.rows == m->cfg.d_model &&
+                    m->L[0].down.rows == m->cfg.d_model && m->L[0].gu.rows % 4 == 0 &&
+                    m->cfg.d_model % 8 == 0;
+    return ok ? fmt : 0;
 }
 
 // the library GEMM of w against the split rows in the context's staging rows
@@ -1092,11 +1099,15 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
     const atlas_model_config& c = m->cfg;
     const bool with_head = !prompt_chunk;
     const int d = c.d_model;
-    const bool bc = prompt_chunk && long_ctx && blas_chunk(m, n);
+    const int bfmt = prompt_chunk && long_ctx ? blas_chunk(m, n) : 0;
+    const bool bc = bfmt != 0, b8 = bfmt == WF_I8;
     uint16_t* xs = bc ? blas_rows_xs(m->blas) : nullptr;      // split GEMM input rows
-    float* dd = bc ? blas_rows_d(m->blas) : nullptr;          // hi / lo product rows
+    int8_t* xd = (int8_t*)xs;                                 // (int8: digit rows)
+    float* xsc = bc ? blas_rows_xscale(m->blas) : nullptr;    // (int8: their row scales)
+    float* dd = bc ? blas_rows_d(m->blas) : nullptr;          // product rows
     TRY(embed_launch(m->embed, c.vocab, d, m->tok_dev, 0, m->x, d, n, m->st));
-    if (bc) TRY(split_rows_launch(m->x, d, n, d, xs, m->st));
+    if (bc && b8) TRY(digits_rows_launch(m->x, d, n, d, xd, xsc, m->st));
+    else if (bc) TRY(split_rows_launch(m->x, d, n, d, xs, m->st));
     for (int li = 0; li < c.n_layers; ++li) {
         LayerW& L = m->L[li];
         const float* xin = m->x;
@@ -1108,7 +1119,13 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
         else TRY(bmm(m, L.qkv, xin, m->qkv, n, EPI_STORE));
         QkvPostArgs q{};
         if (bc) {
-            q.src = dd;
+            if (b8) {
+                q.src_d = (const int*)dd;
+                q.src_ws = L.qkv.scales;
+                q.src_xs = xsc;
+            } else {
+                q.src = dd;
+            }
             q.src_stride = L.qkv.rows;
             q.src_lo = (long)n * L.qkv.rows;
         }
@@ -1139,14 +1156,16 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             // a prompt chunk (one sequence, consecutive positions, one slot):
             // 16 rows share each K/V tile
             if (prompt_chunk && attn_prefill_ok(a)) {
-                if (bc) {
+                if (bc && !b8) {
                     a.out_split = xs;       // the W_o input rows, split
                     a.split_lo = (long)n * d;
                 }
                 TRY(attn_prefill_launch(a, n, m->st));
+                if (b8) TRY(digits_rows_launch(m->att, d, n, d, xd, xsc, m->st));
             } else {
                 TRY(attn_batch_launch(a, sp, n, m->st));
-                if (bc) TRY(split_rows_launch(m->att, d, n, d, xs, m->st));
+                if (b8) TRY(digits_rows_launch(m->att, d, n, d, xd, xsc, m->st));
+                else if (bc) TRY(split_rows_launch(m->att, d, n, d, xs, m->st));
             }
         } else if (m->fused) {
             // one launch: every sequence's QK-norm/RoPE/KV write and attention
@@ -1179,6 +1198,21 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             const size_t np = (size_t)c.n_heads * m->attn_splits_unfused;
             a.part_m = m->attn_part; a.part_l = m->attn_part + np; a.part_o = m->attn_part + 2 * np;
             TRY(attn_launch(a, m->attn_splits_unfused, m->st));
+        }
+        if (bc && b8) {
+            const int h = L.gu.rows / 2;
+            TRY(blas_gemm(m, L.wo, n));
+            TRY(residual_rmsnorm_digits_launch(m->x, (const int*)dd, L.wo.scales, xsc, L.attn_norm, d,
+                                               n, d, c.rms_eps, xd, m->st));
+            TRY(blas_gemm(m, L.gu, n));
+            TRY(combine_digits_launch((const int*)dd, n, L.gu.rows, L.gu.scales, xsc, EPI_SILU_MUL,
+                                      m->h, h, 1, m->st));
+            TRY(digits_rows_launch(m->h, h, n, h, xd, xsc, m->st));
+            TRY(blas_gemm(m, L.down, n));
+            TRY(residual_rmsnorm_digits_launch(m->x, (const int*)dd, L.down.scales, xsc, L.ffn_norm,
+                                               d, n, d, c.rms_eps,
+                                               li + 1 < c.n_layers ? xd : nullptr, m->st));
+            continue;
         }
         if (bc) {
             TRY(blas_gemm(m, L.wo, n));

@@ -109,6 +109,75 @@ int residual_rmsnorm_rows_launch(float* x, const float* d, long lo_off, const fl
     return ATLAS_OK;
 }
 
+// The int8 prompt chunk's form: y[i] = (D0 + (D1 + D2 / 128) / 128) * s_b * ws[i]
+// from the library GEMM's three int32 product planes (row b at d + b*n, the
+// planes `plane` apart; s_b = xscale[b], the input digits' row scale), formed
+// as combine_digits_kernel forms it; then x += rmsnorm(y) * w as above, and,
+// when xd is non-null, the new x row as three int8 digit rows (xd rows b,
+// rows + b, 2 rows + b) with its scale replacing xscale[b], as
+// digits_rows_kernel writes them.
+__global__ __launch_bounds__(1024) void residual_rmsnorm_digits_kernel(
+    float* __restrict__ x, const int* __restrict__ d, long plane, const float* __restrict__ ws,
+    float* __restrict__ xscale, const float* __restrict__ w, int n, long ld, float eps,
+    int8_t* __restrict__ xd) {
+    __shared__ float redm[16];
+    const int b = blockIdx.x, rows = gridDim.x;
+    float* xb = x + b * ld;
+    const int* d0 = d + (long)b * n;
+    const float sb = xscale[b];          // read before any thread replaces it
+    auto yv = [&](int i) {
+        const float lo = (float)d0[i + plane] + (float)d0[i + 2 * plane] * (1.0f / 128.f);
+        return ((float)d0[i] + lo * (1.0f / 128.f)) * sb * ws[i];
+    };
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float y = yv(i);
+        ss += y * y;
+    }
+    ss = block_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = xb[i] + yv(i) * inv * w[i];
+        xb[i] = v;
+        mx = fmaxf(mx, fabsf(v));
+    }
+    if (!xd) return;
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = redm[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) mx = fmaxf(mx, redm[i]);
+    const float dinv = mx > 0.f ? 127.0f / mx : 0.f;
+    if (threadIdx.x == 0) xscale[b] = mx / 127.0f;
+    auto digit = [](float f) { return (int8_t)(int)fminf(fmaxf(rintf(f), -127.f), 127.f); };
+    int8_t* o0 = xd + (long)b * n;
+    int8_t* o1 = xd + (long)(rows + b) * n;
+    int8_t* o2 = xd + (long)(2 * rows + b) * n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float u = xb[i] * dinv;       // this thread's own store above
+        const int8_t q0 = digit(u);
+        const float r1 = (u - (float)q0) * 128.f;
+        const int8_t q1 = digit(r1);
+        const float r2 = (r1 - (float)q1) * 128.f;
+        o0[i] = q0;
+        o1[i] = q1;
+        o2[i] = digit(r2);
+    }
+}
+
+int residual_rmsnorm_digits_launch(float* x, const int* d, const float* ws, float* xscale,
+                                   const float* w, int n, int rows, long ld, float eps, int8_t* xd,
+                                   hipStream_t st) {
+    ATLAS_REQUIRE(x && d && ws && xscale && w && n > 0 && rows > 0,
+                  "residual_rmsnorm_digits: bad arguments");
+    const int threads = n >= 1024 ? 1024 : ((n + 63) / 64) * 64;
+    hipLaunchKernelGGL(residual_rmsnorm_digits_kernel, dim3(rows), dim3(threads), 0, st, x, d,
+                       (long)rows * n, ws, xscale, w, n, ld, eps, xd);
+    ATLAS_LAUNCH_CHECK("residual_rmsnorm_digits");
+    return ATLAS_OK;
+}
+
 int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, long ld, float eps,
                    hipStream_t st) {
     ATLAS_REQUIRE(x && w && out && n > 0 && rows > 0, "rmsnorm: bad arguments");
@@ -143,8 +212,16 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
     const int slot = a.slot_dev ? a.slot_dev[s] : 0;
     const long cache_off = (long)slot * a.slot_stride + ((long)pos * nkv) * HD;
     // element off of this sequence's q|k|v: in place, or hi + lo product rows
-    const long src_off = a.src ? (long)s * a.src_stride : 0;
-    auto in = [&](long off) { return a.src ? a.src[off] + a.src[a.src_lo + off] : qkv[off]; };
+    const long src_off = (a.src || a.src_d) ? (long)s * a.src_stride : 0;
+    auto in = [&](long off) {
+        if (a.src_d) {
+            // int8 digit products: planes src_lo apart, scales per row and column
+            const int* p = a.src_d + off;
+            const float lo = (float)p[a.src_lo] + (float)p[2 * a.src_lo] * (1.0f / 128.f);
+            return ((float)p[0] + lo * (1.0f / 128.f)) * a.src_xs[s] * a.src_ws[off - src_off];
+        }
+        return a.src ? a.src[off] + a.src[a.src_lo + off] : qkv[off];
+    };
 
     if (hidx >= nq + nkv) {
         // V head: copy into the cache

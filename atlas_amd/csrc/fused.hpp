@@ -28,6 +28,12 @@ struct QkvPostArgs {
     // (the library GEMM's hi and lo product rows); q is written to qkv
     const float* src;
     long src_stride, src_lo;
+    // non-null (src null): the int8 digit products instead, element e of
+    // sequence s = (P0 + (P1 + P2 / 128) / 128) * src_xs[s] * src_ws[column]
+    // with planes P0..P2 src_lo apart, as combine_digits_kernel forms it
+    const int* src_d;
+    const float* src_ws;
+    const float* src_xs;
 };
 
 struct ArgmaxArgs {
@@ -84,6 +90,13 @@ int residual_rmsnorm_launch(float* x, const float* y, const float* w, int n, int
 // also written as bf16 hi rows (xs row b) and lo rows (xs row rows + b)
 int residual_rmsnorm_rows_launch(float* x, const float* d, long lo_off, const float* w, int n, int rows,
                                  long ld, float eps, uint16_t* xs, hipStream_t st);
+// x += rmsnorm(y) * w with y from the int8 digit products (three int32 planes
+// of rows x n, weight column scales ws, input row scales xscale); with xd
+// non-null the new x rows are also written as int8 digit rows (xd rows b,
+// rows + b, 2 rows + b) and xscale[b] becomes their scale
+int residual_rmsnorm_digits_launch(float* x, const int* d, const float* ws, float* xscale,
+                                   const float* w, int n, int rows, long ld, float eps, int8_t* xd,
+                                   hipStream_t st);
 int qkv_post_launch(const QkvPostArgs& a, int n_seq, hipStream_t st);
 int qk_norm_launch(float* x, const float* w, int n_heads, int hd, float eps, hipStream_t st);
 int rope_tab_launch(float* x, const float* c, const float* s, int n_heads, int hd, int pos,

@@ -74,12 +74,14 @@ int blas_rows_create(BlasRows** out, int max_n, int max_m, int max_k);
 void blas_rows_destroy(BlasRows* b);
 int blas_rows_launch(BlasRows* b, const GemvArgs& a, hipStream_t st);   // bf16/int8, gemm_rows_ok(a)
 // The library GEMM alone, for callers that fuse the split and the combine into
-// their neighbouring kernels: blas_rows_xs(b) holds the 2n split rows of X (K
-// wide: hi rows 0..n-1, lo rows n..2n-1), blas_rows_d(b) receives the 2n
-// product rows (M wide, f32).  n <= blas_rows_max_n(b).
+// their neighbouring kernels: blas_rows_xs(b) holds X's split rows (K wide;
+// bf16: hi rows 0..n-1, lo rows n..2n-1; int8: digit rows 0..3n-1 with the
+// row scales in blas_rows_xscale(b)), blas_rows_d(b) receives the product
+// rows (M wide; 2n f32 or 3n int32).  n <= blas_rows_max_n(b).
 int blas_rows_gemm(BlasRows* b, const GemvArgs& a, int n, hipStream_t st);
 uint16_t* blas_rows_xs(BlasRows* b);
 float* blas_rows_d(BlasRows* b);
+float* blas_rows_xscale(BlasRows* b);
 int blas_rows_max_n(const BlasRows* b);
 // the two element-wise halves (skinny.hip): rows n of x (f32, stride sn) ->
 // out rows n (bf16 hi) and N + n (bf16 lo); y[n, m] = d[n, m] + d[N + n, m]
