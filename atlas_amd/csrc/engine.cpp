@@ -232,8 +232,10 @@ int gemv(atlas_model* m, const DevMat& w, const float* x, float* y, int epi) {
     return gemv_launch(gemv_args(w, x, y, epi), m->st);
 }
 
-int skinny(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int epi) {
+int skinny(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int epi,
+           int* defer_splits = nullptr) {
     GemvArgs a = gemv_args(w, x, y, epi);
+    a.defer_splits = defer_splits;
     a.N = n;
     a.x_stride_n = w.cols;
     a.x_stride_k = 1;
@@ -1051,6 +1053,31 @@ int bmm(atlas_model* m, const DevMat& w, const float* x, float* y, int n, int ep
     return skinny(m, w, x, y, n, epi);
 }
 
+// y = w . x rows, then x += rmsnorm(y) * norm_w: where the GEMM splits K
+// (the 2-8-row direct-load kernels), the norm sums its partials itself and
+// the split-K reduce launch goes away (same y bit for bit)
+int bmm_resnorm(atlas_model* m, const DevMat& w, const float* x, float* y, int n,
+                const float* norm_w) {
+    const atlas_model_config& c = m->cfg;
+    int splits = 0;
+    const bool fold = n > 1 && c.d_model <= 8192;
+    if (!fold) TRY(bmm(m, w, x, y, n, EPI_STORE));
+    else TRY(skinny(m, w, x, y, n, EPI_STORE, &splits));
+    if (splits > 8) {
+        // more partials than the folded norm unrolls: sum them as the reduce does
+        GemvArgs a = gemv_args(w, x, y, EPI_STORE);
+        a.N = n;
+        a.y_stride_n = w.rows;
+        a.y_stride_m = 1;
+        TRY(skinny_reduce_launch(a, m->gemm_part, splits, m->st));
+        splits = 0;
+    }
+    if (splits > 0)
+        return residual_rmsnorm_parts_launch(m->x, m->gemm_part, splits, norm_w, c.d_model, n,
+                                             c.d_model, c.rms_eps, m->st);
+    return residual_rmsnorm_launch(m->x, y, norm_w, c.d_model, n, c.d_model, c.rms_eps, m->st);
+}
+
 // A prompt chunk of 17..128 rows whose four GEMMs per layer all take the
 // hipBLASLt path (post-norm): their activation split and product combine then
 // live in the neighbouring kernels where those see whole rows -- the split of
@@ -1225,13 +1252,12 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
                                              li + 1 < c.n_layers ? xs : nullptr, m->st));
             continue;
         }
-        TRY(bmm(m, L.wo, m->att, m->y, n, EPI_STORE));
         if (c.post_norm) {
-            TRY(residual_rmsnorm_launch(m->x, m->y, L.attn_norm, d, n, d, c.rms_eps, m->st));
+            TRY(bmm_resnorm(m, L.wo, m->att, m->y, n, L.attn_norm));
             TRY(bmm(m, L.gu, m->x, m->h, n, EPI_SILU_MUL));
-            TRY(bmm(m, L.down, m->h, m->y, n, EPI_STORE));
-            TRY(residual_rmsnorm_launch(m->x, m->y, L.ffn_norm, d, n, d, c.rms_eps, m->st));
+            TRY(bmm_resnorm(m, L.down, m->h, m->y, n, L.ffn_norm));
         } else {
+            TRY(bmm(m, L.wo, m->att, m->y, n, EPI_STORE));
             TRY(ew_launch(EW_ADD, m->x, m->y, m->x, 0.f, (long)n * d, m->st));
             TRY(rmsnorm_launch(m->x, L.ffn_norm, m->xn, d, n, d, c.rms_eps, m->st));
             TRY(bmm(m, L.gu, m->xn, m->h, n, EPI_SILU_MUL));
@@ -1242,7 +1268,11 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
     if (!with_head) return ATLAS_OK;
     TRY(rmsnorm_launch(m->x, m->final_norm, m->xn, d, n, d, c.rms_eps, m->st));
     TRY(bmm(m, m->lm_head, m->xn, m->logits, n, EPI_STORE));
-    // greedy choice of every row into choice_dev (last maximum wins)
+    // greedy choice of every row into choice_dev (last maximum wins): one
+    // launch pair for all rows while their partial keys fit, else per row
+    const int parts = std::min(512, (c.vocab + 255) / 256);
+    if ((long)parts * n <= ARGMAX_MAX_PARTS)
+        return argmax_rows_launch(m->logits, c.vocab, c.vocab, n, m->argpart, m->choice_dev, m->st);
     for (int j = 0; j < n; ++j) {
         ArgmaxArgs g{};
         g.x = m->logits + (size_t)j * c.vocab; g.n = c.vocab; g.part = m->argpart;

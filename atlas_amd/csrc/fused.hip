@@ -178,6 +178,80 @@ int residual_rmsnorm_digits_launch(float* x, const int* d, const float* ws, floa
     return ATLAS_OK;
 }
 
+// residual_rmsnorm_kernel reading y as the split-K partials of the GEMM
+// that produced it: y[b][i] = sum over s of part[(s * rows + b) * n + i], in
+// split order from 0.f as skinny_reduce_kernel sums them (so y, and all that
+// follows, is bit-identical to the reduce-then-norm pair).  One block per row
+// (the norm needs the whole row): a thread holds its EPT elements' y, x and w
+// in registers, every load issued before the first sum (S splits unrolled),
+// so the block waits for one round trip of loads instead of one per split.
+template <int S, int EPT>
+__global__ __launch_bounds__(1024) void residual_rmsnorm_parts_kernel(float* __restrict__ x,
+                                                                      const float* __restrict__ part,
+                                                                      const float* __restrict__ w, int n,
+                                                                      long ld, float eps) {
+    const int b = blockIdx.x, rows = gridDim.x;
+    float* xb = x + b * ld;
+    const float* pb = part + (long)b * n;
+    const long plane = (long)rows * n;
+    float pv[EPT][S], xv[EPT], wv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = threadIdx.x + 1024 * j;
+        const bool ok = i < n;
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) pv[j][sp] = ok ? pb[sp * plane + i] : 0.f;
+        xv[j] = ok ? xb[i] : 0.f;
+        wv[j] = ok ? w[i] : 0.f;
+    }
+    float y[EPT];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        float sum = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) sum += pv[j][sp];
+        y[j] = sum;
+        if (threadIdx.x + 1024 * j < n) ss += sum * sum;
+    }
+    ss = block_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = threadIdx.x + 1024 * j;
+        if (i < n) xb[i] = xv[j] + y[j] * inv * wv[j];
+    }
+}
+
+template <int S>
+static int parts_go(float* x, const float* part, const float* w, int n, int rows, long ld, float eps,
+                    hipStream_t st) {
+    if (n <= 4096)
+        hipLaunchKernelGGL((residual_rmsnorm_parts_kernel<S, 4>), dim3(rows), dim3(1024), 0, st, x, part,
+                           w, n, ld, eps);
+    else
+        hipLaunchKernelGGL((residual_rmsnorm_parts_kernel<S, 8>), dim3(rows), dim3(1024), 0, st, x, part,
+                           w, n, ld, eps);
+    ATLAS_LAUNCH_CHECK("residual_rmsnorm_parts");
+    return ATLAS_OK;
+}
+
+int residual_rmsnorm_parts_launch(float* x, const float* part, int splits, const float* w, int n,
+                                  int rows, long ld, float eps, hipStream_t st) {
+    ATLAS_REQUIRE(x && part && w && splits >= 1 && splits <= 8 && n > 0 && n <= 8192 && rows > 0,
+                  "residual_rmsnorm_parts: %d splits, n %d", splits, n);
+    switch (splits) {
+    case 1: return parts_go<1>(x, part, w, n, rows, ld, eps, st);
+    case 2: return parts_go<2>(x, part, w, n, rows, ld, eps, st);
+    case 3: return parts_go<3>(x, part, w, n, rows, ld, eps, st);
+    case 4: return parts_go<4>(x, part, w, n, rows, ld, eps, st);
+    case 5: return parts_go<5>(x, part, w, n, rows, ld, eps, st);
+    case 6: return parts_go<6>(x, part, w, n, rows, ld, eps, st);
+    case 7: return parts_go<7>(x, part, w, n, rows, ld, eps, st);
+    default: return parts_go<8>(x, part, w, n, rows, ld, eps, st);
+    }
+}
+
 int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, long ld, float eps,
                    hipStream_t st) {
     ATLAS_REQUIRE(x && w && out && n > 0 && rows > 0, "rmsnorm: bad arguments");
@@ -190,6 +264,9 @@ int rmsnorm_launch(const float* x, const float* w, float* out, int n, int rows, 
 int residual_rmsnorm_launch(float* x, const float* y, const float* w, int n, int rows, long ld,
                             float eps, hipStream_t st) {
     ATLAS_REQUIRE(x && y && w && n > 0 && rows > 0, "residual_rmsnorm: bad arguments");
+    // packed rows up to 8192: the register-cached kernel (one split), whose
+    // loads all go out before the first sum (8 rows of 4096: 5.1 -> ~4 us)
+    if (ld == n && n <= 8192) return residual_rmsnorm_parts_launch(x, y, 1, w, n, rows, ld, eps, st);
     const int threads = n >= 1024 ? 1024 : ((n + 63) / 64) * 64;
     hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(threads), 0, st, x, y, w, n, ld,
                        eps);
@@ -535,6 +612,60 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const unsigned long 
         if (step) *step += 1;
         if (pos_inc) *pos_inc += 1;
     }
+}
+
+// Greedy choice of `rows` logit rows (row r at x + r*ld) in two launches:
+// argmax_partial_kernel over a (parts, rows) grid, then one final block per
+// row writing out_u32[r]; the same keys and tie rule (last maximal index) as
+// argmax_launch per row.
+__global__ __launch_bounds__(256) void argmax_partial_rows_kernel(const float* __restrict__ x, int n,
+                                                                  long ld,
+                                                                  unsigned long long* __restrict__ part) {
+    __shared__ unsigned long long red[4];
+    const float* xr = x + blockIdx.y * ld;
+    unsigned long long best = 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        const unsigned long long k = argkey(xr[i], i);
+        best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+        for (int w = 1; w < 4; ++w) b = red[w] > b ? red[w] : b;
+        part[(long)blockIdx.y * gridDim.x + blockIdx.x] = b;
+    }
+}
+
+__global__ __launch_bounds__(1024) void argmax_final_rows_kernel(const unsigned long long* __restrict__ part,
+                                                                 int nparts, uint32_t* __restrict__ out_u32) {
+    __shared__ unsigned long long red[16];
+    const unsigned long long* pr = part + (long)blockIdx.x * nparts;
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < nparts; i += 1024) best = pr[i] > best ? pr[i] : best;
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+        for (int w = 1; w < 16; ++w) b = red[w] > b ? red[w] : b;
+        out_u32[blockIdx.x] = (uint32_t)(b & 0xFFFFFFFFu);
+    }
+}
+
+int argmax_rows_launch(const float* x, int n, long ld, int rows, unsigned long long* part,
+                       uint32_t* out_u32, hipStream_t st) {
+    ATLAS_REQUIRE(x && part && out_u32 && n > 0 && rows > 0 && rows <= 65535, "argmax rows: bad arguments");
+    int parts = (n + 255) / 256;
+    if (parts > 512) parts = 512;
+    ATLAS_REQUIRE((long)parts * rows <= ARGMAX_MAX_PARTS, "argmax rows: %d rows x %d partials exceed %d",
+                  rows, parts, (int)ARGMAX_MAX_PARTS);
+    hipLaunchKernelGGL(argmax_partial_rows_kernel, dim3(parts, rows), dim3(256), 0, st, x, n, ld, part);
+    ATLAS_LAUNCH_CHECK("argmax_partial_rows");
+    hipLaunchKernelGGL(argmax_final_rows_kernel, dim3(rows), dim3(1024), 0, st, part, parts, out_u32);
+    ATLAS_LAUNCH_CHECK("argmax_final_rows");
+    return ATLAS_OK;
 }
 
 int argmax_launch(const ArgmaxArgs& a, hipStream_t st) {

@@ -97,7 +97,16 @@ int residual_rmsnorm_rows_launch(float* x, const float* d, long lo_off, const fl
 int residual_rmsnorm_digits_launch(float* x, const int* d, const float* ws, float* xscale,
                                    const float* w, int n, int rows, long ld, float eps, int8_t* xd,
                                    hipStream_t st);
+// x += rmsnorm(y) * w with y the split-K partials ([splits][rows][n]) of the
+// GEMM that produced it, summed in split order (splits <= 8, n <= 8192)
+int residual_rmsnorm_parts_launch(float* x, const float* part, int splits, const float* w, int n,
+                                  int rows, long ld, float eps, hipStream_t st);
 int qkv_post_launch(const QkvPostArgs& a, int n_seq, hipStream_t st);
+// greedy choice of each of `rows` logit rows (row r at x + r*ld, n logits)
+// into out_u32[r], last maximal index on ties; part holds rows * min(512,
+// ceil(n / 256)) <= ARGMAX_MAX_PARTS keys
+int argmax_rows_launch(const float* x, int n, long ld, int rows, unsigned long long* part,
+                       uint32_t* out_u32, hipStream_t st);
 int qk_norm_launch(float* x, const float* w, int n_heads, int hd, float eps, hipStream_t st);
 int rope_tab_launch(float* x, const float* c, const float* s, int n_heads, int hd, int pos,
                     int max_seq, hipStream_t st);

@@ -42,6 +42,12 @@ struct GemvArgs {
     long ldw;                // bytes between weight rows (multiple of 16); 0 = packed rows
     float* partial;          // skinny / prompt GEMM split-K partials (null: the thread's scratch)
     size_t partial_bytes;    // ... their size
+    // skinny_launch, host side: non-null with EPI_STORE and the caller's
+    // partial buffer, a split-K launch of the 2-8-row direct-load kernels
+    // leaves its partials in `partial` ([splits][N][M], summed in split order
+    // by the consumer) and stores the split count here instead of launching
+    // the reduce; 0 when y was written.
+    int* defer_splits;
     struct BlasRows* blas;   // 17..128 rows of bf16 weights: the caller's hipBLASLt context, or
                              // null (the tiled MFMA kernel)
 };
@@ -59,6 +65,8 @@ constexpr int kGemvMaxNx = 4;
 bool gemv_multi_ok(const GemvArgs& a);
 int gemv_multi_launch(const GemvArgs& a, hipStream_t st);
 size_t skinny_partial_bytes(int M, int N, int K);    // split-K partials of (M, N, K)
+// y = the fixed-order sum of `splits` partials ([splits][N][M]), with a's epilogue
+int skinny_reduce_launch(const GemvArgs& a, const float* partial, int splits, hipStream_t st);
 // 17..128 rows of bf16 weights: the tiled MFMA GEMM (skinny_launch routes there)
 bool gemm_rows_ok(const GemvArgs& a);
 int gemm_rows_launch(const GemvArgs& a, hipStream_t st);

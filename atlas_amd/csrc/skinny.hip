@@ -1043,6 +1043,23 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemvArgs a, const fl
     }
 }
 
+int skinny_reduce_launch(const GemvArgs& a, const float* partial, int splits, hipStream_t st) {
+    ATLAS_REQUIRE(partial && a.y && a.N > 0 && a.M > 0 && splits > 0, "skinny reduce: bad arguments");
+    const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
+    long rb = ((long)a.N * m_out + 255) / 256;
+    if (rb > 4096) rb = 4096;
+    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, a, partial, splits);
+    ATLAS_LAUNCH_CHECK("skinny_reduce");
+    return ATLAS_OK;
+}
+
+// The caller takes the split-K sum over (GemvArgs.defer_splits): plain
+// stores into its own partial buffer only.
+static bool defer_ok(const GemvArgs& a) {
+    return a.defer_splits && a.epi == EPI_STORE && a.partial && a.y_stride_m == 1 &&
+           a.y_stride_n == a.M;
+}
+
 // Split-K partials: the caller's buffer (GemvArgs.partial, e.g. a model's,
 // which a captured step may point at) or the calling thread's scratch.
 static int partial_for(const GemvArgs& a, size_t bytes, float** out) {
@@ -1203,6 +1220,10 @@ static int launch_skinny_i4d(const GemvArgs& a, hipStream_t st) {
     default: i4d_go<8, 4>(a, sv, grid, st, partial, kt_split, cpb_shift); break;
     }
     ATLAS_LAUNCH_CHECK("skinny int4");
+    if (splits > 1 && defer_ok(a)) {
+        *a.defer_splits = splits;
+        return ATLAS_OK;
+    }
     if (splits > 1) {
         const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
         long rb = ((long)a.N * m_out + 255) / 256;
@@ -1245,6 +1266,10 @@ static int launch_skinny_d(const GemvArgs& a, hipStream_t st) {
     default: d_go<FMT, 8, 8>(a, grid, st, partial, pl.kt_split); break;
     }
     ATLAS_LAUNCH_CHECK(FMT == WF_BF16 ? "skinny bf16" : "skinny int8");
+    if (pl.splits > 1 && defer_ok(a)) {
+        *a.defer_splits = pl.splits;
+        return ATLAS_OK;
+    }
     if (pl.splits > 1) {
         const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
         long rb = ((long)a.N * m_out + 255) / 256;
@@ -1759,10 +1784,12 @@ static bool halves_pay(const GemvArgs& a) {
 
 int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
     GemvArgs a = a_in;
+    if (a.defer_splits) *a.defer_splits = 0;
     gemv_fill_int4_index(a);
     if (halves_pay(a)) {
         const int n0 = (a.N + 1) / 2;
         GemvArgs h = a;
+        h.defer_splits = nullptr;        // two launches share the partial buffer
         h.N = n0;
         const int rc = skinny_launch(h, st);
         if (rc) return rc;
