@@ -1105,7 +1105,7 @@ int blas_chunk(atlas_model* m, int n) {
         }
     const bool ok = m->L[0].qkv.rows == m->qkv_rows && m->L[0].wo.rows == m->cfg.d_model &&
                     m->L[0].down.rows == m->cfg.d_model && m->L[0].gu.rows % 4 == 0 &&
-                    m->cfg.d_model % 8 == 0;
+                    m->cfg.d_model % 8 == 0 && (fmt != WF_I8 || m->cfg.d_model <= 8192);
     return ok ? fmt : 0;
 }
 

@@ -116,6 +116,7 @@ int residual_rmsnorm_rows_launch(float* x, const float* d, long lo_off, const fl
 // when xd is non-null, the new x row as three int8 digit rows (xd rows b,
 // rows + b, 2 rows + b) with its scale replacing xscale[b], as
 // digits_rows_kernel writes them.
+template <int EPT>
 __global__ __launch_bounds__(1024) void residual_rmsnorm_digits_kernel(
     float* __restrict__ x, const int* __restrict__ d, long plane, const float* __restrict__ ws,
     float* __restrict__ xscale, const float* __restrict__ w, int n, long ld, float eps,
@@ -125,37 +126,58 @@ __global__ __launch_bounds__(1024) void residual_rmsnorm_digits_kernel(
     float* xb = x + b * ld;
     const int* d0 = d + (long)b * n;
     const float sb = xscale[b];          // read before any thread replaces it
-    auto yv = [&](int i) {
-        const float lo = (float)d0[i + plane] + (float)d0[i + 2 * plane] * (1.0f / 128.f);
-        return ((float)d0[i] + lo * (1.0f / 128.f)) * sb * ws[i];
-    };
+    // every load of the thread's EPT elements before the first use
+    int p0[EPT], p1[EPT], p2[EPT];
+    float xv[EPT], wv[EPT], sv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = threadIdx.x + 1024 * j;
+        const bool ok = i < n;
+        p0[j] = ok ? d0[i] : 0;
+        p1[j] = ok ? d0[i + plane] : 0;
+        p2[j] = ok ? d0[i + 2 * plane] : 0;
+        sv[j] = ok ? ws[i] : 0.f;
+        xv[j] = ok ? xb[i] : 0.f;
+        wv[j] = ok ? w[i] : 0.f;
+    }
+    float y[EPT];
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float y = yv(i);
-        ss += y * y;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const float lo = (float)p1[j] + (float)p2[j] * (1.0f / 128.f);
+        y[j] = ((float)p0[j] + lo * (1.0f / 128.f)) * sb * sv[j];
+        if (threadIdx.x + 1024 * j < n) ss += y[j] * y[j];
     }
     ss = block_sum(ss);
     const float inv = 1.0f / sqrtf(ss / (float)n + eps);
     float mx = 0.f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = xb[i] + yv(i) * inv * w[i];
-        xb[i] = v;
-        mx = fmaxf(mx, fabsf(v));
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = threadIdx.x + 1024 * j;
+        xv[j] = xv[j] + y[j] * inv * wv[j];
+        if (i < n) {
+            xb[i] = xv[j];
+            mx = fmaxf(mx, fabsf(xv[j]));
+        }
     }
     if (!xd) return;
     mx = wave_max(mx);
     if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = mx;
     __syncthreads();
     mx = redm[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) mx = fmaxf(mx, redm[i]);
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, redm[i]);
     const float dinv = mx > 0.f ? 127.0f / mx : 0.f;
     if (threadIdx.x == 0) xscale[b] = mx / 127.0f;
     auto digit = [](float f) { return (int8_t)(int)fminf(fmaxf(rintf(f), -127.f), 127.f); };
     int8_t* o0 = xd + (long)b * n;
     int8_t* o1 = xd + (long)(rows + b) * n;
     int8_t* o2 = xd + (long)(2 * rows + b) * n;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float u = xb[i] * dinv;       // this thread's own store above
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = threadIdx.x + 1024 * j;
+        if (i >= n) break;
+        const float u = xv[j] * dinv;
         const int8_t q0 = digit(u);
         const float r1 = (u - (float)q0) * 128.f;
         const int8_t q1 = digit(r1);
@@ -169,11 +191,14 @@ __global__ __launch_bounds__(1024) void residual_rmsnorm_digits_kernel(
 int residual_rmsnorm_digits_launch(float* x, const int* d, const float* ws, float* xscale,
                                    const float* w, int n, int rows, long ld, float eps, int8_t* xd,
                                    hipStream_t st) {
-    ATLAS_REQUIRE(x && d && ws && xscale && w && n > 0 && rows > 0,
-                  "residual_rmsnorm_digits: bad arguments");
-    const int threads = n >= 1024 ? 1024 : ((n + 63) / 64) * 64;
-    hipLaunchKernelGGL(residual_rmsnorm_digits_kernel, dim3(rows), dim3(threads), 0, st, x, d,
-                       (long)rows * n, ws, xscale, w, n, ld, eps, xd);
+    ATLAS_REQUIRE(x && d && ws && xscale && w && n > 0 && n <= 8192 && rows > 0,
+                  "residual_rmsnorm_digits: bad arguments (n %d)", n);
+    if (n <= 4096)
+        hipLaunchKernelGGL(residual_rmsnorm_digits_kernel<4>, dim3(rows), dim3(1024), 0, st, x, d,
+                           (long)rows * n, ws, xscale, w, n, ld, eps, xd);
+    else
+        hipLaunchKernelGGL(residual_rmsnorm_digits_kernel<8>, dim3(rows), dim3(1024), 0, st, x, d,
+                           (long)rows * n, ws, xscale, w, n, ld, eps, xd);
     ATLAS_LAUNCH_CHECK("residual_rmsnorm_digits");
     return ATLAS_OK;
 }
