@@ -55,6 +55,10 @@ constexpr int kMaxRows = kPrefillChunk;
 // through the tiled MFMA GEMM (gemm_rows_launch), up to this many rows
 // per step, replayed eagerly (the captured steps stop at kMaxRows rows).
 constexpr int kPrefillBig = 128;
+// ... and up to this many rows where the library GEMM serves them (bf16 and
+// int8 weights): at the 7B shapes the GEMMs of a layer cost 1.28 us per
+// prompt token at 127 rows, 0.87 at 255 and 0.68 at 511 (bf16).
+constexpr int kPrefillLib = 512;
 
 struct DevMat {
     int fmt = WF_BF16;
@@ -106,8 +110,10 @@ struct atlas_model {
     std::vector<uint8_t> sliding;
     int hd = 0, kvd = 0, qkv_rows = 0, B = 1;
     int R = 1;                       // rows of the multi-row step buffers: max(B, prefill chunk)
+    int RF = 1;                      // rows with a fused attention, logits and a choice: max(B, 16 or 128)
     int prefill_chunk = kPrefillBig;     // prompt tokens per prefill step (1: token by token)
-    bool big_prefill = false;            // chunks of up to kPrefillBig rows (see kPrefillBig)
+    bool big_prefill = false;            // chunks of up to kPrefillBig rows (kPrefillLib through
+                                         // the library GEMM; see prefill_cap)
     float scale = 1.f;
     std::vector<LayerW> L;
     uint16_t* embed = nullptr;
@@ -439,8 +445,8 @@ int enqueue_step_fused(atlas_model* m, int mode, bool long_ctx) {
             a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
             a.scale = m->scale; a.window = L.window;
             a.part_m = m->attn_part;
-            a.part_l = m->attn_part + (size_t)m->R * c.n_heads * m->attn_splits;
-            a.part_o = m->attn_part + (size_t)2 * m->R * c.n_heads * m->attn_splits;
+            a.part_l = m->attn_part + (size_t)m->RF * c.n_heads * m->attn_splits;
+            a.part_o = m->attn_part + (size_t)2 * m->RF * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
             a.adaptive = 1; a.max_rows = c.max_seq;
             a.rope_row = m->rope_row;
@@ -1206,8 +1212,8 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = m->hd;
             a.scale = m->scale; a.window = L.window;
             a.part_m = m->attn_part;
-            a.part_l = m->attn_part + (size_t)m->R * c.n_heads * m->attn_splits;
-            a.part_o = m->attn_part + (size_t)2 * m->R * c.n_heads * m->attn_splits;
+            a.part_l = m->attn_part + (size_t)m->RF * c.n_heads * m->attn_splits;
+            a.part_o = m->attn_part + (size_t)2 * m->RF * c.n_heads * m->attn_splits;
             a.counters = m->attn_counters;
             a.adaptive = 1; a.max_rows = c.max_seq;
             TRY(attn_fused_launch(a, m->attn_splits, n, m->st));
@@ -1327,11 +1333,19 @@ int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool lo
 // rows of a prefill chunk in one.)
 // k >= 2 prompt tokens of the sequence in KV slot `slot` at positions
 // pos0 .. pos0 + k - 1, as one multi-row step without the lm_head
+// the most prompt rows one step of this model takes
+int prefill_cap(const atlas_model* m) {
+    if (!m->fused) return 1;
+    if (!m->big_prefill) return std::min(m->R, kPrefillChunk);
+    return std::min(m->R, m->blas ? kPrefillLib : kPrefillBig);
+}
+
 int prefill_rows(atlas_model* m, int slot, int pos0, const uint32_t* toks, int k) {
-    ATLAS_REQUIRE(k >= 2 && k <= m->R && k <= kPrefillBig, "prefill: %d rows", k);
+    ATLAS_REQUIRE(k >= 2 && k <= prefill_cap(m), "prefill: %d rows", k);
     ATLAS_REQUIRE(pos0 + k <= m->cfg.max_seq, "prefill: position %d + %d exceeds max_seq %d", pos0,
                   k, m->cfg.max_seq);
-    int host[3][kPrefillBig];
+    static_assert(kPrefillLib >= kPrefillBig, "row caps");
+    int host[3][kPrefillLib];
     for (int j = 0; j < k; ++j) {
         host[0][j] = (int)toks[j];
         host[1][j] = pos0 + j;
@@ -1349,8 +1363,7 @@ int prefill_rows(atlas_model* m, int slot, int pos0, const uint32_t* toks, int k
 }
 
 int prefill(atlas_model* m, const uint32_t* toks, int n) {
-    const int cap = !m->fused ? 1 : m->big_prefill ? kPrefillBig : std::min(m->R, kPrefillChunk);
-    const int chunk = std::min(m->prefill_chunk, cap);
+    const int chunk = std::min(m->prefill_chunk, prefill_cap(m));
     int done = 0;
     while (done < n) {
         const int k = std::min(chunk, n - done);
@@ -1420,7 +1433,10 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
                      attn_fused_supported(c.n_heads, c.n_kv_heads, hd) &&
                      attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && c.d_model % 128 == 0 &&
                      (c.n_heads * hd) % 128 == 0 && c.ffn_hidden % 128 == 0;
-    m->R = std::max(m->B, m->big_prefill ? kPrefillBig : kPrefillChunk);
+    m->RF = std::max(m->B, m->big_prefill ? kPrefillBig : kPrefillChunk);
+    // bf16 / int8 prompt chunks through the library GEMM take up to kPrefillLib rows
+    const bool lib_rows = m->big_prefill && (fmt == WF_BF16 || fmt == WF_I8);
+    m->R = std::max(m->RF, lib_rows ? kPrefillLib : 0);
     // scale = attn_factor / sqrt(head_dim) (lib.rs:632, 1331-1335)
     m->scale = 1.0f / sqrtf((float)hd);
     const float af = c.yarn ? c.yarn_attn_factor : 1.0f;
@@ -1466,12 +1482,12 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         dalloc(m, (void**)&m->att, (size_t)R * d * 4) ||
         dalloc(m, (void**)&m->h, (size_t)R * 2 * big * 4) ||
         dalloc(m, (void**)&m->xb, (size_t)R * d * 4) || dalloc(m, (void**)&m->y2, (size_t)R * d * 4) ||
-        dalloc(m, (void**)&m->logits, (size_t)R * c.vocab * 4) ||
+        dalloc(m, (void**)&m->logits, (size_t)m->RF * c.vocab * 4) ||
         dalloc(m, (void**)&m->pos_dev, (size_t)R * 4) || dalloc(m, (void**)&m->slot_dev, (size_t)R * 4) ||
         dalloc(m, (void**)&m->tok_dev, (size_t)R * 4) || dalloc(m, (void**)&m->step_dev, 4) ||
         dalloc(m, (void**)&m->hist_len, 4) ||
         dalloc(m, (void**)&m->hist, (size_t)(c.max_seq + 2) * 4) ||
-        dalloc(m, (void**)&m->choice_dev, (size_t)R * 4) ||
+        dalloc(m, (void**)&m->choice_dev, (size_t)m->RF * 4) ||
         dalloc(m, (void**)&m->argpart, (size_t)ARGMAX_MAX_PARTS * 8) ||
         dalloc(m, (void**)&m->samp_cfg, sizeof(SampleCfg)) || dalloc(m, (void**)&m->rng_dev, 8) ||
         dalloc(m, (void**)&m->suppress_dev, 64 * 4))
@@ -1522,11 +1538,12 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
                 max_m = std::max(max_m, sh[0]);
                 max_k = std::max(max_k, sh[1]);
             }
-            if (blas_rows_create(&m->blas, kPrefillBig, max_m, max_k) != ATLAS_OK) {
+            if (blas_rows_create(&m->blas, kPrefillLib, max_m, max_k) != ATLAS_OK) {
                 m->blas = nullptr;
                 if (atlas_last_error_code() == ATLAS_ENOMEM) return fail(m);
                 atlas_clear_error();
             }
+            if (m->blas) m->prefill_chunk = kPrefillLib;    // the default: the longest step
         }
     }
     // fused step: post-norm model whose attention shape the fused kernel
@@ -1537,7 +1554,7 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
     // split partials: the fused kernel's B x n_heads x attn_splits, the
     // long-context step's n_heads x attn_splits_long, or the long-context
     // batch step's n x n_heads x attn_splits_batch[n]
-    size_t part_slots = std::max((size_t)R * c.n_heads * m->attn_splits,
+    size_t part_slots = std::max((size_t)m->RF * c.n_heads * m->attn_splits,
                                  (size_t)c.n_heads * m->attn_splits_long);
     for (int n = 1; n <= R; ++n) {
         const int sp = attn_batch_splits_for(c.n_kv_heads, n, c.max_seq);
@@ -1545,9 +1562,9 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         part_slots = std::max(part_slots, (size_t)n * c.n_heads * sp);
     }
     if (dalloc(m, (void**)&m->attn_part, part_slots * (hd + 2) * 4) ||
-        dalloc(m, (void**)&m->attn_counters, (size_t)R * c.n_kv_heads * 4))
+        dalloc(m, (void**)&m->attn_counters, (size_t)m->RF * c.n_kv_heads * 4))
         return fail(m);
-    if (hipMemset(m->attn_counters, 0, (size_t)R * c.n_kv_heads * 4) != hipSuccess) {
+    if (hipMemset(m->attn_counters, 0, (size_t)m->RF * c.n_kv_heads * 4) != hipSuccess) {
         set_error(ATLAS_EHIP, "counter init failed");
         return fail(m);
     }
@@ -1747,8 +1764,8 @@ ATLAS_API int atlas_model_set_long_context(atlas_model* m, int from_pos) {
 
 ATLAS_API int atlas_model_set_prefill_chunk(atlas_model* m, int chunk) {
     ATLAS_REQUIRE(m, "set_prefill_chunk: null model");
-    ATLAS_REQUIRE(chunk >= 1 && chunk <= kPrefillBig, "set_prefill_chunk: %d outside 1..%d", chunk,
-                  kPrefillBig);
+    ATLAS_REQUIRE(chunk >= 1 && chunk <= kPrefillLib, "set_prefill_chunk: %d outside 1..%d", chunk,
+                  kPrefillLib);
     m->prefill_chunk = chunk;
     return ATLAS_OK;
 }
@@ -2264,7 +2281,7 @@ ATLAS_API int atlas_model_generate_batch(atlas_model* m, const uint32_t* prompts
         for (int i = 0; i < n_seqs; ++i) {
             if (done[i]) continue;
             while (prompt_lens[i] - 1 - cursor[i] > kMaxRows) {
-                const int k = std::min(std::min(m->prefill_chunk, kPrefillBig),
+                const int k = std::min(std::min(m->prefill_chunk, prefill_cap(m)),
                                        prompt_lens[i] - 1 - cursor[i]);
                 TRY(prefill_rows(m, i, pos[i], prompts + off[i] + cursor[i], k));
                 cursor[i] += k;

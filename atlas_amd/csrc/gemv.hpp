@@ -67,7 +67,8 @@ int gemv_multi_launch(const GemvArgs& a, hipStream_t st);
 size_t skinny_partial_bytes(int M, int N, int K);    // split-K partials of (M, N, K)
 // y = the fixed-order sum of `splits` partials ([splits][N][M]), with a's epilogue
 int skinny_reduce_launch(const GemvArgs& a, const float* partial, int splits, hipStream_t st);
-// 17..128 rows of bf16 weights: the tiled MFMA GEMM (skinny_launch routes there)
+// 17+ rows: the tiled MFMA GEMM (skinny_launch routes there; 128 rows per
+// launch) or, with a library context, the hipBLASLt prompt GEMM
 bool gemm_rows_ok(const GemvArgs& a);
 int gemm_rows_launch(const GemvArgs& a, hipStream_t st);
 size_t gemm_rows_partial_bytes(int M, int N, int K);

@@ -1493,7 +1493,7 @@ bool gemm_rows_ok(const GemvArgs& a) {
         : a.fmt == WF_I4 ? a.scales && (wa & 3) == 0 && a.ldw == 0 && a.block % 32 == 0 &&
                                a.bpr > 0 && (a.cpb & (a.cpb - 1)) == 0
                          : false;
-    return fmt_ok && a.N > 16 && a.N <= GR_MAX_N && a.K % 128 == 0 && a.M > 0 &&
+    return fmt_ok && a.N > 16 && a.K % 128 == 0 && a.M > 0 &&
            a.x_stride_k == 1 && a.x_stride_n % 4 == 0 && ((uintptr_t)a.x & 15) == 0 &&
            (a.epi == EPI_STORE || (a.epi == EPI_SILU_MUL && a.M % 2 == 0));
 }

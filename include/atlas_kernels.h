@@ -192,9 +192,10 @@ int atlas_gemv_fused_f32(int fmt, const void* w, const float* scales, int block,
 
 /* Ragged micro-batch: Y[n, m] = sum_k dequant(W)[m,k] X[n,k] for 1 <= n <= 16
  * activation rows (X [n x k] row-major, Y [n x m] row-major).  MFMA bf16 with
- * hi/lo split activations.  fmt: BF16, INT8, INT4.  17 <= n <= 128 rows with
+ * hi/lo split activations.  fmt: BF16, INT8, INT4.  n >= 17 rows with
  * k % 128 == 0 (int4: blocks of 32 * 2^j) take the tiled MFMA GEMM of prompt
- * chunks; other shapes outside 1..16 return ATLAS_EINVAL.                   */
+ * chunks (128 rows per launch); other shapes outside 1..16 return
+ * ATLAS_EINVAL.                                                              */
 int atlas_gemm_skinny_f32(int fmt, const void* w, const float* scales, int block,
                           const float* x, float* y, int m, int n, int k);
 /* The same row counts with the SwiGLU epilogue: W has 2*h rows interleaved
