@@ -1154,6 +1154,201 @@ __global__ __launch_bounds__(1024) void attn_prefill_kernel(AttnArgs a, int n) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The prompt chunk's attention on the matrix cores: f32 v_mfma_f32_16x16x4f32
+// (exact f32 products, as the VALU kernel above), flash-attention style.
+//  * a block of NW waves takes 16 NW consecutive rows of one query head (wave
+//    w: rows 16 w .. 16 w + 15) and streams the K/V tiles of 32 positions its
+//    rows need through LDS once for all its waves (NW = 4: the VALU kernel
+//    re-reads every tile per 16 rows);
+//  * S = Q K^T per tile: two 16 x 16 position blocks, 32 k steps of 4 dims
+//    each.  The reduction over the 128 dims may go in any order, so k step s
+//    takes dim 32 g + s from lane group g: a lane's Q stays in 32 registers and
+//    its K row segment is 8 contiguous 16-byte LDS reads;
+//  * online softmax per row in the accumulator layout (lane l holds rows
+//    4 (l / 16) + i, i < 4, of column l % 16), with 16-lane DPP reductions;
+//  * P goes through LDS to the A-operand layout, then O += P V: eight 16-dim
+//    blocks, 8 k steps of 4 positions.
+// Operand layouts (checked on MI355X): A lane l = A[l % 16][l / 16], B lane l =
+// B[l / 16][l % 16], D lane l register i = D[4 (l / 16) + i][l % 16].
+constexpr int APM_TK = 32;
+
+__device__ __forceinline__ float row16_max(float v) {
+    int x = __float_as_int(v);
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false)));
+    x = __float_as_int(v);
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false)));
+    x = __float_as_int(v);
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false)));
+    x = __float_as_int(v);
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false)));
+    return v;
+}
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void attn_prefill_mfma_kernel(AttnArgs a, int n) {
+    constexpr int HD = 128, TK = APM_TK, NT = 64 * NW, PER = 1024 / NT, ROWS = 16 * NW;
+    constexpr int KP = HD + 4, VP = HD + 16, PP = TK + 4;          // padded LDS rows
+    constexpr float LOG2E = 1.4426950408889634f;
+    __shared__ __align__(16) float tk[TK][KP];
+    __shared__ __align__(16) float tv[TK][VP];
+    __shared__ __align__(16) float tp[NW][16][PP];
+    const int qh = blockIdx.x, G = a.n_heads / a.n_kv, kvh = qh / G;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int p0 = a.pos_dev[0];
+    const long kv_stride = (long)a.n_kv * HD;
+    const float* kb = a.k_cache + (long)a.slot_dev[0] * a.slot_stride + (long)kvh * HD;
+    const float* vb = a.v_cache + (long)a.slot_dev[0] * a.slot_stride + (long)kvh * HD;
+    const int r0 = blockIdx.y * ROWS, rw = r0 + 16 * w;
+    // the block's position range: its first row's window start .. its last row
+    const int pf = p0 + r0, pl = p0 + min(r0 + ROWS, n) - 1;
+    const int lo_b = (a.window > 0 && pf >= a.window) ? pf - a.window + 1 : 0;
+    const int ntiles = (pl - lo_b) / TK + 1;
+
+    // A operand of k step s: Q[row lr][32 lg + s], scaled into exp2 space
+    float q[32];
+    {
+        const float* qr = a.q + (long)min(rw + lr, n - 1) * a.q_stride + (long)qh * HD + 32 * lg;
+        const float sc = a.scale * LOG2E;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(qr + 4 * c);
+            q[4 * c] = v.x * sc; q[4 * c + 1] = v.y * sc; q[4 * c + 2] = v.z * sc; q[4 * c + 3] = v.w * sc;
+        }
+    }
+    // this lane's accumulator rows 4 lg + i: their positions and window starts
+    int prow[4], lorow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        prow[i] = p0 + min(rw + 4 * lg + i, n - 1);
+        lorow[i] = (a.window > 0 && prow[i] >= a.window) ? prow[i] - a.window + 1 : 0;
+    }
+    float m[4], l[4];
+    f32x4 o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.f; }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // tile loads: 32 rows x 32 pieces of K and of V, PER + PER pieces per
+    // thread; rows past pl read row pl (their scores are masked)
+    f32x4 pk[PER], pv[PER];
+    auto fetch = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = (int)threadIdx.x + NT * i;
+            const int r = idx >> 5, c = idx & 31;
+            const long row = min(t0 + r, pl);
+            pk[i] = *reinterpret_cast<const f32x4*>(kb + row * kv_stride + 4 * c);
+            pv[i] = *reinterpret_cast<const f32x4*>(vb + row * kv_stride + 4 * c);
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = (int)threadIdx.x + NT * i;
+            const int r = idx >> 5, c = idx & 31;
+            *reinterpret_cast<f32x4*>(&tk[r][4 * c]) = pk[i];
+            *reinterpret_cast<f32x4*>(&tv[r][4 * c]) = pv[i];
+        }
+    };
+    fetch(lo_b);
+    stash();
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {            // block-uniform trip count
+        const int t0 = lo_b + it * TK;
+        if (it + 1 < ntiles) fetch(t0 + TK);
+        // S = Q K^T over two 16-position blocks
+        f32x4 sacc[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            sacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const float* kr = &tk[16 * nt + lr][32 * lg];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const f32x4 kv4 = *reinterpret_cast<const f32x4*>(kr + 4 * c);
+                sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * c], kv4.x, sacc[nt], 0, 0, 0);
+                sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * c + 1], kv4.y, sacc[nt], 0, 0, 0);
+                sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * c + 2], kv4.z, sacc[nt], 0, 0, 0);
+                sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * c + 3], kv4.w, sacc[nt], 0, 0, 0);
+            }
+        }
+        // online softmax of rows 4 lg + i (columns: positions t0 + 16 nt + lr)
+        float pr[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sv[2];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int t = t0 + 16 * nt + lr;
+                sv[nt] = (t >= lorow[i] && t <= prow[i]) ? sacc[nt][i] : -INFINITY;
+                mx = fmaxf(mx, sv[nt]);
+            }
+            mx = row16_max(mx);
+            const float mn = fmaxf(m[i], mx);
+            float alpha = 1.f, ps = 0.f;
+            if (mn != -INFINITY) {
+                alpha = m[i] == -INFINITY ? 0.f : exp2f(m[i] - mn);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    pr[nt][i] = sv[nt] == -INFINITY ? 0.f : exp2f(sv[nt] - mn);
+                    ps += pr[nt][i];
+                }
+                m[i] = mn;
+            } else {
+                pr[0][i] = 0.f;
+                pr[1][i] = 0.f;
+            }
+            ps = row16_sum(ps);
+            l[i] = l[i] * alpha + ps;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) o[d][i] *= alpha;
+        }
+        // P (16 rows x 32 positions of this wave) to the A-operand layout
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tp[w][4 * lg + i][16 * nt + lr] = pr[nt][i];
+        __syncthreads();
+        // O += P V: k step s takes positions 4 s .. 4 s + 3 (lane group lg: 4 s + lg)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float pa = tp[w][lr][4 * s + lg];
+            const float* vr = &tv[4 * s + lg][lr];
+#pragma unroll
+            for (int d = 0; d < 8; ++d)
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vr[16 * d], o[d], 0, 0, 0);
+        }
+        __syncthreads();                 // every wave is done with this tile's K, V and P
+        if (it + 1 < ntiles) {
+            stash();
+            __syncthreads();
+        }
+    }
+    // rows 4 lg + i of the wave, columns 16 d + lr
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int jr = rw + 4 * lg + i;
+        if (jr >= n) continue;
+        const float inv = 1.0f / l[i];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const float v = o[d][i] * inv;
+            const long off = (long)jr * a.out_stride + (long)qh * HD + 16 * d + lr;
+            if (a.out_split) {
+                const uint32_t u = __float_as_uint(v);
+                const uint32_t ur = __float_as_uint(v - __uint_as_float(u & 0xFFFF0000u));
+                a.out_split[off] = (uint16_t)(u >> 16);
+                a.out_split[a.split_lo + off] = (uint16_t)((ur + 0x7FFFu + ((ur >> 16) & 1u)) >> 16);
+            } else {
+                a.out[off] = v;
+            }
+        }
+    }
+}
+
 bool attn_prefill_ok(const AttnArgs& a) {
     const uintptr_t al = (uintptr_t)a.q | (uintptr_t)a.k_cache | (uintptr_t)a.v_cache |
                          (uintptr_t)a.out;
@@ -1165,8 +1360,17 @@ bool attn_prefill_ok(const AttnArgs& a) {
 int attn_prefill_launch(const AttnArgs& a, int n, hipStream_t st) {
     ATLAS_REQUIRE(attn_prefill_ok(a) && n >= 1, "attention: prompt-chunk kernel needs head_dim 128, "
                   "16-byte alignment and device positions/slot (n %d)", n);
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.n_heads, (n + APF_ROWS - 1) / APF_ROWS), dim3(1024),
-                       0, st, a, n);
+    // Chunks above 128 rows: the matrix-core kernel, 64 rows per block (7B
+    // bf16, 2047-token prompt in 512-row chunks: 109.5 -> 76.3 ms).  Up to 128
+    // rows the VALU kernel's 16-row blocks fill more of the chip: the MFMA
+    // kernel with 64-, 32- or 16-row blocks made the 127-token prompt 0.1-0.3 ms
+    // slower.
+    if (n > 128)
+        hipLaunchKernelGGL(attn_prefill_mfma_kernel<4>, dim3(a.n_heads, (n + 63) / 64), dim3(256), 0, st,
+                           a, n);
+    else
+        hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.n_heads, (n + APF_ROWS - 1) / APF_ROWS), dim3(1024),
+                           0, st, a, n);
     ATLAS_LAUNCH_CHECK("attn_prefill");
     return ATLAS_OK;
 }
