@@ -55,9 +55,11 @@ constexpr int kMaxRows = kPrefillChunk;
 // through the tiled MFMA GEMM (gemm_rows_launch), up to this many rows
 // per step, replayed eagerly (the captured steps stop at kMaxRows rows).
 constexpr int kPrefillBig = 128;
-// ... and up to this many rows where the library GEMM serves them (bf16 and
-// int8 weights): at the 7B shapes the GEMMs of a layer cost 1.28 us per
-// prompt token at 127 rows, 0.87 at 255 and 0.68 at 511 (bf16).
+// ... and up to this many rows per step in all: the library GEMM (bf16, int8)
+// takes them at once (at the 7B shapes the GEMMs of a layer cost 1.28 us per
+// prompt token at 127 rows, 0.87 at 255 and 0.68 at 511, bf16), the tiled
+// kernel (int4) in 128-row launches; the chunk's attention then runs on the
+// matrix cores (above 128 rows).
 constexpr int kPrefillLib = 512;
 
 struct DevMat {
@@ -111,9 +113,8 @@ struct atlas_model {
     int hd = 0, kvd = 0, qkv_rows = 0, B = 1;
     int R = 1;                       // rows of the multi-row step buffers: max(B, prefill chunk)
     int RF = 1;                      // rows with a fused attention, logits and a choice: max(B, 16 or 128)
-    int prefill_chunk = kPrefillBig;     // prompt tokens per prefill step (1: token by token)
-    bool big_prefill = false;            // chunks of up to kPrefillBig rows (kPrefillLib through
-                                         // the library GEMM; see prefill_cap)
+    int prefill_chunk = kPrefillLib;     // prompt tokens per prefill step (1: token by token)
+    bool big_prefill = false;            // chunks above 16 rows, up to kPrefillLib (prefill_cap)
     float scale = 1.f;
     std::vector<LayerW> L;
     uint16_t* embed = nullptr;
@@ -1337,7 +1338,7 @@ int run_batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool lo
 int prefill_cap(const atlas_model* m) {
     if (!m->fused) return 1;
     if (!m->big_prefill) return std::min(m->R, kPrefillChunk);
-    return std::min(m->R, m->blas ? kPrefillLib : kPrefillBig);
+    return std::min(m->R, kPrefillLib);
 }
 
 int prefill_rows(atlas_model* m, int slot, int pos0, const uint32_t* toks, int k) {
@@ -1434,9 +1435,8 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
                      attn_rows_fit(c.max_seq, c.n_kv_heads, hd) && c.d_model % 128 == 0 &&
                      (c.n_heads * hd) % 128 == 0 && c.ffn_hidden % 128 == 0;
     m->RF = std::max(m->B, m->big_prefill ? kPrefillBig : kPrefillChunk);
-    // bf16 / int8 prompt chunks through the library GEMM take up to kPrefillLib rows
-    const bool lib_rows = m->big_prefill && (fmt == WF_BF16 || fmt == WF_I8);
-    m->R = std::max(m->RF, lib_rows ? kPrefillLib : 0);
+    // prompt chunks take up to kPrefillLib rows
+    m->R = std::max(m->RF, m->big_prefill ? kPrefillLib : 0);
     // scale = attn_factor / sqrt(head_dim) (lib.rs:632, 1331-1335)
     m->scale = 1.0f / sqrtf((float)hd);
     const float af = c.yarn ? c.yarn_attn_factor : 1.0f;
@@ -1543,7 +1543,7 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
                 if (atlas_last_error_code() == ATLAS_ENOMEM) return fail(m);
                 atlas_clear_error();
             }
-            if (m->blas) m->prefill_chunk = kPrefillLib;    // the default: the longest step
+
         }
     }
     // fused step: post-norm model whose attention shape the fused kernel

@@ -247,9 +247,8 @@ class OlmoModel:
         check(load().atlas_model_prefill(self._h, _p(t), len(tokens)))
 
     def set_prefill_chunk(self, chunk: int) -> None:
-        """Tokens per prefill step, 1..512 (1 = token by token; above 16 needs GEMM
-        inner dims that are multiples of 128, else 16 is used; above 128 needs
-        bf16 or int8 weights, else 128 is used)."""
+        """Tokens per prefill step, 1..512 (default 512; 1 = token by token; above
+        16 needs GEMM inner dims that are multiples of 128, else 16 is used)."""
         check(load().atlas_model_set_prefill_chunk(self._h, chunk))
 
     def use_graph(self, enable: bool) -> None:

@@ -142,11 +142,9 @@ int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits
  * token-by-token loop (lib.rs:1612-1618) would.  Extension: the reference
  * feeds one token per forward.                                              */
 int atlas_model_prefill(atlas_model* m, const uint32_t* tokens, int n);
-/* Tokens per prefill step, 1..512 (1 = token by token).  Chunks above 16
- * need GEMM inner dims that are multiples of 128 and, for int4, blocks of
- * 32 * 2^j (the tiled MFMA GEMM, at most 128 rows); other models cap them at
- * 16.  bf16 and int8 models with the library GEMM take up to 512 rows per
- * step and default to 512; the others default to 128.                      */
+/* Tokens per prefill step, 1..512 (default 512; 1 = token by token).
+ * Chunks above 16 need GEMM inner dims that are multiples of 128 and, for
+ * int4, blocks of 32 * 2^j; other models cap them at 16.                    */
 int atlas_model_set_prefill_chunk(atlas_model* m, int chunk);
 
 /* generate_with_sampling: resets, feeds the prompt (atlas_model_prefill), then

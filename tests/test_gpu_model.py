@@ -294,10 +294,10 @@ def test_prefill_chunks_head_dim_128(orc, fmt):
     # head_dim 128 takes the query-tiled prompt attention (16 rows per K/V
     # tile): chunks of 128 with sliding-window layers (window 16 < chunk),
     # ragged last row blocks and a later chunk that starts mid-window; the
-    # next token's logits agree with the oracle.  The chunks' GEMMs go through
-    # the library for bf16 (hi/lo rows) and int8 (digit rows), up to 512 rows
-    # per step (the 299-token prompt is one chunk), and through the tiled
-    # kernel for int4, 128 rows per step.
+    # next token's logits agree with the oracle.  Up to 512 rows per step (the
+    # 299-token prompt is one chunk, whose attention runs on the matrix cores):
+    # the GEMMs go through the library for bf16 (hi/lo rows) and int8 (digit
+    # rows), and through the tiled kernel in 128-row launches for int4.
     cfg = modelgen.olmo3_small_config(n_heads=2, n_kv_heads=2, max_seq=320)
     W = modelgen.make_weights(cfg, seed=73, fmt=fmt)
     toks = [int(t) for t in np.random.default_rng(14).integers(0, cfg["vocab"], 300)]
