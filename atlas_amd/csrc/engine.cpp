@@ -133,7 +133,7 @@ struct atlas_model {
     // the model's own, so captured steps never point at shared scratch
     float* gemm_part = nullptr;
     size_t gemm_part_bytes = 0;
-    // bf16 prompt chunks (17..128 rows): hipBLASLt context (null: the tiled kernel)
+    // bf16 / int8 prompt chunks (17..512 rows): hipBLASLt context (null: the tiled kernel)
     BlasRows* blas = nullptr;
     bool fused = false;
     int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
@@ -1085,7 +1085,7 @@ int bmm_resnorm(atlas_model* m, const DevMat& w, const float* x, float* y, int n
     return residual_rmsnorm_launch(m->x, y, norm_w, c.d_model, n, c.d_model, c.rms_eps, m->st);
 }
 
-// A prompt chunk of 17..128 rows whose four GEMMs per layer all take the
+// A prompt chunk of 17..512 rows whose four GEMMs per layer all take the
 // hipBLASLt path (post-norm): their activation split and product combine then
 // live in the neighbouring kernels where those see whole rows -- the split of
 // x in the residual RMSNorm that produces it (and once after the embedding),

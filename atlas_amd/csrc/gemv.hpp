@@ -48,7 +48,7 @@ struct GemvArgs {
     // by the consumer) and stores the split count here instead of launching
     // the reduce; 0 when y was written.
     int* defer_splits;
-    struct BlasRows* blas;   // 17..128 rows of bf16 weights: the caller's hipBLASLt context, or
+    struct BlasRows* blas;   // 17+ rows of bf16 / int8 weights: the caller's hipBLASLt context, or
                              // null (the tiled MFMA kernel)
 };
 

@@ -1803,7 +1803,7 @@ int skinny_launch(const GemvArgs& a_in, hipStream_t st) {
         return a.blas && (a.fmt == WF_BF16 || (a.fmt == WF_I8 && a.K <= kDigitsMaxK))
                    ? blas_rows_launch(a.blas, a, st)
                    : gemm_rows_launch(a, st);
-    ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17..128 rows need K %% 128 == 0 "
+    ATLAS_REQUIRE(a.N >= 1 && a.N <= 16, "skinny: N=%d outside 1..16 (17+ rows need K %% 128 == 0 "
                   "and, for int4, blocks of 32 * 2^j)", a.N);
     ATLAS_REQUIRE(a.w && a.x && a.y, "skinny: null pointer");
     ATLAS_REQUIRE(a.fmt == WF_BF16 || a.scales, "skinny: null scales");
