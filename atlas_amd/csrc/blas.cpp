@@ -1,4 +1,4 @@
-// blas.cpp -- the bf16 and int8 prompt GEMMs (17..512 activation rows)
+// blas.cpp -- the bf16 and int8 prompt GEMMs (17..1024 activation rows)
 // through hipBLASLt.
 //
 // Y[n, m] = sum_k W[m, k] X[n, k] with W [M x K] (row pitch ldw) and X f32, as

@@ -57,10 +57,11 @@ constexpr int kMaxRows = kPrefillChunk;
 constexpr int kPrefillBig = 128;
 // ... and up to this many rows per step in all: the library GEMM (bf16, int8)
 // takes them at once (at the 7B shapes the GEMMs of a layer cost 1.28 us per
-// prompt token at 127 rows, 0.87 at 255 and 0.68 at 511, bf16), the tiled
-// kernel (int4) in 128-row launches; the chunk's attention then runs on the
-// matrix cores (above 128 rows).
-constexpr int kPrefillLib = 512;
+// prompt token at 127 rows, 0.87 at 255 and 0.68 at 511, bf16; a 2047-token
+// prompt took 76.8 ms in 512-row chunks and 68.9 in 1024), the tiled kernel
+// (int4) in 128-row launches; the chunk's attention then runs on the matrix
+// cores (above 128 rows).
+constexpr int kPrefillLib = 1024;
 
 struct DevMat {
     int fmt = WF_BF16;
@@ -133,7 +134,7 @@ struct atlas_model {
     // the model's own, so captured steps never point at shared scratch
     float* gemm_part = nullptr;
     size_t gemm_part_bytes = 0;
-    // bf16 / int8 prompt chunks (17..512 rows): hipBLASLt context (null: the tiled kernel)
+    // bf16 / int8 prompt chunks (17..1024 rows): hipBLASLt context (null: the tiled kernel)
     BlasRows* blas = nullptr;
     bool fused = false;
     int *pos_dev = nullptr, *slot_dev = nullptr, *step_dev = nullptr, *hist_len = nullptr;
@@ -1085,7 +1086,7 @@ int bmm_resnorm(atlas_model* m, const DevMat& w, const float* x, float* y, int n
     return residual_rmsnorm_launch(m->x, y, norm_w, c.d_model, n, c.d_model, c.rms_eps, m->st);
 }
 
-// A prompt chunk of 17..512 rows whose four GEMMs per layer all take the
+// A prompt chunk of 17..1024 rows whose four GEMMs per layer all take the
 // hipBLASLt path (post-norm): their activation split and product combine then
 // live in the neighbouring kernels where those see whole rows -- the split of
 // x in the residual RMSNorm that produces it (and once after the embedding),

@@ -247,7 +247,7 @@ class OlmoModel:
         check(load().atlas_model_prefill(self._h, _p(t), len(tokens)))
 
     def set_prefill_chunk(self, chunk: int) -> None:
-        """Tokens per prefill step, 1..512 (default 512; 1 = token by token; above
+        """Tokens per prefill step, 1..1024 (default 1024; 1 = token by token; above
         16 needs GEMM inner dims that are multiples of 128, else 16 is used)."""
         check(load().atlas_model_set_prefill_chunk(self._h, chunk))
 

@@ -142,7 +142,7 @@ int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits
  * token-by-token loop (lib.rs:1612-1618) would.  Extension: the reference
  * feeds one token per forward.                                              */
 int atlas_model_prefill(atlas_model* m, const uint32_t* tokens, int n);
-/* Tokens per prefill step, 1..512 (default 512; 1 = token by token).
+/* Tokens per prefill step, 1..1024 (default 1024; 1 = token by token).
  * Chunks above 16 need GEMM inner dims that are multiples of 128 and, for
  * int4, blocks of 32 * 2^j; other models cap them at 16.                    */
 int atlas_model_set_prefill_chunk(atlas_model* m, int chunk);
