@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -1086,6 +1087,13 @@ int bmm_resnorm(atlas_model* m, const DevMat& w, const float* x, float* y, int n
     return residual_rmsnorm_launch(m->x, y, norm_w, c.d_model, n, c.d_model, c.rms_eps, m->st);
 }
 
+// The hipBLASLt prompt GEMMs are used only when the environment sets
+// ATLAS_PROMPT_BLAS=1 at model creation.
+bool prompt_blas_opt_in() {
+    const char* e = std::getenv("ATLAS_PROMPT_BLAS");
+    return e && std::strcmp(e, "1") == 0;
+}
+
 // A prompt chunk of 17..1024 rows whose four GEMMs per layer all take the
 // hipBLASLt path (post-norm): their activation split and product combine then
 // live in the neighbouring kernels where those see whole rows -- the split of
@@ -1531,9 +1539,14 @@ ATLAS_API atlas_model* atlas_model_create(const atlas_model_config* cfg) {
         if (need && dalloc(m, (void**)&m->gemm_part, need)) return fail(m);
         m->gemm_part_bytes = need;
         // bf16 and int8 prompt chunks through hipBLASLt (bf16 1.6x the tiled
-        // kernel's rate at 127 rows of the 7B shapes); without a library
-        // context the tiled kernel serves them, as it serves int4
-        if (m->big_prefill && (fmt == WF_BF16 || fmt == WF_I8)) {
+        // kernel's rate at 127 rows of the 7B shapes) only when the
+        // environment sets ATLAS_PROMPT_BLAS=1.  Off by default: one process
+        // that had created and destroyed two library contexts (and run an
+        // int4 model between) saw the library report that it could not
+        // initialise its kernel host, then crash, and the cause is not
+        // known.  Without a library context the tiled kernel serves every
+        // prompt chunk, as it serves int4.
+        if (m->big_prefill && (fmt == WF_BF16 || fmt == WF_I8) && prompt_blas_opt_in()) {
             int max_m = 0, max_k = 0;
             for (const auto& sh : shapes) {
                 max_m = std::max(max_m, sh[0]);
