@@ -1317,19 +1317,15 @@ static int launch_skinny_lds(const GemvArgs& a, hipStream_t st) {
 // Per 32-k step a wave issues NT x 2 x 2 MFMAs (tiles x B fragments x hi/lo).
 constexpr int GR_ROWS = 128;        // weight rows per block
 constexpr int GR_MAX_N = 128;       // activation rows per launch
+// (k step, tile) items whose A fragments are read ahead of the current one
+constexpr int GR_AHEAD = 4;
 
-// hi / lo bf16 parts of 8 floats, packed as MFMA operands
+// hi / lo bf16 parts of 8 floats, packed as MFMA operands: hi = the high
+// halves (truncation), lo = the remainder rounded to nearest even (one
+// hardware conversion per pair)
 __device__ __forceinline__ void split8(const f32x4 p0, const f32x4 p1, u32x4& hi, u32x4& lo) {
-    const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-    uint32_t h[8], l[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const uint32_t u = __float_as_uint(v[e]);
-        h[e] = u >> 16;
-        l[e] = bf16_rne_bits(v[e] - __uint_as_float(u & 0xFFFF0000u));
-    }
-    hi = u32x4{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
-    lo = u32x4{pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])};
+    hi = u32x4{bf16_hi2(p0.x, p0.y), bf16_hi2(p0.z, p0.w), bf16_hi2(p1.x, p1.y), bf16_hi2(p1.z, p1.w)};
+    lo = u32x4{bf16_lo2(p0.x, p0.y), bf16_lo2(p0.z, p0.w), bf16_lo2(p1.x, p1.y), bf16_lo2(p1.z, p1.w)};
 }
 
 // int4 at eight tiles runs one block per CU: its per-step scaled products
@@ -1393,45 +1389,98 @@ __global__ __launch_bounds__(256, (FMT == WF_I4 && NT == 8) ? 1 : 2) void gemm_r
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // one chunk: stash the next chunk's items, read the one after, then the
-    // MFMAs of k steps 2c, 2c+1 (B slots u0, u0+1)
+    // One chunk (k steps 2c, 2c+1; B slots u0, u0+1) as 2 NT items (k step,
+    // tile) in order.  Each item's A fragments are read from LDS GR_AHEAD
+    // items before its MFMAs, and X item q of chunk c+1 is split into the
+    // other LDS buffer (then its registers take chunk c+2's item) between the
+    // MFMAs of items 4q and 4q+1; scheduling barriers hold that order, so the
+    // LDS latency and the split's VALU work overlap the matrix cores instead
+    // of preceding them.
     auto chunk_body = [&](int c, int buf, int u0) {
-        if (c + 1 < nchunks) {
-#pragma unroll
-            for (int q = 0; q < ITEMS; ++q) xstore(buf ^ 1, q, xr0[q], xr1[q]);
-        }
         const int cn = min(c + 2, nchunks - 1);
+        if constexpr (FMT == WF_I4 && NT == 8) {
+            // int4 at eight tiles keeps its per-step products in registers
+            // already (one block per CU); the items' extra live fragments
+            // would spill, so its chunk runs the plain order: X items first,
+            // then each k step's MFMAs with the A fragments read as used
+            if (c + 1 < nchunks) {
 #pragma unroll
-        for (int q = 0; q < ITEMS; ++q) xload(cn, q, xr0[q], xr1[q]);
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            const int u = u0 + st, s = s0 + 2 * c + st;
-            bf16x8 b[2];
-            float sc[2] = {1.0f, 1.0f};
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                b[j] = sk_operand<FMT>(B[u][j]);
-                if constexpr (FMT == WF_BF16) asm volatile("" : "+v"(b[j]));
-                if constexpr (FMT == WF_I4) sc[j] = B[u][j].s;
-                // refill: step s + 4
-                sk_load<FMT>(wrow[j], min(s + 4, s1 - 1), g, cpb_shift, B[u][j]);
+                for (int q = 0; q < ITEMS; ++q) xstore(buf ^ 1, q, xr0[q], xr1[q]);
             }
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const bf16x8 ah = __builtin_bit_cast(bf16x8, As[buf][st][t][0][lane]);
-                const bf16x8 al = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane]);
+            for (int q = 0; q < ITEMS; ++q) xload(cn, q, xr0[q], xr1[q]);
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const int u = u0 + st, s = s0 + 2 * c + st;
+                bf16x8 bb[2];
+                float ss[2];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    if constexpr (FMT == WF_I4) {
-                        // the step is one scale block of the lane's row
-                        f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            ah, b[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], d, 0, 0, 0);
-                        acc[t][j] += d * sc[j];
-                    } else {
-                        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[j], acc[t][j], 0, 0, 0);
-                        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], acc[t][j], 0, 0, 0);
+                    bb[j] = sk_operand<FMT>(B[u][j]);
+                    ss[j] = B[u][j].s;
+                    sk_load<FMT>(wrow[j], min(s + 4, s1 - 1), g, cpb_shift, B[u][j]);   // refill: step s + 4
+                }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const bf16x8 xh = __builtin_bit_cast(bf16x8, As[buf][st][t][0][lane]);
+                    const bf16x8 xl = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane]);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, bb[j], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                          0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, bb[j], d, 0, 0, 0);
+                        acc[t][j] += d * ss[j];
                     }
+                }
+            }
+            __syncthreads();
+            return;
+        }
+        constexpr int NI = 2 * NT, D = GR_AHEAD < NI ? GR_AHEAD : NI;
+        bf16x8 ah[NI], al[NI];
+        bf16x8 b[2][2];
+        float sc[2][2];
+        auto aread = [&](int i) {
+            const int st = i / NT, t = i % NT;
+            ah[i] = __builtin_bit_cast(bf16x8, As[buf][st][t][0][lane]);
+            al[i] = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane]);
+        };
+        auto bprep = [&](int st) {
+            const int u = u0 + st, s = s0 + 2 * c + st;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                b[st][j] = sk_operand<FMT>(B[u][j]);
+                if constexpr (FMT == WF_BF16) asm volatile("" : "+v"(b[st][j]));
+                sc[st][j] = 1.0f;
+                if constexpr (FMT == WF_I4) sc[st][j] = B[u][j].s;
+                sk_load<FMT>(wrow[j], min(s + 4, s1 - 1), g, cpb_shift, B[u][j]);   // refill: step s + 4
+            }
+        };
+        bprep(0);
+#pragma unroll
+        for (int i = 0; i < D; ++i) aread(i);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (i + D < NI) aread(i + D);
+            if (i == NT) bprep(1);
+            if (i % 4 == 1) {
+                const int q = i / 4;                  // ITEMS = NI / 4
+                if (c + 1 < nchunks) xstore(buf ^ 1, q, xr0[q], xr1[q]);
+                xload(cn, q, xr0[q], xr1[q]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const int st = i / NT, t = i % NT;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if constexpr (FMT == WF_I4) {
+                    // the step is one scale block of the lane's row
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], b[st][j],
+                                                                      f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], b[st][j], d, 0, 0, 0);
+                    acc[t][j] += d * sc[st][j];
+                } else {
+                    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], b[st][j], acc[t][j], 0, 0, 0);
+                    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], b[st][j], acc[t][j], 0, 0, 0);
                 }
             }
         }
