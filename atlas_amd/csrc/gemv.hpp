@@ -43,10 +43,11 @@ struct GemvArgs {
     float* partial;          // skinny / prompt GEMM split-K partials (null: the thread's scratch)
     size_t partial_bytes;    // ... their size
     // skinny_launch, host side: non-null with EPI_STORE and the caller's
-    // partial buffer, a split-K launch of the 2-8-row direct-load kernels
-    // leaves its partials in `partial` ([splits][N][M], summed in split order
-    // by the consumer) and stores the split count here instead of launching
-    // the reduce; 0 when y was written.
+    // partial buffer, a split-K launch of the 2-8-row direct-load kernels or
+    // of the tiled prompt GEMM (17-128 rows, one launch) leaves its partials
+    // in `partial` ([splits][N][M], summed in split order by the consumer)
+    // and stores the split count here instead of launching the reduce; 0
+    // when y was written.
     int* defer_splits;
     struct BlasRows* blas;   // 17+ rows of bf16 / int8 weights: the caller's hipBLASLt context, or
                              // null (the tiled MFMA kernel)

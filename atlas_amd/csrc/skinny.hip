@@ -1573,7 +1573,8 @@ size_t gemm_rows_partial_bytes(int M, int N, int K) {
     return (size_t)splits * N * M * sizeof(float);
 }
 
-// one launch (+ split-K reduce) over all a.N <= 128 rows
+// one launch (+ split-K reduce, unless a.defer_splits takes the split count)
+// over all a.N <= 128 rows
 static int gemm_rows_part(const GemvArgs& a, hipStream_t st) {
     int splits, steps;
     gemm_rows_split(a.M, a.K, splits, steps);
@@ -1591,6 +1592,10 @@ static int gemm_rows_part(const GemvArgs& a, hipStream_t st) {
     else rc = gemm_rows_go<WF_I4>(a, partial, grid, steps, cpb_shift, st);
     if (rc) return rc;
     ATLAS_LAUNCH_CHECK("gemm_rows");
+    if (splits > 1 && defer_ok(a)) {
+        *a.defer_splits = splits;             // the consumer sums the partials
+        return ATLAS_OK;
+    }
     if (splits > 1) {
         const long m_out = a.epi == EPI_SILU_MUL ? a.M / 2 : a.M;
         long rb = ((long)a.N * m_out + 255) / 256;
@@ -1807,6 +1812,7 @@ int gemm_rows_launch(const GemvArgs& a, hipStream_t st) {
         p.N = std::min(cap, a.N - n0);
         p.x = a.x + (long)n0 * a.x_stride_n;
         p.y = a.y + (long)n0 * a.y_stride_n;
+        if (a.N > cap) p.defer_splits = nullptr;   // the parts share one partial buffer
         int rc = gemm_rows_part(p, st);
         if (rc) return rc;
     }
