@@ -1158,9 +1158,19 @@ int batch_step(atlas_model* m, int n, const std::vector<int>& slots, bool long_c
             TRY(rmsnorm_launch(m->x, L.attn_norm, m->xn, d, n, d, c.rms_eps, m->st));
             xin = m->xn;
         }
+        // the separate-kernel path (long contexts) lets qkv_post sum the
+        // QKV GEMM's split-K partials in place of the reduce launch
+        int qkv_splits = 0;
         if (bc) TRY(blas_gemm(m, L.qkv, n));
+        else if (m->fused && long_ctx && n > 1) TRY(skinny(m, L.qkv, xin, m->qkv, n, EPI_STORE, &qkv_splits));
         else TRY(bmm(m, L.qkv, xin, m->qkv, n, EPI_STORE));
         QkvPostArgs q{};
+        if (qkv_splits > 0) {
+            q.src_parts = m->gemm_part;
+            q.src_splits = qkv_splits;
+            q.src_stride = L.qkv.rows;
+            q.src_lo = (long)n * L.qkv.rows;
+        }
         if (bc) {
             if (b8) {
                 q.src_d = (const int*)dd;

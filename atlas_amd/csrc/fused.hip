@@ -314,8 +314,13 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
     const int slot = a.slot_dev ? a.slot_dev[s] : 0;
     const long cache_off = (long)slot * a.slot_stride + ((long)pos * nkv) * HD;
     // element off of this sequence's q|k|v: in place, or hi + lo product rows
-    const long src_off = (a.src || a.src_d) ? (long)s * a.src_stride : 0;
+    const long src_off = (a.src || a.src_d || a.src_parts) ? (long)s * a.src_stride : 0;
     auto in = [&](long off) {
+        if (a.src_parts) {
+            float sum = 0.f;
+            for (int p = 0; p < a.src_splits; ++p) sum += a.src_parts[p * a.src_lo + off];
+            return sum;
+        }
         if (a.src_d) {
             // int8 digit products: planes src_lo apart, scales per row and column
             const int* p = a.src_d + off;

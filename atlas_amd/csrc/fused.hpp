@@ -34,6 +34,11 @@ struct QkvPostArgs {
     const int* src_d;
     const float* src_ws;
     const float* src_xs;
+    // non-null (src, src_d null): split-K partials of the QKV GEMM instead,
+    // element e of sequence s = the sum over p < src_splits, in p order, of
+    // src_parts[p * src_lo + s * src_stride + e] (the split-K reduce's sum)
+    const float* src_parts;
+    int src_splits;
 };
 
 struct ArgmaxArgs {

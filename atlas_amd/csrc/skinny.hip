@@ -1401,14 +1401,8 @@ __global__ __launch_bounds__(256, (FMT == WF_I4 && NT == 8) ? 1 : 2) void gemm_r
         if constexpr (FMT == WF_I4 && NT == 8) {
             // int4 at eight tiles keeps its per-step products in registers
             // already (one block per CU); the items' extra live fragments
-            // would spill, so its chunk runs the plain order: X items first,
-            // then each k step's MFMAs with the A fragments read as used
-            if (c + 1 < nchunks) {
-#pragma unroll
-                for (int q = 0; q < ITEMS; ++q) xstore(buf ^ 1, q, xr0[q], xr1[q]);
-            }
-#pragma unroll
-            for (int q = 0; q < ITEMS; ++q) xload(cn, q, xr0[q], xr1[q]);
+            // would spill, so its A fragments are read as used, and X item q
+            // of the next chunk is split between k step 0's tiles 2q and 2q+1
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const int u = u0 + st, s = s0 + 2 * c + st;
@@ -1422,6 +1416,12 @@ __global__ __launch_bounds__(256, (FMT == WF_I4 && NT == 8) ? 1 : 2) void gemm_r
                 }
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
+                    if (st == 0 && (t & 1)) {
+                        const int q = t >> 1;
+                        if (c + 1 < nchunks) xstore(buf ^ 1, q, xr0[q], xr1[q]);
+                        xload(cn, q, xr0[q], xr1[q]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                     const bf16x8 xh = __builtin_bit_cast(bf16x8, As[buf][st][t][0][lane]);
                     const bf16x8 xl = __builtin_bit_cast(bf16x8, As[buf][st][t][1][lane]);
 #pragma unroll
