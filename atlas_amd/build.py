@@ -4,7 +4,8 @@ The reference compiles kernels/matmul.cu with nvcc from build.rs
 (crates/atlas-tensor/build.rs:19-107); this is the hipcc equivalent: one
 shared library with the extern "C" ABI of include/atlas_kernels.h and
 include/atlas_engine.h, linked against the HIP runtime and hipBLASLt (the
-bf16 and int8 prompt GEMMs of 17..1024 rows; every other kernel is
+bf16 and int8 prompt GEMMs of 17..1024 rows, used only when ATLAS_PROMPT_BLAS=1
+at model creation; every other kernel, and by default those GEMMs too, is
 hand-written HIP).
 
 Usage: python -m atlas_amd.build   (or atlas_amd.build.build())

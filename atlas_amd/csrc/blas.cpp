@@ -15,7 +15,9 @@
 //    applies both scales.
 // The weights stream once per chunk; the combine applies the store or SwiGLU
 // epilogue.  A plain library GEMM: the hand-written kernel keeps int4 (block
-// dequantisation fused) and every shape this path does not take.
+// dequantisation fused) and every shape this path does not take.  A model
+// creates this context only when ATLAS_PROMPT_BLAS=1 (engine.cpp); otherwise
+// the hand-written kernel serves every prompt chunk.
 //
 // Layouts in the library's column-major terms: W is K x M with leading
 // dimension ldw / element size and is transposed (op T), the split rows are

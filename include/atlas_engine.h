@@ -144,7 +144,10 @@ int atlas_model_forward_one_hooked(atlas_model* m, uint32_t token, float* logits
 int atlas_model_prefill(atlas_model* m, const uint32_t* tokens, int n);
 /* Tokens per prefill step, 1..1024 (default 1024; 1 = token by token).
  * Chunks above 16 need GEMM inner dims that are multiples of 128 and, for
- * int4, blocks of 32 * 2^j; other models cap them at 16.                    */
+ * int4, blocks of 32 * 2^j; other models cap them at 16.  Their GEMMs run on
+ * the library's own tiled kernel; ATLAS_PROMPT_BLAS=1 in the environment at
+ * model creation sends bf16 / int8 chunks through hipBLASLt instead (off by
+ * default: see INTEGRATION.md).                                             */
 int atlas_model_set_prefill_chunk(atlas_model* m, int chunk);
 
 /* generate_with_sampling: resets, feeds the prompt (atlas_model_prefill), then
