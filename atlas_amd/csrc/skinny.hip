@@ -1525,9 +1525,15 @@ __global__ __launch_bounds__(256, (FMT == WF_I4 && NT == 8) ? 1 : 2) void gemm_r
 // CU, each split a multiple of four k steps.  (Two per CU, the occupancy
 // limit, measured 3% slower over the 7B GEMMs at 128 rows and 8% at 64:
 // the extra partials and reduce cost more than the second block gains.)
-static void gemm_rows_split(int M, int K, int& splits, int& steps) {
+// int4 (one block per CU at eight tiles) takes no K split once its row blocks
+// alone cover 60% of the CUs: a second split's blocks would run as a second
+// round, and its partials and reduce cost ~7 us (7B gate/up, 127-token int4
+// prefill 12.0 -> 11.8 ms).  For bf16 and int8 (two blocks per CU) the split
+// stays faster (8.0 against 7.8 ms, 8.1 against 7.5 ms).
+static void gemm_rows_split(int M, int K, int& splits, int& steps, int fmt = WF_BF16) {
     const int bx = (M + GR_ROWS - 1) / GR_ROWS, ksteps = K / 32;
-    int want = (device_cu_count() + bx - 1) / bx;
+    const int cus = device_cu_count();
+    int want = fmt == WF_I4 && 5 * bx >= 3 * cus ? 1 : (cus + bx - 1) / bx;
     want = std::max(1, std::min(want, ksteps / 4));
     steps = ((ksteps + want - 1) / want + 3) / 4 * 4;
     splits = (ksteps + steps - 1) / steps;
@@ -1577,7 +1583,7 @@ size_t gemm_rows_partial_bytes(int M, int N, int K) {
 // over all a.N <= 128 rows
 static int gemm_rows_part(const GemvArgs& a, hipStream_t st) {
     int splits, steps;
-    gemm_rows_split(a.M, a.K, splits, steps);
+    gemm_rows_split(a.M, a.K, splits, steps, a.fmt);
     float* partial = nullptr;
     if (splits > 1) {
         int rc = partial_for(a, (size_t)splits * a.N * a.M * sizeof(float), &partial);
